@@ -1,0 +1,180 @@
+/*
+ * attn_capi.h - C ABI of the MI355X (gfx950) causal multi-head attention library
+ * (libtcamd_attn.so).
+ *
+ * Every entry point takes plain device pointers, int sizes, a float scale and a
+ * hipStream_t (an opaque pointer; pass NULL for the null stream).  Nothing here
+ * allocates device memory, synchronises the host, or keeps state between calls, so
+ * every entry point may be captured into a HIP graph.  Work is enqueued on `stream`.
+ *
+ * Every entry point returns an attn_status.  Arguments are validated on the host
+ * before anything is launched: a non-zero status means nothing was enqueued (except
+ * ATTN_ERROR_LAUNCH, which reports the HIP error of a launch that was attempted).
+ *
+ * Layouts (all row-major, contiguous):
+ *   qkv, dqkv          (B, T, 3*H*d_head)       q | k | v column blocks, head h at [h*d, (h+1)*d)
+ *   q, k, v, o, dO ... (B, H, T, d_head)        head-major
+ *   m, l, D            (B, H, T)                per-row softmax statistics / dot(dO, O)
+ *   scores, probs ...  (B*H*T, T)               materialised score matrices
+ *
+ * bf16 tensors are passed as attn_bf16 (the 16-bit pattern of a bfloat16 value).
+ */
+#ifndef TCAMD_ATTN_CAPI_H
+#define TCAMD_ATTN_CAPI_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef uint16_t attn_bf16;
+
+typedef enum attn_status {
+    ATTN_SUCCESS = 0,
+    ATTN_ERROR_INVALID_DIM = 1,          /* B, H, T or d_head <= 0, or a size that overflows */
+    ATTN_ERROR_UNSUPPORTED_HEAD_DIM = 2, /* tiled kernels: d_head not in {32, 64, 128}        */
+    ATTN_ERROR_NULL_POINTER = 3,         /* a required pointer is NULL                        */
+    ATTN_ERROR_MISALIGNED = 4,           /* a pointer the kernel reads 16 bytes at a time is  */
+                                         /* not 16-byte aligned                               */
+    ATTN_ERROR_LAUNCH = 5,               /* hipGetLastError() after the launch was not success */
+    ATTN_ERROR_INVALID_VALUE = 6         /* scale not finite and > 0, batch count <= 0, ...   */
+} attn_status;
+
+/* Human-readable name of a status code (static storage, never NULL). */
+const char* attn_status_string(int status);
+
+/* Library version: major*10000 + minor*100 + patch. */
+int attn_version(void);
+
+/* ------------------------------------------------------------------------------------------
+ * QKV split-transpose  (B, T, 3*H*d) -> 3 x (B, H, T, d)  and its inverse scatter.
+ * Any d_head >= 1; 16-byte vector path when d_head*sizeof(elem) is a multiple of 16 and
+ * pointers are aligned, element path otherwise.
+ * ------------------------------------------------------------------------------------------ */
+
+/* Replaces qkv_split_transpose_forward, include/kernels/attention.cuh:5-11. */
+int attn_qkv_split_transpose_forward_f32(const float* qkv, float* q, float* k, float* v,
+                                         int B, int T, int H, int d_head, hipStream_t stream);
+/* Replaces qkv_split_transpose_backward, include/kernels/attention.cuh:13-19. */
+int attn_qkv_split_transpose_backward_f32(const float* dq, const float* dk, const float* dv,
+                                          float* dqkv, int B, int T, int H, int d_head,
+                                          hipStream_t stream);
+/* bf16 fast path: no reference counterpart (the reference is fp32-only).  The f32->bf16
+ * forward fuses the round-to-nearest-even cast into the copy; the bf16->f32 backward
+ * widens exactly. */
+int attn_qkv_split_transpose_forward_bf16(const attn_bf16* qkv, attn_bf16* q, attn_bf16* k,
+                                          attn_bf16* v, int B, int T, int H, int d_head,
+                                          hipStream_t stream);
+int attn_qkv_split_transpose_forward_f32_bf16(const float* qkv, attn_bf16* q, attn_bf16* k,
+                                              attn_bf16* v, int B, int T, int H, int d_head,
+                                              hipStream_t stream);
+int attn_qkv_split_transpose_backward_bf16(const attn_bf16* dq, const attn_bf16* dk,
+                                           const attn_bf16* dv, attn_bf16* dqkv, int B, int T,
+                                           int H, int d_head, hipStream_t stream);
+int attn_qkv_split_transpose_backward_bf16_f32(const attn_bf16* dq, const attn_bf16* dk,
+                                               const attn_bf16* dv, float* dqkv, int B, int T,
+                                               int H, int d_head, hipStream_t stream);
+
+/* ------------------------------------------------------------------------------------------
+ * Head merge  (B, H, T, d) <-> (B, T, H*d)
+ * ------------------------------------------------------------------------------------------ */
+
+/* Replaces head_merge_transpose_forward, include/kernels/attention.cuh:91-97. */
+int attn_head_merge_transpose_forward_f32(const float* in, float* out, int B, int H, int T,
+                                          int d_head, hipStream_t stream);
+/* Replaces head_merge_transpose_backward, include/kernels/attention.cuh:99-105. */
+int attn_head_merge_transpose_backward_f32(const float* dout, float* din, int B, int H, int T,
+                                           int d_head, hipStream_t stream);
+
+/* ------------------------------------------------------------------------------------------
+ * Materialised path: fused scaled causal softmax over (B*H*T, T) score rows.
+ *   probs[r, j]   = exp(scale*s[r,j] - max_j'<=i scale*s[r,j']) / (sum + 1e-12)  for j <= i,
+ *                   0 for j > i  (i = r mod T)
+ *   dscores[r, j] = scale * p * (dp - sum_j'<=i dp*p)  for j <= i, else 0
+ * ------------------------------------------------------------------------------------------ */
+
+/* Replaces causal_softmax_forward, include/kernels/attention.cuh:21-31. */
+int attn_causal_softmax_forward_f32(const float* scores, float* probs, int B, int H, int T,
+                                    float scale, hipStream_t stream);
+/* Replaces causal_softmax_backward, include/kernels/attention.cuh:80-89. */
+int attn_causal_softmax_backward_f32(const float* dprobs, const float* probs, float* dscores,
+                                     int B, int H, int T, float scale, hipStream_t stream);
+
+/* ------------------------------------------------------------------------------------------
+ * Tiled (flash) causal attention, fp32 parity path: QK^T and PV on v_mfma_f32_32x32x2_f32.
+ * d_head in {32, 64, 128}.  All (B,H,T,d) tensors and the stats must be 16-byte aligned.
+ *
+ * Forward writes out = softmax(mask(scale*Q K^T)) V and, when non-NULL,
+ *   m_out[r] = max_j<=i scale*q_i.k_j,   l_out[r] = sum_j<=i exp(scale*q_i.k_j - m_out[r]),
+ * so that P_ij = exp(scale*q_i.k_j - m_i) / l_i  (the contract of the reference stats).
+ * ------------------------------------------------------------------------------------------ */
+
+/* Replaces tiled_causal_attention_forward, include/kernels/attention.cuh:33-49. */
+int attn_tiled_causal_forward_f32(const float* q, const float* k, const float* v, float* out,
+                                  int B, int H, int T, int d_head, float scale, float* m_out,
+                                  float* l_out, hipStream_t stream);
+
+/* Replaces attention_precompute_dot_do_o, include/kernels/attention.cuh:51-58:
+ * D[r] = sum_e dO[r,e] * O[r,e]. */
+int attn_precompute_dot_do_o_f32(const float* dO, const float* O, float* D, int B, int H,
+                                 int T, int d_head, hipStream_t stream);
+
+/* Replaces tiled_causal_attention_backward, include/kernels/attention.cuh:60-78.
+ * d_workspace holds B*H*T floats (it receives D).  m_ptr/l_ptr are the forward's stats.
+ * dq, dk, dv are fully overwritten.  Enqueues the two stages below, in this order. */
+int attn_tiled_causal_backward_f32(const float* q, const float* k, const float* v,
+                                   const float* o, const float* do_ptr, const float* m_ptr,
+                                   const float* l_ptr, float* dq, float* dk, float* dv,
+                                   float* d_workspace, int B, int H, int T, int d_head,
+                                   float scale, hipStream_t stream);
+
+/* Stage 1 of attn_tiled_causal_backward_f32 (query-parallel): computes
+ * D = rowsum(dO*O) into d_workspace and dq = scale * sum_j dS_ij k_j.
+ * The reference splits the same work between attention.cu:659-692 and :696-812. */
+int attn_tiled_causal_backward_dq_f32(const float* q, const float* k, const float* v,
+                                      const float* o, const float* do_ptr, const float* m_ptr,
+                                      const float* l_ptr, float* dq, float* d_workspace, int B,
+                                      int H, int T, int d_head, float scale, hipStream_t stream);
+/* Stage 2 (key-parallel): dk, dv from D in d_workspace (written by stage 1).
+ * The reference computes the same in attention.cu:816-955. */
+int attn_tiled_causal_backward_dkdv_f32(const float* q, const float* k, const float* v,
+                                        const float* do_ptr, const float* m_ptr,
+                                        const float* l_ptr, const float* d_workspace, float* dk,
+                                        float* dv, int B, int H, int T, int d_head, float scale,
+                                        hipStream_t stream);
+
+/* ------------------------------------------------------------------------------------------
+ * Tiled causal attention, bf16 fast path (no reference counterpart: the reference is
+ * fp32-only).  bf16 Q/K/V/O/dO/dQ/dK/dV, fp32 statistics, fp32 accumulation on
+ * v_mfma_f32_32x32x16_bf16.  Same stats contract and workspace size (B*H*T floats) as fp32.
+ * ------------------------------------------------------------------------------------------ */
+int attn_tiled_causal_forward_bf16(const attn_bf16* q, const attn_bf16* k, const attn_bf16* v,
+                                   attn_bf16* out, int B, int H, int T, int d_head, float scale,
+                                   float* m_out, float* l_out, hipStream_t stream);
+int attn_tiled_causal_backward_bf16(const attn_bf16* q, const attn_bf16* k,
+                                    const attn_bf16* v, const attn_bf16* o,
+                                    const attn_bf16* do_ptr, const float* m_ptr,
+                                    const float* l_ptr, attn_bf16* dq, attn_bf16* dk,
+                                    attn_bf16* dv, float* d_workspace, int B, int H, int T,
+                                    int d_head, float scale, hipStream_t stream);
+int attn_tiled_causal_backward_dq_bf16(const attn_bf16* q, const attn_bf16* k,
+                                       const attn_bf16* v, const attn_bf16* o,
+                                       const attn_bf16* do_ptr, const float* m_ptr,
+                                       const float* l_ptr, attn_bf16* dq, float* d_workspace,
+                                       int B, int H, int T, int d_head, float scale,
+                                       hipStream_t stream);
+int attn_tiled_causal_backward_dkdv_bf16(const attn_bf16* q, const attn_bf16* k,
+                                         const attn_bf16* v, const attn_bf16* do_ptr,
+                                         const float* m_ptr, const float* l_ptr,
+                                         const float* d_workspace, attn_bf16* dk, attn_bf16* dv,
+                                         int B, int H, int T, int d_head, float scale,
+                                         hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TCAMD_ATTN_CAPI_H */

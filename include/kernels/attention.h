@@ -1,0 +1,166 @@
+// kernels/attention.h - C++ launchers of the causal attention hot path, MI355X build.
+//
+// Same names, parameter order and defaults as the reference's
+// include/kernels/attention.cuh:5-105, with cudaStream_t replaced by hipStream_t.  Each
+// launcher forwards to the C ABI in attn_capi.h and throws std::runtime_error on a
+// non-zero status, the way the reference's callers wrap CUDA calls in CUDA_CHECK
+// (include/common.h:10-20).  Unlike the reference, an unsupported d_head is an error,
+// never a silent no-op (reference: src/kernels/attention.cu:651-655, 1009-1011).
+//
+// bf16 launchers are additions (the reference is fp32-only); they never overload the
+// fp32 names.
+#pragma once
+
+#include <stdexcept>
+#include <string>
+
+#include "attn_capi.h"
+
+namespace tcamd {
+inline void check_status(int status, const char* what) {
+    if (status != ATTN_SUCCESS) {
+        throw std::runtime_error(std::string(what) + ": " + attn_status_string(status));
+    }
+}
+}  // namespace tcamd
+
+// Split & transpose QKV: (B, T, 3*H*d_head) -> 3 tensors of (B, H, T, d_head).
+// Reference: include/kernels/attention.cuh:5-11.
+inline void qkv_split_transpose_forward(const float* qkv, float* q, float* k, float* v, int B,
+                                        int T, int H, int d_head, hipStream_t stream = nullptr) {
+    tcamd::check_status(
+        attn_qkv_split_transpose_forward_f32(qkv, q, k, v, B, T, H, d_head, stream),
+        "qkv_split_transpose_forward");
+}
+
+// Reference: include/kernels/attention.cuh:13-19.
+inline void qkv_split_transpose_backward(const float* dq, const float* dk, const float* dv,
+                                         float* dqkv, int B, int T, int H, int d_head,
+                                         hipStream_t stream = nullptr) {
+    tcamd::check_status(
+        attn_qkv_split_transpose_backward_f32(dq, dk, dv, dqkv, B, T, H, d_head, stream),
+        "qkv_split_transpose_backward");
+}
+
+// probs[b,h,i,j] = softmax(scores[b,h,i,j] * scale) over j <= i, else 0.
+// Reference: include/kernels/attention.cuh:21-31.
+inline void causal_softmax_forward(const float* scores, float* probs, int B, int H, int T,
+                                   float scale, hipStream_t stream = nullptr) {
+    tcamd::check_status(attn_causal_softmax_forward_f32(scores, probs, B, H, T, scale, stream),
+                        "causal_softmax_forward");
+}
+
+// Reference: include/kernels/attention.cuh:33-49.
+inline void tiled_causal_attention_forward(const float* q, const float* k, const float* v,
+                                           float* out, int B, int H, int T, int d_head,
+                                           float scale, float* m_out = nullptr,
+                                           float* l_out = nullptr,
+                                           hipStream_t stream = nullptr) {
+    tcamd::check_status(attn_tiled_causal_forward_f32(q, k, v, out, B, H, T, d_head, scale,
+                                                      m_out, l_out, stream),
+                        "tiled_causal_attention_forward");
+}
+
+// D_i = sum_d dO[i,d] * O[i,d].  Reference: include/kernels/attention.cuh:51-58.
+inline void attention_precompute_dot_do_o(const float* dO, const float* O, float* D, int B,
+                                          int H, int T, int d_head,
+                                          hipStream_t stream = nullptr) {
+    tcamd::check_status(attn_precompute_dot_do_o_f32(dO, O, D, B, H, T, d_head, stream),
+                        "attention_precompute_dot_do_o");
+}
+
+// Reference: include/kernels/attention.cuh:60-78.  d_workspace: B*H*T floats.
+inline void tiled_causal_attention_backward(const float* q, const float* k, const float* v,
+                                            const float* o, const float* do_ptr,
+                                            const float* m_ptr, const float* l_ptr, float* dq,
+                                            float* dk, float* dv, float* d_workspace, int B,
+                                            int H, int T, int d_head, float scale,
+                                            hipStream_t stream = nullptr) {
+    tcamd::check_status(
+        attn_tiled_causal_backward_f32(q, k, v, o, do_ptr, m_ptr, l_ptr, dq, dk, dv,
+                                       d_workspace, B, H, T, d_head, scale, stream),
+        "tiled_causal_attention_backward");
+}
+
+// dscores = scale * probs * (dprobs - sum(dprobs * probs)) for j <= i, else 0.
+// Reference: include/kernels/attention.cuh:80-89.
+inline void causal_softmax_backward(const float* dprobs, const float* probs, float* dscores,
+                                    int B, int H, int T, float scale,
+                                    hipStream_t stream = nullptr) {
+    tcamd::check_status(
+        attn_causal_softmax_backward_f32(dprobs, probs, dscores, B, H, T, scale, stream),
+        "causal_softmax_backward");
+}
+
+// (B, H, T, d_head) -> (B, T, H*d_head).  Reference: include/kernels/attention.cuh:91-97.
+inline void head_merge_transpose_forward(const float* in, float* out, int B, int H, int T,
+                                         int d_head, hipStream_t stream = nullptr) {
+    tcamd::check_status(attn_head_merge_transpose_forward_f32(in, out, B, H, T, d_head, stream),
+                        "head_merge_transpose_forward");
+}
+
+// (B, T, H*d_head) -> (B, H, T, d_head).  Reference: include/kernels/attention.cuh:99-105.
+inline void head_merge_transpose_backward(const float* dout, float* din, int B, int H, int T,
+                                          int d_head, hipStream_t stream = nullptr) {
+    tcamd::check_status(
+        attn_head_merge_transpose_backward_f32(dout, din, B, H, T, d_head, stream),
+        "head_merge_transpose_backward");
+}
+
+// ---- bf16 fast path (additions; bf16 tensors as attn_bf16 bit patterns) ----------------
+
+inline void qkv_split_transpose_forward_bf16(const attn_bf16* qkv, attn_bf16* q, attn_bf16* k,
+                                             attn_bf16* v, int B, int T, int H, int d_head,
+                                             hipStream_t stream = nullptr) {
+    tcamd::check_status(
+        attn_qkv_split_transpose_forward_bf16(qkv, q, k, v, B, T, H, d_head, stream),
+        "qkv_split_transpose_forward_bf16");
+}
+
+inline void qkv_split_transpose_forward_f32_to_bf16(const float* qkv, attn_bf16* q,
+                                                    attn_bf16* k, attn_bf16* v, int B, int T,
+                                                    int H, int d_head,
+                                                    hipStream_t stream = nullptr) {
+    tcamd::check_status(
+        attn_qkv_split_transpose_forward_f32_bf16(qkv, q, k, v, B, T, H, d_head, stream),
+        "qkv_split_transpose_forward_f32_to_bf16");
+}
+
+inline void qkv_split_transpose_backward_bf16(const attn_bf16* dq, const attn_bf16* dk,
+                                              const attn_bf16* dv, attn_bf16* dqkv, int B,
+                                              int T, int H, int d_head,
+                                              hipStream_t stream = nullptr) {
+    tcamd::check_status(
+        attn_qkv_split_transpose_backward_bf16(dq, dk, dv, dqkv, B, T, H, d_head, stream),
+        "qkv_split_transpose_backward_bf16");
+}
+
+inline void qkv_split_transpose_backward_bf16_to_f32(const attn_bf16* dq, const attn_bf16* dk,
+                                                     const attn_bf16* dv, float* dqkv, int B,
+                                                     int T, int H, int d_head,
+                                                     hipStream_t stream = nullptr) {
+    tcamd::check_status(
+        attn_qkv_split_transpose_backward_bf16_f32(dq, dk, dv, dqkv, B, T, H, d_head, stream),
+        "qkv_split_transpose_backward_bf16_to_f32");
+}
+
+inline void tiled_causal_attention_forward_bf16(const attn_bf16* q, const attn_bf16* k,
+                                                const attn_bf16* v, attn_bf16* out, int B,
+                                                int H, int T, int d_head, float scale,
+                                                float* m_out = nullptr, float* l_out = nullptr,
+                                                hipStream_t stream = nullptr) {
+    tcamd::check_status(attn_tiled_causal_forward_bf16(q, k, v, out, B, H, T, d_head, scale,
+                                                       m_out, l_out, stream),
+                        "tiled_causal_attention_forward_bf16");
+}
+
+inline void tiled_causal_attention_backward_bf16(
+    const attn_bf16* q, const attn_bf16* k, const attn_bf16* v, const attn_bf16* o,
+    const attn_bf16* do_ptr, const float* m_ptr, const float* l_ptr, attn_bf16* dq,
+    attn_bf16* dk, attn_bf16* dv, float* d_workspace, int B, int H, int T, int d_head,
+    float scale, hipStream_t stream = nullptr) {
+    tcamd::check_status(
+        attn_tiled_causal_backward_bf16(q, k, v, o, do_ptr, m_ptr, l_ptr, dq, dk, dv,
+                                        d_workspace, B, H, T, d_head, scale, stream),
+        "tiled_causal_attention_backward_bf16");
+}

@@ -1,0 +1,118 @@
+"""The C-ABI library without a GPU: it loads, exports every symbol the headers declare,
+and validates arguments on the host (status codes, no launch)."""
+import ctypes
+import os
+import re
+import shutil
+import subprocess
+
+import pytest
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+CAPI = os.path.join(REPO, "include", "attn_capi.h")
+
+FAKE = 0x10000  # never dereferenced: every call below fails validation before launching
+MISALIGNED = 0x10004
+
+OK, INVALID_DIM, BAD_HEAD_DIM, NULLPTR, MISALIGN, LAUNCH, BAD_VALUE = range(7)
+
+
+def declared_symbols():
+    text = open(CAPI).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(attn_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_every_declared_symbol_is_exported(lib):
+    syms = declared_symbols()
+    assert len(syms) >= 20
+    handle = lib.raw()
+    for s in syms:
+        assert hasattr(handle, s), f"{s} declared in attn_capi.h but not exported"
+    nm = shutil.which("nm")
+    if nm:
+        out = subprocess.run([nm, "-D", "--defined-only", lib.LIB_PATH], capture_output=True,
+                             text=True, check=True).stdout
+        exported = set(re.findall(r"\bT (attn_\w+)", out))
+        assert set(syms) <= exported
+
+
+def test_binding_covers_header(lib):
+    declared = set(declared_symbols()) - {"attn_status_string", "attn_version"}
+    assert declared == set(lib.SIGNATURES)
+
+
+def test_status_strings(lib):
+    assert lib.status_string(0) == "success"
+    for s in range(1, 7):
+        assert lib.status_string(s) not in ("success", "unknown status")
+    assert lib.status_string(99) == "unknown status"
+    assert lib.raw().attn_version() >= 100
+
+
+def fwd(lib, q=FAKE, out=FAKE, B=1, H=1, T=8, d=64, scale=0.125):
+    return lib.call("attn_tiled_causal_forward_f32", q, FAKE, FAKE, out, B, H, T, d,
+                    ctypes.c_float(scale), None, None, None)
+
+
+def test_forward_validation(lib):
+    assert fwd(lib, d=48) == BAD_HEAD_DIM          # reference silently mis-runs d=48
+    assert fwd(lib, d=256) == BAD_HEAD_DIM
+    assert fwd(lib, B=0) == INVALID_DIM
+    assert fwd(lib, T=-1) == INVALID_DIM
+    assert fwd(lib, q=None) == NULLPTR
+    assert fwd(lib, out=None) == NULLPTR
+    assert fwd(lib, q=MISALIGNED) == MISALIGN
+    assert fwd(lib, scale=0.0) == BAD_VALUE
+    assert fwd(lib, scale=float("nan")) == BAD_VALUE
+    assert fwd(lib, scale=float("inf")) == BAD_VALUE
+    assert fwd(lib, B=1 << 16, H=1 << 16) == INVALID_DIM
+
+
+def test_backward_validation(lib):
+    def bwd(name, d=64, ws=FAKE, dk=FAKE):
+        args = [FAKE] * 7 + [FAKE, dk, FAKE, ws, 1, 1, 8, d, ctypes.c_float(0.125), None]
+        return lib.call(name, *args)
+    for name in ("attn_tiled_causal_backward_f32", "attn_tiled_causal_backward_bf16"):
+        assert bwd(name, d=128 + 32) == BAD_HEAD_DIM   # reference: silent no-op for d=128
+        assert bwd(name, ws=None) == NULLPTR
+        assert bwd(name, dk=None) == NULLPTR
+        assert bwd(name, dk=MISALIGNED) == MISALIGN
+
+
+def test_split_and_softmax_validation(lib):
+    f = ctypes.c_float
+    assert lib.call("attn_qkv_split_transpose_forward_f32", FAKE, FAKE, None, FAKE, 1, 4, 2, 8,
+                    None) == NULLPTR
+    assert lib.call("attn_qkv_split_transpose_forward_f32", FAKE, FAKE, FAKE, FAKE, 1, 0, 2, 8,
+                    None) == INVALID_DIM
+    assert lib.call("attn_qkv_split_transpose_backward_bf16", FAKE, FAKE, FAKE, FAKE, 1, 4, 2,
+                    0, None) == INVALID_DIM
+    assert lib.call("attn_causal_softmax_forward_f32", FAKE, None, 1, 1, 4, f(1.0),
+                    None) == NULLPTR
+    assert lib.call("attn_causal_softmax_backward_f32", FAKE, FAKE, FAKE, 1, 1, 4,
+                    f(float("nan")), None) == BAD_VALUE
+    assert lib.call("attn_head_merge_transpose_forward_f32", FAKE, FAKE, 0, 1, 4, 8,
+                    None) == INVALID_DIM
+
+
+def test_python_launchers_reject_host_tensors(lib):
+    import torch
+    x = torch.zeros(2, 2, 8, 32)
+    with pytest.raises(ValueError):
+        lib.tiled_causal_attention_forward(x, x, x, x, 2, 2, 8, 32, 0.1)
+
+
+@pytest.mark.parametrize("lang", ["c", "c++"])
+def test_headers_compile_standalone(tmp_path, lang):
+    """attn_capi.h is a C header; kernels/attention.h compiles as C++17 (syntax only)."""
+    if lang == "c":
+        src = tmp_path / "t.c"
+        src.write_text('#include "attn_capi.h"\nint main(void){return attn_version() > 0 ? 0 : 1;}\n')
+        cmd = ["gcc", "-std=c11", "-fsyntax-only"]
+    else:
+        src = tmp_path / "t.cpp"
+        src.write_text('#include "kernels/attention.h"\n#include "common.h"\nint main(){return 0;}\n')
+        cmd = ["g++", "-std=c++17", "-fsyntax-only"]
+    cmd += ["-D__HIP_PLATFORM_AMD__", f"-I{REPO}/include", "-I/opt/rocm/include", str(src)]
+    subprocess.run(cmd, check=True)

@@ -1,0 +1,313 @@
+"""Python binding of the MI355X causal attention library (libtcamd_attn.so).
+
+The product is the HIP library and its C ABI (include/attn_capi.h); this module binds
+that ABI with ctypes so Python callers (tests, bench) drive exactly the entry points a
+C/C++ caller would.  torch is used only for device memory and the current stream.
+
+Launcher functions keep the reference's names and argument order
+(include/kernels/attention.cuh:5-105) and take torch tensors for the pointer arguments;
+they raise RuntimeError on a non-zero status, like the reference's callers do via
+CUDA_CHECK.  There is no CPU fallback: if the library is missing, importing this module
+fails.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libtcamd_attn.so")
+REPO_ROOT = os.path.dirname(_HERE)
+CAPI_HEADER = os.path.join(REPO_ROOT, "include", "attn_capi.h")
+
+if not os.path.exists(LIB_PATH):
+    raise ImportError(
+        f"{LIB_PATH} is not built; run __graft_entry__.build() (make -C transformer-cuda_amd)")
+
+_lib = ctypes.CDLL(LIB_PATH)
+
+STATUS = {
+    0: "ATTN_SUCCESS",
+    1: "ATTN_ERROR_INVALID_DIM",
+    2: "ATTN_ERROR_UNSUPPORTED_HEAD_DIM",
+    3: "ATTN_ERROR_NULL_POINTER",
+    4: "ATTN_ERROR_MISALIGNED",
+    5: "ATTN_ERROR_LAUNCH",
+    6: "ATTN_ERROR_INVALID_VALUE",
+}
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_F = ctypes.c_float
+
+# name -> argument types (the trailing _P is the hipStream_t)
+SIGNATURES = {
+    "attn_qkv_split_transpose_forward_f32": [_P, _P, _P, _P, _I, _I, _I, _I, _P],
+    "attn_qkv_split_transpose_backward_f32": [_P, _P, _P, _P, _I, _I, _I, _I, _P],
+    "attn_qkv_split_transpose_forward_bf16": [_P, _P, _P, _P, _I, _I, _I, _I, _P],
+    "attn_qkv_split_transpose_forward_f32_bf16": [_P, _P, _P, _P, _I, _I, _I, _I, _P],
+    "attn_qkv_split_transpose_backward_bf16": [_P, _P, _P, _P, _I, _I, _I, _I, _P],
+    "attn_qkv_split_transpose_backward_bf16_f32": [_P, _P, _P, _P, _I, _I, _I, _I, _P],
+    "attn_head_merge_transpose_forward_f32": [_P, _P, _I, _I, _I, _I, _P],
+    "attn_head_merge_transpose_backward_f32": [_P, _P, _I, _I, _I, _I, _P],
+    "attn_causal_softmax_forward_f32": [_P, _P, _I, _I, _I, _F, _P],
+    "attn_causal_softmax_backward_f32": [_P, _P, _P, _I, _I, _I, _F, _P],
+    "attn_tiled_causal_forward_f32": [_P, _P, _P, _P, _I, _I, _I, _I, _F, _P, _P, _P],
+    "attn_precompute_dot_do_o_f32": [_P, _P, _P, _I, _I, _I, _I, _P],
+    "attn_tiled_causal_backward_f32":
+        [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P],
+    "attn_tiled_causal_backward_dq_f32":
+        [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P],
+    "attn_tiled_causal_backward_dkdv_f32":
+        [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P],
+    "attn_tiled_causal_forward_bf16": [_P, _P, _P, _P, _I, _I, _I, _I, _F, _P, _P, _P],
+    "attn_tiled_causal_backward_bf16":
+        [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P],
+    "attn_tiled_causal_backward_dq_bf16":
+        [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P],
+    "attn_tiled_causal_backward_dkdv_bf16":
+        [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P],
+}
+
+for _name, _args in SIGNATURES.items():
+    _fn = getattr(_lib, _name)
+    _fn.argtypes = _args
+    _fn.restype = ctypes.c_int
+_lib.attn_status_string.argtypes = [_I]
+_lib.attn_status_string.restype = ctypes.c_char_p
+_lib.attn_version.argtypes = []
+_lib.attn_version.restype = ctypes.c_int
+
+
+def raw():
+    """The ctypes handle of libtcamd_attn.so (every symbol of include/attn_capi.h)."""
+    return _lib
+
+
+def status_string(status: int) -> str:
+    return _lib.attn_status_string(int(status)).decode()
+
+
+class AttnError(RuntimeError):
+    def __init__(self, what: str, status: int):
+        super().__init__(f"{what}: {status_string(status)} ({STATUS.get(status, status)})")
+        self.status = status
+
+
+def check(status: int, what: str) -> None:
+    if status != 0:
+        raise AttnError(what, status)
+
+
+def call(name: str, *args) -> int:
+    """Call a C-ABI entry point with raw arguments; returns its status."""
+    return getattr(_lib, name)(*args)
+
+
+# ---------------------------------------------------------------------------------------
+# torch-tensor launchers (reference names and argument order)
+# ---------------------------------------------------------------------------------------
+def _torch():
+    import torch
+    return torch
+
+
+def _ptr(t, dtype=None, numel=None, what=""):
+    if t is None:
+        return None
+    torch = _torch()
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{what}: expected a torch.Tensor")
+    if t.device.type != "cuda":
+        raise ValueError(f"{what}: tensor must be on a GPU device, got {t.device}")
+    if not t.is_contiguous():
+        raise ValueError(f"{what}: tensor must be contiguous")
+    if dtype is not None and t.dtype != dtype:
+        raise ValueError(f"{what}: expected {dtype}, got {t.dtype}")
+    if numel is not None and t.numel() < numel:
+        raise ValueError(f"{what}: needs {numel} elements, has {t.numel()}")
+    return t.data_ptr()
+
+
+def _stream(stream):
+    if stream is None:
+        return _torch().cuda.current_stream().cuda_stream
+    if isinstance(stream, int):
+        return stream
+    return stream.cuda_stream
+
+
+def _dt(bf16: bool):
+    torch = _torch()
+    return torch.bfloat16 if bf16 else torch.float32
+
+
+def qkv_split_transpose_forward(qkv, q, k, v, B, T, H, d_head, stream=None):
+    """Reference: include/kernels/attention.cuh:5-11.  dtype pair chosen from the tensors:
+    f32->f32, bf16->bf16 or f32->bf16 (cast fused)."""
+    torch = _torch()
+    n = B * T * H * d_head
+    src_bf = qkv.dtype == torch.bfloat16
+    dst_bf = q.dtype == torch.bfloat16
+    if src_bf and not dst_bf:
+        raise ValueError("bf16 -> f32 split is not provided")
+    name = ("attn_qkv_split_transpose_forward_bf16" if src_bf else
+            "attn_qkv_split_transpose_forward_f32_bf16" if dst_bf else
+            "attn_qkv_split_transpose_forward_f32")
+    check(call(name, _ptr(qkv, _dt(src_bf), 3 * n, "qkv"), _ptr(q, _dt(dst_bf), n, "q"),
+               _ptr(k, _dt(dst_bf), n, "k"), _ptr(v, _dt(dst_bf), n, "v"),
+               B, T, H, d_head, _stream(stream)), "qkv_split_transpose_forward")
+
+
+def qkv_split_transpose_backward(dq, dk, dv, dqkv, B, T, H, d_head, stream=None):
+    """Reference: include/kernels/attention.cuh:13-19.  f32->f32, bf16->bf16 or bf16->f32."""
+    torch = _torch()
+    n = B * T * H * d_head
+    src_bf = dq.dtype == torch.bfloat16
+    dst_bf = dqkv.dtype == torch.bfloat16
+    if dst_bf and not src_bf:
+        raise ValueError("f32 -> bf16 backward split is not provided")
+    name = ("attn_qkv_split_transpose_backward_bf16" if dst_bf else
+            "attn_qkv_split_transpose_backward_bf16_f32" if src_bf else
+            "attn_qkv_split_transpose_backward_f32")
+    check(call(name, _ptr(dq, _dt(src_bf), n, "dq"), _ptr(dk, _dt(src_bf), n, "dk"),
+               _ptr(dv, _dt(src_bf), n, "dv"), _ptr(dqkv, _dt(dst_bf), 3 * n, "dqkv"),
+               B, T, H, d_head, _stream(stream)), "qkv_split_transpose_backward")
+
+
+def head_merge_transpose_forward(inp, out, B, H, T, d_head, stream=None):
+    """Reference: include/kernels/attention.cuh:91-97."""
+    n = B * H * T * d_head
+    f32 = _dt(False)
+    check(call("attn_head_merge_transpose_forward_f32", _ptr(inp, f32, n, "in"),
+               _ptr(out, f32, n, "out"), B, H, T, d_head, _stream(stream)),
+          "head_merge_transpose_forward")
+
+
+def head_merge_transpose_backward(dout, din, B, H, T, d_head, stream=None):
+    """Reference: include/kernels/attention.cuh:99-105."""
+    n = B * H * T * d_head
+    f32 = _dt(False)
+    check(call("attn_head_merge_transpose_backward_f32", _ptr(dout, f32, n, "dout"),
+               _ptr(din, f32, n, "din"), B, H, T, d_head, _stream(stream)),
+          "head_merge_transpose_backward")
+
+
+def causal_softmax_forward(scores, probs, B, H, T, scale, stream=None):
+    """Reference: include/kernels/attention.cuh:21-31."""
+    n = B * H * T * T
+    f32 = _dt(False)
+    check(call("attn_causal_softmax_forward_f32", _ptr(scores, f32, n, "scores"),
+               _ptr(probs, f32, n, "probs"), B, H, T, float(scale), _stream(stream)),
+          "causal_softmax_forward")
+
+
+def causal_softmax_backward(dprobs, probs, dscores, B, H, T, scale, stream=None):
+    """Reference: include/kernels/attention.cuh:80-89."""
+    n = B * H * T * T
+    f32 = _dt(False)
+    check(call("attn_causal_softmax_backward_f32", _ptr(dprobs, f32, n, "dprobs"),
+               _ptr(probs, f32, n, "probs"), _ptr(dscores, f32, n, "dscores"), B, H, T,
+               float(scale), _stream(stream)), "causal_softmax_backward")
+
+
+def tiled_causal_attention_forward(q, k, v, out, B, H, T, d_head, scale, m_out=None,
+                                   l_out=None, stream=None):
+    """Reference: include/kernels/attention.cuh:33-49.  fp32 or bf16 by the tensors' dtype."""
+    torch = _torch()
+    bf = q.dtype == torch.bfloat16
+    n = B * H * T * d_head
+    r = B * H * T
+    dt = _dt(bf)
+    f32 = _dt(False)
+    name = "attn_tiled_causal_forward_bf16" if bf else "attn_tiled_causal_forward_f32"
+    check(call(name, _ptr(q, dt, n, "q"), _ptr(k, dt, n, "k"), _ptr(v, dt, n, "v"),
+               _ptr(out, dt, n, "out"), B, H, T, d_head, float(scale),
+               _ptr(m_out, f32, r, "m_out"), _ptr(l_out, f32, r, "l_out"), _stream(stream)),
+          "tiled_causal_attention_forward")
+
+
+def attention_precompute_dot_do_o(dO, O, D, B, H, T, d_head, stream=None):
+    """Reference: include/kernels/attention.cuh:51-58."""
+    n = B * H * T * d_head
+    f32 = _dt(False)
+    check(call("attn_precompute_dot_do_o_f32", _ptr(dO, f32, n, "dO"), _ptr(O, f32, n, "O"),
+               _ptr(D, f32, B * H * T, "D"), B, H, T, d_head, _stream(stream)),
+          "attention_precompute_dot_do_o")
+
+
+def tiled_causal_attention_backward(q, k, v, o, do, m, l, dq, dk, dv, d_workspace, B, H, T,
+                                    d_head, scale, stream=None):
+    """Reference: include/kernels/attention.cuh:60-78.  fp32 or bf16 by q's dtype."""
+    torch = _torch()
+    bf = q.dtype == torch.bfloat16
+    n = B * H * T * d_head
+    r = B * H * T
+    dt = _dt(bf)
+    f32 = _dt(False)
+    name = "attn_tiled_causal_backward_bf16" if bf else "attn_tiled_causal_backward_f32"
+    check(call(name, _ptr(q, dt, n, "q"), _ptr(k, dt, n, "k"), _ptr(v, dt, n, "v"),
+               _ptr(o, dt, n, "o"), _ptr(do, dt, n, "do"), _ptr(m, f32, r, "m"),
+               _ptr(l, f32, r, "l"), _ptr(dq, dt, n, "dq"), _ptr(dk, dt, n, "dk"),
+               _ptr(dv, dt, n, "dv"), _ptr(d_workspace, f32, r, "d_workspace"),
+               B, H, T, d_head, float(scale), _stream(stream)),
+          "tiled_causal_attention_backward")
+
+
+def tiled_causal_attention_backward_dq(q, k, v, o, do, m, l, dq, d_workspace, B, H, T, d_head,
+                                       scale, stream=None):
+    """Stage 1 of the backward (D and dQ)."""
+    torch = _torch()
+    bf = q.dtype == torch.bfloat16
+    n = B * H * T * d_head
+    r = B * H * T
+    dt = _dt(bf)
+    f32 = _dt(False)
+    name = "attn_tiled_causal_backward_dq_bf16" if bf else "attn_tiled_causal_backward_dq_f32"
+    check(call(name, _ptr(q, dt, n, "q"), _ptr(k, dt, n, "k"), _ptr(v, dt, n, "v"),
+               _ptr(o, dt, n, "o"), _ptr(do, dt, n, "do"), _ptr(m, f32, r, "m"),
+               _ptr(l, f32, r, "l"), _ptr(dq, dt, n, "dq"),
+               _ptr(d_workspace, f32, r, "d_workspace"), B, H, T, d_head, float(scale),
+               _stream(stream)), "tiled_causal_attention_backward_dq")
+
+
+def tiled_causal_attention_backward_dkdv(q, k, v, do, m, l, d_workspace, dk, dv, B, H, T,
+                                         d_head, scale, stream=None):
+    """Stage 2 of the backward (dK, dV from D in d_workspace)."""
+    torch = _torch()
+    bf = q.dtype == torch.bfloat16
+    n = B * H * T * d_head
+    r = B * H * T
+    dt = _dt(bf)
+    f32 = _dt(False)
+    name = ("attn_tiled_causal_backward_dkdv_bf16" if bf else
+            "attn_tiled_causal_backward_dkdv_f32")
+    check(call(name, _ptr(q, dt, n, "q"), _ptr(k, dt, n, "k"), _ptr(v, dt, n, "v"),
+               _ptr(do, dt, n, "do"), _ptr(m, f32, r, "m"), _ptr(l, f32, r, "l"),
+               _ptr(d_workspace, f32, r, "d_workspace"), _ptr(dk, dt, n, "dk"),
+               _ptr(dv, dt, n, "dv"), B, H, T, d_head, float(scale), _stream(stream)),
+          "tiled_causal_attention_backward_dkdv")
+
+
+# ---------------------------------------------------------------------------------------
+# Allocating conveniences for tests and the bench (not part of the reference API).
+# ---------------------------------------------------------------------------------------
+def attention_forward(q, k, v, scale):
+    """(out, m, l) for (B, H, T, d) GPU tensors."""
+    torch = _torch()
+    B, H, T, d = q.shape
+    out = torch.empty_like(q)
+    m = torch.empty((B, H, T), device=q.device, dtype=torch.float32)
+    l = torch.empty_like(m)
+    tiled_causal_attention_forward(q, k, v, out, B, H, T, d, scale, m, l)
+    return out, m, l
+
+
+def attention_backward(q, k, v, o, do, m, l, scale):
+    """(dq, dk, dv, D) for (B, H, T, d) GPU tensors."""
+    torch = _torch()
+    B, H, T, d = q.shape
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(q), torch.empty_like(q)
+    ws = torch.empty((B, H, T), device=q.device, dtype=torch.float32)
+    tiled_causal_attention_backward(q, k, v, o, do, m, l, dq, dk, dv, ws, B, H, T, d, scale)
+    return dq, dk, dv, ws

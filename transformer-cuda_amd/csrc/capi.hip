@@ -1,0 +1,341 @@
+// capi.hip - the extern "C" boundary (include/attn_capi.h).
+//
+// Each entry point validates its arguments on the host and returns a status before any
+// HIP call, so the validation is testable on a machine without a GPU.  Only then does it
+// enqueue the kernels and report the launch status.  Nothing here allocates, synchronises
+// or keeps state.
+#include <math.h>
+#include <stdint.h>
+
+#include "../../include/attn_capi.h"
+#include "launch.hpp"
+
+namespace {
+
+using tcamd::ElemType;
+using tcamd::HeadPtrs;
+
+constexpr int64_t kInt32Max = 2147483647;
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int check_dims4(int B, int H, int T, int d) {
+    if (B <= 0 || H <= 0 || T <= 0 || d <= 0) return ATTN_ERROR_INVALID_DIM;
+    // Kernels index within one head in 32-bit and count (b, h) pairs in 32-bit.
+    if (static_cast<int64_t>(T) * d > kInt32Max) return ATTN_ERROR_INVALID_DIM;
+    if (static_cast<int64_t>(B) * H > 65535LL * 1024) return ATTN_ERROR_INVALID_DIM;
+    return ATTN_SUCCESS;
+}
+
+int check_tiled(int B, int H, int T, int d, float scale) {
+    const int st = check_dims4(B, H, T, d);
+    if (st != ATTN_SUCCESS) return st;
+    if (d != 32 && d != 64 && d != 128) return ATTN_ERROR_UNSUPPORTED_HEAD_DIM;
+    if (!(scale > 0.0f) || !isfinite(scale)) return ATTN_ERROR_INVALID_VALUE;
+    // grid = B*H * ceil(T / 128) workgroups
+    const int64_t tiles = (static_cast<int64_t>(T) + 127) / 128;
+    if (static_cast<int64_t>(B) * H * tiles > kInt32Max) return ATTN_ERROR_INVALID_DIM;
+    return ATTN_SUCCESS;
+}
+
+int check_split(const void* a, const void* b, const void* c, const void* dd, int B, int T,
+                int H, int d) {
+    if (a == nullptr || b == nullptr || c == nullptr || dd == nullptr)
+        return ATTN_ERROR_NULL_POINTER;
+    const int st = check_dims4(B, H, T, d);
+    if (st != ATTN_SUCCESS) return st;
+    if (static_cast<int64_t>(B) * H > 65535) return ATTN_ERROR_INVALID_DIM;  // grid.y
+    return ATTN_SUCCESS;
+}
+
+int launch_status() {
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? ATTN_SUCCESS : ATTN_ERROR_LAUNCH;
+}
+
+void clear_error() { (void)hipGetLastError(); }
+
+int split_common(const void* rm, ElemType rm_t, void* q, void* k, void* v, ElemType h_t,
+                 bool to_heads, int B, int T, int H, int d, hipStream_t stream) {
+    const int st = check_split(rm, q, k, v, B, T, H, d);
+    if (st != ATTN_SUCCESS) return st;
+    HeadPtrs heads{{q, k, v}};
+    clear_error();
+    if (to_heads) {
+        tcamd::launch_stripe_transpose(rm, rm_t, nullptr, h_t, heads, true, B, T, 3, H, d,
+                                       stream);
+    } else {
+        tcamd::launch_stripe_transpose(nullptr, h_t, const_cast<void*>(rm), rm_t, heads, false,
+                                       B, T, 3, H, d, stream);
+    }
+    return launch_status();
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* attn_status_string(int status) {
+    switch (status) {
+        case ATTN_SUCCESS: return "success";
+        case ATTN_ERROR_INVALID_DIM: return "invalid dimension (B, H, T, d_head or a size)";
+        case ATTN_ERROR_UNSUPPORTED_HEAD_DIM: return "unsupported d_head (tiled kernels: 32, 64, 128)";
+        case ATTN_ERROR_NULL_POINTER: return "required pointer is NULL";
+        case ATTN_ERROR_MISALIGNED: return "pointer not 16-byte aligned";
+        case ATTN_ERROR_LAUNCH: return "kernel launch failed";
+        case ATTN_ERROR_INVALID_VALUE: return "invalid value (scale)";
+        default: return "unknown status";
+    }
+}
+
+int attn_version(void) { return 100; }
+
+// ---- split-transpose --------------------------------------------------------------------
+
+int attn_qkv_split_transpose_forward_f32(const float* qkv, float* q, float* k, float* v,
+                                         int B, int T, int H, int d_head, hipStream_t stream) {
+    return split_common(qkv, ElemType::F32, q, k, v, ElemType::F32, true, B, T, H, d_head,
+                        stream);
+}
+
+int attn_qkv_split_transpose_backward_f32(const float* dq, const float* dk, const float* dv,
+                                          float* dqkv, int B, int T, int H, int d_head,
+                                          hipStream_t stream) {
+    return split_common(dqkv, ElemType::F32, const_cast<float*>(dq), const_cast<float*>(dk),
+                        const_cast<float*>(dv), ElemType::F32, false, B, T, H, d_head, stream);
+}
+
+int attn_qkv_split_transpose_forward_bf16(const attn_bf16* qkv, attn_bf16* q, attn_bf16* k,
+                                          attn_bf16* v, int B, int T, int H, int d_head,
+                                          hipStream_t stream) {
+    return split_common(qkv, ElemType::BF16, q, k, v, ElemType::BF16, true, B, T, H, d_head,
+                        stream);
+}
+
+int attn_qkv_split_transpose_forward_f32_bf16(const float* qkv, attn_bf16* q, attn_bf16* k,
+                                              attn_bf16* v, int B, int T, int H, int d_head,
+                                              hipStream_t stream) {
+    return split_common(qkv, ElemType::F32, q, k, v, ElemType::BF16, true, B, T, H, d_head,
+                        stream);
+}
+
+int attn_qkv_split_transpose_backward_bf16(const attn_bf16* dq, const attn_bf16* dk,
+                                           const attn_bf16* dv, attn_bf16* dqkv, int B, int T,
+                                           int H, int d_head, hipStream_t stream) {
+    return split_common(dqkv, ElemType::BF16, const_cast<attn_bf16*>(dq),
+                        const_cast<attn_bf16*>(dk), const_cast<attn_bf16*>(dv), ElemType::BF16,
+                        false, B, T, H, d_head, stream);
+}
+
+int attn_qkv_split_transpose_backward_bf16_f32(const attn_bf16* dq, const attn_bf16* dk,
+                                               const attn_bf16* dv, float* dqkv, int B, int T,
+                                               int H, int d_head, hipStream_t stream) {
+    return split_common(dqkv, ElemType::F32, const_cast<attn_bf16*>(dq),
+                        const_cast<attn_bf16*>(dk), const_cast<attn_bf16*>(dv), ElemType::BF16,
+                        false, B, T, H, d_head, stream);
+}
+
+// ---- head merge -------------------------------------------------------------------------
+
+int attn_head_merge_transpose_forward_f32(const float* in, float* out, int B, int H, int T,
+                                          int d_head, hipStream_t stream) {
+    const int st = check_split(in, out, out, out, B, T, H, d_head);
+    if (st != ATTN_SUCCESS) return st;
+    HeadPtrs heads{{const_cast<float*>(in), nullptr, nullptr}};
+    clear_error();
+    tcamd::launch_stripe_transpose(nullptr, ElemType::F32, out, ElemType::F32, heads, false, B,
+                                   T, 1, H, d_head, stream);
+    return launch_status();
+}
+
+int attn_head_merge_transpose_backward_f32(const float* dout, float* din, int B, int H, int T,
+                                           int d_head, hipStream_t stream) {
+    const int st = check_split(dout, din, din, din, B, T, H, d_head);
+    if (st != ATTN_SUCCESS) return st;
+    HeadPtrs heads{{din, nullptr, nullptr}};
+    clear_error();
+    tcamd::launch_stripe_transpose(dout, ElemType::F32, nullptr, ElemType::F32, heads, true, B,
+                                   T, 1, H, d_head, stream);
+    return launch_status();
+}
+
+// ---- materialised softmax ---------------------------------------------------------------
+
+int attn_causal_softmax_forward_f32(const float* scores, float* probs, int B, int H, int T,
+                                    float scale, hipStream_t stream) {
+    if (scores == nullptr || probs == nullptr) return ATTN_ERROR_NULL_POINTER;
+    if (B <= 0 || H <= 0 || T <= 0) return ATTN_ERROR_INVALID_DIM;
+    if (!isfinite(scale)) return ATTN_ERROR_INVALID_VALUE;
+    const int64_t rows = static_cast<int64_t>(B) * H * T;
+    if ((rows + 3) / 4 > kInt32Max) return ATTN_ERROR_INVALID_DIM;
+    clear_error();
+    tcamd::launch_causal_softmax_fwd_f32(scores, probs, rows, T, scale, stream);
+    return launch_status();
+}
+
+int attn_causal_softmax_backward_f32(const float* dprobs, const float* probs, float* dscores,
+                                     int B, int H, int T, float scale, hipStream_t stream) {
+    if (dprobs == nullptr || probs == nullptr || dscores == nullptr)
+        return ATTN_ERROR_NULL_POINTER;
+    if (B <= 0 || H <= 0 || T <= 0) return ATTN_ERROR_INVALID_DIM;
+    if (!isfinite(scale)) return ATTN_ERROR_INVALID_VALUE;
+    const int64_t rows = static_cast<int64_t>(B) * H * T;
+    if ((rows + 3) / 4 > kInt32Max) return ATTN_ERROR_INVALID_DIM;
+    clear_error();
+    tcamd::launch_causal_softmax_bwd_f32(dprobs, probs, dscores, rows, T, scale, stream);
+    return launch_status();
+}
+
+// ---- tiled fp32 ------------------------------------------------------------------------
+
+int attn_tiled_causal_forward_f32(const float* q, const float* k, const float* v, float* out,
+                                  int B, int H, int T, int d_head, float scale, float* m_out,
+                                  float* l_out, hipStream_t stream) {
+    if (q == nullptr || k == nullptr || v == nullptr || out == nullptr)
+        return ATTN_ERROR_NULL_POINTER;
+    const int st = check_tiled(B, H, T, d_head, scale);
+    if (st != ATTN_SUCCESS) return st;
+    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out))
+        return ATTN_ERROR_MISALIGNED;
+    clear_error();
+    tcamd::launch_flash_fwd_f32(q, k, v, out, m_out, l_out, B * H, T, d_head, scale, stream);
+    return launch_status();
+}
+
+int attn_precompute_dot_do_o_f32(const float* dO, const float* O, float* D, int B, int H,
+                                 int T, int d_head, hipStream_t stream) {
+    if (dO == nullptr || O == nullptr || D == nullptr) return ATTN_ERROR_NULL_POINTER;
+    const int st = check_dims4(B, H, T, d_head);
+    if (st != ATTN_SUCCESS) return st;
+    clear_error();
+    tcamd::launch_dot_do_o_f32(dO, O, D, static_cast<int64_t>(B) * H * T, d_head, stream);
+    return launch_status();
+}
+
+int attn_tiled_causal_backward_dq_f32(const float* q, const float* k, const float* v,
+                                      const float* o, const float* do_ptr, const float* m_ptr,
+                                      const float* l_ptr, float* dq, float* d_workspace, int B,
+                                      int H, int T, int d_head, float scale,
+                                      hipStream_t stream) {
+    if (q == nullptr || k == nullptr || v == nullptr || o == nullptr || do_ptr == nullptr ||
+        m_ptr == nullptr || l_ptr == nullptr || dq == nullptr || d_workspace == nullptr)
+        return ATTN_ERROR_NULL_POINTER;
+    const int st = check_tiled(B, H, T, d_head, scale);
+    if (st != ATTN_SUCCESS) return st;
+    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o) ||
+        !aligned16(do_ptr) || !aligned16(dq))
+        return ATTN_ERROR_MISALIGNED;
+    clear_error();
+    tcamd::launch_flash_bwd_dq_f32(q, k, v, o, do_ptr, m_ptr, l_ptr, dq, d_workspace, B * H, T,
+                                   d_head, scale, stream);
+    return launch_status();
+}
+
+int attn_tiled_causal_backward_dkdv_f32(const float* q, const float* k, const float* v,
+                                        const float* do_ptr, const float* m_ptr,
+                                        const float* l_ptr, const float* d_workspace, float* dk,
+                                        float* dv, int B, int H, int T, int d_head, float scale,
+                                        hipStream_t stream) {
+    if (q == nullptr || k == nullptr || v == nullptr || do_ptr == nullptr || m_ptr == nullptr ||
+        l_ptr == nullptr || d_workspace == nullptr || dk == nullptr || dv == nullptr)
+        return ATTN_ERROR_NULL_POINTER;
+    const int st = check_tiled(B, H, T, d_head, scale);
+    if (st != ATTN_SUCCESS) return st;
+    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(do_ptr) ||
+        !aligned16(dk) || !aligned16(dv))
+        return ATTN_ERROR_MISALIGNED;
+    clear_error();
+    tcamd::launch_flash_bwd_dkdv_f32(q, k, v, do_ptr, m_ptr, l_ptr, d_workspace, dk, dv, B * H,
+                                     T, d_head, scale, stream);
+    return launch_status();
+}
+
+int attn_tiled_causal_backward_f32(const float* q, const float* k, const float* v,
+                                   const float* o, const float* do_ptr, const float* m_ptr,
+                                   const float* l_ptr, float* dq, float* dk, float* dv,
+                                   float* d_workspace, int B, int H, int T, int d_head,
+                                   float scale, hipStream_t stream) {
+    // Validate the second stage's own arguments before the first stage is enqueued.
+    if (dk == nullptr || dv == nullptr) return ATTN_ERROR_NULL_POINTER;
+    if (check_tiled(B, H, T, d_head, scale) == ATTN_SUCCESS && (!aligned16(dk) || !aligned16(dv)))
+        return ATTN_ERROR_MISALIGNED;
+    int st = attn_tiled_causal_backward_dq_f32(q, k, v, o, do_ptr, m_ptr, l_ptr, dq,
+                                               d_workspace, B, H, T, d_head, scale, stream);
+    if (st != ATTN_SUCCESS) return st;
+    return attn_tiled_causal_backward_dkdv_f32(q, k, v, do_ptr, m_ptr, l_ptr, d_workspace, dk,
+                                               dv, B, H, T, d_head, scale, stream);
+}
+
+// ---- tiled bf16 ------------------------------------------------------------------------
+
+int attn_tiled_causal_forward_bf16(const attn_bf16* q, const attn_bf16* k, const attn_bf16* v,
+                                   attn_bf16* out, int B, int H, int T, int d_head, float scale,
+                                   float* m_out, float* l_out, hipStream_t stream) {
+    if (q == nullptr || k == nullptr || v == nullptr || out == nullptr)
+        return ATTN_ERROR_NULL_POINTER;
+    const int st = check_tiled(B, H, T, d_head, scale);
+    if (st != ATTN_SUCCESS) return st;
+    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out))
+        return ATTN_ERROR_MISALIGNED;
+    clear_error();
+    tcamd::launch_flash_fwd_bf16(q, k, v, out, m_out, l_out, B * H, T, d_head, scale, stream);
+    return launch_status();
+}
+
+int attn_tiled_causal_backward_dq_bf16(const attn_bf16* q, const attn_bf16* k,
+                                       const attn_bf16* v, const attn_bf16* o,
+                                       const attn_bf16* do_ptr, const float* m_ptr,
+                                       const float* l_ptr, attn_bf16* dq, float* d_workspace,
+                                       int B, int H, int T, int d_head, float scale,
+                                       hipStream_t stream) {
+    if (q == nullptr || k == nullptr || v == nullptr || o == nullptr || do_ptr == nullptr ||
+        m_ptr == nullptr || l_ptr == nullptr || dq == nullptr || d_workspace == nullptr)
+        return ATTN_ERROR_NULL_POINTER;
+    const int st = check_tiled(B, H, T, d_head, scale);
+    if (st != ATTN_SUCCESS) return st;
+    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o) ||
+        !aligned16(do_ptr) || !aligned16(dq))
+        return ATTN_ERROR_MISALIGNED;
+    clear_error();
+    tcamd::launch_flash_bwd_dq_bf16(q, k, v, o, do_ptr, m_ptr, l_ptr, dq, d_workspace, B * H,
+                                    T, d_head, scale, stream);
+    return launch_status();
+}
+
+int attn_tiled_causal_backward_dkdv_bf16(const attn_bf16* q, const attn_bf16* k,
+                                         const attn_bf16* v, const attn_bf16* do_ptr,
+                                         const float* m_ptr, const float* l_ptr,
+                                         const float* d_workspace, attn_bf16* dk, attn_bf16* dv,
+                                         int B, int H, int T, int d_head, float scale,
+                                         hipStream_t stream) {
+    if (q == nullptr || k == nullptr || v == nullptr || do_ptr == nullptr || m_ptr == nullptr ||
+        l_ptr == nullptr || d_workspace == nullptr || dk == nullptr || dv == nullptr)
+        return ATTN_ERROR_NULL_POINTER;
+    const int st = check_tiled(B, H, T, d_head, scale);
+    if (st != ATTN_SUCCESS) return st;
+    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(do_ptr) ||
+        !aligned16(dk) || !aligned16(dv))
+        return ATTN_ERROR_MISALIGNED;
+    clear_error();
+    tcamd::launch_flash_bwd_dkdv_bf16(q, k, v, do_ptr, m_ptr, l_ptr, d_workspace, dk, dv,
+                                      B * H, T, d_head, scale, stream);
+    return launch_status();
+}
+
+int attn_tiled_causal_backward_bf16(const attn_bf16* q, const attn_bf16* k,
+                                    const attn_bf16* v, const attn_bf16* o,
+                                    const attn_bf16* do_ptr, const float* m_ptr,
+                                    const float* l_ptr, attn_bf16* dq, attn_bf16* dk,
+                                    attn_bf16* dv, float* d_workspace, int B, int H, int T,
+                                    int d_head, float scale, hipStream_t stream) {
+    if (dk == nullptr || dv == nullptr) return ATTN_ERROR_NULL_POINTER;
+    if (check_tiled(B, H, T, d_head, scale) == ATTN_SUCCESS && (!aligned16(dk) || !aligned16(dv)))
+        return ATTN_ERROR_MISALIGNED;
+    int st = attn_tiled_causal_backward_dq_bf16(q, k, v, o, do_ptr, m_ptr, l_ptr, dq,
+                                                d_workspace, B, H, T, d_head, scale, stream);
+    if (st != ATTN_SUCCESS) return st;
+    return attn_tiled_causal_backward_dkdv_bf16(q, k, v, do_ptr, m_ptr, l_ptr, d_workspace, dk,
+                                                dv, B, H, T, d_head, scale, stream);
+}
+
+}  // extern "C"

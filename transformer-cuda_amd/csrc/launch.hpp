@@ -1,0 +1,53 @@
+// launch.hpp - internal launchers, one per kernel family.  The C ABI (capi.hip) validates
+// arguments and then calls these; they assume valid arguments and only enqueue work.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tcamd {
+
+enum class ElemType { F32, BF16 };
+
+// Row-major (B, T, S, H, d) <-> S head-major tensors (B, H, T, d).  S = 3 for the QKV
+// split (heads[0..2] = q, k, v), S = 1 for the head merge.  to_heads selects the
+// direction.  Element types may differ (the cast is fused into the copy).
+struct HeadPtrs {
+    void* p[3];
+};
+void launch_stripe_transpose(const void* src, ElemType src_t, void* dst, ElemType dst_t,
+                             const HeadPtrs& heads, bool to_heads, int B, int T, int S, int H,
+                             int d, hipStream_t stream);
+
+void launch_causal_softmax_fwd_f32(const float* scores, float* probs, int64_t rows, int T,
+                                   float scale, hipStream_t stream);
+void launch_causal_softmax_bwd_f32(const float* dprobs, const float* probs, float* dscores,
+                                   int64_t rows, int T, float scale, hipStream_t stream);
+
+void launch_dot_do_o_f32(const float* dO, const float* O, float* D, int64_t rows, int d,
+                         hipStream_t stream);
+
+void launch_flash_fwd_f32(const float* q, const float* k, const float* v, float* o,
+                          float* m_out, float* l_out, int BH, int T, int d, float scale,
+                          hipStream_t stream);
+void launch_flash_bwd_dq_f32(const float* q, const float* k, const float* v, const float* o,
+                             const float* dO, const float* m, const float* l, float* dq,
+                             float* Dws, int BH, int T, int d, float scale, hipStream_t stream);
+void launch_flash_bwd_dkdv_f32(const float* q, const float* k, const float* v,
+                               const float* dO, const float* m, const float* l,
+                               const float* Dws, float* dk, float* dv, int BH, int T, int d,
+                               float scale, hipStream_t stream);
+
+void launch_flash_fwd_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                           uint16_t* o, float* m_out, float* l_out, int BH, int T, int d,
+                           float scale, hipStream_t stream);
+void launch_flash_bwd_dq_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                              const uint16_t* o, const uint16_t* dO, const float* m,
+                              const float* l, uint16_t* dq, float* Dws, int BH, int T, int d,
+                              float scale, hipStream_t stream);
+void launch_flash_bwd_dkdv_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                const uint16_t* dO, const float* m, const float* l,
+                                const float* Dws, uint16_t* dk, uint16_t* dv, int BH, int T,
+                                int d, float scale, hipStream_t stream);
+
+}  // namespace tcamd

@@ -1,0 +1,221 @@
+// split_transpose.hip - QKV split-transpose and head merge (HBM-bound copies).
+//
+// Both are the same permutation of contiguous d-element rows: the row-major tensor
+// (B, T, S, H, d) and S head-major tensors (B, H, T, d) hold row (b, t, s, h) at
+//     row-major  ((b*T + t)*S + s)*H*d + h*d        head-major[s]  ((b*H + h)*T + t)*d
+// (reference index maps: src/kernels/attention.cu:36-49 for S = 3, :320-327 for S = 1).
+// A workgroup owns one (b, h, s) and a run of t; each thread moves U-element units at a
+// fixed column, so the division-free address update per row is two adds and both sides
+// are read/written in whole d-element rows (>= 128 B for d = 64 bf16).
+#include "device_common.hpp"
+#include "launch.hpp"
+
+namespace tcamd {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kRowIters = 4;  // rows each thread moves (loads issued before stores)
+
+template <typename TS, typename TD, int U>
+struct Unit;
+
+// Same-type 16-byte unit: raw copy.
+template <int U>
+struct Unit<float, float, U> {
+    static_assert(U == 4, "fp32 unit is 4 elements");
+    using In = f32x4;
+    __device__ static In load(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
+    __device__ static void store(float* p, In x) { *reinterpret_cast<f32x4*>(p) = x; }
+};
+template <int U>
+struct Unit<uint16_t, uint16_t, U> {
+    static_assert(U == 8, "bf16 unit is 8 elements");
+    using In = u16x8;
+    __device__ static In load(const uint16_t* p) { return *reinterpret_cast<const u16x8*>(p); }
+    __device__ static void store(uint16_t* p, In x) { *reinterpret_cast<u16x8*>(p) = x; }
+};
+// fp32 -> bf16 (round to nearest even), 16 B in, 8 B out.
+template <int U>
+struct Unit<float, uint16_t, U> {
+    static_assert(U == 4, "f32->bf16 unit is 4 elements");
+    using In = f32x4;
+    __device__ static In load(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
+    __device__ static void store(uint16_t* p, In x) {
+        u16x4 o;
+        o[0] = f32_to_bf16_bits(x[0]);
+        o[1] = f32_to_bf16_bits(x[1]);
+        o[2] = f32_to_bf16_bits(x[2]);
+        o[3] = f32_to_bf16_bits(x[3]);
+        *reinterpret_cast<u16x4*>(p) = o;
+    }
+};
+// bf16 -> fp32 (exact), 8 B in, 16 B out.
+template <int U>
+struct Unit<uint16_t, float, U> {
+    static_assert(U == 4, "bf16->f32 unit is 4 elements");
+    using In = u16x4;
+    __device__ static In load(const uint16_t* p) { return *reinterpret_cast<const u16x4*>(p); }
+    __device__ static void store(float* p, In x) {
+        f32x4 o;
+        o[0] = bf16_bits_to_f32(x[0]);
+        o[1] = bf16_bits_to_f32(x[1]);
+        o[2] = bf16_bits_to_f32(x[2]);
+        o[3] = bf16_bits_to_f32(x[3]);
+        *reinterpret_cast<f32x4*>(p) = o;
+    }
+};
+
+// grid = (ceil(T / rows_per_block), B*H, S); ch = d / U is a power of two <= 256.
+template <typename TS, typename TD, int U, bool kToHeads>
+__global__ __launch_bounds__(kThreads) void stripe_transpose_vec_kernel(
+    const TS* __restrict__ src_rm, TD* __restrict__ dst_rm, HeadPtrs heads, int T, int S,
+    int H, int d, int log2_ch) {
+    const int tid = threadIdx.x;
+    const int c = tid & ((1 << log2_ch) - 1);
+    const int r = tid >> log2_ch;
+    const int rows_per_iter = kThreads >> log2_ch;
+    const int bh = blockIdx.y;
+    const int b = bh / H;
+    const int h = bh - b * H;
+    const int s = blockIdx.z;
+    const int t0 = blockIdx.x * rows_per_iter * kRowIters + r;
+
+    const int64_t rm_stride = static_cast<int64_t>(S) * H * d;  // elements between rows t
+    int64_t rm = ((static_cast<int64_t>(b) * T + t0) * S + s) * static_cast<int64_t>(H) * d +
+                 static_cast<int64_t>(h) * d + c * U;
+    int64_t hm = (static_cast<int64_t>(bh) * T + t0) * d + c * U;
+    const int64_t rm_step = rm_stride * rows_per_iter;
+    const int64_t hm_step = static_cast<int64_t>(d) * rows_per_iter;
+
+    using UnitT = Unit<TS, TD, U>;
+    typename UnitT::In buf[kRowIters];
+    if constexpr (kToHeads) {
+        const TS* src = src_rm;
+        TD* dst = static_cast<TD*>(heads.p[s]);
+#pragma unroll
+        for (int i = 0; i < kRowIters; ++i) {
+            if (t0 + i * rows_per_iter < T) buf[i] = UnitT::load(src + rm + i * rm_step);
+        }
+#pragma unroll
+        for (int i = 0; i < kRowIters; ++i) {
+            if (t0 + i * rows_per_iter < T) UnitT::store(dst + hm + i * hm_step, buf[i]);
+        }
+    } else {
+        const TS* src = static_cast<const TS*>(heads.p[s]);
+        TD* dst = dst_rm;
+#pragma unroll
+        for (int i = 0; i < kRowIters; ++i) {
+            if (t0 + i * rows_per_iter < T) buf[i] = UnitT::load(src + hm + i * hm_step);
+        }
+#pragma unroll
+        for (int i = 0; i < kRowIters; ++i) {
+            if (t0 + i * rows_per_iter < T) UnitT::store(dst + rm + i * rm_step, buf[i]);
+        }
+    }
+}
+
+template <typename TS, typename TD>
+__device__ __forceinline__ TD convert_elem(TS x) {
+    if constexpr (__is_same(TS, TD)) {
+        return x;
+    } else if constexpr (__is_same(TS, float)) {
+        return f32_to_bf16_bits(x);
+    } else {
+        return bf16_bits_to_f32(x);
+    }
+}
+
+// Element path for any d / alignment: one thread per element of the head-major side.
+template <typename TS, typename TD, bool kToHeads>
+__global__ __launch_bounds__(kThreads) void stripe_transpose_elem_kernel(
+    const TS* __restrict__ src_rm, TD* __restrict__ dst_rm, HeadPtrs heads, int B, int T,
+    int S, int H, int d) {
+    const int64_t per_tensor = static_cast<int64_t>(B) * H * T * d;
+    const int64_t total = per_tensor * S;
+    for (int64_t idx = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; idx < total;
+         idx += static_cast<int64_t>(gridDim.x) * kThreads) {
+        const int s = static_cast<int>(idx / per_tensor);
+        const int64_t hm = idx - s * per_tensor;  // ((b*H + h)*T + t)*d + e
+        const int e = static_cast<int>(hm % d);
+        const int64_t row = hm / d;
+        const int t = static_cast<int>(row % T);
+        const int64_t bh = row / T;
+        const int h = static_cast<int>(bh % H);
+        const int64_t b = bh / H;
+        const int64_t rm = ((b * T + t) * S + s) * static_cast<int64_t>(H) * d +
+                           static_cast<int64_t>(h) * d + e;
+        if constexpr (kToHeads) {
+            static_cast<TD*>(heads.p[s])[hm] = convert_elem<TS, TD>(src_rm[rm]);
+        } else {
+            dst_rm[rm] = convert_elem<TS, TD>(static_cast<const TS*>(heads.p[s])[hm]);
+        }
+    }
+}
+
+bool aligned(const void* p, int bytes) {
+    return (reinterpret_cast<uintptr_t>(p) & static_cast<uintptr_t>(bytes - 1)) == 0;
+}
+
+template <typename TS, typename TD, int U>
+void dispatch(const void* src, void* dst, const HeadPtrs& heads, bool to_heads, int B, int T,
+              int S, int H, int d, hipStream_t stream) {
+    const int ch = d / U;
+    bool vec = (d % U == 0) && ch >= 1 && ch <= kThreads && (ch & (ch - 1)) == 0;
+    const int src_bytes = U * static_cast<int>(sizeof(TS));
+    const int dst_bytes = U * static_cast<int>(sizeof(TD));
+    if (vec) {
+        if (to_heads) {
+            vec = aligned(src, src_bytes);
+            for (int s = 0; s < S; ++s) vec = vec && aligned(heads.p[s], dst_bytes);
+        } else {
+            vec = aligned(dst, dst_bytes);
+            for (int s = 0; s < S; ++s) vec = vec && aligned(heads.p[s], src_bytes);
+        }
+    }
+    const TS* src_rm = static_cast<const TS*>(src);
+    TD* dst_rm = static_cast<TD*>(dst);
+    if (vec) {
+        int log2_ch = 0;
+        while ((1 << log2_ch) < ch) ++log2_ch;
+        const int rows_per_block = (kThreads >> log2_ch) * kRowIters;
+        dim3 grid((T + rows_per_block - 1) / rows_per_block, B * H, S);
+        if (to_heads) {
+            hipLaunchKernelGGL((stripe_transpose_vec_kernel<TS, TD, U, true>), grid,
+                               dim3(kThreads), 0, stream, src_rm, dst_rm, heads, T, S, H, d,
+                               log2_ch);
+        } else {
+            hipLaunchKernelGGL((stripe_transpose_vec_kernel<TS, TD, U, false>), grid,
+                               dim3(kThreads), 0, stream, src_rm, dst_rm, heads, T, S, H, d,
+                               log2_ch);
+        }
+    } else {
+        const int64_t total = static_cast<int64_t>(B) * H * T * d * S;
+        const int64_t blocks64 = (total + kThreads - 1) / kThreads;
+        const int blocks = static_cast<int>(blocks64 < 65536 ? blocks64 : 65536);
+        if (to_heads) {
+            hipLaunchKernelGGL((stripe_transpose_elem_kernel<TS, TD, true>), dim3(blocks),
+                               dim3(kThreads), 0, stream, src_rm, dst_rm, heads, B, T, S, H, d);
+        } else {
+            hipLaunchKernelGGL((stripe_transpose_elem_kernel<TS, TD, false>), dim3(blocks),
+                               dim3(kThreads), 0, stream, src_rm, dst_rm, heads, B, T, S, H, d);
+        }
+    }
+}
+
+}  // namespace
+
+void launch_stripe_transpose(const void* src, ElemType src_t, void* dst, ElemType dst_t,
+                             const HeadPtrs& heads, bool to_heads, int B, int T, int S, int H,
+                             int d, hipStream_t stream) {
+    if (src_t == ElemType::F32 && dst_t == ElemType::F32) {
+        dispatch<float, float, 4>(src, dst, heads, to_heads, B, T, S, H, d, stream);
+    } else if (src_t == ElemType::BF16 && dst_t == ElemType::BF16) {
+        dispatch<uint16_t, uint16_t, 8>(src, dst, heads, to_heads, B, T, S, H, d, stream);
+    } else if (src_t == ElemType::F32) {
+        dispatch<float, uint16_t, 4>(src, dst, heads, to_heads, B, T, S, H, d, stream);
+    } else {
+        dispatch<uint16_t, float, 4>(src, dst, heads, to_heads, B, T, S, H, d, stream);
+    }
+}
+
+}  // namespace tcamd

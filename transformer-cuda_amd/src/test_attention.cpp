@@ -1,0 +1,210 @@
+// test_attention.cpp - C++ host tests of the attention launchers (include/kernels/attention.h),
+// the counterpart of the reference's tests/test_kernels.cu.  Each test uses inputs with an
+// exact closed-form answer:
+//   * causal softmax on all-equal scores (reference KAT, tests/test_kernels.cu:91-120):
+//     row i is 1/(i+1) on j <= i, 0 above;
+//   * the reference's tiled KAT (tests/test_kernels.cu:210-284: T=8, d=32, q=k=0.1, v=1,
+//     dO=0.5), strengthened from "finite" to the exact values: O = 1, dQ = dK = 0 and
+//     dV_j = 0.5 * sum_{i=j}^{T-1} 1/(i+1);
+//   * Q = 0 at T not a multiple of the tile: P_ij = 1/(i+1), O_i = mean(v_0..v_i),
+//     m_i = 0, l_i = i+1;
+//   * QKV split followed by its backward is the identity (bitwise), head merge likewise;
+//   * an unsupported head dimension throws instead of silently doing nothing.
+// Exit status 0 iff every test passes.
+#include <cmath>
+#include <cstdio>
+#include <stdexcept>
+#include <vector>
+
+#include "common.h"
+#include "kernels/attention.h"
+
+namespace {
+
+int g_failures = 0;
+
+#define EXPECT(cond, ...)                                   \
+    do {                                                    \
+        if (!(cond)) {                                      \
+            std::printf("    FAILED %s:%d: ", __FILE__, __LINE__); \
+            std::printf(__VA_ARGS__);                       \
+            std::printf("\n");                              \
+            ++g_failures;                                   \
+            return false;                                   \
+        }                                                   \
+    } while (0)
+
+struct DevBuf {
+    float* p = nullptr;
+    size_t n = 0;
+    explicit DevBuf(size_t count) : n(count) { HIP_CHECK(hipMalloc(&p, n * sizeof(float))); }
+    ~DevBuf() { (void)hipFree(p); }
+    DevBuf(const DevBuf&) = delete;
+    DevBuf& operator=(const DevBuf&) = delete;
+    void upload(const std::vector<float>& h) {
+        HIP_CHECK(hipMemcpy(p, h.data(), n * sizeof(float), hipMemcpyHostToDevice));
+    }
+    std::vector<float> download() const {
+        std::vector<float> h(n);
+        HIP_CHECK(hipMemcpy(h.data(), p, n * sizeof(float), hipMemcpyDeviceToHost));
+        return h;
+    }
+};
+
+bool test_causal_softmax() {
+    std::printf("[Test] causal softmax, all-equal scores (reference KAT)...\n");
+    const int B = 1, H = 1, T = 4;
+    DevBuf scores(T * T), probs(T * T);
+    scores.upload(std::vector<float>(T * T, 1.0f));
+    causal_softmax_forward(scores.p, probs.p, B, H, T, 1.0f);
+    HIP_CHECK(hipDeviceSynchronize());
+    const std::vector<float> p = probs.download();
+    for (int i = 0; i < T; ++i)
+        for (int j = 0; j < T; ++j) {
+            const float want = (j <= i) ? 1.0f / (i + 1) : 0.0f;
+            EXPECT(std::fabs(p[i * T + j] - want) <= 1e-6f, "p[%d][%d] = %g, want %g", i, j,
+                   p[i * T + j], want);
+        }
+    return true;
+}
+
+bool test_tiled_kat(int d_head) {
+    std::printf("[Test] tiled causal attention KAT (T=8, d=%d, q=k=0.1, v=1, dO=0.5)...\n",
+                d_head);
+    const int B = 1, H = 1, T = 8;
+    const size_t n = static_cast<size_t>(B) * H * T * d_head;
+    const size_t r = static_cast<size_t>(B) * H * T;
+    DevBuf q(n), k(n), v(n), o(n), dO(n), dq(n), dk(n), dv(n), m(r), l(r), ws(r);
+    q.upload(std::vector<float>(n, 0.1f));
+    k.upload(std::vector<float>(n, 0.1f));
+    v.upload(std::vector<float>(n, 1.0f));
+    dO.upload(std::vector<float>(n, 0.5f));
+    const float scale = 1.0f / std::sqrt(static_cast<float>(d_head));
+    tiled_causal_attention_forward(q.p, k.p, v.p, o.p, B, H, T, d_head, scale, m.p, l.p);
+    tiled_causal_attention_backward(q.p, k.p, v.p, o.p, dO.p, m.p, l.p, dq.p, dk.p, dv.p, ws.p,
+                                    B, H, T, d_head, scale);
+    HIP_CHECK(hipDeviceSynchronize());
+    const auto ho = o.download(), hdq = dq.download(), hdk = dk.download(), hdv = dv.download();
+    const auto hl = l.download();
+    for (size_t i = 0; i < n; ++i) {
+        EXPECT(std::fabs(ho[i] - 1.0f) <= 1e-6f, "O[%zu] = %.9g, want 1", i, ho[i]);
+        EXPECT(std::fabs(hdq[i]) <= 1e-6f, "dQ[%zu] = %g, want 0", i, hdq[i]);
+        EXPECT(std::fabs(hdk[i]) <= 1e-6f, "dK[%zu] = %g, want 0", i, hdk[i]);
+    }
+    for (int t = 0; t < T; ++t) {
+        EXPECT(std::fabs(hl[t] - (t + 1)) <= 1e-5f, "l[%d] = %g, want %d", t, hl[t], t + 1);
+        double want = 0.0;
+        for (int i = t; i < T; ++i) want += 0.5 / (i + 1);
+        for (int e = 0; e < d_head; ++e) {
+            const float got = hdv[t * d_head + e];
+            EXPECT(std::fabs(got - want) <= 1e-6 * want + 1e-7, "dV[%d][%d] = %.9g, want %.9g", t,
+                   e, got, want);
+        }
+    }
+    return true;
+}
+
+bool test_zero_query(int d_head, int T) {
+    std::printf("[Test] Q = 0 closed form (T=%d, d=%d): prefix means of V...\n", T, d_head);
+    const int B = 2, H = 3;
+    const size_t n = static_cast<size_t>(B) * H * T * d_head;
+    const size_t r = static_cast<size_t>(B) * H * T;
+    std::vector<float> hv(n), hk(n);
+    uint32_t state = 12345u;
+    for (size_t i = 0; i < n; ++i) {
+        state = state * 1664525u + 1013904223u;
+        hv[i] = static_cast<float>(static_cast<int>(state >> 9) % 2001 - 1000) / 1000.0f;
+        state = state * 1664525u + 1013904223u;
+        hk[i] = static_cast<float>(static_cast<int>(state >> 9) % 2001 - 1000) / 500.0f;
+    }
+    DevBuf q(n), k(n), v(n), o(n), m(r), l(r);
+    q.upload(std::vector<float>(n, 0.0f));
+    k.upload(hk);
+    v.upload(hv);
+    tiled_causal_attention_forward(q.p, k.p, v.p, o.p, B, H, T, d_head,
+                                   1.0f / std::sqrt(static_cast<float>(d_head)), m.p, l.p);
+    HIP_CHECK(hipDeviceSynchronize());
+    const auto ho = o.download(), hm = m.download(), hl = l.download();
+    for (int bh = 0; bh < B * H; ++bh) {
+        std::vector<double> sum(d_head, 0.0);
+        for (int t = 0; t < T; ++t) {
+            const size_t row = static_cast<size_t>(bh) * T + t;
+            EXPECT(hm[row] == 0.0f, "m[%zu] = %g, want 0", row, hm[row]);
+            EXPECT(std::fabs(hl[row] - (t + 1)) <= 1e-6f * (t + 1), "l[%zu] = %g, want %d", row,
+                   hl[row], t + 1);
+            for (int e = 0; e < d_head; ++e) {
+                sum[e] += hv[row * d_head + e];
+                const double want = sum[e] / (t + 1);
+                const float got = ho[row * d_head + e];
+                EXPECT(std::fabs(got - want) <= 2e-6, "O[%zu][%d] = %.9g, want %.9g", row, e,
+                       got, want);
+            }
+        }
+    }
+    return true;
+}
+
+bool test_split_roundtrip() {
+    std::printf("[Test] QKV split-transpose fwd -> bwd is the identity; head merge too...\n");
+    const int B = 2, T = 37, H = 3, d = 64;
+    const size_t n = static_cast<size_t>(B) * T * H * d;
+    std::vector<float> h(3 * n);
+    for (size_t i = 0; i < h.size(); ++i) h[i] = static_cast<float>(i) * 0.25f - 7.0f;
+    DevBuf qkv(3 * n), q(n), k(n), v(n), back(3 * n), merged(n), unmerged(n);
+    qkv.upload(h);
+    qkv_split_transpose_forward(qkv.p, q.p, k.p, v.p, B, T, H, d);
+    qkv_split_transpose_backward(q.p, k.p, v.p, back.p, B, T, H, d);
+    head_merge_transpose_forward(q.p, merged.p, B, H, T, d);
+    head_merge_transpose_backward(merged.p, unmerged.p, B, H, T, d);
+    HIP_CHECK(hipDeviceSynchronize());
+    const auto hb = back.download();
+    for (size_t i = 0; i < h.size(); ++i) EXPECT(hb[i] == h[i], "dqkv[%zu] = %g != %g", i, hb[i], h[i]);
+    const auto hq = q.download();
+    // q[b,h,t,e] = qkv[b,t,0*C + h*d + e]
+    for (int b = 0; b < B; ++b)
+        for (int hh = 0; hh < H; ++hh)
+            for (int t = 0; t < T; ++t)
+                for (int e = 0; e < d; ++e) {
+                    const size_t hm_i = ((static_cast<size_t>(b) * H + hh) * T + t) * d + e;
+                    const size_t rm_i = (static_cast<size_t>(b) * T + t) * 3 * H * d + hh * d + e;
+                    EXPECT(hq[hm_i] == h[rm_i], "q mismatch at %zu", hm_i);
+                }
+    const auto hu = unmerged.download();
+    for (size_t i = 0; i < n; ++i) EXPECT(hu[i] == hq[i], "head merge round trip at %zu", i);
+    return true;
+}
+
+bool test_bad_head_dim() {
+    std::printf("[Test] unsupported d_head is an error, not a silent no-op...\n");
+    DevBuf buf(1024);
+    bool threw = false;
+    try {
+        tiled_causal_attention_forward(buf.p, buf.p, buf.p, buf.p, 1, 1, 8, 48, 0.1f);
+    } catch (const std::runtime_error&) {
+        threw = true;
+    }
+    EXPECT(threw, "d_head = 48 did not throw");
+    return true;
+}
+
+}  // namespace
+
+int main() {
+    std::printf("========================================\n");
+    std::printf(" MI355X attention host test suite\n");
+    std::printf("========================================\n");
+    std::fflush(stdout);
+    test_causal_softmax();
+    for (int d : {32, 64, 128}) test_tiled_kat(d);
+    test_zero_query(64, 100);
+    test_zero_query(128, 33);
+    test_zero_query(32, 257);
+    test_split_roundtrip();
+    test_bad_head_dim();
+    if (g_failures == 0) {
+        std::printf("All host tests passed.\n");
+        return 0;
+    }
+    std::printf("%d host test(s) failed.\n", g_failures);
+    return 1;
+}

@@ -1,0 +1,356 @@
+#!/usr/bin/env python3
+"""Causal multi-head attention fwd+bwd throughput on one MI355X (gfx950).
+
+One step is one pass of the hot path over one batch, every kernel launched through the
+C ABI (include/attn_capi.h) on torch's current stream:
+    qkv (B,T,3C) --split-transpose--> q,k,v (B,H,T,d)             reference model.cu:305
+    tiled forward          -> O, m, l                             reference model.cu:311
+    backward stage 1       -> D = rowsum(dO*O), dQ                 reference model.cu:609
+    backward stage 2       -> dK, dV                               reference model.cu:609
+    dq,dk,dv --split-transpose backward--> dqkv (B,T,3C)          reference model.cu:653
+Inputs (qkv, dO) are synthetic N(0,1) from a fixed seed and resident in HBM before the
+timed region starts.
+
+value = algorithmic FLOPs of causal attention fwd+bwd, 7*B*H*T^2*d (FlashAttention-2
+convention: fwd 2*B*H*T^2*d, bwd 5*B*H*T^2*d), divided by the wall-clock time of the K
+timed steps.  The roofline object describes the dominant kernel (the longest average
+duration, measured with HIP events recorded on the launch stream around every kernel of
+every timed step) against its algorithmic FLOPs:
+    forward 2 units, backward dK/dV 4 units (S recompute, dP, dV, dK), backward dQ 1 unit
+    (dQ; its S and dP recomputes duplicate work already counted), unit = B*H*T^2*d.
+The split-transpose kernels are HBM-bound: 6*B*T*C*elem_bytes algorithmic bytes each.
+
+cpu_baseline: the torch-CPU fp32 restatement of the reference attention
+(pytorch_src/model.py:43-52, forward + autograd backward) timed on this host on the same
+inputs, which also gives a max-abs parity figure for the GPU result.
+
+Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 5] [--config c2]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+
+# MI355X published dense peaks (TFLOP/s) and HBM bandwidth (GB/s).
+PEAK_TFLOPS = {"f32": 157.3, "bf16": 2516.6}
+PEAK_HBM_GBS = 8000.0
+
+# (B, H, T, d, dtype, qk_scale)
+CONFIGS = {
+    "c2": (8, 12, 1024, 64, "f32", 1.0),
+    "c3": (16, 16, 2048, 64, "bf16", 1.0),
+    "c4": (2, 16, 8192, 128, "bf16", 0.5),
+}
+CONFIG_NAMES = {
+    "c2": "causal attention fwd+bwd, GPT-2-small shape (BASELINE config 2)",
+    "c3": "causal attention fwd+bwd, bf16 (BASELINE config 3)",
+    "c4": "long-context causal attention fwd+bwd, bf16 (BASELINE config 4)",
+}
+METRIC = "causal attn fwd+bwd TFLOP/s & % MFMA peak, B8 H12 T1024 d64 fp32/bf16"
+
+# kernel -> algorithmic FLOP units (unit = B*H*T^2*d) or HBM bytes factor
+KERNELS = ("split_fwd", "attn_fwd", "bwd_dq", "bwd_dkdv", "split_bwd")
+FLOP_UNITS = {"attn_fwd": 2, "bwd_dq": 1, "bwd_dkdv": 4}
+
+
+def parse_args():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", choices=sorted(CONFIGS), default="c2")
+    ap.add_argument("--dtype", choices=["f32", "bf16"], default=None,
+                    help="override the config's dtype")
+    ap.add_argument("--seed", type=int, default=42)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+                    help="target CPU time of the cpu_baseline sample")
+    ap.add_argument("--no-secondary", action="store_true",
+                    help="skip the bf16 secondary measurements")
+    ap.add_argument("--secondary-steps", type=int, default=20)
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="instead of the bench: run 10 plain device copies of MIB MiB (the "
+                         "known-size kernel that scales rocprofv3 FETCH_SIZE/WRITE_SIZE)")
+    return ap.parse_args()
+
+
+def copy_calibration(mib):
+    """10 launches of torch's device copy of `mib` MiB: FETCH_SIZE and WRITE_SIZE of this
+    kernel should each read mib*1024 KiB per dispatch; the ratio calibrates the counters."""
+    import torch
+    n = mib * (1 << 20) // 4
+    src = torch.ones(n, device="cuda:0", dtype=torch.float32)
+    dst = torch.empty_like(src)
+    for _ in range(10):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": n * 4, "launches": 10}), flush=True)
+    return 0
+
+
+def load_lib():
+    sys.path.insert(0, REPO)
+    import __graft_entry__
+    return __graft_entry__.load_package()
+
+
+class PathRunner:
+    """Device buffers of one workload and the launches of one step."""
+
+    def __init__(self, lib, B, H, T, d, dtype, seed, qk_scale):
+        import torch
+        self.lib, self.torch = lib, torch
+        self.B, self.H, self.T, self.d = B, H, T, d
+        self.C = H * d
+        self.dtype = dtype
+        self.tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
+        self.scale = 1.0 / math.sqrt(d)
+        dev = torch.device("cuda:0")
+        g = torch.Generator(device=dev).manual_seed(seed)
+        qkv = torch.randn((B, T, 3, H, d), generator=g, device=dev, dtype=torch.float32)
+        qkv[:, :, :2] *= qk_scale
+        self.qkv = qkv.reshape(B, T, 3 * self.C).to(self.tdt).contiguous()
+        self.do = torch.randn((B, H, T, d), generator=g, device=dev,
+                              dtype=torch.float32).to(self.tdt).contiguous()
+        e = lambda: torch.empty((B, H, T, d), device=dev, dtype=self.tdt)
+        self.q, self.k, self.v, self.o = e(), e(), e(), e()
+        self.dq, self.dk, self.dv = e(), e(), e()
+        st = lambda: torch.empty((B, H, T), device=dev, dtype=torch.float32)
+        self.m, self.l, self.ws = st(), st(), st()
+        self.dqkv = torch.empty_like(self.qkv)
+
+    def launches(self):
+        L, a = self.lib, (self.B, self.H, self.T, self.d)
+        B, H, T, d = a
+        return (
+            ("split_fwd", lambda: L.qkv_split_transpose_forward(
+                self.qkv, self.q, self.k, self.v, B, T, H, d)),
+            ("attn_fwd", lambda: L.tiled_causal_attention_forward(
+                self.q, self.k, self.v, self.o, B, H, T, d, self.scale, self.m, self.l)),
+            ("bwd_dq", lambda: L.tiled_causal_attention_backward_dq(
+                self.q, self.k, self.v, self.o, self.do, self.m, self.l, self.dq, self.ws,
+                B, H, T, d, self.scale)),
+            ("bwd_dkdv", lambda: L.tiled_causal_attention_backward_dkdv(
+                self.q, self.k, self.v, self.do, self.m, self.l, self.ws, self.dk, self.dv,
+                B, H, T, d, self.scale)),
+            ("split_bwd", lambda: L.qkv_split_transpose_backward(
+                self.dq, self.dk, self.dv, self.dqkv, B, T, H, d)),
+        )
+
+    def step(self):
+        for _, fn in self.launches():
+            fn()
+
+    def flops_total(self):
+        return 7.0 * self.B * self.H * self.T * self.T * self.d
+
+    def kernel_work(self, name):
+        """(algorithmic amount per launch, unit) of one kernel."""
+        unit = float(self.B * self.H * self.T * self.T * self.d)
+        if name in FLOP_UNITS:
+            return FLOP_UNITS[name] * unit, "flop"
+        elem = 2 if self.dtype == "bf16" else 4
+        return 6.0 * self.B * self.T * self.C * elem, "byte"
+
+    def timed(self, steps, warmup):
+        """Time `steps` steps; per-kernel durations from events on the launch stream."""
+        torch = self.torch
+        for _ in range(warmup):
+            self.step()
+        torch.cuda.synchronize()
+        stream = torch.cuda.current_stream()
+        launches = self.launches()
+        evs = [[torch.cuda.Event(enable_timing=True) for _ in range(len(launches) + 1)]
+               for _ in range(steps)]
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(steps):
+            evs[i][0].record(stream)
+            for j, (_, fn) in enumerate(launches):
+                fn()
+                evs[i][j + 1].record(stream)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        per_kernel = {}
+        for j, (name, _) in enumerate(launches):
+            ms = [evs[i][j].elapsed_time(evs[i][j + 1]) for i in range(steps)]
+            per_kernel[name] = sum(ms) / len(ms)
+        return wall, per_kernel
+
+    def outputs_finite(self):
+        torch = self.torch
+        return all(bool(torch.isfinite(t.float()).all()) for t in
+                   (self.o, self.dq, self.dk, self.dv, self.dqkv))
+
+
+def roofline_of(runner, per_kernel):
+    name = max(per_kernel, key=per_kernel.get)
+    amount, kind = runner.kernel_work(name)
+    sec = per_kernel[name] * 1e-3
+    if kind == "flop":
+        achieved = amount / sec / 1e12
+        peak = PEAK_TFLOPS[runner.dtype]
+        bound, unit = "mfma", "TFLOP/s"
+    else:
+        achieved = amount / sec / 1e9
+        peak = PEAK_HBM_GBS
+        bound, unit = "hbm", "GB/s"
+    return name, {"bound": bound, "achieved": round(achieved, 3), "peak": peak, "unit": unit,
+                  "frac": round(achieved / peak, 4), "traffic": None}
+
+
+def kernel_table(runner, per_kernel):
+    out = {}
+    for name, ms in per_kernel.items():
+        amount, kind = runner.kernel_work(name)
+        if kind == "flop":
+            rate = amount / (ms * 1e-3) / 1e12
+            out[name] = {"ms": round(ms, 4), "tflops": round(rate, 2),
+                         "frac_mfma": round(rate / PEAK_TFLOPS[runner.dtype], 4)}
+        else:
+            rate = amount / (ms * 1e-3) / 1e9
+            out[name] = {"ms": round(ms, 4), "gbs": round(rate, 1),
+                         "frac_hbm": round(rate / PEAK_HBM_GBS, 4)}
+    return out
+
+
+def cpu_baseline(runner, target_s):
+    """Time the torch-CPU fp32 restatement on this host (bounded sample) and compare its
+    result with the GPU's last step on the same inputs."""
+    import numpy as np
+    import torch
+    from oracle import attention_ref as ref
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    cores = torch.get_num_threads()
+    B, H, T, d = runner.B, runner.H, runner.T, runner.d
+    f = lambda t: t.float().cpu()
+    q, k, v, do = f(runner.q), f(runner.k), f(runner.v), f(runner.do)
+    # sample: whole (b, h) heads, as many as fit about target_s of CPU time
+    heads = [(b, h) for b in range(B) for h in range(H)]
+    t0 = time.perf_counter()
+    r = ref.attention_fwd_bwd(q[:1, :1], k[:1, :1], v[:1, :1], do[:1, :1], runner.scale)
+    one = max(time.perf_counter() - t0, 1e-4)  # warm-up, also sizes the sample
+    n_heads = int(min(len(heads), max(1, target_s / one)))
+    # contiguous group of heads, processed in chunks of up to 8 (b, h) slices
+    sel = heads[:n_heads]
+    done, t_cpu = 0, 0.0
+    errs = {n: 0.0 for n in ("o", "dq", "dk", "dv")}
+    got = {n: f(getattr(runner, n)) for n in ("o", "dq", "dk", "dv")}
+    while done < n_heads:
+        group = sel[done:done + 8]
+        bs = sorted({b for b, _ in group})
+        for b in bs:
+            hs = [h for bb, h in group if bb == b]
+            h0, h1 = hs[0], hs[-1] + 1
+            t0 = time.perf_counter()
+            r = ref.attention_fwd_bwd(q[b:b + 1, h0:h1], k[b:b + 1, h0:h1], v[b:b + 1, h0:h1],
+                                      do[b:b + 1, h0:h1], runner.scale)
+            t_cpu += time.perf_counter() - t0
+            for n in errs:
+                diff = (got[n][b:b + 1, h0:h1] - getattr(r, n)).abs().max().item()
+                errs[n] = max(errs[n], diff)
+        done += len(group)
+    frac = n_heads / len(heads)
+    flops = runner.flops_total() * frac
+    return {
+        "value": round(flops / t_cpu / 1e12, 5),
+        "unit": "TFLOP/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": (f"{n_heads} of {len(heads)} (b,h) heads of the same workload and inputs "
+                   f"(T={T}, d={d}), torch {torch.__version__} CPU fp32 restatement of "
+                   f"pytorch_src/model.py:43-52 fwd + autograd bwd, {t_cpu:.1f} s; "
+                   f"{os.cpu_count()} host CPUs"),
+        "seconds": round(t_cpu, 2),
+        "gpu_vs_cpu_max_abs": {n: float(f"{e:.3e}") for n, e in errs.items()},
+    }
+
+
+def secondary(lib, cfg, dtype, steps, seed):
+    B, H, T, d, _, qk = CONFIGS[cfg]
+    r = PathRunner(lib, B, H, T, d, dtype, seed, qk)
+    wall, per_kernel = r.timed(steps, 3)
+    ms = wall / steps * 1e3
+    tf = r.flops_total() / (ms * 1e-3) / 1e12
+    attn_ms = sum(per_kernel[n] for n in FLOP_UNITS)
+    out = {"config": cfg, "shape": f"B{B} H{H} T{T} d{d}", "dtype": dtype,
+           "ms_per_step": round(ms, 4), "tflops": round(tf, 2),
+           "frac_mfma_peak": round(tf / PEAK_TFLOPS[dtype], 4),
+           "attn_only_tflops": round(r.flops_total() / (attn_ms * 1e-3) / 1e12, 2),
+           "kernels": kernel_table(r, per_kernel), "finite": r.outputs_finite()}
+    del r
+    return out
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
+              "(the attention path shards by batch/head with no exchange inside the path; "
+              "see the sharding paragraph of the design notes)", file=sys.stderr)
+        return 2
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        return 1
+    if args.copy_calibration:
+        return copy_calibration(args.copy_calibration)
+    lib = load_lib()
+    B, H, T, d, cdt, qk = CONFIGS[args.config]
+    dtype = args.dtype or cdt
+    runner = PathRunner(lib, B, H, T, d, dtype, args.seed, qk)
+    wall, per_kernel = runner.timed(args.steps, args.warmup)
+    ms = wall / args.steps * 1e3
+    value = runner.flops_total() / (ms * 1e-3) / 1e12
+    dom, roof = roofline_of(runner, per_kernel)
+    attn_ms = sum(per_kernel[n] for n in FLOP_UNITS)
+    props = torch.cuda.get_device_properties(0)
+    line = {
+        "metric": METRIC,
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": dtype,
+        "data": "synthetic N(0,1) qkv and dO from a fixed seed, resident in HBM",
+        "config": {"workload": CONFIG_NAMES[args.config], "B": B, "H": H, "T": T,
+                   "d_head": d, "causal": True,
+                   "step": "split_fwd + attn_fwd + bwd_dq + bwd_dkdv + split_bwd",
+                   "flops_per_step": runner.flops_total()},
+        "frac_mfma_peak": round(value / PEAK_TFLOPS[dtype], 4),
+        "attn_only_tflops": round(runner.flops_total() / (attn_ms * 1e-3) / 1e12, 3),
+        "roofline": dict(roof, kernel=dom),
+        "kernels": kernel_table(runner, per_kernel),
+        "finite": runner.outputs_finite(),
+        "device": {"name": props.name, "cus": props.multi_processor_count,
+                   "torch": torch.__version__},
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(runner, args.cpu_seconds)
+    else:
+        line["cpu_baseline"] = None
+    del runner
+    torch.cuda.empty_cache()
+    if not args.no_secondary:
+        sec = [secondary(lib, args.config, "bf16", args.secondary_steps, args.seed)] \
+            if dtype != "bf16" else []
+        sec.append(secondary(lib, "c3", "bf16", args.secondary_steps, args.seed))
+        line["secondary"] = sec
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -114,7 +114,8 @@ def test_stats_and_stages_match_reference_kernels(lib):
     scale = default_scale(d)
     c_o, c_m, c_l = co.tiled_fwd(q, k, v, scale)
     got = gpu_fwd_bwd(lib, q, k, v, do, scale)
-    np.testing.assert_allclose(got["m"], c_m, atol=1e-6)
+    # m is a max of fp32 dot products whose summation order differs (MFMA vs a C loop)
+    np.testing.assert_allclose(got["m"], c_m, rtol=2e-6, atol=1e-6)
     np.testing.assert_allclose(got["l"], c_l, rtol=2e-6)
     np.testing.assert_allclose(got["o"], c_o, atol=1e-5)
     c_dq, c_dk, c_dv, c_D = co.tiled_bwd(q, k, v, got["o"], do, got["m"], got["l"], scale)

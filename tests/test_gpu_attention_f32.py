@@ -33,6 +33,13 @@ def test_config2_parity(lib, config2):
     errs = {n: max_abs(got[n], getattr(want, n).numpy()) for n in ("o", "dq", "dk", "dv")}
     errs["lse"] = max_abs(lse, want.lse.numpy())
     print("config2 max-abs vs torch fp32:", {k: f"{e:.2e}" for k, e in errs.items()})
+    # distance of both fp32 results to fp64 (reported; the gate is the one above)
+    w64 = ref.attention_fwd_bwd(q, k, v, do, 0.125, dtype=torch.float64)
+    d64 = {n: (max_abs(got[n], getattr(w64, n).numpy()),
+               max_abs(getattr(want, n).numpy(), getattr(w64, n).numpy()))
+           for n in ("o", "dq", "dk", "dv")}
+    print("config2 max-abs to fp64 (gpu, torch fp32):",
+          {k: f"{a:.2e}, {b:.2e}" for k, (a, b) in d64.items()})
     for n, e in errs.items():
         assert e <= TOL, f"{n}: max-abs {e:.3e} > {TOL}"
 

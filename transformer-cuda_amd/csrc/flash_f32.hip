@@ -138,6 +138,33 @@ __device__ __forceinline__ void store_acc_row(float* __restrict__ head, int row,
     }
 }
 
+// Compensated (Kahan) running sum of per-tile partial products: sum += x with the rounding
+// error carried in comp.  Each tile's contraction is accumulated by the MFMA into a fresh
+// zero accumulator (16 fp32 adds per element per tile) and only tile totals enter the
+// running sum, so the rounding error no longer grows with the sequence length.  Used for
+// d_head <= 64; at d_head = 128 the compensation terms do not fit the register file of the
+// dK/dV kernel, which then adds the tile totals without compensation (two-level sum).
+template <int D>
+constexpr bool kCompensated = D <= 64;
+
+template <int N>
+__device__ __forceinline__ void plain_add(f32x16 (&sum)[N], const f32x16 (&x)[N]) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) sum[i] += x[i];
+}
+
+template <int N>
+__device__ __forceinline__ void kahan_add(f32x16 (&sum)[N], f32x16 (&comp)[N],
+                                          const f32x16 (&x)[N]) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        const f32x16 y = x[i] - comp[i];
+        const f32x16 t = sum[i] + y;
+        comp[i] = (t - sum[i]) - y;
+        sum[i] = t;
+    }
+}
+
 // --------------------------------------------------------------------------------------
 // Forward.  Workgroup = NW waves = 32*NW queries of one (b, h); wave w owns queries
 // [q0 + 32w, q0 + 32w + 32).  grid = BH * nqt, heaviest query tile first.
@@ -316,9 +343,12 @@ __global__ __launch_bounds__(kWave* NW) void flash_bwd_dq_f32_kernel(
     const float m_row = row_ok ? m[stat_off + qi] : 0.0f;
     const float inv_l = row_ok ? 1.0f / l[stat_off + qi] : 0.0f;
 
-    f32x16 acc[D / 32];
+    f32x16 acc[D / 32], comp[D / 32];
 #pragma unroll
-    for (int dt = 0; dt < D / 32; ++dt) acc[dt] = f32x16{};
+    for (int dt = 0; dt < D / 32; ++dt) {
+        acc[dt] = f32x16{};
+        comp[dt] = f32x16{};
+    }
 
     const int kend = min(T, q0 + kTile * NW);
     const int ntiles = (kend + kTile - 1) / kTile;
@@ -351,7 +381,15 @@ __global__ __launch_bounds__(kWave* NW) void flash_bwd_dq_f32_kernel(
                 if (diag && t * kTile + acc_row(r, half) > qi) p = 0.0f;
                 s[r] = p * (dp[r] - Dval);  // dS^T (without the scale)
             }
-            mma_cols<D, KS>(Ks[buf], col, half, s, acc);
+            f32x16 part[D / 32];
+#pragma unroll
+            for (int dt = 0; dt < D / 32; ++dt) part[dt] = f32x16{};
+            mma_cols<D, KS>(Ks[buf], col, half, s, part);
+            if constexpr (kCompensated<D>) {
+                kahan_add(acc, comp, part);
+            } else {
+                plain_add(acc, part);
+            }
         }
         if (t + 1 < ntiles) {
             kcp.store(Ks[buf ^ 1], tid);
@@ -403,11 +441,13 @@ __global__ __launch_bounds__(kWave* NW) void flash_bwd_dkdv_f32_kernel(
     load_row_half<D>(kreg, k + head_off, kj, T, half);
     load_row_half<D>(vreg, v + head_off, kj, T, half);
 
-    f32x16 dk_acc[D / 32], dv_acc[D / 32];
+    f32x16 dk_acc[D / 32], dv_acc[D / 32], dk_comp[D / 32], dv_comp[D / 32];
 #pragma unroll
     for (int dt = 0; dt < D / 32; ++dt) {
         dk_acc[dt] = f32x16{};
         dv_acc[dt] = f32x16{};
+        dk_comp[dt] = f32x16{};
+        dv_comp[dt] = f32x16{};
     }
 
     const int qt_first = k0 / kTile;
@@ -460,8 +500,23 @@ __global__ __launch_bounds__(kWave* NW) void flash_bwd_dkdv_f32_kernel(
                 s[r] = p;
                 ds[r] = p * (dp[r] - sd[qr]);
             }
-            mma_cols<D, QS>(Ps[buf], col, half, s, dv_acc);
-            mma_cols<D, QS>(Qs[buf], col, half, ds, dk_acc);
+            f32x16 part[D / 32];
+#pragma unroll
+            for (int dt = 0; dt < D / 32; ++dt) part[dt] = f32x16{};
+            mma_cols<D, QS>(Ps[buf], col, half, s, part);
+            if constexpr (kCompensated<D>) {
+                kahan_add(dv_acc, dv_comp, part);
+            } else {
+                plain_add(dv_acc, part);
+            }
+#pragma unroll
+            for (int dt = 0; dt < D / 32; ++dt) part[dt] = f32x16{};
+            mma_cols<D, QS>(Qs[buf], col, half, ds, part);
+            if constexpr (kCompensated<D>) {
+                kahan_add(dk_acc, dk_comp, part);
+            } else {
+                plain_add(dk_acc, part);
+            }
         }
         if (t + 1 < nqt) {
             qcp.store(Qs[buf ^ 1], tid);

@@ -293,8 +293,8 @@ def main():
     args = parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
-              "(the attention path shards by batch/head with no exchange inside the path; "
-              "see the sharding paragraph of the design notes)", file=sys.stderr)
+              "(attention is independent per (batch, head): it shards by batch or head with no "
+              "exchange inside the path, and each GPU runs this same single-GPU kernel set)", file=sys.stderr)
         return 2
     import torch
     if not torch.cuda.is_available():

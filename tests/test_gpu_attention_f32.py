@@ -105,7 +105,9 @@ def test_closed_forms(lib, d, T):
     np.testing.assert_allclose(got["l"], np.broadcast_to(np.arange(1, T + 1), (B, H, T)), rtol=1e-6)
     q = rng.standard_normal((B, H, T, d)).astype(np.float32)
     got = gpu_fwd_bwd(lib, q, k, np.full_like(q, 0.75), do, default_scale(d))
-    np.testing.assert_allclose(got["o"], 0.75, atol=1e-6)
+    # O = sum_j p_j * 0.75 / sum_j p_j: the two sums run over up to T terms in different
+    # orders (MFMA vs VALU), so fp32 leaves ~sqrt(T)*eps relative: 4e-6 bounds T = 1000.
+    np.testing.assert_allclose(got["o"], 0.75, atol=4e-6)
     np.testing.assert_allclose(got["dq"], 0.0, atol=1e-5)
     np.testing.assert_allclose(got["dk"], 0.0, atol=1e-5)
     got = gpu_fwd_bwd(lib, q, k, v, np.zeros_like(q), default_scale(d))

@@ -14,12 +14,26 @@
 //     of O^T += V^T P^T (and dQ^T += K^T dS^T): no LDS round trip for P.
 //   * dK/dV compute S = Q K^T (keys = columns), so P and dS are the B operands of
 //     dV^T += dO^T P and dK^T += Q^T dS.
-// Operands that a wave reuses for its whole life (its Q rows, or its K and V rows) sit in
-// VGPRs; tiles shared by the workgroup's waves (K/V, or Q/dO/stats) are staged through LDS
-// from coalesced 16-byte global loads, double-buffered so that the next tile's loads are
-// in flight while the current one is multiplied.  Causal skipping is per wave (a wave
-// stops at its diagonal tile) and per workgroup (tiles past the last query are never
-// loaded).  Workgroups are issued heaviest-first to shorten the causal tail.
+//
+// Work decomposition.  A workgroup is ONE wavefront with private LDS tiles, so there is no
+// workgroup barrier anywhere.  A causal problem has blocks of very different cost (query
+// block qb sees qb+1 key tiles); with one-wave workgroups there are several times more
+// blocks than resident wave slots, and issuing the heaviest blocks first lets the hardware
+// dispatcher balance the tail (longest-processing-time-first list scheduling).  When the
+// number of (b,h) heads is a multiple of 8, all blocks of one head are issued to the same
+// XCD (the dispatcher assigns workgroup i to XCD i % 8), so a head's K/V stays in one L2.
+//
+// Staging.  The 32-row tiles streamed over the sequence (K/V, or Q/dO) are copied from HBM
+// straight into LDS with global_load_lds (4 bytes per lane, one row segment of 64 floats
+// per instruction), bypassing VGPRs, into rows padded to a bank-conflict-free stride.  Each
+// tensor has one LDS tile: the next tile's copy is issued as soon as the current tile's
+// last LDS read has returned, and waited for (vmcnt) just before its first read, so the
+// copy overlaps the other tensor's contraction and the softmax; a second resident wave on
+// the SIMD covers what remains.
+//
+// Summation.  The backward kernels accumulate each 32-row tile's contraction in a fresh
+// MFMA accumulator and add the tile totals into the running sum (two-level summation), so
+// the fp32 rounding error grows with the number of tiles, not with the sequence length.
 #include <math.h>
 
 #include "device_common.hpp"
@@ -29,46 +43,79 @@ namespace tcamd {
 namespace {
 
 constexpr int kTile = 32;  // rows per wave and per LDS tile
+constexpr float kLog2e = 1.4426950408889634f;
 
-// 32 rows x D floats, global -> registers -> LDS (row stride STRIDE floats).
-template <int D, int NTHREADS, int STRIDE>
-struct TileCopy {
-    static constexpr int kF4PerRow = D / 4;
-    static constexpr int kPerThread = kTile * kF4PerRow / NTHREADS;
-    static_assert(kPerThread >= 1 && kTile * kF4PerRow % NTHREADS == 0, "tile split");
-    f32x4 r[kPerThread];
+// 2^x on the transcendental unit (v_exp_f32).  The softmax runs in the log2 domain:
+// exp(scale*s - m) = 2^(s*c - m*log2 e) with c = scale*log2 e folded into one FMA.
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
-    __device__ __forceinline__ void load(const float* __restrict__ head, int row0, int T,
-                                         int tid) {
+#define TCAMD_LDS __attribute__((address_space(3)))
+
+// Wait until at most N vector-memory operations of this wave are outstanding (loads return
+// in issue order, so every earlier tile copy has landed in LDS).  Inline asm with a memory
+// clobber: no LDS read is moved above it.
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N < 63 ? N : 63) : "memory");  // 6-bit field
+}
+// Wait until this wave's LDS reads have returned (the tile may then be overwritten).
+__device__ __forceinline__ void wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+// DMA instructions that copy one 32-row tile of a (T, D) head into LDS.
+template <int D>
+constexpr int kTileDma = kTile * (D >= 64 ? D / 64 : 1);
+
+// LDS byte address of a __shared__ array.
+#define lds_addr(arr) \
+    static_cast<uint32_t>(reinterpret_cast<uintptr_t>((TCAMD_LDS const void*)(arr)))
+
+// One global_load_lds_dword: lane i copies row_ptr[i] (row_ptr wave-uniform) to LDS byte
+// address lds_byte + 4*i.  Issued as inline asm so that the compiler's wait-count pass,
+// which cannot tell the LDS tiles apart, does not insert a full vmcnt(0) before every LDS
+// read; the kernels order the copies against their reads with wait_vm / wait_lds.
+// M0 carries the LDS address.  These asm statements are the only users of M0 in the kernels
+// of this file (gfx9-class LDS instructions do not read it), so declaring it clobbered is
+// exact; the compiler's generic warning about clobbering a reserved register is silenced.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma_row(const float* row_ptr, uint32_t lds_byte, uint32_t voff) {
+    asm volatile(
+        "s_mov_b32 m0, %0\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dword %1, %2"
+        :
+        : "s"(lds_byte), "v"(voff), "s"(row_ptr)
+        : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// Copy rows [row0, row0 + 32) of a row-major (T, D) fp32 head into LDS rows of STRIDE
+// floats starting at byte address lds.  Rows past T are read from row T-1 (finite values;
+// every consumer masks them).  D = 32 uses the lower half-wave per row.
+template <int D, int STRIDE>
+__device__ __forceinline__ void dma_tile(const float* __restrict__ head, int row0, int T,
+                                         uint32_t lds, int lane) {
+    constexpr int kSeg = D >= 64 ? D / 64 : 1;
+    const uint32_t voff = static_cast<uint32_t>(lane) * 4u;
 #pragma unroll
-        for (int i = 0; i < kPerThread; ++i) {
-            const int idx = tid + i * NTHREADS;
-            const int row = idx / kF4PerRow;
-            const int c4 = idx - row * kF4PerRow;
-            if (row0 + row < T) {
-                r[i] = *reinterpret_cast<const f32x4*>(head + (row0 + row) * D + c4 * 4);
-            } else {
-                r[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int r = 0; r < kTile; ++r) {
+        const float* rowp = head + static_cast<size_t>(min(row0 + r, T - 1)) * D;
+#pragma unroll
+        for (int sg = 0; sg < kSeg; ++sg) {
+            if (D >= 64 || lane < D) {
+                dma_row(rowp + sg * 64, lds + static_cast<uint32_t>((r * STRIDE + sg * 64) * 4),
+                        voff);
             }
         }
     }
-    __device__ __forceinline__ void store(float* lds, int tid) const {
-#pragma unroll
-        for (int i = 0; i < kPerThread; ++i) {
-            const int idx = tid + i * NTHREADS;
-            const int row = idx / kF4PerRow;
-            const int c4 = idx - row * kF4PerRow;
-            *reinterpret_cast<f32x4*>(lds + row * STRIDE + c4 * 4) = r[i];
-        }
-    }
-};
+}
 
 // Lane (col, half) loads its row's half: dst[j] = src[row][half*D/2 + j], zeros if row >= T.
 template <int D>
 __device__ __forceinline__ void load_row_half(float (&dst)[D / 2], const float* __restrict__ head,
                                               int row, int T, int half) {
     if (row < T) {
-        const float* p = head + row * D + half * (D / 2);
+        const float* p = head + static_cast<size_t>(row) * D + half * (D / 2);
 #pragma unroll
         for (int j = 0; j < D / 2; j += 4) {
             const f32x4 x = *reinterpret_cast<const f32x4*>(p + j);
@@ -123,7 +170,7 @@ __device__ __forceinline__ void mma_cols(const float* lds, int col, int half, co
 template <int D>
 __device__ __forceinline__ void store_acc_row(float* __restrict__ head, int row, int half,
                                               const f32x16 (&acc)[D / 32], float mul) {
-    float* p = head + row * D + 4 * half;
+    float* p = head + static_cast<size_t>(row) * D + 4 * half;
 #pragma unroll
     for (int dt = 0; dt < D / 32; ++dt) {
 #pragma unroll
@@ -138,133 +185,116 @@ __device__ __forceinline__ void store_acc_row(float* __restrict__ head, int row,
     }
 }
 
-// Compensated (Kahan) running sum of per-tile partial products: sum += x with the rounding
-// error carried in comp.  Each tile's contraction is accumulated by the MFMA into a fresh
-// zero accumulator (16 fp32 adds per element per tile) and only tile totals enter the
-// running sum, so the rounding error no longer grows with the sequence length.  Used for
-// d_head <= 64; at d_head = 128 the compensation terms do not fit the register file of the
-// dK/dV kernel, which then adds the tile totals without compensation (two-level sum).
-template <int D>
-constexpr bool kCompensated = D <= 64;
+template <int N>
+__device__ __forceinline__ void zero(f32x16 (&x)[N]) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) x[i] = f32x16{};
+}
 
 template <int N>
-__device__ __forceinline__ void plain_add(f32x16 (&sum)[N], const f32x16 (&x)[N]) {
+__device__ __forceinline__ void add_into(f32x16 (&sum)[N], const f32x16 (&x)[N]) {
 #pragma unroll
     for (int i = 0; i < N; ++i) sum[i] += x[i];
 }
 
-template <int N>
-__device__ __forceinline__ void kahan_add(f32x16 (&sum)[N], f32x16 (&comp)[N],
-                                          const f32x16 (&x)[N]) {
-#pragma unroll
-    for (int i = 0; i < N; ++i) {
-        const f32x16 y = x[i] - comp[i];
-        const f32x16 t = sum[i] + y;
-        comp[i] = (t - sum[i]) - y;
-        sum[i] = t;
+// Workgroup id -> (head bh, block b).  Blocks come in rank order (b = nb-1-rank when
+// `descending`, else b = rank) and, when BH % 8 == 0, every block of a head is on one XCD.
+__device__ __forceinline__ void map_block(int id, int BH, int nb, bool descending, int& bh,
+                                          int& b) {
+    int rank;
+    if ((BH & 7) == 0) {
+        const int hpx = BH >> 3;
+        const int slot = id >> 3;
+        bh = (id & 7) * hpx + slot % hpx;
+        rank = slot / hpx;
+    } else {
+        bh = id % BH;
+        rank = id / BH;
     }
+    b = descending ? nb - 1 - rank : rank;
 }
 
 // --------------------------------------------------------------------------------------
-// Forward.  Workgroup = NW waves = 32*NW queries of one (b, h); wave w owns queries
-// [q0 + 32w, q0 + 32w + 32).  grid = BH * nqt, heaviest query tile first.
+// Forward.  Wave = 32 queries of one (b, h), Q in VGPRs; K and V tiles through LDS.
 // --------------------------------------------------------------------------------------
-template <int D, int NW>
-__global__ __launch_bounds__(kWave* NW) void flash_fwd_f32_kernel(
+template <int D>
+__global__ __launch_bounds__(kWave) void flash_fwd_f32_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
     float* __restrict__ o, float* __restrict__ m_out, float* __restrict__ l_out, int BH, int T,
-    float scale, int nqt) {
-    constexpr int NT = kWave * NW;
+    float scale, int nqb) {
     constexpr int KS = D + 4;  // K rows: 16-byte reads along a row
     constexpr int VS = D + 8;  // V rows: read down a column by the two wave halves
-    __shared__ float Ks[2][kTile * KS];
-    __shared__ float Vs[2][kTile * VS];
+    __shared__ float Ks[kTile * KS];
+    __shared__ float Vs[kTile * VS];
 
-    const int tid = threadIdx.x;
-    const int lane = tid & (kWave - 1);
-    const int wave = tid >> 6;
+    const int lane = threadIdx.x;
     const int col = lane & 31;
     const int half = lane >> 5;
-
-    const int id = blockIdx.x;
-    const int qt = nqt - 1 - id / BH;
-    const int bh = id - (id / BH) * BH;
-    const int q0 = qt * kTile * NW;
-    const int qw = q0 + kTile * wave;
-    const int qi = qw + col;
-    const bool wave_live = qw < T;
+    int bh, qb;
+    map_block(blockIdx.x, BH, nqb, true, bh, qb);
+    const int qi = qb * kTile + col;
 
     const size_t head_off = static_cast<size_t>(bh) * T * D;
-    const float* qh = q + head_off;
     const float* kh = k + head_off;
     const float* vh = v + head_off;
 
     float qreg[D / 2];
-    load_row_half<D>(qreg, qh, qi, T, half);
+    load_row_half<D>(qreg, q + head_off, qi, T, half);
+    dma_tile<D, KS>(kh, 0, T, lds_addr(Ks), lane);
+    dma_tile<D, VS>(vh, 0, T, lds_addr(Vs), lane);
 
     f32x16 acc[D / 32];
-#pragma unroll
-    for (int dt = 0; dt < D / 32; ++dt) acc[dt] = f32x16{};
-    float m_i = -INFINITY;
+    zero(acc);
+    const float c = scale * kLog2e;
+    float m_raw = -INFINITY;  // running max of the raw scores q.k (scale > 0)
     float l_i = 0.0f;
 
-    const int kend = min(T, q0 + kTile * NW);
-    const int ntiles = (kend + kTile - 1) / kTile;
-    const int wave_last = qw / kTile;  // diagonal tile of this wave
-
-    TileCopy<D, NT, KS> kcp;
-    TileCopy<D, NT, VS> vcp;
-    kcp.load(kh, 0, T, tid);
-    vcp.load(vh, 0, T, tid);
-    kcp.store(Ks[0], tid);
-    vcp.store(Vs[0], tid);
-    __syncthreads();
-
-    for (int t = 0; t < ntiles; ++t) {
-        const int buf = t & 1;
-        if (t + 1 < ntiles) {
-            kcp.load(kh, (t + 1) * kTile, T, tid);
-            vcp.load(vh, (t + 1) * kTile, T, tid);
-        }
-        if (wave_live && t <= wave_last) {
-            f32x16 s = mma_rows<D>(Ks[buf] + col * KS + half * (D / 2), qreg, f32x16{});
-            if (t == wave_last) {
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    if (t * kTile + acc_row(r, half) > qi) s[r] = -INFINITY;
-                }
-            }
-            float mx = s[0];
-#pragma unroll
-            for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[r]);
-            mx = xhalf_max(mx);
-            const float m_new = fmaxf(m_i, mx * scale);
-            const float alpha = expf(m_i - m_new);
-            float rs = 0.0f;
+    for (int t = 0; t <= qb; ++t) {
+        const bool more = t < qb;
+        wait_vm<kTileDma<D>>();  // K tile t landed
+        f32x16 s = mma_rows<D>(Ks + col * KS + half * (D / 2), qreg, f32x16{});
+        wait_lds();
+        if (more) dma_tile<D, KS>(kh, (t + 1) * kTile, T, lds_addr(Ks), lane);
+        if (!more) {  // diagonal tile
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                s[r] = expf(fmaf(s[r], scale, -m_new));
-                rs += s[r];
+                if (t * kTile + acc_row(r, half) > qi) s[r] = -INFINITY;
             }
-            rs = xhalf_sum(rs);
-            l_i = l_i * alpha + rs;
-            m_i = m_new;
+        }
+        float mx = s[0];
 #pragma unroll
-            for (int dt = 0; dt < D / 32; ++dt) acc[dt] *= alpha;
-            mma_cols<D, VS>(Vs[buf], col, half, s, acc);
+        for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[r]);
+        mx = xhalf_max(mx);
+        const float m_new = fmaxf(m_raw, mx);
+        const float alpha = exp2_fast((m_raw - m_new) * c);  // 0 on the first tile
+        const float mc = m_new * c;
+        float rs = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            s[r] = exp2_fast(fmaf(s[r], c, -mc));
+            rs += s[r];
         }
-        if (t + 1 < ntiles) {
-            kcp.store(Ks[buf ^ 1], tid);
-            vcp.store(Vs[buf ^ 1], tid);
+        rs = xhalf_sum(rs);
+        l_i = l_i * alpha + rs;
+        m_raw = m_new;
+#pragma unroll
+        for (int dt = 0; dt < D / 32; ++dt) acc[dt] *= alpha;
+        if (more) {
+            wait_vm<kTileDma<D>>();  // V tile t (K t+1 in flight)
+        } else {
+            wait_vm<0>();
         }
-        __syncthreads();
+        mma_cols<D, VS>(Vs, col, half, s, acc);
+        wait_lds();
+        if (more) dma_tile<D, VS>(vh, (t + 1) * kTile, T, lds_addr(Vs), lane);
     }
 
-    if (wave_live && qi < T) {
+    if (qi < T) {
         const float inv_l = 1.0f / l_i;  // l_i >= 1 (the row maximum contributes exp(0))
         store_acc_row<D>(o + head_off, qi, half, acc, inv_l);
         if (half == 0) {
-            if (m_out != nullptr) m_out[static_cast<size_t>(bh) * T + qi] = m_i;
+            // max_j scale*s_j = scale * max_j s_j exactly (rounding is monotone)
+            if (m_out != nullptr) m_out[static_cast<size_t>(bh) * T + qi] = m_raw * scale;
             if (l_out != nullptr) l_out[static_cast<size_t>(bh) * T + qi] = l_i;
         }
     }
@@ -293,42 +323,36 @@ __global__ __launch_bounds__(256) void dot_do_o_f32_kernel(const float* __restri
 // --------------------------------------------------------------------------------------
 // Backward stage 1 (query-parallel): D = rowsum(dO*O) and
 //     dQ_i = scale * sum_j P_ij (dP_ij - D_i) k_j,   dP = dO V^T.
-// Wave = 32 queries; K/V tiles through LDS.
+// Wave = 32 queries (Q, dO in VGPRs); K and V tiles through LDS.
 // --------------------------------------------------------------------------------------
-template <int D, int NW>
-__global__ __launch_bounds__(kWave* NW) void flash_bwd_dq_f32_kernel(
+template <int D>
+__global__ __launch_bounds__(kWave) void flash_bwd_dq_f32_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
     const float* __restrict__ o, const float* __restrict__ dO, const float* __restrict__ m,
     const float* __restrict__ l, float* __restrict__ dq, float* __restrict__ Dws, int BH,
-    int T, float scale, int nqt) {
-    constexpr int NT = kWave * NW;
-    constexpr int KS = D + 4;
-    __shared__ float Ks[2][kTile * KS];
-    __shared__ float Vs[2][kTile * KS];
+    int T, float scale, int nqb) {
+    constexpr int KS = D + 4;  // K: row reads (S^T) and column reads (dQ^T)
+    constexpr int VS = D + 4;  // V: row reads (dP^T)
+    __shared__ float Ks[kTile * KS];
+    __shared__ float Vs[kTile * VS];
 
-    const int tid = threadIdx.x;
-    const int lane = tid & (kWave - 1);
-    const int wave = tid >> 6;
+    const int lane = threadIdx.x;
     const int col = lane & 31;
     const int half = lane >> 5;
-
-    const int id = blockIdx.x;
-    const int qt = nqt - 1 - id / BH;
-    const int bh = id - (id / BH) * BH;
-    const int q0 = qt * kTile * NW;
-    const int qw = q0 + kTile * wave;
-    const int qi = qw + col;
-    const bool wave_live = qw < T;
+    int bh, qb;
+    map_block(blockIdx.x, BH, nqb, true, bh, qb);
+    const int qi = qb * kTile + col;
     const bool row_ok = qi < T;
 
     const size_t head_off = static_cast<size_t>(bh) * T * D;
     const size_t stat_off = static_cast<size_t>(bh) * T;
+    const float* kh = k + head_off;
+    const float* vh = v + head_off;
 
     float qreg[D / 2];
     float doreg[D / 2];
     load_row_half<D>(qreg, q + head_off, qi, T, half);
     load_row_half<D>(doreg, dO + head_off, qi, T, half);
-
     // D_i from this lane's half row of O, completed across the halves.
     float Dval;
     {
@@ -339,229 +363,156 @@ __global__ __launch_bounds__(kWave* NW) void flash_bwd_dq_f32_kernel(
         for (int j = 0; j < D / 2; ++j) part = fmaf(doreg[j], orow[j], part);
         Dval = xhalf_sum(part);
     }
+    // P_ij = exp(scale*s - m)/l = 2^(s*c - lse2), lse2 = m*log2 e + log2 l; +inf on padded rows
+    const float c = scale * kLog2e;
+    const float lse2 =
+        row_ok ? fmaf(m[stat_off + qi], kLog2e, __builtin_amdgcn_logf(l[stat_off + qi]))
+               : INFINITY;
+    dma_tile<D, KS>(kh, 0, T, lds_addr(Ks), lane);
+    dma_tile<D, VS>(vh, 0, T, lds_addr(Vs), lane);
     if (row_ok && half == 0) Dws[stat_off + qi] = Dval;
-    const float m_row = row_ok ? m[stat_off + qi] : 0.0f;
-    const float inv_l = row_ok ? 1.0f / l[stat_off + qi] : 0.0f;
 
-    f32x16 acc[D / 32], comp[D / 32];
+    f32x16 acc[D / 32];
+    zero(acc);
+
+    for (int t = 0; t <= qb; ++t) {
+        const bool more = t < qb;
+        wait_vm<0>();  // K and V tiles t landed
+        f32x16 dp = mma_rows<D>(Vs + col * VS + half * (D / 2), doreg, f32x16{});
+        f32x16 s = mma_rows<D>(Ks + col * KS + half * (D / 2), qreg, f32x16{});
+        wait_lds();
+        if (more) dma_tile<D, VS>(vh, (t + 1) * kTile, T, lds_addr(Vs), lane);
 #pragma unroll
-    for (int dt = 0; dt < D / 32; ++dt) {
-        acc[dt] = f32x16{};
-        comp[dt] = f32x16{};
+        for (int r = 0; r < 16; ++r) {
+            float p = exp2_fast(fmaf(s[r], c, -lse2));
+            if (!more && t * kTile + acc_row(r, half) > qi) p = 0.0f;
+            s[r] = p * (dp[r] - Dval);  // dS^T (without the scale)
+        }
+        f32x16 part[D / 32];
+        zero(part);
+        mma_cols<D, KS>(Ks, col, half, s, part);
+        add_into(acc, part);
+        wait_lds();
+        if (more) dma_tile<D, KS>(kh, (t + 1) * kTile, T, lds_addr(Ks), lane);
     }
 
-    const int kend = min(T, q0 + kTile * NW);
-    const int ntiles = (kend + kTile - 1) / kTile;
-    const int wave_last = qw / kTile;
-
-    const float* kh = k + head_off;
-    const float* vh = v + head_off;
-    TileCopy<D, NT, KS> kcp;
-    TileCopy<D, NT, KS> vcp;
-    kcp.load(kh, 0, T, tid);
-    vcp.load(vh, 0, T, tid);
-    kcp.store(Ks[0], tid);
-    vcp.store(Vs[0], tid);
-    __syncthreads();
-
-    for (int t = 0; t < ntiles; ++t) {
-        const int buf = t & 1;
-        if (t + 1 < ntiles) {
-            kcp.load(kh, (t + 1) * kTile, T, tid);
-            vcp.load(vh, (t + 1) * kTile, T, tid);
-        }
-        if (wave_live && t <= wave_last) {
-            const int rbase = col * KS + half * (D / 2);
-            f32x16 s = mma_rows<D>(Ks[buf] + rbase, qreg, f32x16{});
-            f32x16 dp = mma_rows<D>(Vs[buf] + rbase, doreg, f32x16{});
-            const bool diag = (t == wave_last);
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                float p = expf(fmaf(s[r], scale, -m_row)) * inv_l;
-                if (diag && t * kTile + acc_row(r, half) > qi) p = 0.0f;
-                s[r] = p * (dp[r] - Dval);  // dS^T (without the scale)
-            }
-            f32x16 part[D / 32];
-#pragma unroll
-            for (int dt = 0; dt < D / 32; ++dt) part[dt] = f32x16{};
-            mma_cols<D, KS>(Ks[buf], col, half, s, part);
-            if constexpr (kCompensated<D>) {
-                kahan_add(acc, comp, part);
-            } else {
-                plain_add(acc, part);
-            }
-        }
-        if (t + 1 < ntiles) {
-            kcp.store(Ks[buf ^ 1], tid);
-            vcp.store(Vs[buf ^ 1], tid);
-        }
-        __syncthreads();
-    }
-
-    if (wave_live && row_ok) store_acc_row<D>(dq + head_off, qi, half, acc, scale);
+    if (row_ok) store_acc_row<D>(dq + head_off, qi, half, acc, scale);
 }
 
 // --------------------------------------------------------------------------------------
 // Backward stage 2 (key-parallel):
 //     dV_j = sum_i P_ij dO_i,   dK_j = scale * sum_i P_ij (dP_ij - D_i) q_i.
-// Wave = 32 keys (K and V rows in VGPRs); Q/dO tiles and per-query m, 1/l, D through LDS.
-// grid = BH * nkt, lowest key tile (most queries) first.
+// Wave = 32 keys (K and V rows in VGPRs); Q/dO tiles and per-query statistics through LDS.
+// Key block kb sees query tiles kb..nb-1; blocks are issued lowest kb (most work) first.
 // --------------------------------------------------------------------------------------
-template <int D, int NW>
-__global__ __launch_bounds__(kWave* NW) void flash_bwd_dkdv_f32_kernel(
+template <int D>
+__global__ __launch_bounds__(kWave) void flash_bwd_dkdv_f32_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
     const float* __restrict__ dO, const float* __restrict__ m, const float* __restrict__ l,
     const float* __restrict__ Dws, float* __restrict__ dk, float* __restrict__ dv, int BH,
-    int T, float scale, int nkt) {
-    constexpr int NT = kWave * NW;
+    int T, float scale, int nkb) {
     constexpr int QS = D + 4;
-    __shared__ float Qs[2][kTile * QS];
-    __shared__ float Ps[2][kTile * QS];  // dO tile
-    __shared__ float St[2][3][kTile];    // m, 1/l, D of the tile's queries
+    constexpr int GS = D + 4;  // dO tile
+    __shared__ float Qs[kTile * QS];
+    __shared__ float Gs[kTile * GS];
+    __shared__ float St[2][kTile];  // per query of the tile: lse2, D
 
-    const int tid = threadIdx.x;
-    const int lane = tid & (kWave - 1);
-    const int wave = tid >> 6;
+    const int lane = threadIdx.x;
     const int col = lane & 31;
     const int half = lane >> 5;
-
-    const int id = blockIdx.x;
-    const int kt = id / BH;
-    const int bh = id - kt * BH;
-    const int k0 = kt * kTile * NW;
-    const int kw = k0 + kTile * wave;
-    const int kj = kw + col;
-    const bool wave_live = kw < T;
+    int bh, kb;
+    map_block(blockIdx.x, BH, nkb, false, bh, kb);
+    const int kj = kb * kTile + col;
 
     const size_t head_off = static_cast<size_t>(bh) * T * D;
     const size_t stat_off = static_cast<size_t>(bh) * T;
+    const float* qh = q + head_off;
+    const float* doh = dO + head_off;
 
     float kreg[D / 2];
     float vreg[D / 2];
     load_row_half<D>(kreg, k + head_off, kj, T, half);
     load_row_half<D>(vreg, v + head_off, kj, T, half);
 
-    f32x16 dk_acc[D / 32], dv_acc[D / 32], dk_comp[D / 32], dv_comp[D / 32];
-#pragma unroll
-    for (int dt = 0; dt < D / 32; ++dt) {
-        dk_acc[dt] = f32x16{};
-        dv_acc[dt] = f32x16{};
-        dk_comp[dt] = f32x16{};
-        dv_comp[dt] = f32x16{};
-    }
-
-    const int qt_first = k0 / kTile;
-    const int nqt = (T + kTile - 1) / kTile;
-    const int wave_first = kw / kTile;  // diagonal query tile of this wave
-
-    const float* qh = q + head_off;
-    const float* doh = dO + head_off;
-    TileCopy<D, NT, QS> qcp;
-    TileCopy<D, NT, QS> docp;
-    // Stats: threads [0, 96) each stage one value (m, 1/l or D) of one query row.
-    const int st_kind = tid >> 5;  // 0: m, 1: 1/l, 2: D (only tid < 96)
-    const int st_row = tid & 31;
+    // Lane (col, half) fetches statistic `half` of query row0 + col: 0: lse2 = m*log2 e +
+    // log2 l, so that P = 2^(s*c - lse2); 1: D.  Padded query rows get lse2 = +inf (P = 0)
+    // and D = 0.
+    const float c = scale * kLog2e;
     auto load_stat = [&](int row0) -> float {
-        const int r = row0 + st_row;
-        if (tid >= 3 * kTile || r >= T) return 0.0f;
-        if (st_kind == 0) return m[stat_off + r];
-        if (st_kind == 1) return 1.0f / l[stat_off + r];
+        const int r = row0 + col;
+        if (r >= T) return half == 0 ? INFINITY : 0.0f;
+        if (half == 0) return fmaf(m[stat_off + r], kLog2e, __builtin_amdgcn_logf(l[stat_off + r]));
         return Dws[stat_off + r];
     };
+    St[half][col] = load_stat(kb * kTile);
+    dma_tile<D, QS>(qh, kb * kTile, T, lds_addr(Qs), lane);
+    dma_tile<D, GS>(doh, kb * kTile, T, lds_addr(Gs), lane);
 
-    qcp.load(qh, qt_first * kTile, T, tid);
-    docp.load(doh, qt_first * kTile, T, tid);
-    float st = load_stat(qt_first * kTile);
-    qcp.store(Qs[0], tid);
-    docp.store(Ps[0], tid);
-    if (tid < 3 * kTile) St[0][st_kind][st_row] = st;
-    __syncthreads();
+    f32x16 dk_acc[D / 32], dv_acc[D / 32];
+    zero(dk_acc);
+    zero(dv_acc);
 
-    for (int t = qt_first; t < nqt; ++t) {
-        const int buf = (t - qt_first) & 1;
-        if (t + 1 < nqt) {
-            qcp.load(qh, (t + 1) * kTile, T, tid);
-            docp.load(doh, (t + 1) * kTile, T, tid);
-            st = load_stat((t + 1) * kTile);
-        }
-        if (wave_live && t >= wave_first) {
-            const int rbase = col * QS + half * (D / 2);
-            f32x16 s = mma_rows<D>(Qs[buf] + rbase, kreg, f32x16{});
-            f32x16 dp = mma_rows<D>(Ps[buf] + rbase, vreg, f32x16{});
-            const float* sm = St[buf][0];
-            const float* sl = St[buf][1];
-            const float* sd = St[buf][2];
-            f32x16 ds;
+    const int nqb = (T + kTile - 1) / kTile;
+    for (int t = kb; t < nqb; ++t) {
+        const bool more = t + 1 < nqb;
+        wait_vm<0>();  // Q and dO tiles t landed
+        const float st_n = more ? load_stat((t + 1) * kTile) : 0.0f;
+        f32x16 s = mma_rows<D>(Qs + col * QS + half * (D / 2), kreg, f32x16{});
+        f32x16 dp = mma_rows<D>(Gs + col * GS + half * (D / 2), vreg, f32x16{});
+        f32x16 ds;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int qr = acc_row(r, half);
-                float p = expf(fmaf(s[r], scale, -sm[qr])) * sl[qr];
-                if (t * kTile + qr < kj) p = 0.0f;
-                s[r] = p;
-                ds[r] = p * (dp[r] - sd[qr]);
-            }
-            f32x16 part[D / 32];
-#pragma unroll
-            for (int dt = 0; dt < D / 32; ++dt) part[dt] = f32x16{};
-            mma_cols<D, QS>(Ps[buf], col, half, s, part);
-            if constexpr (kCompensated<D>) {
-                kahan_add(dv_acc, dv_comp, part);
-            } else {
-                plain_add(dv_acc, part);
-            }
-#pragma unroll
-            for (int dt = 0; dt < D / 32; ++dt) part[dt] = f32x16{};
-            mma_cols<D, QS>(Qs[buf], col, half, ds, part);
-            if constexpr (kCompensated<D>) {
-                kahan_add(dk_acc, dk_comp, part);
-            } else {
-                plain_add(dk_acc, part);
-            }
+        for (int r = 0; r < 16; ++r) {
+            const int qr = acc_row(r, half);
+            float p = exp2_fast(fmaf(s[r], c, -St[0][qr]));
+            if (t == kb && qr < col) p = 0.0f;  // diagonal tile: query < key
+            s[r] = p;
+            ds[r] = p * (dp[r] - St[1][qr]);
         }
-        if (t + 1 < nqt) {
-            qcp.store(Qs[buf ^ 1], tid);
-            docp.store(Ps[buf ^ 1], tid);
-            if (tid < 3 * kTile) St[buf ^ 1][st_kind][st_row] = st;
+        f32x16 part[D / 32];
+        zero(part);
+        mma_cols<D, GS>(Gs, col, half, s, part);
+        add_into(dv_acc, part);
+        zero(part);
+        mma_cols<D, QS>(Qs, col, half, ds, part);
+        add_into(dk_acc, part);
+        wait_lds();
+        if (more) {
+            St[half][col] = st_n;
+            dma_tile<D, QS>(qh, (t + 1) * kTile, T, lds_addr(Qs), lane);
+            dma_tile<D, GS>(doh, (t + 1) * kTile, T, lds_addr(Gs), lane);
         }
-        __syncthreads();
     }
 
-    if (wave_live && kj < T) {
+    if (kj < T) {
         store_acc_row<D>(dk + head_off, kj, half, dk_acc, scale);
         store_acc_row<D>(dv + head_off, kj, half, dv_acc, 1.0f);
     }
 }
 
-constexpr int kWavesFwd = 4;
-constexpr int kWavesBwd = 4;
-
 template <int D>
 void fwd_dispatch(const float* q, const float* k, const float* v, float* o, float* m_out,
                   float* l_out, int BH, int T, float scale, hipStream_t stream) {
-    const int nqt = (T + kTile * kWavesFwd - 1) / (kTile * kWavesFwd);
-    hipLaunchKernelGGL((flash_fwd_f32_kernel<D, kWavesFwd>), dim3(BH * nqt),
-                       dim3(kWave * kWavesFwd), 0, stream, q, k, v, o, m_out, l_out, BH, T,
-                       scale, nqt);
+    const int nqb = (T + kTile - 1) / kTile;
+    hipLaunchKernelGGL(flash_fwd_f32_kernel<D>, dim3(BH * nqb), dim3(kWave), 0, stream, q, k,
+                       v, o, m_out, l_out, BH, T, scale, nqb);
 }
 
 template <int D>
 void dq_dispatch(const float* q, const float* k, const float* v, const float* o,
                  const float* dO, const float* m, const float* l, float* dq, float* Dws, int BH,
                  int T, float scale, hipStream_t stream) {
-    const int nqt = (T + kTile * kWavesBwd - 1) / (kTile * kWavesBwd);
-    hipLaunchKernelGGL((flash_bwd_dq_f32_kernel<D, kWavesBwd>), dim3(BH * nqt),
-                       dim3(kWave * kWavesBwd), 0, stream, q, k, v, o, dO, m, l, dq, Dws, BH,
-                       T, scale, nqt);
+    const int nqb = (T + kTile - 1) / kTile;
+    hipLaunchKernelGGL(flash_bwd_dq_f32_kernel<D>, dim3(BH * nqb), dim3(kWave), 0, stream, q,
+                       k, v, o, dO, m, l, dq, Dws, BH, T, scale, nqb);
 }
 
 template <int D>
 void dkdv_dispatch(const float* q, const float* k, const float* v, const float* dO,
                    const float* m, const float* l, const float* Dws, float* dk, float* dv,
                    int BH, int T, float scale, hipStream_t stream) {
-    const int nkt = (T + kTile * kWavesBwd - 1) / (kTile * kWavesBwd);
-    hipLaunchKernelGGL((flash_bwd_dkdv_f32_kernel<D, kWavesBwd>), dim3(BH * nkt),
-                       dim3(kWave * kWavesBwd), 0, stream, q, k, v, dO, m, l, Dws, dk, dv, BH,
-                       T, scale, nkt);
+    const int nkb = (T + kTile - 1) / kTile;
+    hipLaunchKernelGGL(flash_bwd_dkdv_f32_kernel<D>, dim3(BH * nkb), dim3(kWave), 0, stream,
+                       q, k, v, dO, m, l, Dws, dk, dv, BH, T, scale, nkb);
 }
 
 }  // namespace

@@ -159,3 +159,23 @@ def test_optional_stats_pointers(lib):
     torch.cuda.synchronize()
     want = ref.attention_fwd_bwd(q, k, v, q, default_scale(d), with_grad=False)
     assert max_abs(out.cpu().numpy(), want.o.numpy()) <= TOL
+
+
+def test_concurrent_streams_match_serial(lib):
+    """The persistent kernels take their tasks from a per-launch queue slot: launches that run
+    at the same time on different streams must not take each other's tasks."""
+    B, H, T, d = 2, 8, 512, 64  # B*H = 16: per-XCD queues
+    ins = [ref.seeded_inputs(B, H, T, d, seed=100 + i) for i in range(4)]
+    serial = [gpu_fwd_bwd(lib, *x, 0.125) for x in ins]
+    streams = [torch.cuda.Stream() for _ in ins]
+    outs = []
+    for x, st in zip(ins, streams):
+        with torch.cuda.stream(st):
+            qg, kg, vg, dog = (to_dev(a) for a in x)
+            o, m, l = lib.attention_forward(qg, kg, vg, 0.125)
+            dq, dk, dv, _ = lib.attention_backward(qg, kg, vg, o, dog, m, l, 0.125)
+            outs.append((o, dq, dk, dv))
+    torch.cuda.synchronize()
+    for got, want in zip(outs, serial):
+        for t, n in zip(got, ("o", "dq", "dk", "dv")):
+            np.testing.assert_array_equal(t.cpu().numpy(), want[n])

@@ -16,12 +16,10 @@
 //     dV^T += dO^T P and dK^T += Q^T dS.
 //
 // Work decomposition.  A workgroup is ONE wavefront with private LDS tiles, so there is no
-// workgroup barrier anywhere.  A causal problem has blocks of very different cost (query
-// block qb sees qb+1 key tiles); with one-wave workgroups there are several times more
-// blocks than resident wave slots, and issuing the heaviest blocks first lets the hardware
-// dispatcher balance the tail (longest-processing-time-first list scheduling).  When the
-// number of (b,h) heads is a multiple of 8, all blocks of one head are issued to the same
-// XCD (the dispatcher assigns workgroup i to XCD i % 8), so a head's K/V stays in one L2.
+// workgroup barrier anywhere.  The kernels are persistent: as many one-wave workgroups as
+// fit resident are launched, and each wave pulls (head, block) tasks heaviest first from a
+// per-XCD atomic queue (sched.hpp), which balances the very unequal causal blocks across
+// SIMDs and keeps a head's K/V in one XCD's L2.
 //
 // Staging.  The 32-row tiles streamed over the sequence (K/V, or Q/dO) are copied from HBM
 // straight into LDS with global_load_lds (4 bytes per lane, one row segment of 64 floats
@@ -38,6 +36,7 @@
 
 #include "device_common.hpp"
 #include "launch.hpp"
+#include "sched.hpp"
 
 namespace tcamd {
 namespace {
@@ -197,65 +196,95 @@ __device__ __forceinline__ void add_into(f32x16 (&sum)[N], const f32x16 (&x)[N])
     for (int i = 0; i < N; ++i) sum[i] += x[i];
 }
 
-// Workgroup id -> (head bh, block b).  Blocks come in rank order (b = nb-1-rank when
-// `descending`, else b = rank) and, when BH % 8 == 0, every block of a head is on one XCD.
-__device__ __forceinline__ void map_block(int id, int BH, int nb, bool descending, int& bh,
-                                          int& b) {
-    int rank;
-    if ((BH & 7) == 0) {
-        const int hpx = BH >> 3;
-        const int slot = id >> 3;
-        bh = (id & 7) * hpx + slot % hpx;
-        rank = slot / hpx;
-    } else {
-        bh = id % BH;
-        rank = id / BH;
+// A wave's accumulator tiles in LDS, lane-major (conflict-free): element (i, r) of lane l at
+// part[(i*16 + r)*64 + l].
+template <int N>
+__device__ __forceinline__ void put_part(float* part, const f32x16 (&x)[N], int lane) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) part[(i * 16 + r) * kWave + lane] = x[i][r];
     }
-    b = descending ? nb - 1 - rank : rank;
+}
+// Store element (i, r) of an accumulator set, i.e. column i*32 + acc_row(r, half) of row
+// `row` of a row-major (T, D) tensor, for the flat indices f = i*16 + r in [f0, f0 + 8):
+// two float4 stores (f0 is a multiple of 8, so the 8 elements are rows acc_row(8u..8u+7)).
+template <int D>
+__device__ __forceinline__ void store_slice8(float* __restrict__ head, int row, int half,
+                                             int f0, const float (&x)[8], float mul) {
+    const int i = f0 >> 4;
+    const int u = (f0 & 15) >> 3;  // which 8 of the 16 accumulator rows
+    float* p = head + static_cast<size_t>(row) * D + i * 32 + 16 * u + 4 * half;
+    f32x4 a, b;
+    a[0] = x[0] * mul; a[1] = x[1] * mul; a[2] = x[2] * mul; a[3] = x[3] * mul;
+    b[0] = x[4] * mul; b[1] = x[5] * mul; b[2] = x[6] * mul; b[3] = x[7] * mul;
+    *reinterpret_cast<f32x4*>(p) = a;
+    *reinterpret_cast<f32x4*>(p + 8) = b;
 }
 
+// Work split of a task over the 4 waves of a workgroup (one per SIMD): wave w takes the
+// contiguous tile range [n*w/4, n*(w+1)/4) of the task's n tiles.
+constexpr int kWaves = 4;
+__device__ __forceinline__ void wave_range(int n, int wave, int& t0, int& t1) {
+    t0 = n * wave / kWaves;
+    t1 = n * (wave + 1) / kWaves;
+}
+
+// The next task is fetched by lane 0 of wave 0, right after that wave's first tile copies
+// are issued, so the atomic's round trip overlaps the chunk's work.
+struct Fetch {
+    const TaskQueue* q;  // non-null only for the fetching wave
+    unsigned value;
+    __device__ __forceinline__ void issue(int lane) {
+        if (q != nullptr && lane == 0) value = q->fetch();
+    }
+};
+
 // --------------------------------------------------------------------------------------
-// Forward.  Wave = 32 queries of one (b, h), Q in VGPRs; K and V tiles through LDS.
+// Forward.  Task = query block qb (32 queries) of one (b, h); wave w of the workgroup
+// runs key tiles [n*w/4, n*(w+1)/4) of the qb+1 tiles with Q in VGPRs and its own K/V
+// LDS tiles, and the four partial (O, m, l) are merged through LDS by wave 0.
 // --------------------------------------------------------------------------------------
 template <int D>
-__global__ __launch_bounds__(kWave) void flash_fwd_f32_kernel(
-    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
-    float* __restrict__ o, float* __restrict__ m_out, float* __restrict__ l_out, int BH, int T,
-    float scale, int nqb) {
-    constexpr int KS = D + 4;  // K rows: 16-byte reads along a row
-    constexpr int VS = D + 8;  // V rows: read down a column by the two wave halves
-    __shared__ float Ks[kTile * KS];
-    __shared__ float Vs[kTile * VS];
+struct FwdLds {
+    static constexpr int KS = D + 4;  // K rows: 16-byte reads along a row
+    static constexpr int VS = D + 8;  // V rows: read down a column by the two wave halves
+    float k[kTile * KS];
+    float v[kTile * VS];
+};
+static_assert(sizeof(FwdLds<32>) >= (32 * 32 + 128) * 4, "partial exchange fits");
 
-    const int lane = threadIdx.x;
+template <int D>
+__device__ __forceinline__ void fwd_chunk(const float* __restrict__ kh,
+                                          const float* __restrict__ vh, int T, float c, int qb,
+                                          int t0, int t1, const float (&qreg)[D / 2],
+                                          FwdLds<D>& L, int lane, Fetch& fetch,
+                                          f32x16 (&acc)[D / 32], float& m_raw, float& l_i) {
+    constexpr int KS = FwdLds<D>::KS;
+    constexpr int VS = FwdLds<D>::VS;
+    const float* Ks = L.k;
+    const float* Vs = L.v;
     const int col = lane & 31;
     const int half = lane >> 5;
-    int bh, qb;
-    map_block(blockIdx.x, BH, nqb, true, bh, qb);
     const int qi = qb * kTile + col;
-
-    const size_t head_off = static_cast<size_t>(bh) * T * D;
-    const float* kh = k + head_off;
-    const float* vh = v + head_off;
-
-    float qreg[D / 2];
-    load_row_half<D>(qreg, q + head_off, qi, T, half);
-    dma_tile<D, KS>(kh, 0, T, lds_addr(Ks), lane);
-    dma_tile<D, VS>(vh, 0, T, lds_addr(Vs), lane);
-
-    f32x16 acc[D / 32];
     zero(acc);
-    const float c = scale * kLog2e;
-    float m_raw = -INFINITY;  // running max of the raw scores q.k (scale > 0)
-    float l_i = 0.0f;
+    m_raw = -INFINITY;  // running max of the raw scores q.k (scale > 0)
+    l_i = 0.0f;
+    if (t0 >= t1) {
+        fetch.issue(lane);
+        return;
+    }
+    dma_tile<D, KS>(kh, t0 * kTile, T, lds_addr(L.k), lane);
+    dma_tile<D, VS>(vh, t0 * kTile, T, lds_addr(L.v), lane);
+    fetch.issue(lane);
 
-    for (int t = 0; t <= qb; ++t) {
-        const bool more = t < qb;
+    for (int t = t0; t < t1; ++t) {
+        const bool more = t + 1 < t1;
         wait_vm<kTileDma<D>>();  // K tile t landed
         f32x16 s = mma_rows<D>(Ks + col * KS + half * (D / 2), qreg, f32x16{});
         wait_lds();
-        if (more) dma_tile<D, KS>(kh, (t + 1) * kTile, T, lds_addr(Ks), lane);
-        if (!more) {  // diagonal tile
+        if (more) dma_tile<D, KS>(kh, (t + 1) * kTile, T, lds_addr(L.k), lane);
+        if (t == qb) {  // diagonal tile
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 if (t * kTile + acc_row(r, half) > qi) s[r] = -INFINITY;
@@ -286,17 +315,82 @@ __global__ __launch_bounds__(kWave) void flash_fwd_f32_kernel(
         }
         mma_cols<D, VS>(Vs, col, half, s, acc);
         wait_lds();
-        if (more) dma_tile<D, VS>(vh, (t + 1) * kTile, T, lds_addr(Vs), lane);
+        if (more) dma_tile<D, VS>(vh, (t + 1) * kTile, T, lds_addr(L.v), lane);
     }
+}
 
-    if (qi < T) {
-        const float inv_l = 1.0f / l_i;  // l_i >= 1 (the row maximum contributes exp(0))
-        store_acc_row<D>(o + head_off, qi, half, acc, inv_l);
-        if (half == 0) {
-            // max_j scale*s_j = scale * max_j s_j exactly (rounding is monotone)
-            if (m_out != nullptr) m_out[static_cast<size_t>(bh) * T + qi] = m_raw * scale;
-            if (l_out != nullptr) l_out[static_cast<size_t>(bh) * T + qi] = l_i;
+template <int D>
+__global__ __launch_bounds__(kWave* kWaves) void flash_fwd_f32_kernel(
+    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
+    float* __restrict__ o, float* __restrict__ m_out, float* __restrict__ l_out, int BH, int T,
+    float scale, int nqb, QueueSlot* slot, int per_xcd) {
+    __shared__ FwdLds<D> L[kWaves];
+    __shared__ unsigned s_next;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+    const int lane = threadIdx.x & (kWave - 1);
+    const int col = lane & 31;
+    const int half = lane >> 5;
+    const float c = scale * kLog2e;
+    const TaskQueue tq = TaskQueue::bind(slot, BH, nqb, per_xcd != 0);
+    unsigned task = tq.first();
+    while (task < tq.n_tasks) {
+        int bh, rank;
+        tq.decode(task, bh, rank);
+        const int qb = nqb - 1 - rank;
+        const int qi = qb * kTile + col;
+        const size_t head_off = static_cast<size_t>(bh) * T * D;
+        int t0, t1;
+        wave_range(qb + 1, wave, t0, t1);
+
+        float qreg[D / 2];
+        load_row_half<D>(qreg, q + head_off, qi, T, half);
+        Fetch fetch{wave == 0 ? &tq : nullptr, 0u};
+        f32x16 acc[D / 32];
+        float m_raw, l_i;
+        fwd_chunk<D>(k + head_off, v + head_off, T, c, qb, t0, t1, qreg, L[wave], lane, fetch,
+                     acc, m_raw, l_i);
+
+        // Merge: every wave publishes (acc, m, l) over its own tiles; then wave w reduces
+        // and stores the 8-element chunks w, w+4, ... of the flat accumulator.
+        constexpr int NP = D / 2;  // accumulator floats per lane (a multiple of 8)
+        float* part = reinterpret_cast<float*>(&L[wave]);
+        put_part(part, acc, lane);
+        part[D * 32 + lane] = m_raw;
+        part[D * 32 + kWave + lane] = l_i;
+        if (wave == 0 && lane == 0) s_next = fetch.value;
+        __syncthreads();
+        float mw[kWaves], m_tot = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            mw[w] = reinterpret_cast<const float*>(&L[w])[D * 32 + lane];
+            m_tot = fmaxf(m_tot, mw[w]);
         }
+        float aw[kWaves], l_tot = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            aw[w] = exp2_fast((mw[w] - m_tot) * c);  // 0 for an empty chunk
+            l_tot += reinterpret_cast<const float*>(&L[w])[D * 32 + kWave + lane] * aw[w];
+        }
+#pragma unroll 1
+        for (int f0 = wave * 8; f0 < NP; f0 += 8 * kWaves) {  // 8-element chunks, round robin
+            float x[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                float sum = 0.0f;
+#pragma unroll
+                for (int w = 0; w < kWaves; ++w)
+                    sum += reinterpret_cast<const float*>(&L[w])[(f0 + e) * kWave + lane] * aw[w];
+                x[e] = sum;
+            }
+            if (qi < T) store_slice8<D>(o + head_off, qi, half, f0, x, 1.0f / l_tot);
+        }
+        if (wave == 0 && half == 0 && qi < T) {
+            // max_j scale*s_j = scale * max_j s_j exactly (rounding is monotone); l_tot >= 1
+            if (m_out != nullptr) m_out[static_cast<size_t>(bh) * T + qi] = m_tot * scale;
+            if (l_out != nullptr) l_out[static_cast<size_t>(bh) * T + qi] = l_tot;
+        }
+        __syncthreads();
+        task = s_next;
     }
 }
 
@@ -323,69 +417,51 @@ __global__ __launch_bounds__(256) void dot_do_o_f32_kernel(const float* __restri
 // --------------------------------------------------------------------------------------
 // Backward stage 1 (query-parallel): D = rowsum(dO*O) and
 //     dQ_i = scale * sum_j P_ij (dP_ij - D_i) k_j,   dP = dO V^T.
-// Wave = 32 queries (Q, dO in VGPRs); K and V tiles through LDS.
+// Task = query block qb; wave w runs key tiles [n*w/4, n*(w+1)/4) of the qb+1 tiles with
+// Q, dO in VGPRs and its own K/V LDS tiles; the four partial dQ are summed by wave 0.
 // --------------------------------------------------------------------------------------
 template <int D>
-__global__ __launch_bounds__(kWave) void flash_bwd_dq_f32_kernel(
-    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
-    const float* __restrict__ o, const float* __restrict__ dO, const float* __restrict__ m,
-    const float* __restrict__ l, float* __restrict__ dq, float* __restrict__ Dws, int BH,
-    int T, float scale, int nqb) {
-    constexpr int KS = D + 4;  // K: row reads (S^T) and column reads (dQ^T)
-    constexpr int VS = D + 4;  // V: row reads (dP^T)
-    __shared__ float Ks[kTile * KS];
-    __shared__ float Vs[kTile * VS];
+struct DqLds {
+    static constexpr int KS = D + 4;  // K: row reads (S^T) and column reads (dQ^T)
+    static constexpr int VS = D + 4;  // V: row reads (dP^T)
+    float k[kTile * KS];
+    float v[kTile * VS];
+};
 
-    const int lane = threadIdx.x;
+template <int D>
+__device__ __forceinline__ void dq_chunk(const float* __restrict__ kh,
+                                         const float* __restrict__ vh, int T, float c,
+                                         float lse2, float Dval, int qb, int t0, int t1,
+                                         const float (&qreg)[D / 2],
+                                         const float (&doreg)[D / 2], DqLds<D>& L, int lane,
+                                         Fetch& fetch, f32x16 (&acc)[D / 32]) {
+    constexpr int KS = DqLds<D>::KS;
+    constexpr int VS = DqLds<D>::VS;
+    const float* Ks = L.k;
+    const float* Vs = L.v;
     const int col = lane & 31;
     const int half = lane >> 5;
-    int bh, qb;
-    map_block(blockIdx.x, BH, nqb, true, bh, qb);
     const int qi = qb * kTile + col;
-    const bool row_ok = qi < T;
-
-    const size_t head_off = static_cast<size_t>(bh) * T * D;
-    const size_t stat_off = static_cast<size_t>(bh) * T;
-    const float* kh = k + head_off;
-    const float* vh = v + head_off;
-
-    float qreg[D / 2];
-    float doreg[D / 2];
-    load_row_half<D>(qreg, q + head_off, qi, T, half);
-    load_row_half<D>(doreg, dO + head_off, qi, T, half);
-    // D_i from this lane's half row of O, completed across the halves.
-    float Dval;
-    {
-        float orow[D / 2];
-        load_row_half<D>(orow, o + head_off, qi, T, half);
-        float part = 0.0f;
-#pragma unroll
-        for (int j = 0; j < D / 2; ++j) part = fmaf(doreg[j], orow[j], part);
-        Dval = xhalf_sum(part);
-    }
-    // P_ij = exp(scale*s - m)/l = 2^(s*c - lse2), lse2 = m*log2 e + log2 l; +inf on padded rows
-    const float c = scale * kLog2e;
-    const float lse2 =
-        row_ok ? fmaf(m[stat_off + qi], kLog2e, __builtin_amdgcn_logf(l[stat_off + qi]))
-               : INFINITY;
-    dma_tile<D, KS>(kh, 0, T, lds_addr(Ks), lane);
-    dma_tile<D, VS>(vh, 0, T, lds_addr(Vs), lane);
-    if (row_ok && half == 0) Dws[stat_off + qi] = Dval;
-
-    f32x16 acc[D / 32];
     zero(acc);
+    if (t0 >= t1) {
+        fetch.issue(lane);
+        return;
+    }
+    dma_tile<D, KS>(kh, t0 * kTile, T, lds_addr(L.k), lane);
+    dma_tile<D, VS>(vh, t0 * kTile, T, lds_addr(L.v), lane);
+    fetch.issue(lane);
 
-    for (int t = 0; t <= qb; ++t) {
-        const bool more = t < qb;
+    for (int t = t0; t < t1; ++t) {
+        const bool more = t + 1 < t1;
         wait_vm<0>();  // K and V tiles t landed
         f32x16 dp = mma_rows<D>(Vs + col * VS + half * (D / 2), doreg, f32x16{});
         f32x16 s = mma_rows<D>(Ks + col * KS + half * (D / 2), qreg, f32x16{});
         wait_lds();
-        if (more) dma_tile<D, VS>(vh, (t + 1) * kTile, T, lds_addr(Vs), lane);
+        if (more) dma_tile<D, VS>(vh, (t + 1) * kTile, T, lds_addr(L.v), lane);
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             float p = exp2_fast(fmaf(s[r], c, -lse2));
-            if (!more && t * kTile + acc_row(r, half) > qi) p = 0.0f;
+            if (t == qb && t * kTile + acc_row(r, half) > qi) p = 0.0f;
             s[r] = p * (dp[r] - Dval);  // dS^T (without the scale)
         }
         f32x16 part[D / 32];
@@ -393,68 +469,143 @@ __global__ __launch_bounds__(kWave) void flash_bwd_dq_f32_kernel(
         mma_cols<D, KS>(Ks, col, half, s, part);
         add_into(acc, part);
         wait_lds();
-        if (more) dma_tile<D, KS>(kh, (t + 1) * kTile, T, lds_addr(Ks), lane);
+        if (more) dma_tile<D, KS>(kh, (t + 1) * kTile, T, lds_addr(L.k), lane);
     }
+}
 
-    if (row_ok) store_acc_row<D>(dq + head_off, qi, half, acc, scale);
+template <int D>
+__global__ __launch_bounds__(kWave* kWaves) void flash_bwd_dq_f32_kernel(
+    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
+    const float* __restrict__ o, const float* __restrict__ dO, const float* __restrict__ m,
+    const float* __restrict__ l, float* __restrict__ dq, float* __restrict__ Dws, int BH,
+    int T, float scale, int nqb, QueueSlot* slot, int per_xcd) {
+    __shared__ DqLds<D> L[kWaves];
+    __shared__ unsigned s_next;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+    const int lane = threadIdx.x & (kWave - 1);
+    const int col = lane & 31;
+    const int half = lane >> 5;
+    const float c = scale * kLog2e;
+    const TaskQueue tq = TaskQueue::bind(slot, BH, nqb, per_xcd != 0);
+    unsigned task = tq.first();
+    while (task < tq.n_tasks) {
+        int bh, rank;
+        tq.decode(task, bh, rank);
+        const int qb = nqb - 1 - rank;
+        const int qi = qb * kTile + col;
+        const bool row_ok = qi < T;
+        const size_t head_off = static_cast<size_t>(bh) * T * D;
+        const size_t stat_off = static_cast<size_t>(bh) * T;
+        int t0, t1;
+        wave_range(qb + 1, wave, t0, t1);
+
+        float qreg[D / 2];
+        float doreg[D / 2];
+        load_row_half<D>(qreg, q + head_off, qi, T, half);
+        load_row_half<D>(doreg, dO + head_off, qi, T, half);
+        // D_i from this lane's half row of O, completed across the halves.
+        float Dval;
+        {
+            float orow[D / 2];
+            load_row_half<D>(orow, o + head_off, qi, T, half);
+            float pd = 0.0f;
+#pragma unroll
+            for (int j = 0; j < D / 2; ++j) pd = fmaf(doreg[j], orow[j], pd);
+            Dval = xhalf_sum(pd);
+        }
+        // P_ij = exp(scale*s - m)/l = 2^(s*c - lse2), lse2 = m*log2 e + log2 l; +inf on
+        // padded rows
+        const float lse2 =
+            row_ok ? fmaf(m[stat_off + qi], kLog2e, __builtin_amdgcn_logf(l[stat_off + qi]))
+                   : INFINITY;
+        Fetch fetch{wave == 0 ? &tq : nullptr, 0u};
+        f32x16 acc[D / 32];
+        dq_chunk<D>(k + head_off, v + head_off, T, c, lse2, Dval, qb, t0, t1, qreg, doreg,
+                    L[wave], lane, fetch, acc);
+
+        // Merge: every wave publishes its partial dQ; wave w sums (in wave order) and stores
+        // the 8-element chunks w, w+4, ... of the flat accumulator.
+        constexpr int NP = D / 2;
+        put_part(reinterpret_cast<float*>(&L[wave]), acc, lane);
+        if (wave == 0 && lane == 0) s_next = fetch.value;
+        __syncthreads();
+#pragma unroll 1
+        for (int f0 = wave * 8; f0 < NP; f0 += 8 * kWaves) {  // 8-element chunks, round robin
+            float x[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                float sum = reinterpret_cast<const float*>(&L[0])[(f0 + e) * kWave + lane];
+#pragma unroll
+                for (int w = 1; w < kWaves; ++w)
+                    sum += reinterpret_cast<const float*>(&L[w])[(f0 + e) * kWave + lane];
+                x[e] = sum;
+            }
+            if (row_ok) store_slice8<D>(dq + head_off, qi, half, f0, x, scale);
+        }
+        if (wave == 0 && half == 0 && row_ok) Dws[stat_off + qi] = Dval;
+        __syncthreads();
+        task = s_next;
+    }
 }
 
 // --------------------------------------------------------------------------------------
 // Backward stage 2 (key-parallel):
 //     dV_j = sum_i P_ij dO_i,   dK_j = scale * sum_i P_ij (dP_ij - D_i) q_i.
-// Wave = 32 keys (K and V rows in VGPRs); Q/dO tiles and per-query statistics through LDS.
-// Key block kb sees query tiles kb..nb-1; blocks are issued lowest kb (most work) first.
+// Task = key block kb (query tiles kb .. nb-1); wave w runs query tiles kb + [n*w/4,
+// n*(w+1)/4) of the n = nb - kb tiles with K, V in VGPRs and its own Q/dO/statistics LDS
+// tiles; the four partial dK/dV are summed by wave 0.  Key blocks are issued lowest kb
+// (most work) first.
 // --------------------------------------------------------------------------------------
 template <int D>
-__global__ __launch_bounds__(kWave) void flash_bwd_dkdv_f32_kernel(
-    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
-    const float* __restrict__ dO, const float* __restrict__ m, const float* __restrict__ l,
-    const float* __restrict__ Dws, float* __restrict__ dk, float* __restrict__ dv, int BH,
-    int T, float scale, int nkb) {
-    constexpr int QS = D + 4;
-    constexpr int GS = D + 4;  // dO tile
-    __shared__ float Qs[kTile * QS];
-    __shared__ float Gs[kTile * GS];
-    __shared__ float St[2][kTile];  // per query of the tile: lse2, D
+struct DkdvLds {
+    static constexpr int QS = D + 4;
+    static constexpr int GS = D + 4;  // dO tile
+    float q[kTile * QS];
+    float g[kTile * GS];
+    float st[2][kTile];  // per query of the tile: lse2, D
+};
 
-    const int lane = threadIdx.x;
+template <int D>
+__device__ __forceinline__ void dkdv_chunk(const float* __restrict__ qh,
+                                           const float* __restrict__ doh,
+                                           const float* __restrict__ m,
+                                           const float* __restrict__ l,
+                                           const float* __restrict__ Dws, size_t stat_off,
+                                           int T, float c, int kb, int t0, int t1,
+                                           const float (&kreg)[D / 2],
+                                           const float (&vreg)[D / 2], DkdvLds<D>& L, int lane,
+                                           Fetch& fetch, f32x16 (&dk_acc)[D / 32],
+                                           f32x16 (&dv_acc)[D / 32]) {
+    constexpr int QS = DkdvLds<D>::QS;
+    constexpr int GS = DkdvLds<D>::GS;
+    const float* Qs = L.q;
+    const float* Gs = L.g;
+    auto& St = L.st;
     const int col = lane & 31;
     const int half = lane >> 5;
-    int bh, kb;
-    map_block(blockIdx.x, BH, nkb, false, bh, kb);
-    const int kj = kb * kTile + col;
-
-    const size_t head_off = static_cast<size_t>(bh) * T * D;
-    const size_t stat_off = static_cast<size_t>(bh) * T;
-    const float* qh = q + head_off;
-    const float* doh = dO + head_off;
-
-    float kreg[D / 2];
-    float vreg[D / 2];
-    load_row_half<D>(kreg, k + head_off, kj, T, half);
-    load_row_half<D>(vreg, v + head_off, kj, T, half);
-
+    zero(dk_acc);
+    zero(dv_acc);
+    if (t0 >= t1) {
+        fetch.issue(lane);
+        return;
+    }
     // Lane (col, half) fetches statistic `half` of query row0 + col: 0: lse2 = m*log2 e +
     // log2 l, so that P = 2^(s*c - lse2); 1: D.  Padded query rows get lse2 = +inf (P = 0)
     // and D = 0.
-    const float c = scale * kLog2e;
     auto load_stat = [&](int row0) -> float {
         const int r = row0 + col;
         if (r >= T) return half == 0 ? INFINITY : 0.0f;
-        if (half == 0) return fmaf(m[stat_off + r], kLog2e, __builtin_amdgcn_logf(l[stat_off + r]));
+        if (half == 0)
+            return fmaf(m[stat_off + r], kLog2e, __builtin_amdgcn_logf(l[stat_off + r]));
         return Dws[stat_off + r];
     };
-    St[half][col] = load_stat(kb * kTile);
-    dma_tile<D, QS>(qh, kb * kTile, T, lds_addr(Qs), lane);
-    dma_tile<D, GS>(doh, kb * kTile, T, lds_addr(Gs), lane);
+    St[half][col] = load_stat(t0 * kTile);
+    dma_tile<D, QS>(qh, t0 * kTile, T, lds_addr(L.q), lane);
+    dma_tile<D, GS>(doh, t0 * kTile, T, lds_addr(L.g), lane);
+    fetch.issue(lane);
 
-    f32x16 dk_acc[D / 32], dv_acc[D / 32];
-    zero(dk_acc);
-    zero(dv_acc);
-
-    const int nqb = (T + kTile - 1) / kTile;
-    for (int t = kb; t < nqb; ++t) {
-        const bool more = t + 1 < nqb;
+    for (int t = t0; t < t1; ++t) {
+        const bool more = t + 1 < t1;
         wait_vm<0>();  // Q and dO tiles t landed
         const float st_n = more ? load_stat((t + 1) * kTile) : 0.0f;
         f32x16 s = mma_rows<D>(Qs + col * QS + half * (D / 2), kreg, f32x16{});
@@ -478,23 +629,118 @@ __global__ __launch_bounds__(kWave) void flash_bwd_dkdv_f32_kernel(
         wait_lds();
         if (more) {
             St[half][col] = st_n;
-            dma_tile<D, QS>(qh, (t + 1) * kTile, T, lds_addr(Qs), lane);
-            dma_tile<D, GS>(doh, (t + 1) * kTile, T, lds_addr(Gs), lane);
+            dma_tile<D, QS>(qh, (t + 1) * kTile, T, lds_addr(L.q), lane);
+            dma_tile<D, GS>(doh, (t + 1) * kTile, T, lds_addr(L.g), lane);
         }
     }
+}
 
-    if (kj < T) {
-        store_acc_row<D>(dk + head_off, kj, half, dk_acc, scale);
-        store_acc_row<D>(dv + head_off, kj, half, dv_acc, 1.0f);
+template <int D>
+__global__ __launch_bounds__(kWave* kWaves) void flash_bwd_dkdv_f32_kernel(
+    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
+    const float* __restrict__ dO, const float* __restrict__ m, const float* __restrict__ l,
+    const float* __restrict__ Dws, float* __restrict__ dk, float* __restrict__ dv, int BH,
+    int T, float scale, int nkb, QueueSlot* slot, int per_xcd) {
+    __shared__ DkdvLds<D> L[kWaves];
+    __shared__ unsigned s_next;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+    const int lane = threadIdx.x & (kWave - 1);
+    const int col = lane & 31;
+    const int half = lane >> 5;
+    const float c = scale * kLog2e;
+    const TaskQueue tq = TaskQueue::bind(slot, BH, nkb, per_xcd != 0);
+    unsigned task = tq.first();
+    while (task < tq.n_tasks) {
+        int bh, kb;
+        tq.decode(task, bh, kb);
+        const int kj = kb * kTile + col;
+        const size_t head_off = static_cast<size_t>(bh) * T * D;
+        const size_t stat_off = static_cast<size_t>(bh) * T;
+        int t0, t1;
+        wave_range(nkb - kb, wave, t0, t1);
+
+        float kreg[D / 2];
+        float vreg[D / 2];
+        load_row_half<D>(kreg, k + head_off, kj, T, half);
+        load_row_half<D>(vreg, v + head_off, kj, T, half);
+        Fetch fetch{wave == 0 ? &tq : nullptr, 0u};
+        f32x16 dk_acc[D / 32], dv_acc[D / 32];
+        dkdv_chunk<D>(q + head_off, dO + head_off, m, l, Dws, stat_off, T, c, kb, kb + t0,
+                      kb + t1, kreg, vreg, L[wave], lane, fetch, dk_acc, dv_acc);
+
+        // Merge: every wave publishes its partial dK, dV; wave w sums (in wave order) and
+        // stores the 8-element chunks w, w+4, ... of the concatenated (dK, dV) accumulators.
+        constexpr int NP = D;  // D/2 floats of dK then D/2 of dV per lane
+        float* part = reinterpret_cast<float*>(&L[wave]);
+        put_part(part, dk_acc, lane);
+        put_part(part + D * 32, dv_acc, lane);
+        if (wave == 0 && lane == 0) s_next = fetch.value;
+        __syncthreads();
+#pragma unroll 1
+        for (int f0 = wave * 8; f0 < NP; f0 += 8 * kWaves) {  // 8-element chunks, round robin
+            float x[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                float sum = reinterpret_cast<const float*>(&L[0])[(f0 + e) * kWave + lane];
+#pragma unroll
+                for (int w = 1; w < kWaves; ++w)
+                    sum += reinterpret_cast<const float*>(&L[w])[(f0 + e) * kWave + lane];
+                x[e] = sum;
+            }
+            if (kj < T) {
+                if (f0 < D / 2) {
+                    store_slice8<D>(dk + head_off, kj, half, f0, x, scale);
+                } else {
+                    store_slice8<D>(dv + head_off, kj, half, f0 - D / 2, x, 1.0f);
+                }
+            }
+        }
+        __syncthreads();
+        task = s_next;
     }
+}
+
+__device__ QueueSlot g_fwd_queue[kQueueSlots];
+__device__ QueueSlot g_dq_queue[kQueueSlots];
+__device__ QueueSlot g_dkdv_queue[kQueueSlots];
+std::atomic<unsigned> g_fwd_ticket{0};
+std::atomic<unsigned> g_dq_ticket{0};
+std::atomic<unsigned> g_dkdv_ticket{0};
+
+// Device address of a queue array on the current device (the host-side name of a
+// __device__ array is not a device address).
+enum class Family { Fwd = 0, Dq = 1, Dkdv = 2 };
+QueueSlot* queue_base(Family f) {
+    constexpr int kMaxDev = 64;
+    static std::atomic<QueueSlot*> cache[3][kMaxDev] = {};
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    if (dev < 0 || dev >= kMaxDev) dev = 0;
+    QueueSlot* p = cache[static_cast<int>(f)][dev].load(std::memory_order_acquire);
+    if (p == nullptr) {
+        void* addr = nullptr;
+        hipError_t e = hipErrorInvalidSymbol;
+        switch (f) {
+            case Family::Fwd: e = hipGetSymbolAddress(&addr, HIP_SYMBOL(g_fwd_queue)); break;
+            case Family::Dq: e = hipGetSymbolAddress(&addr, HIP_SYMBOL(g_dq_queue)); break;
+            case Family::Dkdv: e = hipGetSymbolAddress(&addr, HIP_SYMBOL(g_dkdv_queue)); break;
+        }
+        if (e != hipSuccess) return nullptr;
+        p = static_cast<QueueSlot*>(addr);
+        cache[static_cast<int>(f)][dev].store(p, std::memory_order_release);
+    }
+    return p;
 }
 
 template <int D>
 void fwd_dispatch(const float* q, const float* k, const float* v, float* o, float* m_out,
                   float* l_out, int BH, int T, float scale, hipStream_t stream) {
     const int nqb = (T + kTile - 1) / kTile;
-    hipLaunchKernelGGL(flash_fwd_f32_kernel<D>, dim3(BH * nqb), dim3(kWave), 0, stream, q, k,
-                       v, o, m_out, l_out, BH, T, scale, nqb);
+    QueueSlot* slot = queue_base(Family::Fwd) + next_queue_slot(g_fwd_ticket);
+    const int grid = persistent_grid(flash_fwd_f32_kernel<D>, kWave * kWaves, 0,
+                                     static_cast<long long>(BH) * nqb);
+    hipLaunchKernelGGL(flash_fwd_f32_kernel<D>, dim3(grid), dim3(kWave * kWaves), 0, stream, q, k, v, o,
+                       m_out, l_out, BH, T, scale, nqb, slot, (BH % kXcds) == 0 ? 1 : 0);
 }
 
 template <int D>
@@ -502,8 +748,12 @@ void dq_dispatch(const float* q, const float* k, const float* v, const float* o,
                  const float* dO, const float* m, const float* l, float* dq, float* Dws, int BH,
                  int T, float scale, hipStream_t stream) {
     const int nqb = (T + kTile - 1) / kTile;
-    hipLaunchKernelGGL(flash_bwd_dq_f32_kernel<D>, dim3(BH * nqb), dim3(kWave), 0, stream, q,
-                       k, v, o, dO, m, l, dq, Dws, BH, T, scale, nqb);
+    QueueSlot* slot = queue_base(Family::Dq) + next_queue_slot(g_dq_ticket);
+    const int grid = persistent_grid(flash_bwd_dq_f32_kernel<D>, kWave * kWaves, 0,
+                                     static_cast<long long>(BH) * nqb);
+    hipLaunchKernelGGL(flash_bwd_dq_f32_kernel<D>, dim3(grid), dim3(kWave * kWaves), 0, stream, q, k, v,
+                       o, dO, m, l, dq, Dws, BH, T, scale, nqb, slot,
+                       (BH % kXcds) == 0 ? 1 : 0);
 }
 
 template <int D>
@@ -511,8 +761,12 @@ void dkdv_dispatch(const float* q, const float* k, const float* v, const float* 
                    const float* m, const float* l, const float* Dws, float* dk, float* dv,
                    int BH, int T, float scale, hipStream_t stream) {
     const int nkb = (T + kTile - 1) / kTile;
-    hipLaunchKernelGGL(flash_bwd_dkdv_f32_kernel<D>, dim3(BH * nkb), dim3(kWave), 0, stream,
-                       q, k, v, dO, m, l, Dws, dk, dv, BH, T, scale, nkb);
+    QueueSlot* slot = queue_base(Family::Dkdv) + next_queue_slot(g_dkdv_ticket);
+    const int grid = persistent_grid(flash_bwd_dkdv_f32_kernel<D>, kWave * kWaves, 0,
+                                     static_cast<long long>(BH) * nkb);
+    hipLaunchKernelGGL(flash_bwd_dkdv_f32_kernel<D>, dim3(grid), dim3(kWave * kWaves), 0, stream, q, k,
+                       v, dO, m, l, Dws, dk, dv, BH, T, scale, nkb, slot,
+                       (BH % kXcds) == 0 ? 1 : 0);
 }
 
 }  // namespace

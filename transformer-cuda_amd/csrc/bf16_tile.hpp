@@ -1,0 +1,171 @@
+// bf16_tile.hpp - LDS tiles and MFMA operand helpers shared by the bf16 attention kernels.
+//
+// A K/V/Q/dO tile is 64 rows (sequence positions) x D bf16, copied HBM -> LDS with
+// global_load_lds_dwordx4 into rows whose 16-byte chunks are XOR-swizzled by row:
+//   * 16-byte reads of one chunk index by 32 lanes on 32 rows (the A operand of a product
+//     that contracts over the head dimension) hit distinct banks;
+//   * ds_read_tr16_b64, which hands lane i of a 16-lane group element i%4 of the 8-byte
+//     read of lane 4e + i/4 (e = 0..3), turns a row-major tile into the A operand of a
+//     product that contracts over the sequence: two reads 8 rows apart give a lane the
+//     positions 16u + 4g + {0..3} and 16u + 8 + 4g + {0..3} of one head dimension,
+//     exactly the k-slots of the B operand packed from a 32x32 accumulator (pack_b).
+#pragma once
+
+#include <math.h>
+
+#include "device_common.hpp"
+#include "lds_dma.hpp"
+
+namespace tcamd {
+namespace bf16t {
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kWaves = 4;      // waves per workgroup, one per SIMD of a CU
+constexpr int kSub = 32;       // rows per sub-block (MFMA width)
+constexpr int kRowTile = 64;   // sequence rows per LDS tile
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// A 64-row x D bf16 tile in LDS: row r, 16-byte chunk c at byte r*2D + 16*(c ^ swz(r)).
+// swz(r) = 2*(r%4) + (r/4)%2 (d >= 64): eight consecutive rows get eight distinct chunk
+// slots (conflict-free 16-byte row reads), and the 4 rows x 2 chunks that a 16-lane group
+// of a transposing read touches land in 8 distinct slots (conflict-free transposing reads).
+// swz depends on r % 8 only, so row offsets that are multiples of 8 commute with it.
+template <int D>
+struct Swz {
+    static constexpr int kCpr = D / 8;  // 16-byte chunks per row
+    static constexpr int kRowBytes = 2 * D;
+    static constexpr int kBytes = kRowTile * kRowBytes;
+    static constexpr int kDma = kBytes / 1024;  // wave instructions per tile
+    static_assert(kDma % kWaves == 0 || kDma < kWaves, "tile copy split");
+    __device__ static int swz(int r) {
+        return kCpr >= 8 ? 2 * (r & 3) + ((r >> 2) & 1) : (r & (kCpr - 1));
+    }
+    __device__ static uint32_t off(int r, int c) {
+        return static_cast<uint32_t>(r * kRowBytes + ((c ^ swz(r)) << 4));
+    }
+};
+
+// Wave `wave` issues its share of the copy of rows [row0, row0 + 64) of a (T, D) bf16 head
+// into the tile at LDS byte address lds.  Rows past T are read from row T-1 (finite values;
+// every consumer masks or zero-weights them).
+template <int D>
+__device__ __forceinline__ void dma_tile(const uint16_t* __restrict__ head, int row0, int T,
+                                         uint32_t lds, int wave, int lane) {
+    using S = Swz<D>;
+    const uint16_t* base = head + static_cast<size_t>(row0) * D;
+#pragma unroll
+    for (int i = wave; i < S::kDma; i += kWaves) {
+        const int p = i * kWave + lane;  // 16-byte slot of the tile
+        const int r = p / S::kCpr;
+        const int c = (p % S::kCpr) ^ S::swz(r);
+        const int gr = min(r, T - 1 - row0);
+        dma_dwordx4(base, lds + static_cast<uint32_t>(i * 1024),
+                    static_cast<uint32_t>(gr * S::kRowBytes + c * 16));
+    }
+}
+
+// Lane (col, half) loads row `row` as a B operand over the head dimension:
+// dst[s] = row[16s + 8*half .. +8], zeros if row >= T.
+template <int D>
+__device__ __forceinline__ void load_rowop(bf16x8 (&dst)[D / 16],
+                                          const uint16_t* __restrict__ head, int row, int T,
+                                          int half) {
+#pragma unroll
+    for (int s = 0; s < D / 16; ++s) {
+        u16x8 x = u16x8{};
+        if (row < T)
+            x = *reinterpret_cast<const u16x8*>(head + static_cast<size_t>(row) * D + 16 * s +
+                                                8 * half);
+        dst[s] = __builtin_bit_cast(bf16x8, x);
+    }
+}
+
+// Pack accumulator rows acc_row(8u .. 8u+7, half) of a 32x32 fp32 tile into a B operand.
+__device__ __forceinline__ bf16x8 pack_b(const f32x16& x, int u) {
+    bf16x8 r;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) r[e] = static_cast<__bf16>(x[8 * u + e]);
+    return r;
+}
+
+// Store a (D x 32) transposed accumulator (acc[dt][v] = element (row, dt*32 +
+// acc_row(v, half))) of a row-major (T, D) bf16 tensor, times mul.
+template <int D>
+__device__ __forceinline__ void store_row(uint16_t* __restrict__ head, int row, int half,
+                                          const f32x16 (&acc)[D / 32], float mul) {
+    uint16_t* p = head + static_cast<size_t>(row) * D + 4 * half;
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            u16x4 o;
+            o[0] = f32_to_bf16_bits(acc[dt][4 * g + 0] * mul);
+            o[1] = f32_to_bf16_bits(acc[dt][4 * g + 1] * mul);
+            o[2] = f32_to_bf16_bits(acc[dt][4 * g + 2] * mul);
+            o[3] = f32_to_bf16_bits(acc[dt][4 * g + 3] * mul);
+            *reinterpret_cast<u16x4*>(p + dt * 32 + 8 * g) = o;
+        }
+    }
+}
+
+// Workgroup id -> (head bh, block b) in rank order: b = nb-1-rank when `descending`, else
+// b = rank; when BH % 8 == 0, every block of a head on one XCD (workgroup i runs on XCD
+// i % 8), so a head's tiles stay in one L2.
+__device__ __forceinline__ void map_block(int id, int BH, int nb, bool descending, int& bh,
+                                          int& b) {
+    int rank;
+    if ((BH & 7) == 0) {
+        const int hpx = BH >> 3;
+        const int slot = id >> 3;
+        bh = (id & 7) * hpx + slot % hpx;
+        rank = slot / hpx;
+    } else {
+        bh = id % BH;
+        rank = id / BH;
+    }
+    b = descending ? nb - 1 - rank : rank;
+}
+
+// 16 bytes from LDS at a byte address.
+__device__ __forceinline__ bf16x8 lds_b128(uint32_t addr) {
+    return __builtin_bit_cast(bf16x8, *(TCAMD_LDS const u16x8*)(uintptr_t)addr);
+}
+// 16 bytes of fp32 from LDS at a byte address.
+__device__ __forceinline__ f32x4 lds_f32x4(uint32_t addr) {
+    return *(TCAMD_LDS const f32x4*)(uintptr_t)addr;
+}
+// A operand of a product contracting over the 16 sequence rows 16u.. of a tile (see
+// above): two transposing reads, 8 rows apart.
+__device__ __forceinline__ bf16x8 lds_tr(uint32_t addr, uint32_t row8_bytes) {
+    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((TCAMD_LDS s16x4*)(uintptr_t)addr);
+    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (TCAMD_LDS s16x4*)(uintptr_t)(addr + row8_bytes));
+    return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+// This lane's byte offsets within a tile: row reads (row col, chunk 2*st + half) and the
+// transposing reads of head-dim tile dt (16-lane group G reads dims d0(G) + 4*(j%4) .. of
+// rows 4*(G/2) + j/4).
+template <int D>
+__device__ __forceinline__ void lane_offsets(int lane, uint32_t (&roff)[D / 16],
+                                             uint32_t (&troff)[D / 32]) {
+    using S = Swz<D>;
+    const int col = lane & 31;
+    const int half = lane >> 5;
+#pragma unroll
+    for (int st = 0; st < D / 16; ++st) roff[st] = S::off(col, 2 * st + half);
+    const int G = lane >> 4;
+    const int j16 = lane & 15;
+    const int tr_row = 4 * (G >> 1) + (j16 >> 2);
+    const int tr_dim = 16 * (G & 1) + 4 * (j16 & 3);
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt) {
+        const int d = dt * 32 + tr_dim;
+        troff[dt] = S::off(tr_row, d >> 3) + static_cast<uint32_t>((d & 7) << 1);
+    }
+}
+
+}  // namespace bf16t
+}  // namespace tcamd

@@ -1,4 +1,5 @@
-// flash_bf16.hip - tiled causal attention, bf16 fast path, on v_mfma_f32_32x32x16_bf16.
+// flash_bf16.hip - tiled causal attention backward, bf16 fast path, on
+// v_mfma_f32_32x32x16_bf16 (the forward is in flash_bf16_fwd.hip).
 //
 // Same algorithm, wave/tile structure and statistics contract as flash_f32.hip (reference:
 // src/kernels/attention.cu:518-955), with bf16 operands and fp32 accumulation:
@@ -23,7 +24,6 @@ namespace {
 
 constexpr int kTile = 32;
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr float kLn2 = 0.6931471805599453f;
 constexpr int kTStride = kTile + 4;  // transposed tiles: 72-byte rows, conflict-free 8-B reads
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u16x8 x) { return __builtin_bit_cast(bf16x8, x); }
@@ -160,109 +160,6 @@ __device__ __forceinline__ void store_acc_row(uint16_t* __restrict__ head, int r
             o[2] = f32_to_bf16_bits(acc[dt][4 * g + 2] * mul);
             o[3] = f32_to_bf16_bits(acc[dt][4 * g + 3] * mul);
             *reinterpret_cast<u16x4*>(p + dt * 32 + 8 * g) = o;
-        }
-    }
-}
-
-// ---------------------------------------------------------------------------------------
-// Forward.  Wave = 32 queries (Q in VGPRs); K row-major and V transposed through LDS.
-// ---------------------------------------------------------------------------------------
-template <int D, int NW>
-__global__ __launch_bounds__(kWave* NW) void flash_fwd_bf16_kernel(
-    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
-    const uint16_t* __restrict__ v, uint16_t* __restrict__ o, float* __restrict__ m_out,
-    float* __restrict__ l_out, int BH, int T, float scale, int nqt) {
-    constexpr int NT = kWave * NW;
-    constexpr int RS = D + 8;
-    __shared__ __attribute__((aligned(16))) uint16_t Ks[2][kTile * RS];
-    __shared__ __attribute__((aligned(16))) uint16_t Vt[2][D * kTStride];
-
-    const int tid = threadIdx.x;
-    const int lane = tid & (kWave - 1);
-    const int wave = tid >> 6;
-    const int col = lane & 31;
-    const int half = lane >> 5;
-
-    const int id = blockIdx.x;
-    const int qt = nqt - 1 - id / BH;
-    const int bh = id - (id / BH) * BH;
-    const int q0 = qt * kTile * NW;
-    const int qw = q0 + kTile * wave;
-    const int qi = qw + col;
-    const bool wave_live = qw < T;
-
-    const size_t head_off = static_cast<size_t>(bh) * T * D;
-    const uint16_t* kh = k + head_off;
-    const uint16_t* vh = v + head_off;
-
-    bf16x8 qreg[D / 16];
-    load_row<D>(qreg, q + head_off, qi, T, half);
-
-    f32x16 acc[D / 32];
-#pragma unroll
-    for (int dt = 0; dt < D / 32; ++dt) acc[dt] = f32x16{};
-    const float c = scale * kLog2e;
-    float m2 = -INFINITY;  // running max of c*s (log2 domain)
-    float l_i = 0.0f;
-
-    const int kend = min(T, q0 + kTile * NW);
-    const int ntiles = (kend + kTile - 1) / kTile;
-    const int wave_last = qw / kTile;
-
-    RowTile<D, NT, RS> kcp;
-    TransTile<D, NT> vcp;
-    kcp.load(kh, 0, T, tid);
-    vcp.load(vh, 0, T, tid);
-    kcp.store(Ks[0], tid);
-    vcp.store(Vt[0], tid);
-    __syncthreads();
-
-    for (int t = 0; t < ntiles; ++t) {
-        const int buf = t & 1;
-        if (t + 1 < ntiles) {
-            kcp.load(kh, (t + 1) * kTile, T, tid);
-            vcp.load(vh, (t + 1) * kTile, T, tid);
-        }
-        if (wave_live && t <= wave_last) {
-            f32x16 s = mma_rows<D>(Ks[buf] + col * RS + 8 * half, qreg, f32x16{});
-            if (t == wave_last) {
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    if (t * kTile + acc_row(r, half) > qi) s[r] = -INFINITY;
-                }
-            }
-            float mx = s[0];
-#pragma unroll
-            for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[r]);
-            mx = xhalf_max(mx);
-            const float m_new = fmaxf(m2, mx * c);
-            const float alpha = fast_exp2(m2 - m_new);
-            float rs = 0.0f;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                s[r] = fast_exp2(fmaf(s[r], c, -m_new));
-                rs += s[r];
-            }
-            rs = xhalf_sum(rs);
-            l_i = l_i * alpha + rs;
-            m2 = m_new;
-#pragma unroll
-            for (int dt = 0; dt < D / 32; ++dt) acc[dt] *= alpha;
-            const bf16x8 pb[2] = {pack_b(s, 0), pack_b(s, 1)};
-            mma_cols<D>(Vt[buf], col, half, pb, acc);
-        }
-        if (t + 1 < ntiles) {
-            kcp.store(Ks[buf ^ 1], tid);
-            vcp.store(Vt[buf ^ 1], tid);
-        }
-        __syncthreads();
-    }
-
-    if (wave_live && qi < T) {
-        store_acc_row<D>(o + head_off, qi, half, acc, 1.0f / l_i);
-        if (half == 0) {
-            if (m_out != nullptr) m_out[static_cast<size_t>(bh) * T + qi] = m2 * kLn2;
-            if (l_out != nullptr) l_out[static_cast<size_t>(bh) * T + qi] = l_i;
         }
     }
 }
@@ -503,14 +400,6 @@ __global__ __launch_bounds__(kWave* NW) void flash_bwd_dkdv_bf16_kernel(
 constexpr int kWaves = 4;
 
 template <int D>
-void fwd_dispatch(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o,
-                  float* m_out, float* l_out, int BH, int T, float scale, hipStream_t stream) {
-    const int nqt = (T + kTile * kWaves - 1) / (kTile * kWaves);
-    hipLaunchKernelGGL((flash_fwd_bf16_kernel<D, kWaves>), dim3(BH * nqt), dim3(kWave * kWaves),
-                       0, stream, q, k, v, o, m_out, l_out, BH, T, scale, nqt);
-}
-
-template <int D>
 void dq_dispatch(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* o,
                  const uint16_t* dO, const float* m, const float* l, uint16_t* dq, float* Dws,
                  int BH, int T, float scale, hipStream_t stream) {
@@ -531,16 +420,6 @@ void dkdv_dispatch(const uint16_t* q, const uint16_t* k, const uint16_t* v, cons
 }
 
 }  // namespace
-
-void launch_flash_fwd_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v,
-                           uint16_t* o, float* m_out, float* l_out, int BH, int T, int d,
-                           float scale, hipStream_t stream) {
-    switch (d) {
-        case 32: fwd_dispatch<32>(q, k, v, o, m_out, l_out, BH, T, scale, stream); break;
-        case 64: fwd_dispatch<64>(q, k, v, o, m_out, l_out, BH, T, scale, stream); break;
-        default: fwd_dispatch<128>(q, k, v, o, m_out, l_out, BH, T, scale, stream); break;
-    }
-}
 
 void launch_flash_bwd_dq_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                               const uint16_t* o, const uint16_t* dO, const float* m,

@@ -36,6 +36,7 @@
 
 #include "device_common.hpp"
 #include "launch.hpp"
+#include "lds_dma.hpp"
 #include "sched.hpp"
 
 namespace tcamd {
@@ -48,45 +49,9 @@ constexpr float kLog2e = 1.4426950408889634f;
 // exp(scale*s - m) = 2^(s*c - m*log2 e) with c = scale*log2 e folded into one FMA.
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
-#define TCAMD_LDS __attribute__((address_space(3)))
-
-// Wait until at most N vector-memory operations of this wave are outstanding (loads return
-// in issue order, so every earlier tile copy has landed in LDS).  Inline asm with a memory
-// clobber: no LDS read is moved above it.
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N < 63 ? N : 63) : "memory");  // 6-bit field
-}
-// Wait until this wave's LDS reads have returned (the tile may then be overwritten).
-__device__ __forceinline__ void wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
-
 // DMA instructions that copy one 32-row tile of a (T, D) head into LDS.
 template <int D>
 constexpr int kTileDma = kTile * (D >= 64 ? D / 64 : 1);
-
-// LDS byte address of a __shared__ array.
-#define lds_addr(arr) \
-    static_cast<uint32_t>(reinterpret_cast<uintptr_t>((TCAMD_LDS const void*)(arr)))
-
-// One global_load_lds_dword: lane i copies row_ptr[i] (row_ptr wave-uniform) to LDS byte
-// address lds_byte + 4*i.  Issued as inline asm so that the compiler's wait-count pass,
-// which cannot tell the LDS tiles apart, does not insert a full vmcnt(0) before every LDS
-// read; the kernels order the copies against their reads with wait_vm / wait_lds.
-// M0 carries the LDS address.  These asm statements are the only users of M0 in the kernels
-// of this file (gfx9-class LDS instructions do not read it), so declaring it clobbered is
-// exact; the compiler's generic warning about clobbering a reserved register is silenced.
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void dma_row(const float* row_ptr, uint32_t lds_byte, uint32_t voff) {
-    asm volatile(
-        "s_mov_b32 m0, %0\n\t"
-        "s_nop 0\n\t"
-        "global_load_lds_dword %1, %2"
-        :
-        : "s"(lds_byte), "v"(voff), "s"(row_ptr)
-        : "memory", "m0");
-}
-#pragma clang diagnostic pop
 
 // Copy rows [row0, row0 + 32) of a row-major (T, D) fp32 head into LDS rows of STRIDE
 // floats starting at byte address lds.  Rows past T are read from row T-1 (finite values;
@@ -102,8 +67,8 @@ __device__ __forceinline__ void dma_tile(const float* __restrict__ head, int row
 #pragma unroll
         for (int sg = 0; sg < kSeg; ++sg) {
             if (D >= 64 || lane < D) {
-                dma_row(rowp + sg * 64, lds + static_cast<uint32_t>((r * STRIDE + sg * 64) * 4),
-                        voff);
+                dma_dword(rowp + sg * 64, lds + static_cast<uint32_t>((r * STRIDE + sg * 64) * 4),
+                          voff);
             }
         }
     }

@@ -87,14 +87,24 @@ inline unsigned next_queue_slot(std::atomic<unsigned>& ticket) {
 }
 
 // Host side: persistent grid size: every resident workgroup slot of the device, a multiple
-// of kXcds, and no more workgroups than tasks (rounded up).
+// of kXcds, and no more workgroups than tasks (rounded up).  The resident capacity is cached
+// per (thread, kernel, device).
 template <typename Kernel>
 int persistent_grid(Kernel kernel, int block, size_t lds_bytes, long long n_tasks) {
-    static thread_local int cached_dev = -1;
-    static thread_local int cached_cap = 0;
+    struct Entry {
+        const void* fn;
+        int dev;
+        int cap;
+    };
+    static thread_local Entry cache[16] = {};
+    static thread_local int cache_next = 0;
     int dev = 0;
     (void)hipGetDevice(&dev);
-    if (dev != cached_dev) {
+    const void* fn = reinterpret_cast<const void*>(kernel);
+    int cap = 0;
+    for (const Entry& e : cache)
+        if (e.fn == fn && e.dev == dev) cap = e.cap;
+    if (cap == 0) {
         int per_cu = 0, cus = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, block, lds_bytes) !=
             hipSuccess)
@@ -102,10 +112,11 @@ int persistent_grid(Kernel kernel, int block, size_t lds_bytes, long long n_task
         if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
             hipSuccess)
             cus = 256;
-        cached_cap = (per_cu < 1 ? 1 : per_cu) * cus;
-        cached_dev = dev;
+        cap = (per_cu < 1 ? 1 : per_cu) * cus;
+        cache[cache_next] = Entry{fn, dev, cap};
+        cache_next = (cache_next + 1) % 16;
     }
-    long long g = cached_cap;
+    long long g = cap;
     const long long want = ((n_tasks + kXcds - 1) / kXcds) * kXcds;
     if (want < g) g = want;
     g = (g / kXcds) * kXcds;

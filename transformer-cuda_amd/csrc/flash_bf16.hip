@@ -1,422 +1,412 @@
 // flash_bf16.hip - tiled causal attention backward, bf16 fast path, on
-// v_mfma_f32_32x32x16_bf16 (the forward is in flash_bf16_fwd.hip).
+// v_mfma_f32_32x32x16_bf16 with fp32 accumulation (the forward is in flash_bf16_fwd.hip).
 //
-// Same algorithm, wave/tile structure and statistics contract as flash_f32.hip (reference:
-// src/kernels/attention.cu:518-955), with bf16 operands and fp32 accumulation:
-//   * softmax runs in the log2 domain: scores are scaled by scale*log2(e) with one FMA and
-//     exponentiated with v_exp_f32 (exp2); m_out/l_out are converted back to the natural
-//     domain so the reference contract P = exp(scale*q.k - m)/l holds;
-//   * P and dS are rounded to bf16 as MFMA B operands; O/dQ/dK/dV are rounded once, at
-//     the store.
-// A 32x32x16 MFMA takes eight consecutive k per lane.  Products that contract over the
-// head dimension read 16 contiguous bytes per lane from a row-major LDS tile.  Products
-// that contract over the sequence (O^T += V^T P^T, dQ^T += K^T dS^T, dV^T += dO^T P,
-// dK^T += Q^T dS) take their A operand from a transposed LDS copy of the tile, written
-// while staging: the eight k of a lane are then two 8-byte runs that match the rows the
-// accumulator layout gives to P / dS (acc_row(8u..8u+7, half)).
+// Algorithm: the reference's analytical backward (src/kernels/attention.cu:626-955) in the
+// split form of the fp32 path: stage 1 (query-parallel) writes D = rowsum(dO * O) and dQ,
+// stage 2 (key-parallel) dK and dV, both recomputing P = 2^(s*c - lse2) from the forward's
+// statistics (lse2 = m*log2 e + log2 l, the log2-domain log-sum-exp).  P and dS are rounded
+// to bf16 as MFMA operands; dQ/dK/dV are rounded once, at the store.
+//
+// Both stages use the forward's staging: 64-row tiles copied HBM -> LDS with
+// global_load_lds_dwordx4 into XOR-swizzled rows, double buffered and shared by the 4 waves
+// of a workgroup.  A product that contracts over the head dimension reads its A operand as
+// 16-byte row reads of a tile and its B operand from VGPRs; a product that contracts over
+// the sequence reads its A operand with ds_read_tr16_b64 from the same row-major tile and
+// takes its B operand (P or dS, rounded to bf16) straight from the accumulator of the
+// score product, whose rows are the contracted positions.
+//
+// Stage 1, per 32-key half tile and 32-query sub-block (d = 64: 12 MFMAs):
+//   S^T  = K Q^T      A = K rows,  B = Q (VGPRs)
+//   dP^T = V dO^T     A = V rows,  B = dO (VGPRs)
+//   dS^T = P^T o (dP^T - D)        lane l holds query l%32: lse2 and D are per lane
+//   dQ^T += K^T dS^T  A = K^T (transposing reads of the K tile), B = dS^T
+// A workgroup owns 256 queries (d <= 64; wave w: sub-blocks w and 7-w, as the forward) or
+// 128 (d = 128, one sub-block per wave, for registers).
+//
+// Stage 2, per 32-query half tile and a wave's 32 keys (d = 64: 16 MFMAs):
+//   S  = Q K^T        A = Q rows,  B = K (VGPRs)
+//   dP = dO V^T       A = dO rows, B = V (VGPRs)
+//   dS = P o (dP - D)              per-query lse2 and D from LDS (4 x 16-byte reads each)
+//   dV^T += dO^T P    A = dO^T (transposing reads), B = P
+//   dK^T += Q^T dS    A = Q^T (transposing reads),  B = dS
+// A workgroup owns 128 keys; query tiles start at the workgroup's first key, and wave w
+// joins at the half tile that holds its first key (the only one it masks).
 #include <math.h>
 
+#include "bf16_tile.hpp"
 #include "device_common.hpp"
 #include "launch.hpp"
 
 namespace tcamd {
 namespace {
 
-constexpr int kTile = 32;
-constexpr float kLog2e = 1.4426950408889634f;
-constexpr int kTStride = kTile + 4;  // transposed tiles: 72-byte rows, conflict-free 8-B reads
+using namespace bf16t;
 
-__device__ __forceinline__ bf16x8 as_bf16x8(u16x8 x) { return __builtin_bit_cast(bf16x8, x); }
-
-__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
-
-// 32 rows x D bf16: global (16-byte chunks) -> registers -> LDS row-major, stride RS.
-template <int D, int NT, int RS>
-struct RowTile {
-    static constexpr int kChunksPerRow = D / 8;
-    static constexpr int kChunks = kTile * kChunksPerRow;
-    static constexpr int kPerThread = (kChunks + NT - 1) / NT;
-    u16x8 r[kPerThread];
-
-    __device__ __forceinline__ void load(const uint16_t* __restrict__ head, int row0, int T,
-                                         int tid) {
-#pragma unroll
-        for (int i = 0; i < kPerThread; ++i) {
-            const int idx = tid + i * NT;
-            const int row = idx / kChunksPerRow;
-            const int c = idx - row * kChunksPerRow;
-            if ((kChunks % NT == 0 || idx < kChunks) && row0 + row < T) {
-                r[i] = *reinterpret_cast<const u16x8*>(head + (row0 + row) * D + c * 8);
-            } else {
-                r[i] = u16x8{};
-            }
-        }
-    }
-    __device__ __forceinline__ void store(uint16_t* lds, int tid) const {
-#pragma unroll
-        for (int i = 0; i < kPerThread; ++i) {
-            const int idx = tid + i * NT;
-            if (kChunks % NT == 0 || idx < kChunks) {
-                const int row = idx / kChunksPerRow;
-                const int c = idx - row * kChunksPerRow;
-                *reinterpret_cast<u16x8*>(lds + row * RS + c * 8) = r[i];
-            }
-        }
-    }
+// K and V tiles of stage 1 (same shape as the forward's).
+template <int D>
+struct KvSmem {
+    uint16_t k[2][kRowTile * D];
+    uint16_t v[2][kRowTile * D];
 };
 
-// 32 rows x D bf16 -> LDS transposed (D rows of kTStride), element (row, c) at
-// lds[c*kTStride + row].  A thread owns a pair of rows and CW columns; it writes packed
-// (row 2p, row 2p+1) dwords.
-template <int D, int NT>
-struct TransTile {
-    static constexpr int kThreadsPerPair = NT / (kTile / 2);
-    static constexpr int CW = D / kThreadsPerPair;  // columns per thread
-    static_assert(CW >= 2 && CW % 2 == 0 && CW <= 8, "transposed tile split");
-    typedef uint16_t vec_t __attribute__((ext_vector_type(CW)));
-    vec_t a, b;
-
-    __device__ __forceinline__ void load(const uint16_t* __restrict__ head, int row0, int T,
-                                         int tid) {
-        const int p = tid / kThreadsPerPair;
-        const int c0 = (tid - p * kThreadsPerPair) * CW;
-        const int r = row0 + 2 * p;
-        a = (r < T) ? *reinterpret_cast<const vec_t*>(head + r * D + c0) : vec_t{};
-        b = (r + 1 < T) ? *reinterpret_cast<const vec_t*>(head + (r + 1) * D + c0) : vec_t{};
-    }
-    __device__ __forceinline__ void store(uint16_t* lds, int tid) const {
-        const int p = tid / kThreadsPerPair;
-        const int c0 = (tid - p * kThreadsPerPair) * CW;
-#pragma unroll
-        for (int e = 0; e < CW; ++e) {
-            const uint32_t w = static_cast<uint32_t>(a[e]) | (static_cast<uint32_t>(b[e]) << 16);
-            *reinterpret_cast<uint32_t*>(lds + (c0 + e) * kTStride + 2 * p) = w;
-        }
-    }
+// Q and dO tiles of stage 2 with the per-query statistics of each tile.
+template <int D>
+struct QgSmem {
+    uint16_t q[2][kRowTile * D];
+    uint16_t g[2][kRowTile * D];
+    float lse2[2][kRowTile];
+    float dlt[2][kRowTile];
 };
 
-// Lane (col, half) loads its row: dst[j] = row[16j + 8*half .. +8], zeros if row >= T.
+// ---------------------------------------------------------------------------------------
+// Stage 1: D and dQ.
+// ---------------------------------------------------------------------------------------
+
+// One 32-query sub-block of a wave.
 template <int D>
-__device__ __forceinline__ void load_row(bf16x8 (&dst)[D / 16], const uint16_t* __restrict__ head,
-                                         int row, int T, int half) {
+struct DqSub {
+    bf16x8 q[D / 16];    // Q row of query col (B operand over d)
+    bf16x8 g[D / 16];    // dO row
+    f32x16 acc[D / 32];  // dQ^T
+    float lse2;          // +inf for padded queries: P = 0
+    float dlt;           // D = rowsum(dO * O)
+};
+
+template <int D>
+__device__ __forceinline__ void dq_init(DqSub<D>& sb, const uint16_t* __restrict__ q,
+                                        const uint16_t* __restrict__ o,
+                                        const uint16_t* __restrict__ dO,
+                                        const float* __restrict__ m, const float* __restrict__ l,
+                                        float* __restrict__ Dws, size_t head_off,
+                                        size_t stat_off, int qi, int T, int half) {
+    load_rowop<D>(sb.q, q + head_off, qi, T, half);
+    load_rowop<D>(sb.g, dO + head_off, qi, T, half);
+    bf16x8 orow[D / 16];
+    load_rowop<D>(orow, o + head_off, qi, T, half);
+    float part = 0.0f;
 #pragma unroll
     for (int j = 0; j < D / 16; ++j) {
-        dst[j] = (row < T) ? as_bf16x8(*reinterpret_cast<const u16x8*>(head + row * D + 16 * j +
-                                                                        8 * half))
-                           : as_bf16x8(u16x8{});
-    }
-}
-
-// acc += (row-major LDS tile rows) x breg, contracting over the head dimension.
-//   lds_row = lds + (lane%32)*RS + 8*half
-template <int D>
-__device__ __forceinline__ f32x16 mma_rows(const uint16_t* lds_row, const bf16x8 (&breg)[D / 16],
-                                           f32x16 acc) {
 #pragma unroll
-    for (int j = 0; j < D / 16; ++j) {
-        const bf16x8 a = as_bf16x8(*reinterpret_cast<const u16x8*>(lds_row + 16 * j));
-        acc = mfma_32x32x16_bf16(a, breg[j], acc);
+        for (int e = 0; e < 8; ++e)
+            part = fmaf(static_cast<float>(sb.g[j][e]), static_cast<float>(orow[j][e]), part);
     }
-    return acc;
-}
-
-// Pack accumulator rows acc_row(8u .. 8u+7, half) of a 32x32 fp32 tile into a B operand.
-__device__ __forceinline__ bf16x8 pack_b(const f32x16& x, int u) {
-    bf16x8 r;
+    sb.dlt = xhalf_sum(part);
+    sb.lse2 = INFINITY;
+    if (qi < T) {
+        if (half == 0) Dws[stat_off + qi] = sb.dlt;
+        sb.lse2 = m[stat_off + qi] * kLog2e + log2f(l[stat_off + qi]);
+    }
 #pragma unroll
-    for (int e = 0; e < 8; ++e) r[e] = static_cast<__bf16>(x[8 * u + e]);
-    return r;
+    for (int dt = 0; dt < D / 32; ++dt) sb.acc[dt] = f32x16{};
 }
 
-// acc[dt] += X^T * Y over the 32 sequence rows of a tile: A from the transposed tile
-// (row dt*32 + col), B = packed Y rows (pb[u] = rows acc_row(8u..8u+7, half)).
+// s = S^T, dp = dP^T of keys kb.. (rows) x queries qj + col (columns) -> dS^T as the two B
+// operands of dQ^T += K^T dS^T.  Keys past the query get P = 0.
 template <int D>
-__device__ __forceinline__ void mma_cols(const uint16_t* ldsT, int col, int half,
-                                         const bf16x8 (&pb)[2], f32x16 (&acc)[D / 32]) {
+__device__ __forceinline__ void dq_ds(f32x16& s, const f32x16& dp, const DqSub<D>& sb,
+                                      bf16x8 (&db)[2], int kb, int qj, int col, int half,
+                                      float c) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s[r] = exp2_fast(fmaf(s[r], c, -sb.lse2));
+    if (kb + 31 > qj) {  // the half tile crosses the diagonal of this sub-block
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+            if (kb + acc_row(r, half) > qj + col) s[r] = 0.0f;
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s[r] *= dp[r] - sb.dlt;
+    db[0] = pack_b(s, 0);
+    db[1] = pack_b(s, 1);
+}
+
+// One 32-key half tile for sub-block 1, and sub-block 0 too when BOTH.  ka/va: this lane's
+// row-read addresses in the K / V tile; kta: transposing-read addresses in the K tile.
+template <int D, bool BOTH>
+__device__ __forceinline__ void dq_half(int kb, const uint32_t (&ka)[D / 16],
+                                        const uint32_t (&va)[D / 16],
+                                        const uint32_t (&kta)[D / 32], DqSub<D>& sb0,
+                                        DqSub<D>& sb1, int qj0, int qj1, int col, int half,
+                                        float c) {
+    constexpr uint32_t RB = Swz<D>::kRowBytes;
+    f32x16 s0 = f32x16{}, s1 = f32x16{}, p0 = f32x16{}, p1 = f32x16{};
+#pragma unroll
+    for (int st = 0; st < D / 16; ++st) {
+        const bf16x8 a = lds_b128(ka[st]);
+        s1 = mfma_32x32x16_bf16(a, sb1.q[st], s1);
+        if constexpr (BOTH) s0 = mfma_32x32x16_bf16(a, sb0.q[st], s0);
+    }
+#pragma unroll
+    for (int st = 0; st < D / 16; ++st) {
+        const bf16x8 a = lds_b128(va[st]);
+        p1 = mfma_32x32x16_bf16(a, sb1.g[st], p1);
+        if constexpr (BOTH) p0 = mfma_32x32x16_bf16(a, sb0.g[st], p0);
+    }
+    bf16x8 d0[2], d1[2];
+    dq_ds<D>(s1, p1, sb1, d1, kb, qj1, col, half, c);
+    if constexpr (BOTH) dq_ds<D>(s0, p0, sb0, d0, kb, qj0, col, half, c);
 #pragma unroll
     for (int dt = 0; dt < D / 32; ++dt) {
-        const uint16_t* rowp = ldsT + (dt * 32 + col) * kTStride + 4 * half;
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-            const u16x4 lo = *reinterpret_cast<const u16x4*>(rowp + 16 * u);
-            const u16x4 hi = *reinterpret_cast<const u16x4*>(rowp + 16 * u + 8);
-            const u16x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-            acc[dt] = mfma_32x32x16_bf16(as_bf16x8(a), pb[u], acc[dt]);
+            const bf16x8 a = lds_tr(kta[dt] + 16u * u * RB, 8u * RB);
+            sb1.acc[dt] = mfma_32x32x16_bf16(a, d1[u], sb1.acc[dt]);
+            if constexpr (BOTH) sb0.acc[dt] = mfma_32x32x16_bf16(a, d0[u], sb0.acc[dt]);
         }
     }
 }
 
-template <int D>
-__device__ __forceinline__ void store_acc_row(uint16_t* __restrict__ head, int row, int half,
-                                              const f32x16 (&acc)[D / 32], float mul) {
-    uint16_t* p = head + row * D + 4 * half;
-#pragma unroll
-    for (int dt = 0; dt < D / 32; ++dt) {
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            u16x4 o;
-            o[0] = f32_to_bf16_bits(acc[dt][4 * g + 0] * mul);
-            o[1] = f32_to_bf16_bits(acc[dt][4 * g + 1] * mul);
-            o[2] = f32_to_bf16_bits(acc[dt][4 * g + 2] * mul);
-            o[3] = f32_to_bf16_bits(acc[dt][4 * g + 3] * mul);
-            *reinterpret_cast<u16x4*>(p + dt * 32 + 8 * g) = o;
-        }
-    }
-}
-
-// ---------------------------------------------------------------------------------------
-// Backward stage 1 (query-parallel): D = rowsum(dO*O) (fp32) and dQ.
-// LDS: K row-major (S^T), V row-major (dP^T), K transposed (dQ^T += K^T dS^T).
-// ---------------------------------------------------------------------------------------
-template <int D, int NW>
-__global__ __launch_bounds__(kWave* NW) void flash_bwd_dq_bf16_kernel(
+// NSUB = 2: 256 queries per workgroup, wave w owns sub-blocks w (0) and 7-w (1).
+// NSUB = 1: 128 queries per workgroup, wave w owns sub-block w (1).
+template <int D, int NSUB>
+__global__ __launch_bounds__(kWave* kWaves) void flash_bwd_dq_bf16_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, const uint16_t* __restrict__ o,
     const uint16_t* __restrict__ dO, const float* __restrict__ m, const float* __restrict__ l,
-    uint16_t* __restrict__ dq, float* __restrict__ Dws, int BH, int T, float scale, int nqt) {
-    constexpr int NT = kWave * NW;
-    constexpr int RS = D + 8;
-    __shared__ __attribute__((aligned(16))) uint16_t Ks[2][kTile * RS];
-    __shared__ __attribute__((aligned(16))) uint16_t Vs[2][kTile * RS];
-    __shared__ __attribute__((aligned(16))) uint16_t Kt[2][D * kTStride];
-
-    const int tid = threadIdx.x;
-    const int lane = tid & (kWave - 1);
-    const int wave = tid >> 6;
+    uint16_t* __restrict__ dq, float* __restrict__ Dws, int BH, int T, float scale, int nblk) {
+    using S = Swz<D>;
+    constexpr int kBlock = kWaves * NSUB * kSub;
+    __shared__ __attribute__((aligned(1024))) KvSmem<D> sm;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+    const int lane = threadIdx.x & (kWave - 1);
     const int col = lane & 31;
     const int half = lane >> 5;
-
-    const int id = blockIdx.x;
-    const int qt = nqt - 1 - id / BH;
-    const int bh = id - (id / BH) * BH;
-    const int q0 = qt * kTile * NW;
-    const int qw = q0 + kTile * wave;
-    const int qi = qw + col;
-    const bool wave_live = qw < T;
-    const bool row_ok = qi < T;
-
+    int bh, blk;
+    map_block(blockIdx.x, BH, nblk, true, bh, blk);
+    const int q0 = blk * kBlock;
+    const int qj0 = q0 + kSub * wave;
+    const int qj1 = NSUB == 2 ? q0 + kSub * (2 * kWaves - 1 - wave) : qj0;
     const size_t head_off = static_cast<size_t>(bh) * T * D;
     const size_t stat_off = static_cast<size_t>(bh) * T;
-
-    bf16x8 qreg[D / 16];
-    bf16x8 doreg[D / 16];
-    load_row<D>(qreg, q + head_off, qi, T, half);
-    load_row<D>(doreg, dO + head_off, qi, T, half);
-
-    float Dval;
-    {
-        bf16x8 orow[D / 16];
-        load_row<D>(orow, o + head_off, qi, T, half);
-        float part = 0.0f;
-#pragma unroll
-        for (int j = 0; j < D / 16; ++j) {
-#pragma unroll
-            for (int e = 0; e < 8; ++e)
-                part = fmaf(static_cast<float>(doreg[j][e]), static_cast<float>(orow[j][e]), part);
-        }
-        Dval = xhalf_sum(part);
-    }
-    if (row_ok && half == 0) Dws[stat_off + qi] = Dval;
-    const float c = scale * kLog2e;
-    const float lse2 = row_ok ? m[stat_off + qi] * kLog2e + log2f(l[stat_off + qi]) : INFINITY;
-
-    f32x16 acc[D / 32];
-#pragma unroll
-    for (int dt = 0; dt < D / 32; ++dt) acc[dt] = f32x16{};
-
-    const int kend = min(T, q0 + kTile * NW);
-    const int ntiles = (kend + kTile - 1) / kTile;
-    const int wave_last = qw / kTile;
-
     const uint16_t* kh = k + head_off;
     const uint16_t* vh = v + head_off;
-    RowTile<D, NT, RS> kcp, vcp;
-    TransTile<D, NT> ktcp;
-    kcp.load(kh, 0, T, tid);
-    vcp.load(vh, 0, T, tid);
-    ktcp.load(kh, 0, T, tid);
-    kcp.store(Ks[0], tid);
-    vcp.store(Vs[0], tid);
-    ktcp.store(Kt[0], tid);
-    __syncthreads();
+    const float c = scale * kLog2e;
 
-    for (int t = 0; t < ntiles; ++t) {
-        const int buf = t & 1;
-        if (t + 1 < ntiles) {
-            kcp.load(kh, (t + 1) * kTile, T, tid);
-            vcp.load(vh, (t + 1) * kTile, T, tid);
-            ktcp.load(kh, (t + 1) * kTile, T, tid);
-        }
-        if (wave_live && t <= wave_last) {
-            const int rbase = col * RS + 8 * half;
-            f32x16 s = mma_rows<D>(Ks[buf] + rbase, qreg, f32x16{});
-            f32x16 dp = mma_rows<D>(Vs[buf] + rbase, doreg, f32x16{});
-            const bool diag = (t == wave_last);
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                float p = fast_exp2(fmaf(s[r], c, -lse2));
-                if (diag && t * kTile + acc_row(r, half) > qi) p = 0.0f;
-                s[r] = p * (dp[r] - Dval);
+    const int kend = min(T, q0 + kBlock);
+    const int ntile = (kend + kRowTile - 1) / kRowTile;
+    const uint32_t k_lds = lds_addr(sm.k[0]);
+    const uint32_t v_lds = lds_addr(sm.v[0]);
+    dma_tile<D>(kh, 0, T, k_lds, wave, lane);
+    dma_tile<D>(vh, 0, T, v_lds, wave, lane);
+
+    DqSub<D> sb0, sb1;
+    dq_init<D>(sb1, q, o, dO, m, l, Dws, head_off, stat_off, qj1 + col, T, half);
+    if constexpr (NSUB == 2)
+        dq_init<D>(sb0, q, o, dO, m, l, Dws, head_off, stat_off, qj0 + col, T, half);
+
+    uint32_t roff[D / 16], troff[D / 32];
+    lane_offsets<D>(lane, roff, troff);
+
+    const int nhalf_t = (T + 31) / 32;
+    const int hA = NSUB == 2 ? min(qj0 / 32 + 1, nhalf_t) : 0;
+    const int hB = min(qj1 / 32 + 1, nhalf_t);
+    const int hend = 2 * ntile;
+    uint32_t ka[D / 16], va[D / 16], kta[D / 32];
+    auto tile_sync = [&](int hh) {
+        const int kt = hh >> 1;
+        if ((hh & 1) == 0) {
+            wait_vm<0>();     // this wave's copies of tile kt landed ...
+            __syncthreads();  // ... and every wave's; tile kt-1 is no longer read by anyone
+            if (kt + 1 < ntile) {
+                const uint32_t nbuf = static_cast<uint32_t>((kt + 1) & 1) * S::kBytes;
+                dma_tile<D>(kh, (kt + 1) * kRowTile, T, k_lds + nbuf, wave, lane);
+                dma_tile<D>(vh, (kt + 1) * kRowTile, T, v_lds + nbuf, wave, lane);
             }
-            const bf16x8 pb[2] = {pack_b(s, 0), pack_b(s, 1)};
-            mma_cols<D>(Kt[buf], col, half, pb, acc);
         }
-        if (t + 1 < ntiles) {
-            kcp.store(Ks[buf ^ 1], tid);
-            vcp.store(Vs[buf ^ 1], tid);
-            ktcp.store(Kt[buf ^ 1], tid);
+        const uint32_t base = static_cast<uint32_t>(kt & 1) * S::kBytes +
+                              static_cast<uint32_t>(hh & 1) * 32u * S::kRowBytes;
+#pragma unroll
+        for (int st = 0; st < D / 16; ++st) {
+            ka[st] = k_lds + base + roff[st];
+            va[st] = v_lds + base + roff[st];
         }
-        __syncthreads();
+#pragma unroll
+        for (int dt = 0; dt < D / 32; ++dt) kta[dt] = k_lds + base + troff[dt];
+    };
+    int hh = 0;
+    for (; hh < hA; ++hh) {
+        tile_sync(hh);
+        dq_half<D, true>(32 * hh, ka, va, kta, sb0, sb1, qj0, qj1, col, half, c);
     }
+    for (; hh < hB; ++hh) {
+        tile_sync(hh);
+        dq_half<D, false>(32 * hh, ka, va, kta, sb0, sb1, qj0, qj1, col, half, c);
+    }
+    for (; hh < hend; ++hh) tile_sync(hh);
 
-    if (wave_live && row_ok) store_acc_row<D>(dq + head_off, qi, half, acc, scale);
+    if (qj1 + col < T) store_row<D>(dq + head_off, qj1 + col, half, sb1.acc, scale);
+    if constexpr (NSUB == 2)
+        if (qj0 + col < T) store_row<D>(dq + head_off, qj0 + col, half, sb0.acc, scale);
 }
 
 // ---------------------------------------------------------------------------------------
-// Backward stage 2 (key-parallel): dK, dV.  Wave = 32 keys (K, V in VGPRs).
-// LDS: Q and dO row-major (S, dP) and transposed (dK^T, dV^T); per-query lse2 and D.
+// Stage 2: dK, dV.
 // ---------------------------------------------------------------------------------------
-template <int D, int NW>
-__global__ __launch_bounds__(kWave* NW) void flash_bwd_dkdv_bf16_kernel(
+
+template <int D>
+__global__ __launch_bounds__(kWave* kWaves) void flash_bwd_dkdv_bf16_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, const uint16_t* __restrict__ dO,
     const float* __restrict__ m, const float* __restrict__ l, const float* __restrict__ Dws,
-    uint16_t* __restrict__ dk, uint16_t* __restrict__ dv, int BH, int T, float scale, int nkt) {
-    constexpr int NT = kWave * NW;
-    constexpr int RS = D + 8;
-    __shared__ __attribute__((aligned(16))) uint16_t Qs[2][kTile * RS];
-    __shared__ __attribute__((aligned(16))) uint16_t Gs[2][kTile * RS];  // dO
-    __shared__ __attribute__((aligned(16))) uint16_t Qt[2][D * kTStride];
-    __shared__ __attribute__((aligned(16))) uint16_t Gt[2][D * kTStride];
-    __shared__ float St[2][2][kTile];  // lse2, D
-
-    const int tid = threadIdx.x;
-    const int lane = tid & (kWave - 1);
-    const int wave = tid >> 6;
+    uint16_t* __restrict__ dk, uint16_t* __restrict__ dv, int BH, int T, float scale,
+    int nblk) {
+    using S = Swz<D>;
+    constexpr int kBlock = kWaves * kSub;  // keys per workgroup
+    constexpr uint32_t RB = S::kRowBytes;
+    __shared__ __attribute__((aligned(1024))) QgSmem<D> sm;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+    const int lane = threadIdx.x & (kWave - 1);
     const int col = lane & 31;
     const int half = lane >> 5;
-
-    const int id = blockIdx.x;
-    const int kt = id / BH;
-    const int bh = id - kt * BH;
-    const int k0 = kt * kTile * NW;
-    const int kw = k0 + kTile * wave;
+    int bh, blk;
+    map_block(blockIdx.x, BH, nblk, false, bh, blk);  // block 0 sees every query
+    const int k0 = blk * kBlock;
+    const int kw = k0 + kSub * wave;
     const int kj = kw + col;
-    const bool wave_live = kw < T;
-
     const size_t head_off = static_cast<size_t>(bh) * T * D;
     const size_t stat_off = static_cast<size_t>(bh) * T;
+    const uint16_t* qh = q + head_off;
+    const uint16_t* gh = dO + head_off;
+    const float c = scale * kLog2e;
 
-    bf16x8 kreg[D / 16];
-    bf16x8 vreg[D / 16];
-    load_row<D>(kreg, k + head_off, kj, T, half);
-    load_row<D>(vreg, v + head_off, kj, T, half);
+    const int t0 = k0 / kRowTile;
+    const int ntile = (T + kRowTile - 1) / kRowTile;
+    const uint32_t q_lds = lds_addr(sm.q[0]);
+    const uint32_t g_lds = lds_addr(sm.g[0]);
+    const uint32_t l_lds = lds_addr(sm.lse2[0]);
+    const uint32_t d_lds = lds_addr(sm.dlt[0]);
+    dma_tile<D>(qh, t0 * kRowTile, T, q_lds, wave, lane);
+    dma_tile<D>(gh, t0 * kRowTile, T, g_lds, wave, lane);
+    // Wave 0 stages the statistics of a tile through VGPRs: lane i holds query 64t + i.
+    float st_m = 0.0f, st_l = 1.0f, st_d = 0.0f;
+    auto load_stats = [&](int t) {
+        const int r = t * kRowTile + lane;
+        if (r < T) {
+            st_m = m[stat_off + r];
+            st_l = l[stat_off + r];
+            st_d = Dws[stat_off + r];
+        } else {
+            st_m = INFINITY;  // lse2 = +inf: P = 0 for padded queries
+            st_l = 1.0f;
+            st_d = 0.0f;
+        }
+    };
+    if (wave == 0) load_stats(t0);
 
+    bf16x8 kr[D / 16], vr[D / 16];
+    load_rowop<D>(kr, k + head_off, kj, T, half);
+    load_rowop<D>(vr, v + head_off, kj, T, half);
     f32x16 dk_acc[D / 32], dv_acc[D / 32];
 #pragma unroll
     for (int dt = 0; dt < D / 32; ++dt) {
         dk_acc[dt] = f32x16{};
         dv_acc[dt] = f32x16{};
     }
-    const float c = scale * kLog2e;
+    uint32_t roff[D / 16], troff[D / 32];
+    lane_offsets<D>(lane, roff, troff);
 
-    const int qt_first = k0 / kTile;
-    const int nqt = (T + kTile - 1) / kTile;
-    const int wave_first = kw / kTile;
-
-    const uint16_t* qh = q + head_off;
-    const uint16_t* doh = dO + head_off;
-    RowTile<D, NT, RS> qcp, gcp;
-    TransTile<D, NT> qtcp, gtcp;
-    const int st_kind = tid >> 5;  // 0: lse2, 1: D  (tid < 64)
-    const int st_row = tid & 31;
-    auto load_stat = [&](int row0) -> float {
-        const int r = row0 + st_row;
-        if (tid >= 2 * kTile) return 0.0f;
-        if (r >= T) return st_kind == 0 ? INFINITY : 0.0f;  // exp2(-inf) = 0: padded queries
-        if (st_kind == 0) return m[stat_off + r] * kLog2e + log2f(l[stat_off + r]);
-        return Dws[stat_off + r];
+    // Half tiles hh = 2*t0 .. 2*ntile-1 (queries 32*hh ..); wave w computes from the half
+    // tile holding its first key on (none if its keys start past T).
+    const int hend = 2 * ntile;
+    const int hstart = kw < T ? kw / 32 : hend;
+    uint32_t qa[D / 16], ga[D / 16], qta[D / 32], gta[D / 32], sa;
+    auto tile_sync = [&](int hh) {
+        const int kt = hh >> 1;
+        if ((hh & 1) == 0) {
+            wait_vm<0>();  // this wave's copies (and statistics loads) of tile kt landed
+            if (wave == 0) {
+                sm.lse2[kt & 1][lane] = st_m * kLog2e + log2f(st_l);
+                sm.dlt[kt & 1][lane] = st_d;
+            }
+            __syncthreads();  // every wave's copies landed; tile kt-1 is no longer read
+            if (kt + 1 < ntile) {
+                if (wave == 0) load_stats(kt + 1);
+                const uint32_t nbuf = static_cast<uint32_t>((kt + 1) & 1) * S::kBytes;
+                dma_tile<D>(qh, (kt + 1) * kRowTile, T, q_lds + nbuf, wave, lane);
+                dma_tile<D>(gh, (kt + 1) * kRowTile, T, g_lds + nbuf, wave, lane);
+            }
+        }
+        const uint32_t base = static_cast<uint32_t>(kt & 1) * S::kBytes +
+                              static_cast<uint32_t>(hh & 1) * 32u * RB;
+#pragma unroll
+        for (int st = 0; st < D / 16; ++st) {
+            qa[st] = q_lds + base + roff[st];
+            ga[st] = g_lds + base + roff[st];
+        }
+#pragma unroll
+        for (int dt = 0; dt < D / 32; ++dt) {
+            qta[dt] = q_lds + base + troff[dt];
+            gta[dt] = g_lds + base + troff[dt];
+        }
+        // statistics of rows acc_row(4j.., half) of this half tile: 16 bytes at +32 B * j
+        sa = static_cast<uint32_t>(((kt & 1) * kRowTile + (hh & 1) * 32 + 4 * half) * 4);
     };
 
-    const int r0 = qt_first * kTile;
-    qcp.load(qh, r0, T, tid);
-    gcp.load(doh, r0, T, tid);
-    qtcp.load(qh, r0, T, tid);
-    gtcp.load(doh, r0, T, tid);
-    float st = load_stat(r0);
-    qcp.store(Qs[0], tid);
-    gcp.store(Gs[0], tid);
-    qtcp.store(Qt[0], tid);
-    gtcp.store(Gt[0], tid);
-    if (tid < 2 * kTile) St[0][st_kind][st_row] = st;
-    __syncthreads();
-
-    for (int t = qt_first; t < nqt; ++t) {
-        const int buf = (t - qt_first) & 1;
-        if (t + 1 < nqt) {
-            const int rn = (t + 1) * kTile;
-            qcp.load(qh, rn, T, tid);
-            gcp.load(doh, rn, T, tid);
-            qtcp.load(qh, rn, T, tid);
-            gtcp.load(doh, rn, T, tid);
-            st = load_stat(rn);
-        }
-        if (wave_live && t >= wave_first) {
-            const int rbase = col * RS + 8 * half;
-            f32x16 s = mma_rows<D>(Qs[buf] + rbase, kreg, f32x16{});
-            f32x16 dp = mma_rows<D>(Gs[buf] + rbase, vreg, f32x16{});
-            const float* sl = St[buf][0];
-            const float* sd = St[buf][1];
-            f32x16 ds;
+    int hh = 2 * t0;
+    for (; hh < hstart; ++hh) tile_sync(hh);
+    for (; hh < hend; ++hh) {
+        tile_sync(hh);
+        f32x16 s = f32x16{}, dp = f32x16{};
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int qr = acc_row(r, half);
-                float p = fast_exp2(fmaf(s[r], c, -sl[qr]));
-                if (t * kTile + qr < kj) p = 0.0f;
-                s[r] = p;
-                ds[r] = p * (dp[r] - sd[qr]);
+        for (int st = 0; st < D / 16; ++st) s = mfma_32x32x16_bf16(lds_b128(qa[st]), kr[st], s);
+#pragma unroll
+        for (int st = 0; st < D / 16; ++st)
+            dp = mfma_32x32x16_bf16(lds_b128(ga[st]), vr[st], dp);
+        f32x4 L[4], Dl[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            L[j] = lds_f32x4(l_lds + sa + 32u * j);
+            Dl[j] = lds_f32x4(d_lds + sa + 32u * j);
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[r] = exp2_fast(fmaf(s[r], c, -L[r >> 2][r & 3]));
+        const int qb = 32 * hh;
+        if (qb < kw + 32) {  // the diagonal half tile: queries before the key get P = 0
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                if (qb + acc_row(r, half) < kj) s[r] = 0.0f;
+        }
+        const bf16x8 pb[2] = {pack_b(s, 0), pack_b(s, 1)};
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[r] *= dp[r] - Dl[r >> 2][r & 3];
+        const bf16x8 db[2] = {pack_b(s, 0), pack_b(s, 1)};
+#pragma unroll
+        for (int dt = 0; dt < D / 32; ++dt) {
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                dv_acc[dt] =
+                    mfma_32x32x16_bf16(lds_tr(gta[dt] + 16u * u * RB, 8u * RB), pb[u], dv_acc[dt]);
+                dk_acc[dt] =
+                    mfma_32x32x16_bf16(lds_tr(qta[dt] + 16u * u * RB, 8u * RB), db[u], dk_acc[dt]);
             }
-            const bf16x8 pb[2] = {pack_b(s, 0), pack_b(s, 1)};
-            const bf16x8 db[2] = {pack_b(ds, 0), pack_b(ds, 1)};
-            mma_cols<D>(Gt[buf], col, half, pb, dv_acc);
-            mma_cols<D>(Qt[buf], col, half, db, dk_acc);
         }
-        if (t + 1 < nqt) {
-            qcp.store(Qs[buf ^ 1], tid);
-            gcp.store(Gs[buf ^ 1], tid);
-            qtcp.store(Qt[buf ^ 1], tid);
-            gtcp.store(Gt[buf ^ 1], tid);
-            if (tid < 2 * kTile) St[buf ^ 1][st_kind][st_row] = st;
-        }
-        __syncthreads();
     }
 
-    if (wave_live && kj < T) {
-        store_acc_row<D>(dk + head_off, kj, half, dk_acc, scale);
-        store_acc_row<D>(dv + head_off, kj, half, dv_acc, 1.0f);
+    if (kj < T) {
+        store_row<D>(dk + head_off, kj, half, dk_acc, scale);
+        store_row<D>(dv + head_off, kj, half, dv_acc, 1.0f);
     }
 }
-
-constexpr int kWaves = 4;
 
 template <int D>
 void dq_dispatch(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* o,
                  const uint16_t* dO, const float* m, const float* l, uint16_t* dq, float* Dws,
                  int BH, int T, float scale, hipStream_t stream) {
-    const int nqt = (T + kTile * kWaves - 1) / (kTile * kWaves);
-    hipLaunchKernelGGL((flash_bwd_dq_bf16_kernel<D, kWaves>), dim3(BH * nqt),
+    constexpr int NSUB = D >= 128 ? 1 : 2;
+    constexpr int kBlock = kWaves * NSUB * kSub;
+    const int nblk = (T + kBlock - 1) / kBlock;
+    hipLaunchKernelGGL((flash_bwd_dq_bf16_kernel<D, NSUB>), dim3(BH * nblk),
                        dim3(kWave * kWaves), 0, stream, q, k, v, o, dO, m, l, dq, Dws, BH, T,
-                       scale, nqt);
+                       scale, nblk);
 }
 
 template <int D>
 void dkdv_dispatch(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* dO,
                    const float* m, const float* l, const float* Dws, uint16_t* dk, uint16_t* dv,
                    int BH, int T, float scale, hipStream_t stream) {
-    const int nkt = (T + kTile * kWaves - 1) / (kTile * kWaves);
-    hipLaunchKernelGGL((flash_bwd_dkdv_bf16_kernel<D, kWaves>), dim3(BH * nkt),
-                       dim3(kWave * kWaves), 0, stream, q, k, v, dO, m, l, Dws, dk, dv, BH, T,
-                       scale, nkt);
+    constexpr int kBlock = kWaves * kSub;
+    const int nblk = (T + kBlock - 1) / kBlock;
+    hipLaunchKernelGGL(flash_bwd_dkdv_bf16_kernel<D>, dim3(BH * nblk), dim3(kWave * kWaves), 0,
+                       stream, q, k, v, dO, m, l, Dws, dk, dv, BH, T, scale, nblk);
 }
 
 }  // namespace

@@ -23,15 +23,20 @@
 // A workgroup owns 256 queries (d <= 64; wave w: sub-blocks w and 7-w, as the forward) or
 // 128 (d = 128, one sub-block per wave, for registers).
 //
-// Stage 2, per 32-query half tile and a wave's 32 keys (d = 64: 16 MFMAs):
+// Stage 2, per 32-query half tile and a wave's 32 keys (d = 64: 18 MFMAs):
 //   S  = Q K^T        A = Q rows,  B = K (VGPRs)
 //   dP = dO V^T       A = dO rows, B = V (VGPRs)
-//   dS = P o (dP - D)              per-query lse2 and D from LDS (4 x 16-byte reads each)
+//   dS = P o (dP - D)              -lse2/c and -D enter S and dP as one more contraction step
+//                                  over a per-row (hi, lo) bf16 chunk (see dkdv_scores)
 //   dV^T += dO^T P    A = dO^T (transposing reads), B = P
 //   dK^T += Q^T dS    A = Q^T (transposing reads),  B = dS
 // A workgroup owns 128 keys; query tiles start at the workgroup's first key, and wave w
-// joins at the half tile that holds its first key (the only one it masks).
+// joins at the half tile that holds its first key (the only one it masks).  A wave handles
+// both half tiles of a 64-query tile per step, so the MFMAs of one overlap the softmax
+// arithmetic of the other.
 #include <math.h>
+
+#include <type_traits>
 
 #include "bf16_tile.hpp"
 #include "device_common.hpp"
@@ -49,13 +54,14 @@ struct KvSmem {
     uint16_t v[2][kRowTile * D];
 };
 
-// Q and dO tiles of stage 2 with the per-query statistics of each tile.
+// Q and dO tiles of stage 2, each with an extra 8-element column chunk per row that carries
+// the row's statistic (see dkdv_scores).
 template <int D>
 struct QgSmem {
     uint16_t q[2][kRowTile * D];
     uint16_t g[2][kRowTile * D];
-    float lse2[2][kRowTile];
-    float dlt[2][kRowTile];
+    uint16_t qx[2][kRowTile * 8];  // row r: (-lse2/c)_hi, (-lse2/c)_lo, 0 x 6
+    uint16_t gx[2][kRowTile * 8];  // row r: (-D)_hi, (-D)_lo, 0 x 6
 };
 
 // ---------------------------------------------------------------------------------------
@@ -242,6 +248,68 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_bwd_dq_bf16_kernel(
 // Stage 2: dK, dV.
 // ---------------------------------------------------------------------------------------
 
+// Per-lane operands of one 32-query half tile of stage 2.
+template <int D>
+struct HalfAddr {
+    uint32_t q[D / 16], g[D / 16];    // row reads, chunk step st
+    uint32_t qt[D / 32], gt[D / 32];  // transposing reads, head-dim tile dt
+    uint32_t qx, gx;                  // statistic chunks of row col
+};
+
+// x as the bf16 pair (hi, lo), hi + lo = x to ~2^-16 relative, packed into one dword.
+__device__ __forceinline__ uint32_t split_bf16x2(float x) {
+    const uint16_t hi = f32_to_bf16_bits(x);
+    const uint16_t lo = f32_to_bf16_bits(x - bf16_bits_to_f32(hi));
+    return static_cast<uint32_t>(hi) | (static_cast<uint32_t>(lo) << 16);
+}
+
+// S' = Q K^T - lse2/c and dP' = dO V^T - D of one half tile.  The statistics ride in the
+// products: a fifth 16-wide contraction step multiplies the row's chunk (hi, lo, 0, ...)
+// by the B operand `one` = (1, 1, 0, ...) (lanes of k-group 1 hold zeros), so that
+// 2^(c*S') = P and P o dP' = dS need no per-row values in VGPRs.
+template <int D>
+__device__ __forceinline__ void dkdv_scores(const HalfAddr<D>& a, const bf16x8 (&kr)[D / 16],
+                                            const bf16x8 (&vr)[D / 16], const bf16x8& one,
+                                            f32x16& s, f32x16& dp) {
+    s = mfma_32x32x16_bf16(lds_b128(a.qx), one, f32x16{});
+#pragma unroll
+    for (int st = 0; st < D / 16; ++st) s = mfma_32x32x16_bf16(lds_b128(a.q[st]), kr[st], s);
+    dp = mfma_32x32x16_bf16(lds_b128(a.gx), one, f32x16{});
+#pragma unroll
+    for (int st = 0; st < D / 16; ++st) dp = mfma_32x32x16_bf16(lds_b128(a.g[st]), vr[st], dp);
+}
+
+// P = 2^(c*S') (0 where the query precedes the key, on the diagonal half tile) and
+// dS = P o dP'; dV^T += dO^T P, dK^T += Q^T dS.
+template <int D, bool MASK>
+__device__ __forceinline__ void dkdv_update(const HalfAddr<D>& a, f32x16& s, const f32x16& dp,
+                                            f32x16 (&dk_acc)[D / 32],
+                                            f32x16 (&dv_acc)[D / 32], int qb, int kj, int half,
+                                            float c) {
+    constexpr uint32_t RB = Swz<D>::kRowBytes;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s[r] = exp2_fast(s[r] * c);
+    if constexpr (MASK) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+            if (qb + acc_row(r, half) < kj) s[r] = 0.0f;
+    }
+    const bf16x8 pb[2] = {pack_b(s, 0), pack_b(s, 1)};
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s[r] *= dp[r];
+    const bf16x8 db[2] = {pack_b(s, 0), pack_b(s, 1)};
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            dv_acc[dt] =
+                mfma_32x32x16_bf16(lds_tr(a.gt[dt] + 16u * u * RB, 8u * RB), pb[u], dv_acc[dt]);
+            dk_acc[dt] =
+                mfma_32x32x16_bf16(lds_tr(a.qt[dt] + 16u * u * RB, 8u * RB), db[u], dk_acc[dt]);
+        }
+    }
+}
+
 template <int D>
 __global__ __launch_bounds__(kWave* kWaves) void flash_bwd_dkdv_bf16_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
@@ -267,13 +335,14 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_bwd_dkdv_bf16_kernel(
     const uint16_t* qh = q + head_off;
     const uint16_t* gh = dO + head_off;
     const float c = scale * kLog2e;
+    const float inv_c = 1.0f / c;
 
     const int t0 = k0 / kRowTile;
     const int ntile = (T + kRowTile - 1) / kRowTile;
     const uint32_t q_lds = lds_addr(sm.q[0]);
     const uint32_t g_lds = lds_addr(sm.g[0]);
-    const uint32_t l_lds = lds_addr(sm.lse2[0]);
-    const uint32_t d_lds = lds_addr(sm.dlt[0]);
+    const uint32_t qx_lds = lds_addr(sm.qx[0]);
+    const uint32_t gx_lds = lds_addr(sm.gx[0]);
     dma_tile<D>(qh, t0 * kRowTile, T, q_lds, wave, lane);
     dma_tile<D>(gh, t0 * kRowTile, T, g_lds, wave, lane);
     // Wave 0 stages the statistics of a tile through VGPRs: lane i holds query 64t + i.
@@ -285,12 +354,25 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_bwd_dkdv_bf16_kernel(
             st_l = l[stat_off + r];
             st_d = Dws[stat_off + r];
         } else {
-            st_m = INFINITY;  // lse2 = +inf: P = 0 for padded queries
+            st_m = -INFINITY;  // padded query: P = 0 (see tile_sync)
             st_l = 1.0f;
             st_d = 0.0f;
         }
     };
-    if (wave == 0) load_stats(t0);
+    if (wave == 0) {
+        load_stats(t0);
+        const u16x8 z = u16x8{};  // the constant zeros of the statistic chunks
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            *reinterpret_cast<u16x8*>(&sm.qx[b][lane * 8]) = z;
+            *reinterpret_cast<u16x8*>(&sm.gx[b][lane * 8]) = z;
+        }
+    }
+    bf16x8 one = bf16x8{};
+    if (half == 0) {
+        one[0] = static_cast<__bf16>(1.0f);
+        one[1] = static_cast<__bf16>(1.0f);
+    }
 
     bf16x8 kr[D / 16], vr[D / 16];
     load_rowop<D>(kr, k + head_off, kj, T, half);
@@ -304,81 +386,76 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_bwd_dkdv_bf16_kernel(
     uint32_t roff[D / 16], troff[D / 32];
     lane_offsets<D>(lane, roff, troff);
 
-    // Half tiles hh = 2*t0 .. 2*ntile-1 (queries 32*hh ..); wave w computes from the half
-    // tile holding its first key on (none if its keys start past T).
-    const int hend = 2 * ntile;
-    const int hstart = kw < T ? kw / 32 : hend;
-    uint32_t qa[D / 16], ga[D / 16], qta[D / 32], gta[D / 32], sa;
-    auto tile_sync = [&](int hh) {
-        const int kt = hh >> 1;
-        if ((hh & 1) == 0) {
-            wait_vm<0>();  // this wave's copies (and statistics loads) of tile kt landed
-            if (wave == 0) {
-                sm.lse2[kt & 1][lane] = st_m * kLog2e + log2f(st_l);
-                sm.dlt[kt & 1][lane] = st_d;
-            }
-            __syncthreads();  // every wave's copies landed; tile kt-1 is no longer read
-            if (kt + 1 < ntile) {
-                if (wave == 0) load_stats(kt + 1);
-                const uint32_t nbuf = static_cast<uint32_t>((kt + 1) & 1) * S::kBytes;
-                dma_tile<D>(qh, (kt + 1) * kRowTile, T, q_lds + nbuf, wave, lane);
-                dma_tile<D>(gh, (kt + 1) * kRowTile, T, g_lds + nbuf, wave, lane);
-            }
+    // Tile kt: wait for its copies, publish its statistics, barrier, start the next copy.
+    auto tile_sync = [&](int kt) {
+        wait_vm<0>();  // this wave's copies (and statistics loads) of tile kt landed
+        if (wave == 0) {  // -lse2/c (-1e30 for padded queries: P = 0) and -D as bf16 pairs
+            const float nl = st_m == -INFINITY ? -1e30f : -(st_m * kLog2e + log2f(st_l)) * inv_c;
+            *reinterpret_cast<uint32_t*>(&sm.qx[kt & 1][lane * 8]) = split_bf16x2(nl);
+            *reinterpret_cast<uint32_t*>(&sm.gx[kt & 1][lane * 8]) = split_bf16x2(-st_d);
         }
+        __syncthreads();  // every wave's copies landed; tile kt-1 is no longer read
+        if (kt + 1 < ntile) {
+            if (wave == 0) load_stats(kt + 1);
+            const uint32_t nbuf = static_cast<uint32_t>((kt + 1) & 1) * S::kBytes;
+            dma_tile<D>(qh, (kt + 1) * kRowTile, T, q_lds + nbuf, wave, lane);
+            dma_tile<D>(gh, (kt + 1) * kRowTile, T, g_lds + nbuf, wave, lane);
+        }
+    };
+    // Operand addresses of half tile hh (queries 32*hh ..).
+    auto half_addr = [&](int hh) {
+        HalfAddr<D> a;
+        const int kt = hh >> 1;
         const uint32_t base = static_cast<uint32_t>(kt & 1) * S::kBytes +
                               static_cast<uint32_t>(hh & 1) * 32u * RB;
 #pragma unroll
         for (int st = 0; st < D / 16; ++st) {
-            qa[st] = q_lds + base + roff[st];
-            ga[st] = g_lds + base + roff[st];
+            a.q[st] = q_lds + base + roff[st];
+            a.g[st] = g_lds + base + roff[st];
         }
 #pragma unroll
         for (int dt = 0; dt < D / 32; ++dt) {
-            qta[dt] = q_lds + base + troff[dt];
-            gta[dt] = g_lds + base + troff[dt];
+            a.qt[dt] = q_lds + base + troff[dt];
+            a.gt[dt] = g_lds + base + troff[dt];
         }
-        // statistics of rows acc_row(4j.., half) of this half tile: 16 bytes at +32 B * j
-        sa = static_cast<uint32_t>(((kt & 1) * kRowTile + (hh & 1) * 32 + 4 * half) * 4);
+        const uint32_t xrow = static_cast<uint32_t>(((kt & 1) * kRowTile + (hh & 1) * 32 + col) * 16);
+        a.qx = qx_lds + xrow;
+        a.gx = gx_lds + xrow;
+        return a;
+    };
+    // Both half tiles of tile kt; the first is the diagonal one when MASK0.  The score
+    // products of the second half tile are issued before the first half tile's softmax.
+    auto pair = [&](int kt, auto mask0) {
+        const HalfAddr<D> a0 = half_addr(2 * kt), a1 = half_addr(2 * kt + 1);
+        f32x16 s0, dp0, s1, dp1;
+        dkdv_scores<D>(a0, kr, vr, one, s0, dp0);
+        dkdv_scores<D>(a1, kr, vr, one, s1, dp1);
+        dkdv_update<D, decltype(mask0)::value>(a0, s0, dp0, dk_acc, dv_acc, 64 * kt, kj, half,
+                                               c);
+        dkdv_update<D, false>(a1, s1, dp1, dk_acc, dv_acc, 64 * kt + 32, kj, half, c);
     };
 
-    int hh = 2 * t0;
-    for (; hh < hstart; ++hh) tile_sync(hh);
-    for (; hh < hend; ++hh) {
-        tile_sync(hh);
-        f32x16 s = f32x16{}, dp = f32x16{};
-#pragma unroll
-        for (int st = 0; st < D / 16; ++st) s = mfma_32x32x16_bf16(lds_b128(qa[st]), kr[st], s);
-#pragma unroll
-        for (int st = 0; st < D / 16; ++st)
-            dp = mfma_32x32x16_bf16(lds_b128(ga[st]), vr[st], dp);
-        f32x4 L[4], Dl[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            L[j] = lds_f32x4(l_lds + sa + 32u * j);
-            Dl[j] = lds_f32x4(d_lds + sa + 32u * j);
+    // Half tiles before hstart (= kw/32, the one holding the wave's first key) hold only
+    // queries that precede every key of the wave; a wave whose keys start past T computes
+    // nothing.  Every wave takes part in every tile's barrier and copies.
+    const int hstart = kw < T ? kw / 32 : 2 * ntile;
+    int kt = t0;
+    for (; 2 * kt + 1 < hstart; ++kt) tile_sync(kt);
+    if (kt < ntile) {  // the tile holding the diagonal half tile
+        tile_sync(kt);
+        if (hstart & 1) {  // only its second half tile, the diagonal one
+            const HalfAddr<D> a1 = half_addr(hstart);
+            f32x16 s1, dp1;
+            dkdv_scores<D>(a1, kr, vr, one, s1, dp1);
+            dkdv_update<D, true>(a1, s1, dp1, dk_acc, dv_acc, 32 * hstart, kj, half, c);
+        } else {
+            pair(kt, std::true_type{});
         }
-#pragma unroll
-        for (int r = 0; r < 16; ++r) s[r] = exp2_fast(fmaf(s[r], c, -L[r >> 2][r & 3]));
-        const int qb = 32 * hh;
-        if (qb < kw + 32) {  // the diagonal half tile: queries before the key get P = 0
-#pragma unroll
-            for (int r = 0; r < 16; ++r)
-                if (qb + acc_row(r, half) < kj) s[r] = 0.0f;
-        }
-        const bf16x8 pb[2] = {pack_b(s, 0), pack_b(s, 1)};
-#pragma unroll
-        for (int r = 0; r < 16; ++r) s[r] *= dp[r] - Dl[r >> 2][r & 3];
-        const bf16x8 db[2] = {pack_b(s, 0), pack_b(s, 1)};
-#pragma unroll
-        for (int dt = 0; dt < D / 32; ++dt) {
-#pragma unroll
-            for (int u = 0; u < 2; ++u) {
-                dv_acc[dt] =
-                    mfma_32x32x16_bf16(lds_tr(gta[dt] + 16u * u * RB, 8u * RB), pb[u], dv_acc[dt]);
-                dk_acc[dt] =
-                    mfma_32x32x16_bf16(lds_tr(qta[dt] + 16u * u * RB, 8u * RB), db[u], dk_acc[dt]);
-            }
-        }
+        ++kt;
+    }
+    for (; kt < ntile; ++kt) {
+        tile_sync(kt);
+        pair(kt, std::false_type{});
     }
 
     if (kj < T) {

@@ -19,6 +19,9 @@ every timed step) against its algorithmic FLOPs:
     forward 2 units, backward dK/dV 4 units (S recompute, dP, dV, dK), backward dQ 1 unit
     (dQ; its S and dP recomputes duplicate work already counted), unit = B*H*T^2*d.
 The split-transpose kernels are HBM-bound: 6*B*T*C*elem_bytes algorithmic bytes each.
+roofline.traffic is the dominant kernel's measured HBM bytes per dispatch, read from
+profiles/hbm_traffic.md (rocprofv3 FETCH_SIZE and WRITE_SIZE of this same bench command,
+scaled by a device-copy calibration); null when that file has no row for the workload.
 
 cpu_baseline: the torch-CPU fp32 restatement of the reference attention
 (pytorch_src/model.py:43-52, forward + autograd backward) timed on this host on the same
@@ -189,7 +192,26 @@ class PathRunner:
                    (self.o, self.dq, self.dk, self.dv, self.dqkv))
 
 
-def roofline_of(runner, per_kernel):
+def measured_traffic(config, dtype, kernel):
+    """HBM bytes per dispatch of `kernel` from profiles/hbm_traffic.md (rocprofv3
+    FETCH_SIZE + WRITE_SIZE of this bench command, scaled by the copy calibration that file
+    states), or None when the file has no row for this (config, dtype, kernel)."""
+    path = os.path.join(REPO, "profiles", "hbm_traffic.md")
+    try:
+        lines = open(path).read().splitlines()
+    except OSError:
+        return None
+    for ln in lines:
+        cells = [c.strip() for c in ln.strip().strip("|").split("|")]
+        if len(cells) >= 6 and cells[:3] == [config, dtype, kernel]:
+            try:
+                return int(cells[5])
+            except ValueError:
+                return None
+    return None
+
+
+def roofline_of(runner, per_kernel, config):
     name = max(per_kernel, key=per_kernel.get)
     amount, kind = runner.kernel_work(name)
     sec = per_kernel[name] * 1e-3
@@ -202,7 +224,8 @@ def roofline_of(runner, per_kernel):
         peak = PEAK_HBM_GBS
         bound, unit = "hbm", "GB/s"
     return name, {"bound": bound, "achieved": round(achieved, 3), "peak": peak, "unit": unit,
-                  "frac": round(achieved / peak, 4), "traffic": None}
+                  "frac": round(achieved / peak, 4),
+                  "traffic": measured_traffic(config, runner.dtype, name)}
 
 
 def kernel_table(runner, per_kernel):
@@ -309,7 +332,7 @@ def main():
     wall, per_kernel = runner.timed(args.steps, args.warmup)
     ms = wall / args.steps * 1e3
     value = runner.flops_total() / (ms * 1e-3) / 1e12
-    dom, roof = roofline_of(runner, per_kernel)
+    dom, roof = roofline_of(runner, per_kernel, args.config)
     attn_ms = sum(per_kernel[n] for n in FLOP_UNITS)
     props = torch.cuda.get_device_properties(0)
     line = {

@@ -23,6 +23,9 @@ roofline.traffic is the dominant kernel's measured HBM bytes per dispatch, read 
 profiles/hbm_traffic.md (rocprofv3 FETCH_SIZE and WRITE_SIZE of this same bench command,
 scaled by a device-copy calibration); null when that file has no row for the workload.
 
+secondary: the same step in bf16 at config 2's shape and at config 3, and the reference's
+materialised mode (full-square GEMMs + fused softmax, fp32, config 2) as a timed fwd+bwd.
+
 cpu_baseline: the torch-CPU fp32 restatement of the reference attention
 (pytorch_src/model.py:43-52, forward + autograd backward) timed on this host on the same
 inputs, which also gives a max-abs parity figure for the GPU result.
@@ -312,6 +315,43 @@ def secondary(lib, cfg, dtype, steps, seed):
     return out
 
 
+def materialized(lib, steps, seed):
+    """The reference's materialised mode (src/model.cu:313-332 forward, 617-650 backward) at
+    config 2 fp32: 6 full-square GEMMs (12 units executed, no causal skip) and the two
+    softmax passes; time per fwd+bwd and the GEMMs' executed rate."""
+    import torch
+    B, H, T, d, _, _ = CONFIGS["c2"]
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    q, k, v, do = (torch.randn((B, H, T, d), generator=g).to("cuda:0") for _ in range(4))
+    sq = lambda: torch.empty((B * H * T, T), device="cuda:0")
+    scores, probs, dprobs, dscores = sq(), sq(), sq(), sq()
+    out, dq, dk, dv = (torch.empty_like(q) for _ in range(4))
+    scale = 1.0 / math.sqrt(d)
+
+    def step():
+        lib.materialized_causal_attention_forward(q, k, v, scores, probs, out, B, H, T, d, scale)
+        lib.materialized_causal_attention_backward(q, k, v, probs, do, dprobs, dscores, dq, dk,
+                                                   dv, B, H, T, d, scale)
+    for _ in range(3):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    unit = float(B * H * T * T * d)
+    out_d = {"config": "c2", "mode": "materialised (full-square GEMMs + fused softmax)",
+             "dtype": "f32", "ms_per_step": round(ms, 4),
+             "tflops_algorithmic": round(7 * unit / (ms * 1e-3) / 1e12, 2),
+             "gemm_tflops_executed_upper": round(12 * unit / (ms * 1e-3) / 1e12, 2),
+             "finite": bool(torch.isfinite(dq).all() and torch.isfinite(out).all())}
+    del scores, probs, dprobs, dscores
+    return out_d
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -370,6 +410,7 @@ def main():
         sec = [secondary(lib, args.config, "bf16", args.secondary_steps, args.seed)] \
             if dtype != "bf16" else []
         sec.append(secondary(lib, "c3", "bf16", args.secondary_steps, args.seed))
+        sec.append(materialized(lib, max(3, args.secondary_steps // 4), args.seed))
         line["secondary"] = sec
     print(json.dumps(line), flush=True)
     return 0

@@ -104,6 +104,37 @@ int attn_causal_softmax_backward_f32(const float* dprobs, const float* probs, fl
                                      int B, int H, int T, float scale, hipStream_t stream);
 
 /* ------------------------------------------------------------------------------------------
+ * Materialised path: strided-batched fp32 GEMM (v_mfma_f32_32x32x2_f32) and the reference's
+ * materialised attention sequences built from it and the softmax kernels above.
+ * ------------------------------------------------------------------------------------------ */
+
+/* Replaces matmul_batched_strided, include/kernels/matmul.cuh:44 (src/kernels/matmul.cu:167-207,
+ * cublasSgemmStridedBatched).  Row-major, for b in [0, batch_count):
+ *   C[b*strideC] (M x N, ldc = N) = alpha * op(A[b*strideA]) * op(B[b*strideB]) + beta * C
+ * op(A) = A (M x K, lda = K) or, if transA, A^T of A stored K x M (lda = M); op(B) = B (K x N,
+ * ldb = N) or, if transB, B^T of B stored N x K (ldb = K).  beta == 0 does not read C.
+ * Strides >= 0; alpha, beta finite (else ATTN_ERROR_INVALID_VALUE).  No alignment needed. */
+int attn_matmul_batched_strided_f32(const float* A, const float* B, float* C, int M, int N,
+                                    int K, long long strideA, long long strideB,
+                                    long long strideC, int batch_count, int transA, int transB,
+                                    float alpha, float beta, hipStream_t stream);
+
+/* The reference's materialised forward (src/model.cu:313-332), scores and probs (B*H*T, T):
+ *   scores = Q K^T  ->  probs = causal_softmax_forward(scores, scale)  ->  out = probs V. */
+int attn_materialized_causal_forward_f32(const float* q, const float* k, const float* v,
+                                         float* scores, float* probs, float* out, int B, int H,
+                                         int T, int d_head, float scale, hipStream_t stream);
+
+/* The reference's materialised backward (src/model.cu:617-650): dprobs = dO V^T,
+ * dv = probs^T dO, dscores = causal_softmax_backward(dprobs, probs, scale), dq = dscores K,
+ * dk = dscores^T Q.  dprobs and dscores are (B*H*T, T) scratch; dq, dk, dv are overwritten. */
+int attn_materialized_causal_backward_f32(const float* q, const float* k, const float* v,
+                                          const float* probs, const float* dout, float* dprobs,
+                                          float* dscores, float* dq, float* dk, float* dv,
+                                          int B, int H, int T, int d_head, float scale,
+                                          hipStream_t stream);
+
+/* ------------------------------------------------------------------------------------------
  * Tiled (flash) causal attention, fp32 parity path: QK^T and PV on v_mfma_f32_32x32x2_f32.
  * d_head in {32, 64, 128}.  All (B,H,T,d) tensors and the stats must be 16-byte aligned.
  *

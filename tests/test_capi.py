@@ -96,6 +96,29 @@ def test_split_and_softmax_validation(lib):
                     None) == INVALID_DIM
 
 
+def test_materialized_validation(lib):
+    f = ctypes.c_float
+    gemm = lambda A=FAKE, M=4, N=4, K=4, sA=16, batch=2, alpha=1.0, beta=0.0: lib.call(
+        "attn_matmul_batched_strided_f32", A, FAKE, FAKE, M, N, K, sA, 16, 16, batch, 0, 1,
+        f(alpha), f(beta), None)
+    assert gemm(A=None) == NULLPTR
+    assert gemm(M=0) == INVALID_DIM
+    assert gemm(K=-3) == INVALID_DIM
+    assert gemm(batch=0) == BAD_VALUE
+    assert gemm(sA=-1) == BAD_VALUE
+    assert gemm(alpha=float("inf")) == BAD_VALUE
+    assert gemm(beta=float("nan")) == BAD_VALUE
+    assert gemm(M=1 << 20, N=1 << 20, batch=16) == INVALID_DIM  # grid beyond 2^31 tiles
+    assert lib.call("attn_materialized_causal_forward_f32", FAKE, FAKE, FAKE, FAKE, None, FAKE,
+                    1, 1, 8, 32, f(0.1), None) == NULLPTR
+    assert lib.call("attn_materialized_causal_forward_f32", FAKE, FAKE, FAKE, FAKE, FAKE, FAKE,
+                    1, 1, 8, 32, f(0.0), None) == BAD_VALUE
+    assert lib.call("attn_materialized_causal_backward_f32", FAKE, FAKE, FAKE, FAKE, FAKE, FAKE,
+                    FAKE, FAKE, FAKE, FAKE, 1, 0, 8, 32, f(0.1), None) == INVALID_DIM
+    assert lib.call("attn_materialized_causal_backward_f32", FAKE, FAKE, FAKE, FAKE, FAKE, FAKE,
+                    FAKE, FAKE, None, FAKE, 1, 1, 8, 32, f(0.1), None) == NULLPTR
+
+
 def test_python_launchers_reject_host_tensors(lib):
     import torch
     x = torch.zeros(2, 2, 8, 32)
@@ -105,14 +128,15 @@ def test_python_launchers_reject_host_tensors(lib):
 
 @pytest.mark.parametrize("lang", ["c", "c++"])
 def test_headers_compile_standalone(tmp_path, lang):
-    """attn_capi.h is a C header; kernels/attention.h compiles as C++17 (syntax only)."""
+    """attn_capi.h is a C header; kernels/attention.h and kernels/matmul.h compile as C++17
+    (syntax only)."""
     if lang == "c":
         src = tmp_path / "t.c"
         src.write_text('#include "attn_capi.h"\nint main(void){return attn_version() > 0 ? 0 : 1;}\n')
         cmd = ["gcc", "-std=c11", "-fsyntax-only"]
     else:
         src = tmp_path / "t.cpp"
-        src.write_text('#include "kernels/attention.h"\n#include "common.h"\nint main(){return 0;}\n')
+        src.write_text('#include "kernels/attention.h"\n#include "kernels/matmul.h"\n#include "common.h"\nint main(){return 0;}\n')
         cmd = ["g++", "-std=c++17", "-fsyntax-only"]
     cmd += ["-D__HIP_PLATFORM_AMD__", f"-I{REPO}/include", "-I/opt/rocm/include", str(src)]
     subprocess.run(cmd, check=True)

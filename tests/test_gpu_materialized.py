@@ -1,0 +1,111 @@
+"""Materialised attention mode on the GPU: the strided-batched fp32 GEMM against fp64
+products, and the reference's materialised forward/backward sequences (src/model.cu:313-332,
+617-650) against the CPU oracle and the tiled fp32 path."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import default_scale, max_abs, to_dev
+from oracle import attention_ref as ref
+
+pytestmark = pytest.mark.gpu
+
+
+def gemm_ref(a, b, M, N, K, sA, sB, sC, batch, ta, tb, alpha, beta, c0):
+    """fp64 restatement of the row-major strided-batched GEMM (matmul.cu:167-207)."""
+    c = c0.astype(np.float64).copy()
+    for i in range(batch):
+        A = a[i * sA:i * sA + M * K].astype(np.float64)
+        B = b[i * sB:i * sB + K * N].astype(np.float64)
+        A = A.reshape(K, M).T if ta else A.reshape(M, K)
+        B = B.reshape(N, K).T if tb else B.reshape(K, N)
+        prev = c[i * sC:i * sC + M * N].reshape(M, N)
+        out = alpha * (A @ B) + (beta * prev if beta != 0 else 0.0)
+        c[i * sC:i * sC + M * N] = out.reshape(-1)
+    return c
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 1, 1), (17, 33, 5), (64, 64, 16), (100, 70, 130),
+                                   (65, 129, 64), (256, 256, 1024)])
+@pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
+def test_gemm_vs_fp64(lib, M, N, K, ta, tb):
+    rng = np.random.default_rng(M * 1000 + N * 10 + K + 2 * ta + tb)
+    batch = 3
+    pad = 7  # strides larger than one matrix: batches are not packed
+    sA, sB, sC = M * K + pad, K * N + pad, M * N + pad
+    a = rng.standard_normal(batch * sA).astype(np.float32)
+    b = rng.standard_normal(batch * sB).astype(np.float32)
+    c0 = rng.standard_normal(batch * sC).astype(np.float32)
+    for alpha, beta in ((1.0, 0.0), (0.5, -1.25)):
+        cg = to_dev(c0)
+        if beta == 0.0:
+            cg.fill_(float("nan"))  # beta = 0 must not read C
+        lib.matmul_batched_strided(to_dev(a), to_dev(b), cg, M, N, K, sA, sB, sC, batch, ta, tb,
+                                   alpha, beta)
+        torch.cuda.synchronize()
+        got = cg.cpu().numpy()
+        want = gemm_ref(a, b, M, N, K, sA, sB, sC, batch, ta, tb, alpha, beta, c0)
+        for i in range(batch):
+            g = got[i * sC:i * sC + M * N]
+            w = want[i * sC:i * sC + M * N]
+            assert np.isfinite(g).all()
+            np.testing.assert_allclose(g, w, rtol=0, atol=2e-6 * K + 1e-6,
+                                       err_msg=f"batch {i} alpha {alpha} beta {beta}")
+        # the padding between batch matrices is never written
+        for i in range(batch - 1):
+            gap = got[i * sC + M * N:(i + 1) * sC]
+            ref_gap = c0[i * sC + M * N:(i + 1) * sC]
+            if beta == 0.0:
+                assert np.isnan(gap).all()
+            else:
+                np.testing.assert_array_equal(gap, ref_gap)
+
+
+def materialized(lib, q, k, v, do, B, H, T, d, scale):
+    qg, kg, vg, dog = (to_dev(x) for x in (q, k, v, do))
+    nan = lambda shape: torch.full(shape, float("nan"), device="cuda:0")
+    scores, probs = nan((B * H * T, T)), nan((B * H * T, T))
+    out = nan((B, H, T, d))
+    lib.materialized_causal_attention_forward(qg, kg, vg, scores, probs, out, B, H, T, d, scale)
+    dprobs, dscores = nan((B * H * T, T)), nan((B * H * T, T))
+    dq, dk, dv = nan((B, H, T, d)), nan((B, H, T, d)), nan((B, H, T, d))
+    lib.materialized_causal_attention_backward(qg, kg, vg, probs, dog, dprobs, dscores, dq, dk,
+                                               dv, B, H, T, d, scale)
+    torch.cuda.synchronize()
+    f = lambda t: t.cpu().numpy()
+    return dict(o=f(out), dq=f(dq), dk=f(dk), dv=f(dv), probs=f(probs).reshape(B, H, T, T))
+
+
+@pytest.mark.parametrize("B,H,T,d", [(1, 1, 1, 32), (2, 3, 17, 64), (1, 2, 100, 128),
+                                     (2, 2, 257, 64), (1, 1, 64, 48)])
+def test_materialized_vs_oracle(lib, B, H, T, d):
+    q, k, v, do = ref.seeded_inputs(B, H, T, d, seed=T + d)
+    scale = default_scale(d)
+    got = materialized(lib, q, k, v, do, B, H, T, d, scale)
+    want = ref.attention_fwd_bwd(q, k, v, do, scale)
+    for name in ("o", "dq", "dk", "dv"):
+        err = max_abs(got[name], getattr(want, name).numpy())
+        assert err <= 1e-5, f"{name}: max-abs {err:.3e}"
+    assert np.all(got["probs"][..., np.triu(np.ones((T, T), bool), 1)] == 0)
+
+
+def test_materialized_config2_vs_oracle_and_tiled(lib):
+    """Config 2 (B8 H12 T1024 d64, fp32): the materialised mode against the oracle on three
+    heads and against the tiled fp32 path on every head."""
+    B, H, T, d = 8, 12, 1024, 64
+    q, k, v, do = ref.seeded_inputs(B, H, T, d, seed=42)
+    scale = default_scale(d)
+    got = materialized(lib, q, k, v, do, B, H, T, d, scale)
+    from gpu_util import gpu_fwd_bwd
+    tiled = gpu_fwd_bwd(lib, q, k, v, do, scale)
+    for name in ("o", "dq", "dk", "dv"):
+        err = max_abs(got[name], tiled[name])
+        assert err <= 2e-5, f"{name} vs tiled: max-abs {err:.3e}"
+    for b, h in ((0, 0), (3, 7), (B - 1, H - 1)):
+        sl = lambda x: x[b:b + 1, h:h + 1]
+        want = ref.attention_fwd_bwd(sl(q), sl(k), sl(v), sl(do), scale)
+        for name in ("o", "dq", "dk", "dv"):
+            err = max_abs(sl(got[name]), getattr(want, name).numpy())
+            assert err <= 1e-5, f"{name} head ({b},{h}): max-abs {err:.3e}"

@@ -39,6 +39,7 @@ STATUS = {
 _P = ctypes.c_void_p
 _I = ctypes.c_int
 _F = ctypes.c_float
+_L = ctypes.c_longlong
 
 # name -> argument types (the trailing _P is the hipStream_t)
 SIGNATURES = {
@@ -52,6 +53,11 @@ SIGNATURES = {
     "attn_head_merge_transpose_backward_f32": [_P, _P, _I, _I, _I, _I, _P],
     "attn_causal_softmax_forward_f32": [_P, _P, _I, _I, _I, _F, _P],
     "attn_causal_softmax_backward_f32": [_P, _P, _P, _I, _I, _I, _F, _P],
+    "attn_matmul_batched_strided_f32":
+        [_P, _P, _P, _I, _I, _I, _L, _L, _L, _I, _I, _I, _F, _F, _P],
+    "attn_materialized_causal_forward_f32": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P],
+    "attn_materialized_causal_backward_f32":
+        [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P],
     "attn_tiled_causal_forward_f32": [_P, _P, _P, _P, _I, _I, _I, _I, _F, _P, _P, _P],
     "attn_precompute_dot_do_o_f32": [_P, _P, _P, _I, _I, _I, _I, _P],
     "attn_tiled_causal_backward_f32":
@@ -209,6 +215,44 @@ def causal_softmax_backward(dprobs, probs, dscores, B, H, T, scale, stream=None)
     check(call("attn_causal_softmax_backward_f32", _ptr(dprobs, f32, n, "dprobs"),
                _ptr(probs, f32, n, "probs"), _ptr(dscores, f32, n, "dscores"), B, H, T,
                float(scale), _stream(stream)), "causal_softmax_backward")
+
+
+def matmul_batched_strided(A, B, C, M, N, K, strideA, strideB, strideC, batch_count, transA,
+                           transB, alpha=1.0, beta=0.0, stream=None):
+    """Reference: include/kernels/matmul.cuh:44 (src/kernels/matmul.cu:167-207) without the
+    cuBLAS handle.  Row-major C_b (M x N) = alpha*op(A_b)*op(B_b) + beta*C_b; A, B, C are
+    fp32 tensors holding `batch_count` matrices at the given element strides."""
+    f32 = _dt(False)
+    last = batch_count - 1
+    check(call("attn_matmul_batched_strided_f32",
+               _ptr(A, f32, last * strideA + M * K, "A"), _ptr(B, f32, last * strideB + K * N, "B"),
+               _ptr(C, f32, last * strideC + M * N, "C"), M, N, K, strideA, strideB, strideC,
+               batch_count, int(bool(transA)), int(bool(transB)), float(alpha), float(beta),
+               _stream(stream)), "matmul_batched_strided")
+
+
+def materialized_causal_attention_forward(q, k, v, scores, probs, out, B, H, T, d_head, scale,
+                                          stream=None):
+    """The reference's materialised forward, src/model.cu:313-332 (fp32)."""
+    f32 = _dt(False)
+    n, nn = B * H * T * d_head, B * H * T * T
+    check(call("attn_materialized_causal_forward_f32", _ptr(q, f32, n, "q"), _ptr(k, f32, n, "k"),
+               _ptr(v, f32, n, "v"), _ptr(scores, f32, nn, "scores"), _ptr(probs, f32, nn, "probs"),
+               _ptr(out, f32, n, "out"), B, H, T, d_head, float(scale), _stream(stream)),
+          "materialized_causal_attention_forward")
+
+
+def materialized_causal_attention_backward(q, k, v, probs, dout, dprobs, dscores, dq, dk, dv,
+                                           B, H, T, d_head, scale, stream=None):
+    """The reference's materialised backward, src/model.cu:617-650 (fp32)."""
+    f32 = _dt(False)
+    n, nn = B * H * T * d_head, B * H * T * T
+    check(call("attn_materialized_causal_backward_f32", _ptr(q, f32, n, "q"),
+               _ptr(k, f32, n, "k"), _ptr(v, f32, n, "v"), _ptr(probs, f32, nn, "probs"),
+               _ptr(dout, f32, n, "dout"), _ptr(dprobs, f32, nn, "dprobs"),
+               _ptr(dscores, f32, nn, "dscores"), _ptr(dq, f32, n, "dq"), _ptr(dk, f32, n, "dk"),
+               _ptr(dv, f32, n, "dv"), B, H, T, d_head, float(scale), _stream(stream)),
+          "materialized_causal_attention_backward")
 
 
 def tiled_causal_attention_forward(q, k, v, out, B, H, T, d_head, scale, m_out=None,

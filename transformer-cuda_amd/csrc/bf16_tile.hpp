@@ -39,7 +39,6 @@ struct Swz {
     static constexpr int kRowBytes = 2 * D;
     static constexpr int kBytes = kRowTile * kRowBytes;
     static constexpr int kDma = kBytes / 1024;  // wave instructions per tile
-    static_assert(kDma % kWaves == 0 || kDma < kWaves, "tile copy split");
     __device__ static int swz(int r) {
         return kCpr >= 8 ? 2 * (r & 3) + ((r >> 2) & 1) : (r & (kCpr - 1));
     }
@@ -48,16 +47,16 @@ struct Swz {
     }
 };
 
-// Wave `wave` issues its share of the copy of rows [row0, row0 + 64) of a (T, D) bf16 head
-// into the tile at LDS byte address lds.  Rows past T are read from row T-1 (finite values;
-// every consumer masks or zero-weights them).
-template <int D>
+// Wave `wave` of NW issues its share of the copy of rows [row0, row0 + 64) of a (T, D) bf16
+// head into the tile at LDS byte address lds.  Rows past T are read from row T-1 (finite
+// values; every consumer masks or zero-weights them).
+template <int D, int NW = kWaves>
 __device__ __forceinline__ void dma_tile(const uint16_t* __restrict__ head, int row0, int T,
                                          uint32_t lds, int wave, int lane) {
     using S = Swz<D>;
     const uint16_t* base = head + static_cast<size_t>(row0) * D;
 #pragma unroll
-    for (int i = wave; i < S::kDma; i += kWaves) {
+    for (int i = wave; i < S::kDma; i += NW) {
         const int p = i * kWave + lane;  // 16-byte slot of the tile
         const int r = p / S::kCpr;
         const int c = (p % S::kCpr) ^ S::swz(r);

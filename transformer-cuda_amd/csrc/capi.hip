@@ -48,6 +48,15 @@ int check_split(const void* a, const void* b, const void* c, const void* dd, int
     return ATTN_SUCCESS;
 }
 
+int check_materialized(int B, int H, int T, int d, float scale) {
+    const int st = check_dims4(B, H, T, d);
+    if (st != ATTN_SUCCESS) return st;
+    if (!(scale > 0.0f) || !isfinite(scale)) return ATTN_ERROR_INVALID_VALUE;
+    const int64_t tiles = ((static_cast<int64_t>(T) + 63) / 64) * ((static_cast<int64_t>(T) + 63) / 64);
+    if (tiles * B * H > kInt32Max) return ATTN_ERROR_INVALID_DIM;
+    return ATTN_SUCCESS;
+}
+
 int launch_status() {
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? ATTN_SUCCESS : ATTN_ERROR_LAUNCH;
@@ -83,7 +92,7 @@ const char* attn_status_string(int status) {
         case ATTN_ERROR_NULL_POINTER: return "required pointer is NULL";
         case ATTN_ERROR_MISALIGNED: return "pointer not 16-byte aligned";
         case ATTN_ERROR_LAUNCH: return "kernel launch failed";
-        case ATTN_ERROR_INVALID_VALUE: return "invalid value (scale)";
+        case ATTN_ERROR_INVALID_VALUE: return "invalid value (scale, alpha/beta, batch count or stride)";
         default: return "unknown status";
     }
 }
@@ -183,6 +192,78 @@ int attn_causal_softmax_backward_f32(const float* dprobs, const float* probs, fl
     if ((rows + 3) / 4 > kInt32Max) return ATTN_ERROR_INVALID_DIM;
     clear_error();
     tcamd::launch_causal_softmax_bwd_f32(dprobs, probs, dscores, rows, T, scale, stream);
+    return launch_status();
+}
+
+// ---- materialised path ------------------------------------------------------------------
+
+int attn_matmul_batched_strided_f32(const float* A, const float* B, float* C, int M, int N,
+                                    int K, long long strideA, long long strideB,
+                                    long long strideC, int batch_count, int transA, int transB,
+                                    float alpha, float beta, hipStream_t stream) {
+    if (A == nullptr || B == nullptr || C == nullptr) return ATTN_ERROR_NULL_POINTER;
+    if (M <= 0 || N <= 0 || K <= 0) return ATTN_ERROR_INVALID_DIM;
+    if (batch_count <= 0 || strideA < 0 || strideB < 0 || strideC < 0)
+        return ATTN_ERROR_INVALID_VALUE;
+    if (!isfinite(alpha) || !isfinite(beta)) return ATTN_ERROR_INVALID_VALUE;
+    const int64_t tiles = ((static_cast<int64_t>(M) + 63) / 64) * ((static_cast<int64_t>(N) + 63) / 64);
+    if (tiles * batch_count > kInt32Max) return ATTN_ERROR_INVALID_DIM;
+    clear_error();
+    tcamd::launch_batched_gemm_f32(A, B, C, M, N, K, strideA, strideB, strideC, batch_count,
+                                   transA != 0, transB != 0, alpha, beta, stream);
+    return launch_status();
+}
+
+int attn_materialized_causal_forward_f32(const float* q, const float* k, const float* v,
+                                         float* scores, float* probs, float* out, int B, int H,
+                                         int T, int d_head, float scale, hipStream_t stream) {
+    if (q == nullptr || k == nullptr || v == nullptr || scores == nullptr ||
+        probs == nullptr || out == nullptr)
+        return ATTN_ERROR_NULL_POINTER;
+    const int st = check_materialized(B, H, T, d_head, scale);
+    if (st != ATTN_SUCCESS) return st;
+    const int BH = B * H;
+    const long long sh = static_cast<long long>(T) * d_head, ss = static_cast<long long>(T) * T;
+    clear_error();
+    // src/model.cu:314-320: scores = Q K^T (alpha 1; the scale is applied in the softmax)
+    tcamd::launch_batched_gemm_f32(q, k, scores, T, T, d_head, sh, sh, ss, BH, false, true,
+                                   1.0f, 0.0f, stream);
+    tcamd::launch_causal_softmax_fwd_f32(scores, probs, static_cast<int64_t>(BH) * T, T, scale,
+                                         stream);
+    // src/model.cu:326-332: out = probs V
+    tcamd::launch_batched_gemm_f32(probs, v, out, T, d_head, T, ss, sh, sh, BH, false, false,
+                                   1.0f, 0.0f, stream);
+    return launch_status();
+}
+
+int attn_materialized_causal_backward_f32(const float* q, const float* k, const float* v,
+                                          const float* probs, const float* dout, float* dprobs,
+                                          float* dscores, float* dq, float* dk, float* dv,
+                                          int B, int H, int T, int d_head, float scale,
+                                          hipStream_t stream) {
+    if (q == nullptr || k == nullptr || v == nullptr || probs == nullptr || dout == nullptr ||
+        dprobs == nullptr || dscores == nullptr || dq == nullptr || dk == nullptr ||
+        dv == nullptr)
+        return ATTN_ERROR_NULL_POINTER;
+    const int st = check_materialized(B, H, T, d_head, scale);
+    if (st != ATTN_SUCCESS) return st;
+    const int BH = B * H;
+    const long long sh = static_cast<long long>(T) * d_head, ss = static_cast<long long>(T) * T;
+    clear_error();
+    // src/model.cu:618-623: dprobs = dO V^T
+    tcamd::launch_batched_gemm_f32(dout, v, dprobs, T, T, d_head, sh, sh, ss, BH, false, true,
+                                   1.0f, 0.0f, stream);
+    // :626-631: dv = probs^T dO
+    tcamd::launch_batched_gemm_f32(probs, dout, dv, T, d_head, T, ss, sh, sh, BH, true, false,
+                                   1.0f, 0.0f, stream);
+    // :634: dscores = softmax backward (scale inside)
+    tcamd::launch_causal_softmax_bwd_f32(dprobs, probs, dscores, static_cast<int64_t>(BH) * T,
+                                         T, scale, stream);
+    // :637-642: dq = dscores K;  :644-649: dk = dscores^T Q
+    tcamd::launch_batched_gemm_f32(dscores, k, dq, T, d_head, T, ss, sh, sh, BH, false, false,
+                                   1.0f, 0.0f, stream);
+    tcamd::launch_batched_gemm_f32(dscores, q, dk, T, d_head, T, ss, sh, sh, BH, true, false,
+                                   1.0f, 0.0f, stream);
     return launch_status();
 }
 

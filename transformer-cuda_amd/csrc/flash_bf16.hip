@@ -310,15 +310,16 @@ __device__ __forceinline__ void dkdv_update(const HalfAddr<D>& a, f32x16& s, con
     }
 }
 
-template <int D>
-__global__ __launch_bounds__(kWave* kWaves) void flash_bwd_dkdv_bf16_kernel(
+// NW waves per workgroup; wave w owns keys k0 + 32w ...
+template <int D, int NW>
+__global__ __launch_bounds__(kWave* NW) void flash_bwd_dkdv_bf16_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, const uint16_t* __restrict__ dO,
     const float* __restrict__ m, const float* __restrict__ l, const float* __restrict__ Dws,
     uint16_t* __restrict__ dk, uint16_t* __restrict__ dv, int BH, int T, float scale,
     int nblk) {
     using S = Swz<D>;
-    constexpr int kBlock = kWaves * kSub;  // keys per workgroup
+    constexpr int kBlock = NW * kSub;  // keys per workgroup
     constexpr uint32_t RB = S::kRowBytes;
     __shared__ __attribute__((aligned(1024))) QgSmem<D> sm;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
@@ -343,8 +344,8 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_bwd_dkdv_bf16_kernel(
     const uint32_t g_lds = lds_addr(sm.g[0]);
     const uint32_t qx_lds = lds_addr(sm.qx[0]);
     const uint32_t gx_lds = lds_addr(sm.gx[0]);
-    dma_tile<D>(qh, t0 * kRowTile, T, q_lds, wave, lane);
-    dma_tile<D>(gh, t0 * kRowTile, T, g_lds, wave, lane);
+    dma_tile<D, NW>(qh, t0 * kRowTile, T, q_lds, wave, lane);
+    dma_tile<D, NW>(gh, t0 * kRowTile, T, g_lds, wave, lane);
     // Wave 0 stages the statistics of a tile through VGPRs: lane i holds query 64t + i.
     float st_m = 0.0f, st_l = 1.0f, st_d = 0.0f;
     auto load_stats = [&](int t) {
@@ -398,8 +399,8 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_bwd_dkdv_bf16_kernel(
         if (kt + 1 < ntile) {
             if (wave == 0) load_stats(kt + 1);
             const uint32_t nbuf = static_cast<uint32_t>((kt + 1) & 1) * S::kBytes;
-            dma_tile<D>(qh, (kt + 1) * kRowTile, T, q_lds + nbuf, wave, lane);
-            dma_tile<D>(gh, (kt + 1) * kRowTile, T, g_lds + nbuf, wave, lane);
+            dma_tile<D, NW>(qh, (kt + 1) * kRowTile, T, q_lds + nbuf, wave, lane);
+            dma_tile<D, NW>(gh, (kt + 1) * kRowTile, T, g_lds + nbuf, wave, lane);
         }
     };
     // Operand addresses of half tile hh (queries 32*hh ..).
@@ -480,9 +481,10 @@ template <int D>
 void dkdv_dispatch(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* dO,
                    const float* m, const float* l, const float* Dws, uint16_t* dk, uint16_t* dv,
                    int BH, int T, float scale, hipStream_t stream) {
-    constexpr int kBlock = kWaves * kSub;
+    constexpr int NW = kWaves;
+    constexpr int kBlock = NW * kSub;
     const int nblk = (T + kBlock - 1) / kBlock;
-    hipLaunchKernelGGL(flash_bwd_dkdv_bf16_kernel<D>, dim3(BH * nblk), dim3(kWave * kWaves), 0,
+    hipLaunchKernelGGL((flash_bwd_dkdv_bf16_kernel<D, NW>), dim3(BH * nblk), dim3(kWave * NW), 0,
                        stream, q, k, v, dO, m, l, Dws, dk, dv, BH, T, scale, nblk);
 }
 

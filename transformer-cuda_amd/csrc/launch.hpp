@@ -24,6 +24,11 @@ void launch_causal_softmax_fwd_f32(const float* scores, float* probs, int64_t ro
 void launch_causal_softmax_bwd_f32(const float* dprobs, const float* probs, float* dscores,
                                    int64_t rows, int T, float scale, hipStream_t stream);
 
+// Row-major strided-batched C = alpha*op(A)*op(B) + beta*C, C (M x N) with ldc = N.
+void launch_batched_gemm_f32(const float* A, const float* B, float* C, int M, int N, int K,
+                             long long sA, long long sB, long long sC, int batch, bool transA,
+                             bool transB, float alpha, float beta, hipStream_t stream);
+
 void launch_dot_do_o_f32(const float* dO, const float* O, float* D, int64_t rows, int d,
                          hipStream_t stream);
 

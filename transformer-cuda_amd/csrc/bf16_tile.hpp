@@ -166,5 +166,23 @@ __device__ __forceinline__ void lane_offsets(int lane, uint32_t (&roff)[D / 16],
     }
 }
 
+// Host side: whether a query-parallel kernel should run one 32-query sub-block per wave
+// (128 queries per workgroup) instead of two (256): when 256-query blocks would give fewer
+// than two workgroups per CU, halving the block doubles the parallelism.
+inline bool use_single_subblock(int BH, int T) {
+    static thread_local int cached_dev = -1, cached_cus = 256;
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    if (dev != cached_dev) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+            cus > 0)
+            cached_cus = cus;
+        cached_dev = dev;
+    }
+    const long long blocks = static_cast<long long>(BH) * ((T + 255) / 256);
+    return blocks < 2LL * cached_cus;
+}
+
 }  // namespace bf16t
 }  // namespace tcamd

@@ -465,16 +465,26 @@ __global__ __launch_bounds__(kWave* NW) void flash_bwd_dkdv_bf16_kernel(
     }
 }
 
-template <int D>
-void dq_dispatch(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* o,
-                 const uint16_t* dO, const float* m, const float* l, uint16_t* dq, float* Dws,
-                 int BH, int T, float scale, hipStream_t stream) {
-    constexpr int NSUB = D >= 128 ? 1 : 2;
+template <int D, int NSUB>
+void dq_launch(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* o,
+               const uint16_t* dO, const float* m, const float* l, uint16_t* dq, float* Dws,
+               int BH, int T, float scale, hipStream_t stream) {
     constexpr int kBlock = kWaves * NSUB * kSub;
     const int nblk = (T + kBlock - 1) / kBlock;
     hipLaunchKernelGGL((flash_bwd_dq_bf16_kernel<D, NSUB>), dim3(BH * nblk),
                        dim3(kWave * kWaves), 0, stream, q, k, v, o, dO, m, l, dq, Dws, BH, T,
                        scale, nblk);
+}
+
+template <int D>
+void dq_dispatch(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* o,
+                 const uint16_t* dO, const float* m, const float* l, uint16_t* dq, float* Dws,
+                 int BH, int T, float scale, hipStream_t stream) {
+    // d = 128 holds one sub-block per wave (registers)
+    if (D >= 128 || use_single_subblock(BH, T))
+        dq_launch<D, 1>(q, k, v, o, dO, m, l, dq, Dws, BH, T, scale, stream);
+    else
+        dq_launch<D, (D >= 128 ? 1 : 2)>(q, k, v, o, dO, m, l, dq, Dws, BH, T, scale, stream);
 }
 
 template <int D>

@@ -38,7 +38,6 @@ namespace {
 
 using namespace bf16t;
 
-constexpr int kBlockQ = 8 * kSub;     // queries per workgroup
 constexpr int kKeyTile = kRowTile;    // keys per LDS tile
 constexpr float kRescaleLog2 = 8.0f;  // raise the running max only beyond p = 2^8
 
@@ -123,7 +122,9 @@ __device__ __forceinline__ void half_step(int kb, const uint32_t (&ka)[D / 16],
     }
 }
 
-template <int D>
+// NSUB = 2: 256 queries per workgroup, wave w owns sub-blocks w (0) and 7-w (1).
+// NSUB = 1: 128 queries per workgroup, wave w owns sub-block w (1) (small grids).
+template <int D, int NSUB>
 __global__ __launch_bounds__(kWave* kWaves) void flash_fwd_bf16_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, uint16_t* __restrict__ o, float* __restrict__ m_out,
@@ -136,19 +137,20 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_fwd_bf16_kernel(
     const int half = lane >> 5;
     int bh, blk;
     map_block(blockIdx.x, BH, nblk, true, bh, blk);
-    const int q0 = blk * kBlockQ;
-    const int qj0 = q0 + kSub * wave;        // first query of sub-block w
-    const int qj1 = q0 + kSub * (7 - wave);  // first query of sub-block 7 - w (>= qj0)
+    constexpr int kBlock = kWaves * NSUB * kSub;
+    const int q0 = blk * kBlock;
+    const int qj0 = q0 + kSub * wave;                                     // sub-block 0
+    const int qj1 = NSUB == 2 ? q0 + kSub * (2 * kWaves - 1 - wave) : qj0;  // sub-block 1
     const size_t head_off = static_cast<size_t>(bh) * T * D;
     const uint16_t* kh = k + head_off;
     const uint16_t* vh = v + head_off;
     const float c = scale * kLog2e;
 
     bf16x8 qr0[D / 16], qr1[D / 16];
-    load_rowop<D>(qr0, q + head_off, qj0 + col, T, half);
+    if constexpr (NSUB == 2) load_rowop<D>(qr0, q + head_off, qj0 + col, T, half);
     load_rowop<D>(qr1, q + head_off, qj1 + col, T, half);
 
-    const int kend = min(T, q0 + kBlockQ);
+    const int kend = min(T, q0 + kBlock);
     const int ntile = (kend + kKeyTile - 1) / kKeyTile;
     const uint32_t k_lds = lds_addr(sm.k[0]);
     const uint32_t v_lds = lds_addr(sm.v[0]);
@@ -173,7 +175,7 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_fwd_bf16_kernel(
     // hh < hA, sub-block 7-w for hh < hB; every wave takes part in every tile's barrier and
     // copy.  Three straight loops keep the accumulators out of any control-flow join.
     const int nhalf_t = (T + 31) / 32;
-    const int hA = min(qj0 / 32 + 1, nhalf_t);
+    const int hA = NSUB == 2 ? min(qj0 / 32 + 1, nhalf_t) : 0;
     const int hB = min(qj1 / 32 + 1, nhalf_t);
     const int hend = 2 * ntile;
     uint32_t ka[D / 16], va[D / 32];
@@ -207,7 +209,7 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_fwd_bf16_kernel(
     for (; hh < hend; ++hh) tile_sync(hh);
 
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 2 - NSUB; j < 2; ++j) {
         const SubState<D>& st = j == 0 ? st0 : st1;
         const int qi = (j == 0 ? qj0 : qj1) + col;
         if (qi < T) {
@@ -222,12 +224,22 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_fwd_bf16_kernel(
     }
 }
 
+template <int D, int NSUB>
+void fwd_launch(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o,
+                float* m_out, float* l_out, int BH, int T, float scale, hipStream_t stream) {
+    constexpr int kBlock = kWaves * NSUB * kSub;
+    const int nblk = (T + kBlock - 1) / kBlock;
+    hipLaunchKernelGGL((flash_fwd_bf16_kernel<D, NSUB>), dim3(BH * nblk), dim3(kWave * kWaves),
+                       0, stream, q, k, v, o, m_out, l_out, BH, T, scale, nblk);
+}
+
 template <int D>
 void fwd_dispatch(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o,
                   float* m_out, float* l_out, int BH, int T, float scale, hipStream_t stream) {
-    const int nblk = (T + kBlockQ - 1) / kBlockQ;
-    hipLaunchKernelGGL(flash_fwd_bf16_kernel<D>, dim3(BH * nblk), dim3(kWave * kWaves), 0,
-                       stream, q, k, v, o, m_out, l_out, BH, T, scale, nblk);
+    if (use_single_subblock(BH, T))
+        fwd_launch<D, 1>(q, k, v, o, m_out, l_out, BH, T, scale, stream);
+    else
+        fwd_launch<D, 2>(q, k, v, o, m_out, l_out, BH, T, scale, stream);
 }
 
 }  // namespace

@@ -236,7 +236,8 @@ void fwd_launch(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_
 template <int D>
 void fwd_dispatch(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o,
                   float* m_out, float* l_out, int BH, int T, float scale, hipStream_t stream) {
-    if (use_single_subblock(BH, T))
+    // d = 128: one sub-block per wave fits two waves per SIMD (two sub-blocks do not)
+    if (D >= 128 || use_single_subblock(BH, T))
         fwd_launch<D, 1>(q, k, v, o, m_out, l_out, BH, T, scale, stream);
     else
         fwd_launch<D, 2>(q, k, v, o, m_out, l_out, BH, T, scale, stream);

@@ -26,8 +26,10 @@
 // Stage 2, per 32-query half tile and a wave's 32 keys (d = 64: 18 MFMAs):
 //   S  = Q K^T        A = Q rows,  B = K (VGPRs)
 //   dP = dO V^T       A = dO rows, B = V (VGPRs)
-//   dS = P o (dP - D)              -lse2/c and -D enter S and dP as one more contraction step
-//                                  over a per-row (hi, lo) bf16 chunk (see dkdv_scores)
+//   dS = P o (dP - D)              -lse2 and -D enter S and dP as one more contraction step
+//                                  over a per-row (hi, lo) bf16 chunk (see dkdv_scores); K is
+//                                  held pre-multiplied by c = scale*log2 e, so P = 2^S
+//                                  needs no per-element multiply
 //   dV^T += dO^T P    A = dO^T (transposing reads), B = P
 //   dK^T += Q^T dS    A = Q^T (transposing reads),  B = dS
 // A workgroup owns 128 keys; query tiles start at the workgroup's first key, and wave w
@@ -60,7 +62,7 @@ template <int D>
 struct QgSmem {
     uint16_t q[2][kRowTile * D];
     uint16_t g[2][kRowTile * D];
-    uint16_t qx[2][kRowTile * 8];  // row r: (-lse2/c)_hi, (-lse2/c)_lo, 0 x 6
+    uint16_t qx[2][kRowTile * 8];  // row r: (-lse2)_hi, (-lse2)_lo, 0 x 6
     uint16_t gx[2][kRowTile * 8];  // row r: (-D)_hi, (-D)_lo, 0 x 6
 };
 
@@ -263,10 +265,10 @@ __device__ __forceinline__ uint32_t split_bf16x2(float x) {
     return static_cast<uint32_t>(hi) | (static_cast<uint32_t>(lo) << 16);
 }
 
-// S' = Q K^T - lse2/c and dP' = dO V^T - D of one half tile.  The statistics ride in the
+// S' = Q (cK)^T - lse2 and dP' = dO V^T - D of one half tile.  The statistics ride in the
 // products: a fifth 16-wide contraction step multiplies the row's chunk (hi, lo, 0, ...)
 // by the B operand `one` = (1, 1, 0, ...) (lanes of k-group 1 hold zeros), so that
-// 2^(c*S') = P and P o dP' = dS need no per-row values in VGPRs.
+// 2^S' = P and P o dP' = dS need no per-row values in VGPRs.
 template <int D>
 __device__ __forceinline__ void dkdv_scores(const HalfAddr<D>& a, const bf16x8 (&kr)[D / 16],
                                             const bf16x8 (&vr)[D / 16], const bf16x8& one,
@@ -279,16 +281,16 @@ __device__ __forceinline__ void dkdv_scores(const HalfAddr<D>& a, const bf16x8 (
     for (int st = 0; st < D / 16; ++st) dp = mfma_32x32x16_bf16(lds_b128(a.g[st]), vr[st], dp);
 }
 
-// P = 2^(c*S') (0 where the query precedes the key, on the diagonal half tile) and
+// P = 2^S' (0 where the query precedes the key, on the diagonal half tile) and
 // dS = P o dP'; dV^T += dO^T P, dK^T += Q^T dS.
 template <int D, bool MASK>
 __device__ __forceinline__ void dkdv_update(const HalfAddr<D>& a, f32x16& s, const f32x16& dp,
                                             f32x16 (&dk_acc)[D / 32],
-                                            f32x16 (&dv_acc)[D / 32], int qb, int kj, int half,
-                                            float c) {
+                                            f32x16 (&dv_acc)[D / 32], int qb, int kj,
+                                            int half) {
     constexpr uint32_t RB = Swz<D>::kRowBytes;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) s[r] = exp2_fast(s[r] * c);
+    for (int r = 0; r < 16; ++r) s[r] = exp2_fast(s[r]);
     if constexpr (MASK) {
 #pragma unroll
         for (int r = 0; r < 16; ++r)
@@ -336,7 +338,6 @@ __global__ __launch_bounds__(kWave* NW) void flash_bwd_dkdv_bf16_kernel(
     const uint16_t* qh = q + head_off;
     const uint16_t* gh = dO + head_off;
     const float c = scale * kLog2e;
-    const float inv_c = 1.0f / c;
 
     const int t0 = k0 / kRowTile;
     const int ntile = (T + kRowTile - 1) / kRowTile;
@@ -377,6 +378,12 @@ __global__ __launch_bounds__(kWave* NW) void flash_bwd_dkdv_bf16_kernel(
 
     bf16x8 kr[D / 16], vr[D / 16];
     load_rowop<D>(kr, k + head_off, kj, T, half);
+    // c*K rounded to bf16 (one extra rounding, ~2^-9 relative per element; the score error it
+    // causes is a random sum over d, ~1e-3 in log2 units for unit-variance inputs)
+#pragma unroll
+    for (int st = 0; st < D / 16; ++st)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) kr[st][e] = static_cast<__bf16>(static_cast<float>(kr[st][e]) * c);
     load_rowop<D>(vr, v + head_off, kj, T, half);
     f32x16 dk_acc[D / 32], dv_acc[D / 32];
 #pragma unroll
@@ -386,12 +393,13 @@ __global__ __launch_bounds__(kWave* NW) void flash_bwd_dkdv_bf16_kernel(
     }
     uint32_t roff[D / 16], troff[D / 32];
     lane_offsets<D>(lane, roff, troff);
+    const uint32_t xoff = static_cast<uint32_t>(col * 16);  // statistic chunk of row col
 
     // Tile kt: wait for its copies, publish its statistics, barrier, start the next copy.
     auto tile_sync = [&](int kt) {
         wait_vm<0>();  // this wave's copies (and statistics loads) of tile kt landed
-        if (wave == 0) {  // -lse2/c (-1e30 for padded queries: P = 0) and -D as bf16 pairs
-            const float nl = st_m == -INFINITY ? -1e30f : -(st_m * kLog2e + log2f(st_l)) * inv_c;
+        if (wave == 0) {  // -lse2 (-1e30 for padded queries: P = 0) and -D as bf16 pairs
+            const float nl = st_m == -INFINITY ? -1e30f : -(st_m * kLog2e + log2f(st_l));
             *reinterpret_cast<uint32_t*>(&sm.qx[kt & 1][lane * 8]) = split_bf16x2(nl);
             *reinterpret_cast<uint32_t*>(&sm.gx[kt & 1][lane * 8]) = split_bf16x2(-st_d);
         }
@@ -424,6 +432,38 @@ __global__ __launch_bounds__(kWave* NW) void flash_bwd_dkdv_bf16_kernel(
         a.gx = gx_lds + xrow;
         return a;
     };
+    // The same with the buffer parity and half a compile-time constant: every address is a
+    // lane offset plus an immediate.
+    auto half_addr_c = [&](auto buf, auto hsel) {
+        HalfAddr<D> a;
+        constexpr uint32_t base = static_cast<uint32_t>(decltype(buf)::value) * S::kBytes +
+                                  static_cast<uint32_t>(decltype(hsel)::value) * 32u * RB;
+        constexpr uint32_t xbase = static_cast<uint32_t>(decltype(buf)::value * kRowTile +
+                                                         decltype(hsel)::value * 32) * 16u;
+#pragma unroll
+        for (int st = 0; st < D / 16; ++st) {
+            a.q[st] = roff[st] + (q_lds + base);
+            a.g[st] = roff[st] + (g_lds + base);
+        }
+#pragma unroll
+        for (int dt = 0; dt < D / 32; ++dt) {
+            a.qt[dt] = troff[dt] + (q_lds + base);
+            a.gt[dt] = troff[dt] + (g_lds + base);
+        }
+        a.qx = xoff + (qx_lds + xbase);
+        a.gx = xoff + (gx_lds + xbase);
+        return a;
+    };
+    // Both half tiles of tile kt (held in buffer `buf`), no diagonal.
+    auto pair_c = [&](int kt, auto buf) {
+        const HalfAddr<D> a0 = half_addr_c(buf, std::integral_constant<int, 0>{});
+        const HalfAddr<D> a1 = half_addr_c(buf, std::integral_constant<int, 1>{});
+        f32x16 s0, dp0, s1, dp1;
+        dkdv_scores<D>(a0, kr, vr, one, s0, dp0);
+        dkdv_scores<D>(a1, kr, vr, one, s1, dp1);
+        dkdv_update<D, false>(a0, s0, dp0, dk_acc, dv_acc, 64 * kt, kj, half);
+        dkdv_update<D, false>(a1, s1, dp1, dk_acc, dv_acc, 64 * kt + 32, kj, half);
+    };
     // Both half tiles of tile kt; the first is the diagonal one when MASK0.  The score
     // products of the second half tile are issued before the first half tile's softmax.
     auto pair = [&](int kt, auto mask0) {
@@ -431,9 +471,8 @@ __global__ __launch_bounds__(kWave* NW) void flash_bwd_dkdv_bf16_kernel(
         f32x16 s0, dp0, s1, dp1;
         dkdv_scores<D>(a0, kr, vr, one, s0, dp0);
         dkdv_scores<D>(a1, kr, vr, one, s1, dp1);
-        dkdv_update<D, decltype(mask0)::value>(a0, s0, dp0, dk_acc, dv_acc, 64 * kt, kj, half,
-                                               c);
-        dkdv_update<D, false>(a1, s1, dp1, dk_acc, dv_acc, 64 * kt + 32, kj, half, c);
+        dkdv_update<D, decltype(mask0)::value>(a0, s0, dp0, dk_acc, dv_acc, 64 * kt, kj, half);
+        dkdv_update<D, false>(a1, s1, dp1, dk_acc, dv_acc, 64 * kt + 32, kj, half);
     };
 
     // Half tiles before hstart (= kw/32, the one holding the wave's first key) hold only
@@ -448,15 +487,29 @@ __global__ __launch_bounds__(kWave* NW) void flash_bwd_dkdv_bf16_kernel(
             const HalfAddr<D> a1 = half_addr(hstart);
             f32x16 s1, dp1;
             dkdv_scores<D>(a1, kr, vr, one, s1, dp1);
-            dkdv_update<D, true>(a1, s1, dp1, dk_acc, dv_acc, 32 * hstart, kj, half, c);
+            dkdv_update<D, true>(a1, s1, dp1, dk_acc, dv_acc, 32 * hstart, kj, half);
         } else {
             pair(kt, std::true_type{});
         }
         ++kt;
     }
-    for (; kt < ntile; ++kt) {
+    // Steady state, unrolled by the buffer parity (tile kt is in buffer kt & 1).
+    using B0 = std::integral_constant<int, 0>;
+    using B1 = std::integral_constant<int, 1>;
+    if (kt < ntile && (kt & 1)) {
         tile_sync(kt);
-        pair(kt, std::false_type{});
+        pair_c(kt, B1{});
+        ++kt;
+    }
+    for (; kt + 1 < ntile; kt += 2) {
+        tile_sync(kt);
+        pair_c(kt, B0{});
+        tile_sync(kt + 1);
+        pair_c(kt + 1, B1{});
+    }
+    if (kt < ntile) {
+        tile_sync(kt);
+        pair_c(kt, B0{});
     }
 
     if (kj < T) {

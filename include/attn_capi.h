@@ -204,6 +204,33 @@ int attn_tiled_causal_backward_dkdv_bf16(const attn_bf16* q, const attn_bf16* k,
                                          int B, int H, int T, int d_head, float scale,
                                          hipStream_t stream);
 
+/* ------------------------------------------------------------------------------------------
+ * Packed QKV layout: attention straight from the QKV projection's output.
+ * qkv (B, T, 3*H*d_head) as qkv_split_transpose_forward (include/kernels/attention.cuh:5-11)
+ * reads it; dqkv (B, T, 3*H*d_head) as qkv_split_transpose_backward (:13-19) writes it.  The
+ * split-transpose moves happen inside the attention kernels' tile copies and stores (no
+ * head-major q/k/v/dq/dk/dv buffers).  Results are bitwise those of split-transpose + the
+ * tiled entry points above.  out, o, dO stay head-major (B, H, T, d); stats and workspace as
+ * above.  No counterpart in the reference: a fused form of its
+ * split -> tiled_causal_attention_forward and tiled_causal_attention_backward -> split-back
+ * sequence (src/model.cu:305-311, 609-653).
+ * ------------------------------------------------------------------------------------------ */
+int attn_packed_causal_forward_f32(const float* qkv, float* out, int B, int H, int T,
+                                   int d_head, float scale, float* m_out, float* l_out,
+                                   hipStream_t stream);
+int attn_packed_causal_backward_f32(const float* qkv, const float* o, const float* do_ptr,
+                                    const float* m_ptr, const float* l_ptr, float* dqkv,
+                                    float* d_workspace, int B, int H, int T, int d_head,
+                                    float scale, hipStream_t stream);
+int attn_packed_causal_forward_bf16(const attn_bf16* qkv, attn_bf16* out, int B, int H, int T,
+                                    int d_head, float scale, float* m_out, float* l_out,
+                                    hipStream_t stream);
+int attn_packed_causal_backward_bf16(const attn_bf16* qkv, const attn_bf16* o,
+                                     const attn_bf16* do_ptr, const float* m_ptr,
+                                     const float* l_ptr, attn_bf16* dqkv, float* d_workspace,
+                                     int B, int H, int T, int d_head, float scale,
+                                     hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

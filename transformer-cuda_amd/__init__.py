@@ -56,6 +56,10 @@ SIGNATURES = {
     "attn_matmul_batched_strided_f32":
         [_P, _P, _P, _I, _I, _I, _L, _L, _L, _I, _I, _I, _F, _F, _P],
     "attn_materialized_causal_forward_f32": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P],
+    "attn_packed_causal_forward_f32": [_P, _P, _I, _I, _I, _I, _F, _P, _P, _P],
+    "attn_packed_causal_backward_f32": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P],
+    "attn_packed_causal_forward_bf16": [_P, _P, _I, _I, _I, _I, _F, _P, _P, _P],
+    "attn_packed_causal_backward_bf16": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P],
     "attn_materialized_causal_backward_f32":
         [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P],
     "attn_tiled_causal_forward_f32": [_P, _P, _P, _P, _I, _I, _I, _I, _F, _P, _P, _P],
@@ -269,6 +273,38 @@ def tiled_causal_attention_forward(q, k, v, out, B, H, T, d_head, scale, m_out=N
                _ptr(out, dt, n, "out"), B, H, T, d_head, float(scale),
                _ptr(m_out, f32, r, "m_out"), _ptr(l_out, f32, r, "l_out"), _stream(stream)),
           "tiled_causal_attention_forward")
+
+
+def packed_causal_attention_forward(qkv, out, B, H, T, d_head, scale, m_out=None,
+                                    l_out=None, stream=None):
+    """Attention straight from the QKV projection's packed output qkv (B, T, 3*H*d): the
+    split-transpose (include/kernels/attention.cuh:5-11) happens in the kernels' tile
+    copies.  out (B, H, T, d); fp32 or bf16 by the tensors' dtype."""
+    torch = _torch()
+    bf = qkv.dtype == torch.bfloat16
+    n = B * H * T * d_head
+    r = B * H * T
+    dt, f32 = _dt(bf), _dt(False)
+    name = "attn_packed_causal_forward_" + ("bf16" if bf else "f32")
+    check(call(name, _ptr(qkv, dt, 3 * n, "qkv"), _ptr(out, dt, n, "out"), B, H, T, d_head,
+               float(scale), _ptr(m_out, f32, r, "m_out"), _ptr(l_out, f32, r, "l_out"),
+               _stream(stream)), "packed_causal_attention_forward")
+
+
+def packed_causal_attention_backward(qkv, o, dO, m, l, dqkv, workspace, B, H, T, d_head, scale,
+                                     stream=None):
+    """Backward from the packed qkv, writing dq, dk, dv straight into dqkv (B, T, 3*H*d), the
+    layout qkv_split_transpose_backward (include/kernels/attention.cuh:13-19) produces."""
+    torch = _torch()
+    bf = qkv.dtype == torch.bfloat16
+    n = B * H * T * d_head
+    r = B * H * T
+    dt, f32 = _dt(bf), _dt(False)
+    name = "attn_packed_causal_backward_" + ("bf16" if bf else "f32")
+    check(call(name, _ptr(qkv, dt, 3 * n, "qkv"), _ptr(o, dt, n, "o"), _ptr(dO, dt, n, "dO"),
+               _ptr(m, f32, r, "m"), _ptr(l, f32, r, "l"), _ptr(dqkv, dt, 3 * n, "dqkv"),
+               _ptr(workspace, f32, r, "workspace"), B, H, T, d_head, float(scale),
+               _stream(stream)), "packed_causal_attention_backward")
 
 
 def attention_precompute_dot_do_o(dO, O, D, B, H, T, d_head, stream=None):

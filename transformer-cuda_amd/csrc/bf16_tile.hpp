@@ -47,14 +47,15 @@ struct Swz {
     }
 };
 
-// Wave `wave` of NW issues its share of the copy of rows [row0, row0 + 64) of a (T, D) bf16
-// head into the tile at LDS byte address lds.  Rows past T are read from row T-1 (finite
-// values; every consumer masks or zero-weights them).
+// Wave `wave` of NW issues its share of the copy of rows [row0, row0 + 64) of a head (T rows
+// of D bf16, consecutive rows rs elements apart) into the tile at LDS byte address lds.
+// Rows past T are read from row T-1 (finite values; every consumer masks or zero-weights
+// them).
 template <int D, int NW = kWaves>
 __device__ __forceinline__ void dma_tile(const uint16_t* __restrict__ head, int row0, int T,
-                                         uint32_t lds, int wave, int lane) {
+                                         uint32_t lds, int wave, int lane, int rs) {
     using S = Swz<D>;
-    const uint16_t* base = head + static_cast<size_t>(row0) * D;
+    const uint16_t* base = head + static_cast<size_t>(row0) * rs;
 #pragma unroll
     for (int i = wave; i < S::kDma; i += NW) {
         const int p = i * kWave + lane;  // 16-byte slot of the tile
@@ -62,21 +63,21 @@ __device__ __forceinline__ void dma_tile(const uint16_t* __restrict__ head, int 
         const int c = (p % S::kCpr) ^ S::swz(r);
         const int gr = min(r, T - 1 - row0);
         dma_dwordx4(base, lds + static_cast<uint32_t>(i * 1024),
-                    static_cast<uint32_t>(gr * S::kRowBytes + c * 16));
+                    static_cast<uint32_t>(gr * rs * 2 + c * 16));
     }
 }
 
 // Lane (col, half) loads row `row` as a B operand over the head dimension:
-// dst[s] = row[16s + 8*half .. +8], zeros if row >= T.
+// dst[s] = row[16s + 8*half .. +8], zeros if row >= T (rows rs elements apart).
 template <int D>
 __device__ __forceinline__ void load_rowop(bf16x8 (&dst)[D / 16],
                                           const uint16_t* __restrict__ head, int row, int T,
-                                          int half) {
+                                          int half, int rs) {
 #pragma unroll
     for (int s = 0; s < D / 16; ++s) {
         u16x8 x = u16x8{};
         if (row < T)
-            x = *reinterpret_cast<const u16x8*>(head + static_cast<size_t>(row) * D + 16 * s +
+            x = *reinterpret_cast<const u16x8*>(head + static_cast<size_t>(row) * rs + 16 * s +
                                                 8 * half);
         dst[s] = __builtin_bit_cast(bf16x8, x);
     }
@@ -91,11 +92,11 @@ __device__ __forceinline__ bf16x8 pack_b(const f32x16& x, int u) {
 }
 
 // Store a (D x 32) transposed accumulator (acc[dt][v] = element (row, dt*32 +
-// acc_row(v, half))) of a row-major (T, D) bf16 tensor, times mul.
+// acc_row(v, half))) of a head (rows rs elements apart) in bf16, times mul.
 template <int D>
 __device__ __forceinline__ void store_row(uint16_t* __restrict__ head, int row, int half,
-                                          const f32x16 (&acc)[D / 32], float mul) {
-    uint16_t* p = head + static_cast<size_t>(row) * D + 4 * half;
+                                          const f32x16 (&acc)[D / 32], float mul, int rs) {
+    uint16_t* p = head + static_cast<size_t>(row) * rs + 4 * half;
 #pragma unroll
     for (int dt = 0; dt < D / 32; ++dt) {
 #pragma unroll

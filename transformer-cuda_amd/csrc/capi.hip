@@ -279,7 +279,9 @@ int attn_tiled_causal_forward_f32(const float* q, const float* k, const float* v
     if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out))
         return ATTN_ERROR_MISALIGNED;
     clear_error();
-    tcamd::launch_flash_fwd_f32(q, k, v, out, m_out, l_out, B * H, T, d_head, scale, stream);
+    const tcamd::HeadView hm = tcamd::head_major_view(H, T, d_head);
+    tcamd::launch_flash_fwd_f32(q, k, v, out, m_out, l_out, B * H, T, d_head, scale, hm, hm,
+                                stream);
     return launch_status();
 }
 
@@ -307,8 +309,9 @@ int attn_tiled_causal_backward_dq_f32(const float* q, const float* k, const floa
         !aligned16(do_ptr) || !aligned16(dq))
         return ATTN_ERROR_MISALIGNED;
     clear_error();
+    const tcamd::HeadView hm = tcamd::head_major_view(H, T, d_head);
     tcamd::launch_flash_bwd_dq_f32(q, k, v, o, do_ptr, m_ptr, l_ptr, dq, d_workspace, B * H, T,
-                                   d_head, scale, stream);
+                                   d_head, scale, hm, hm, hm, stream);
     return launch_status();
 }
 
@@ -326,8 +329,9 @@ int attn_tiled_causal_backward_dkdv_f32(const float* q, const float* k, const fl
         !aligned16(dk) || !aligned16(dv))
         return ATTN_ERROR_MISALIGNED;
     clear_error();
+    const tcamd::HeadView hm = tcamd::head_major_view(H, T, d_head);
     tcamd::launch_flash_bwd_dkdv_f32(q, k, v, do_ptr, m_ptr, l_ptr, d_workspace, dk, dv, B * H,
-                                     T, d_head, scale, stream);
+                                     T, d_head, scale, hm, hm, hm, stream);
     return launch_status();
 }
 
@@ -359,7 +363,9 @@ int attn_tiled_causal_forward_bf16(const attn_bf16* q, const attn_bf16* k, const
     if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out))
         return ATTN_ERROR_MISALIGNED;
     clear_error();
-    tcamd::launch_flash_fwd_bf16(q, k, v, out, m_out, l_out, B * H, T, d_head, scale, stream);
+    const tcamd::HeadView hm = tcamd::head_major_view(H, T, d_head);
+    tcamd::launch_flash_fwd_bf16(q, k, v, out, m_out, l_out, B * H, T, d_head, scale, hm, hm,
+                                 stream);
     return launch_status();
 }
 
@@ -378,8 +384,9 @@ int attn_tiled_causal_backward_dq_bf16(const attn_bf16* q, const attn_bf16* k,
         !aligned16(do_ptr) || !aligned16(dq))
         return ATTN_ERROR_MISALIGNED;
     clear_error();
+    const tcamd::HeadView hm = tcamd::head_major_view(H, T, d_head);
     tcamd::launch_flash_bwd_dq_bf16(q, k, v, o, do_ptr, m_ptr, l_ptr, dq, d_workspace, B * H,
-                                    T, d_head, scale, stream);
+                                    T, d_head, scale, hm, hm, hm, stream);
     return launch_status();
 }
 
@@ -398,8 +405,9 @@ int attn_tiled_causal_backward_dkdv_bf16(const attn_bf16* q, const attn_bf16* k,
         !aligned16(dk) || !aligned16(dv))
         return ATTN_ERROR_MISALIGNED;
     clear_error();
+    const tcamd::HeadView hm = tcamd::head_major_view(H, T, d_head);
     tcamd::launch_flash_bwd_dkdv_bf16(q, k, v, do_ptr, m_ptr, l_ptr, d_workspace, dk, dv,
-                                      B * H, T, d_head, scale, stream);
+                                      B * H, T, d_head, scale, hm, hm, hm, stream);
     return launch_status();
 }
 
@@ -417,6 +425,87 @@ int attn_tiled_causal_backward_bf16(const attn_bf16* q, const attn_bf16* k,
     if (st != ATTN_SUCCESS) return st;
     return attn_tiled_causal_backward_dkdv_bf16(q, k, v, do_ptr, m_ptr, l_ptr, d_workspace, dk,
                                                 dv, B, H, T, d_head, scale, stream);
+}
+
+// ---- packed QKV layout (split-transpose fused into the attention kernels) --------------
+
+int attn_packed_causal_forward_f32(const float* qkv, float* out, int B, int H, int T,
+                                   int d_head, float scale, float* m_out, float* l_out,
+                                   hipStream_t stream) {
+    if (qkv == nullptr || out == nullptr) return ATTN_ERROR_NULL_POINTER;
+    const int st = check_tiled(B, H, T, d_head, scale);
+    if (st != ATTN_SUCCESS) return st;
+    if (!aligned16(qkv) || !aligned16(out)) return ATTN_ERROR_MISALIGNED;
+    const size_t C = static_cast<size_t>(H) * d_head;
+    const tcamd::HeadView xv = tcamd::packed_qkv_view(H, T, d_head);
+    const tcamd::HeadView hm = tcamd::head_major_view(H, T, d_head);
+    clear_error();
+    tcamd::launch_flash_fwd_f32(qkv, qkv + C, qkv + 2 * C, out, m_out, l_out, B * H, T, d_head,
+                                scale, xv, hm, stream);
+    return launch_status();
+}
+
+int attn_packed_causal_backward_f32(const float* qkv, const float* o, const float* do_ptr,
+                                    const float* m_ptr, const float* l_ptr, float* dqkv,
+                                    float* d_workspace, int B, int H, int T, int d_head,
+                                    float scale, hipStream_t stream) {
+    if (qkv == nullptr || o == nullptr || do_ptr == nullptr || m_ptr == nullptr ||
+        l_ptr == nullptr || dqkv == nullptr || d_workspace == nullptr)
+        return ATTN_ERROR_NULL_POINTER;
+    const int st = check_tiled(B, H, T, d_head, scale);
+    if (st != ATTN_SUCCESS) return st;
+    if (!aligned16(qkv) || !aligned16(o) || !aligned16(do_ptr) || !aligned16(dqkv))
+        return ATTN_ERROR_MISALIGNED;
+    const size_t C = static_cast<size_t>(H) * d_head;
+    const tcamd::HeadView xv = tcamd::packed_qkv_view(H, T, d_head);
+    const tcamd::HeadView hm = tcamd::head_major_view(H, T, d_head);
+    clear_error();
+    tcamd::launch_flash_bwd_dq_f32(qkv, qkv + C, qkv + 2 * C, o, do_ptr, m_ptr, l_ptr, dqkv,
+                                   d_workspace, B * H, T, d_head, scale, xv, hm, xv, stream);
+    tcamd::launch_flash_bwd_dkdv_f32(qkv, qkv + C, qkv + 2 * C, do_ptr, m_ptr, l_ptr,
+                                     d_workspace, dqkv + C, dqkv + 2 * C, B * H, T, d_head,
+                                     scale, xv, hm, xv, stream);
+    return launch_status();
+}
+
+int attn_packed_causal_forward_bf16(const attn_bf16* qkv, attn_bf16* out, int B, int H, int T,
+                                    int d_head, float scale, float* m_out, float* l_out,
+                                    hipStream_t stream) {
+    if (qkv == nullptr || out == nullptr) return ATTN_ERROR_NULL_POINTER;
+    const int st = check_tiled(B, H, T, d_head, scale);
+    if (st != ATTN_SUCCESS) return st;
+    if (!aligned16(qkv) || !aligned16(out)) return ATTN_ERROR_MISALIGNED;
+    const size_t C = static_cast<size_t>(H) * d_head;
+    const tcamd::HeadView xv = tcamd::packed_qkv_view(H, T, d_head);
+    const tcamd::HeadView hm = tcamd::head_major_view(H, T, d_head);
+    clear_error();
+    tcamd::launch_flash_fwd_bf16(qkv, qkv + C, qkv + 2 * C, out, m_out, l_out, B * H, T, d_head,
+                                 scale, xv, hm, stream);
+    return launch_status();
+}
+
+int attn_packed_causal_backward_bf16(const attn_bf16* qkv, const attn_bf16* o,
+                                     const attn_bf16* do_ptr, const float* m_ptr,
+                                     const float* l_ptr, attn_bf16* dqkv, float* d_workspace,
+                                     int B, int H, int T, int d_head, float scale,
+                                     hipStream_t stream) {
+    if (qkv == nullptr || o == nullptr || do_ptr == nullptr || m_ptr == nullptr ||
+        l_ptr == nullptr || dqkv == nullptr || d_workspace == nullptr)
+        return ATTN_ERROR_NULL_POINTER;
+    const int st = check_tiled(B, H, T, d_head, scale);
+    if (st != ATTN_SUCCESS) return st;
+    if (!aligned16(qkv) || !aligned16(o) || !aligned16(do_ptr) || !aligned16(dqkv))
+        return ATTN_ERROR_MISALIGNED;
+    const size_t C = static_cast<size_t>(H) * d_head;
+    const tcamd::HeadView xv = tcamd::packed_qkv_view(H, T, d_head);
+    const tcamd::HeadView hm = tcamd::head_major_view(H, T, d_head);
+    clear_error();
+    tcamd::launch_flash_bwd_dq_bf16(qkv, qkv + C, qkv + 2 * C, o, do_ptr, m_ptr, l_ptr, dqkv,
+                                    d_workspace, B * H, T, d_head, scale, xv, hm, xv, stream);
+    tcamd::launch_flash_bwd_dkdv_bf16(qkv, qkv + C, qkv + 2 * C, do_ptr, m_ptr, l_ptr,
+                                      d_workspace, dqkv + C, dqkv + 2 * C, B * H, T, d_head,
+                                      scale, xv, hm, xv, stream);
+    return launch_status();
 }
 
 }  // extern "C"

@@ -53,6 +53,26 @@ __device__ __forceinline__ float xhalf_sum(float x) {
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// Where head bh = b*H + h of a (B, H, T, d) operand lives: element (t, e) is at
+// off(bh) + t*row + e.  Head-major tensors (B, H, T, d): batch = H*T*d, head = T*d, row = d.
+// The packed QKV layout (B, T, 3*H*d), pointer advanced to the q, k or v column block:
+// batch = 3*H*T*d, head = d, row = 3*H*d.
+struct HeadView {
+    long long batch;
+    long long head;
+    int row;
+    int H;
+    __device__ __forceinline__ size_t off(int bh) const {
+        return static_cast<size_t>((bh / H) * batch + (bh % H) * head);
+    }
+};
+inline HeadView head_major_view(int H, int T, int d) {
+    return HeadView{static_cast<long long>(H) * T * d, static_cast<long long>(T) * d, d, H};
+}
+inline HeadView packed_qkv_view(int H, int T, int d) {
+    return HeadView{3LL * H * T * d, d, 3 * H * d, H};
+}
+
 // fp32 -> bf16 bits, round to nearest even (v_cvt_pk_bf16_f32 on gfx950).
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float x) {
     __bf16 h = static_cast<__bf16>(x);

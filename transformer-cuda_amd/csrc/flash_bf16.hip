@@ -80,17 +80,18 @@ struct DqSub {
     float dlt;           // D = rowsum(dO * O)
 };
 
+// qh: this head's q (rows xrs apart); oh, gh: its o and dO (rows ors apart).
 template <int D>
-__device__ __forceinline__ void dq_init(DqSub<D>& sb, const uint16_t* __restrict__ q,
-                                        const uint16_t* __restrict__ o,
-                                        const uint16_t* __restrict__ dO,
+__device__ __forceinline__ void dq_init(DqSub<D>& sb, const uint16_t* __restrict__ qh,
+                                        const uint16_t* __restrict__ oh,
+                                        const uint16_t* __restrict__ gh,
                                         const float* __restrict__ m, const float* __restrict__ l,
-                                        float* __restrict__ Dws, size_t head_off,
+                                        float* __restrict__ Dws, int xrs, int ors,
                                         size_t stat_off, int qi, int T, int half) {
-    load_rowop<D>(sb.q, q + head_off, qi, T, half);
-    load_rowop<D>(sb.g, dO + head_off, qi, T, half);
+    load_rowop<D>(sb.q, qh, qi, T, half, xrs);
+    load_rowop<D>(sb.g, gh, qi, T, half, ors);
     bf16x8 orow[D / 16];
-    load_rowop<D>(orow, o + head_off, qi, T, half);
+    load_rowop<D>(orow, oh, qi, T, half, ors);
     float part = 0.0f;
 #pragma unroll
     for (int j = 0; j < D / 16; ++j) {
@@ -170,7 +171,8 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_bwd_dq_bf16_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, const uint16_t* __restrict__ o,
     const uint16_t* __restrict__ dO, const float* __restrict__ m, const float* __restrict__ l,
-    uint16_t* __restrict__ dq, float* __restrict__ Dws, int BH, int T, float scale, int nblk) {
+    uint16_t* __restrict__ dq, float* __restrict__ Dws, int BH, int T, float scale, int nblk,
+    HeadView xv, HeadView ov, HeadView gv) {
     using S = Swz<D>;
     constexpr int kBlock = kWaves * NSUB * kSub;
     __shared__ __attribute__((aligned(1024))) KvSmem<D> sm;
@@ -183,23 +185,26 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_bwd_dq_bf16_kernel(
     const int q0 = blk * kBlock;
     const int qj0 = q0 + kSub * wave;
     const int qj1 = NSUB == 2 ? q0 + kSub * (2 * kWaves - 1 - wave) : qj0;
-    const size_t head_off = static_cast<size_t>(bh) * T * D;
+    const size_t xoff = xv.off(bh), ooff = ov.off(bh), goff = gv.off(bh);
+    const int xrs = xv.row, ors = ov.row, grs = gv.row;
     const size_t stat_off = static_cast<size_t>(bh) * T;
-    const uint16_t* kh = k + head_off;
-    const uint16_t* vh = v + head_off;
+    const uint16_t* kh = k + xoff;
+    const uint16_t* vh = v + xoff;
     const float c = scale * kLog2e;
 
     const int kend = min(T, q0 + kBlock);
     const int ntile = (kend + kRowTile - 1) / kRowTile;
     const uint32_t k_lds = lds_addr(sm.k[0]);
     const uint32_t v_lds = lds_addr(sm.v[0]);
-    dma_tile<D>(kh, 0, T, k_lds, wave, lane);
-    dma_tile<D>(vh, 0, T, v_lds, wave, lane);
+    dma_tile<D>(kh, 0, T, k_lds, wave, lane, xrs);
+    dma_tile<D>(vh, 0, T, v_lds, wave, lane, xrs);
 
     DqSub<D> sb0, sb1;
-    dq_init<D>(sb1, q, o, dO, m, l, Dws, head_off, stat_off, qj1 + col, T, half);
+    dq_init<D>(sb1, q + xoff, o + ooff, dO + ooff, m, l, Dws, xrs, ors, stat_off, qj1 + col, T,
+               half);
     if constexpr (NSUB == 2)
-        dq_init<D>(sb0, q, o, dO, m, l, Dws, head_off, stat_off, qj0 + col, T, half);
+        dq_init<D>(sb0, q + xoff, o + ooff, dO + ooff, m, l, Dws, xrs, ors, stat_off, qj0 + col,
+                   T, half);
 
     uint32_t roff[D / 16], troff[D / 32];
     lane_offsets<D>(lane, roff, troff);
@@ -216,8 +221,8 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_bwd_dq_bf16_kernel(
             __syncthreads();  // ... and every wave's; tile kt-1 is no longer read by anyone
             if (kt + 1 < ntile) {
                 const uint32_t nbuf = static_cast<uint32_t>((kt + 1) & 1) * S::kBytes;
-                dma_tile<D>(kh, (kt + 1) * kRowTile, T, k_lds + nbuf, wave, lane);
-                dma_tile<D>(vh, (kt + 1) * kRowTile, T, v_lds + nbuf, wave, lane);
+                dma_tile<D>(kh, (kt + 1) * kRowTile, T, k_lds + nbuf, wave, lane, xrs);
+                dma_tile<D>(vh, (kt + 1) * kRowTile, T, v_lds + nbuf, wave, lane, xrs);
             }
         }
         const uint32_t base = static_cast<uint32_t>(kt & 1) * S::kBytes +
@@ -241,9 +246,9 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_bwd_dq_bf16_kernel(
     }
     for (; hh < hend; ++hh) tile_sync(hh);
 
-    if (qj1 + col < T) store_row<D>(dq + head_off, qj1 + col, half, sb1.acc, scale);
+    if (qj1 + col < T) store_row<D>(dq + goff, qj1 + col, half, sb1.acc, scale, grs);
     if constexpr (NSUB == 2)
-        if (qj0 + col < T) store_row<D>(dq + head_off, qj0 + col, half, sb0.acc, scale);
+        if (qj0 + col < T) store_row<D>(dq + goff, qj0 + col, half, sb0.acc, scale, grs);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -319,7 +324,7 @@ __global__ __launch_bounds__(kWave* NW) void flash_bwd_dkdv_bf16_kernel(
     const uint16_t* __restrict__ v, const uint16_t* __restrict__ dO,
     const float* __restrict__ m, const float* __restrict__ l, const float* __restrict__ Dws,
     uint16_t* __restrict__ dk, uint16_t* __restrict__ dv, int BH, int T, float scale,
-    int nblk) {
+    int nblk, HeadView xv, HeadView ov, HeadView gv) {
     using S = Swz<D>;
     constexpr int kBlock = NW * kSub;  // keys per workgroup
     constexpr uint32_t RB = S::kRowBytes;
@@ -333,10 +338,11 @@ __global__ __launch_bounds__(kWave* NW) void flash_bwd_dkdv_bf16_kernel(
     const int k0 = blk * kBlock;
     const int kw = k0 + kSub * wave;
     const int kj = kw + col;
-    const size_t head_off = static_cast<size_t>(bh) * T * D;
+    const size_t xoff = xv.off(bh), ooff = ov.off(bh), goff = gv.off(bh);
+    const int xrs = xv.row, ors = ov.row, grs = gv.row;
     const size_t stat_off = static_cast<size_t>(bh) * T;
-    const uint16_t* qh = q + head_off;
-    const uint16_t* gh = dO + head_off;
+    const uint16_t* qh = q + xoff;
+    const uint16_t* gh = dO + ooff;
     const float c = scale * kLog2e;
 
     const int t0 = k0 / kRowTile;
@@ -345,8 +351,8 @@ __global__ __launch_bounds__(kWave* NW) void flash_bwd_dkdv_bf16_kernel(
     const uint32_t g_lds = lds_addr(sm.g[0]);
     const uint32_t qx_lds = lds_addr(sm.qx[0]);
     const uint32_t gx_lds = lds_addr(sm.gx[0]);
-    dma_tile<D, NW>(qh, t0 * kRowTile, T, q_lds, wave, lane);
-    dma_tile<D, NW>(gh, t0 * kRowTile, T, g_lds, wave, lane);
+    dma_tile<D, NW>(qh, t0 * kRowTile, T, q_lds, wave, lane, xrs);
+    dma_tile<D, NW>(gh, t0 * kRowTile, T, g_lds, wave, lane, ors);
     // Wave 0 stages the statistics of a tile through VGPRs: lane i holds query 64t + i.
     float st_m = 0.0f, st_l = 1.0f, st_d = 0.0f;
     auto load_stats = [&](int t) {
@@ -377,14 +383,14 @@ __global__ __launch_bounds__(kWave* NW) void flash_bwd_dkdv_bf16_kernel(
     }
 
     bf16x8 kr[D / 16], vr[D / 16];
-    load_rowop<D>(kr, k + head_off, kj, T, half);
+    load_rowop<D>(kr, k + xoff, kj, T, half, xrs);
     // c*K rounded to bf16 (one extra rounding, ~2^-9 relative per element; the score error it
     // causes is a random sum over d, ~1e-3 in log2 units for unit-variance inputs)
 #pragma unroll
     for (int st = 0; st < D / 16; ++st)
 #pragma unroll
         for (int e = 0; e < 8; ++e) kr[st][e] = static_cast<__bf16>(static_cast<float>(kr[st][e]) * c);
-    load_rowop<D>(vr, v + head_off, kj, T, half);
+    load_rowop<D>(vr, v + xoff, kj, T, half, xrs);
     f32x16 dk_acc[D / 32], dv_acc[D / 32];
 #pragma unroll
     for (int dt = 0; dt < D / 32; ++dt) {
@@ -393,7 +399,7 @@ __global__ __launch_bounds__(kWave* NW) void flash_bwd_dkdv_bf16_kernel(
     }
     uint32_t roff[D / 16], troff[D / 32];
     lane_offsets<D>(lane, roff, troff);
-    const uint32_t xoff = static_cast<uint32_t>(col * 16);  // statistic chunk of row col
+    const uint32_t soff = static_cast<uint32_t>(col * 16);  // statistic chunk of row col
 
     // Tile kt: wait for its copies, publish its statistics, barrier, start the next copy.
     auto tile_sync = [&](int kt) {
@@ -407,8 +413,8 @@ __global__ __launch_bounds__(kWave* NW) void flash_bwd_dkdv_bf16_kernel(
         if (kt + 1 < ntile) {
             if (wave == 0) load_stats(kt + 1);
             const uint32_t nbuf = static_cast<uint32_t>((kt + 1) & 1) * S::kBytes;
-            dma_tile<D, NW>(qh, (kt + 1) * kRowTile, T, q_lds + nbuf, wave, lane);
-            dma_tile<D, NW>(gh, (kt + 1) * kRowTile, T, g_lds + nbuf, wave, lane);
+            dma_tile<D, NW>(qh, (kt + 1) * kRowTile, T, q_lds + nbuf, wave, lane, xrs);
+            dma_tile<D, NW>(gh, (kt + 1) * kRowTile, T, g_lds + nbuf, wave, lane, ors);
         }
     };
     // Operand addresses of half tile hh (queries 32*hh ..).
@@ -450,8 +456,8 @@ __global__ __launch_bounds__(kWave* NW) void flash_bwd_dkdv_bf16_kernel(
             a.qt[dt] = troff[dt] + (q_lds + base);
             a.gt[dt] = troff[dt] + (g_lds + base);
         }
-        a.qx = xoff + (qx_lds + xbase);
-        a.gx = xoff + (gx_lds + xbase);
+        a.qx = soff + (qx_lds + xbase);
+        a.gx = soff + (gx_lds + xbase);
         return a;
     };
     // Both half tiles of tile kt (held in buffer `buf`), no diagonal.
@@ -513,42 +519,46 @@ __global__ __launch_bounds__(kWave* NW) void flash_bwd_dkdv_bf16_kernel(
     }
 
     if (kj < T) {
-        store_row<D>(dk + head_off, kj, half, dk_acc, scale);
-        store_row<D>(dv + head_off, kj, half, dv_acc, 1.0f);
+        store_row<D>(dk + goff, kj, half, dk_acc, scale, grs);
+        store_row<D>(dv + goff, kj, half, dv_acc, 1.0f, grs);
     }
 }
 
 template <int D, int NSUB>
 void dq_launch(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* o,
                const uint16_t* dO, const float* m, const float* l, uint16_t* dq, float* Dws,
-               int BH, int T, float scale, hipStream_t stream) {
+               int BH, int T, float scale, const HeadView& xv, const HeadView& ov,
+               const HeadView& gv, hipStream_t stream) {
     constexpr int kBlock = kWaves * NSUB * kSub;
     const int nblk = (T + kBlock - 1) / kBlock;
     hipLaunchKernelGGL((flash_bwd_dq_bf16_kernel<D, NSUB>), dim3(BH * nblk),
                        dim3(kWave * kWaves), 0, stream, q, k, v, o, dO, m, l, dq, Dws, BH, T,
-                       scale, nblk);
+                       scale, nblk, xv, ov, gv);
 }
 
 template <int D>
 void dq_dispatch(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* o,
                  const uint16_t* dO, const float* m, const float* l, uint16_t* dq, float* Dws,
-                 int BH, int T, float scale, hipStream_t stream) {
+                 int BH, int T, float scale, const HeadView& xv, const HeadView& ov,
+                 const HeadView& gv, hipStream_t stream) {
     // d = 128 holds one sub-block per wave (registers)
     if (D >= 128 || use_single_subblock(BH, T))
-        dq_launch<D, 1>(q, k, v, o, dO, m, l, dq, Dws, BH, T, scale, stream);
+        dq_launch<D, 1>(q, k, v, o, dO, m, l, dq, Dws, BH, T, scale, xv, ov, gv, stream);
     else
-        dq_launch<D, (D >= 128 ? 1 : 2)>(q, k, v, o, dO, m, l, dq, Dws, BH, T, scale, stream);
+        dq_launch<D, (D >= 128 ? 1 : 2)>(q, k, v, o, dO, m, l, dq, Dws, BH, T, scale, xv, ov, gv,
+                                         stream);
 }
 
 template <int D>
 void dkdv_dispatch(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* dO,
                    const float* m, const float* l, const float* Dws, uint16_t* dk, uint16_t* dv,
-                   int BH, int T, float scale, hipStream_t stream) {
+                   int BH, int T, float scale, const HeadView& xv, const HeadView& ov,
+                   const HeadView& gv, hipStream_t stream) {
     constexpr int NW = kWaves;
     constexpr int kBlock = NW * kSub;
     const int nblk = (T + kBlock - 1) / kBlock;
     hipLaunchKernelGGL((flash_bwd_dkdv_bf16_kernel<D, NW>), dim3(BH * nblk), dim3(kWave * NW), 0,
-                       stream, q, k, v, dO, m, l, Dws, dk, dv, BH, T, scale, nblk);
+                       stream, q, k, v, dO, m, l, Dws, dk, dv, BH, T, scale, nblk, xv, ov, gv);
 }
 
 }  // namespace
@@ -556,22 +566,24 @@ void dkdv_dispatch(const uint16_t* q, const uint16_t* k, const uint16_t* v, cons
 void launch_flash_bwd_dq_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                               const uint16_t* o, const uint16_t* dO, const float* m,
                               const float* l, uint16_t* dq, float* Dws, int BH, int T, int d,
-                              float scale, hipStream_t stream) {
+                              float scale, const HeadView& xv, const HeadView& ov,
+                              const HeadView& gv, hipStream_t stream) {
     switch (d) {
-        case 32: dq_dispatch<32>(q, k, v, o, dO, m, l, dq, Dws, BH, T, scale, stream); break;
-        case 64: dq_dispatch<64>(q, k, v, o, dO, m, l, dq, Dws, BH, T, scale, stream); break;
-        default: dq_dispatch<128>(q, k, v, o, dO, m, l, dq, Dws, BH, T, scale, stream); break;
+        case 32: dq_dispatch<32>(q, k, v, o, dO, m, l, dq, Dws, BH, T, scale, xv, ov, gv, stream); break;
+        case 64: dq_dispatch<64>(q, k, v, o, dO, m, l, dq, Dws, BH, T, scale, xv, ov, gv, stream); break;
+        default: dq_dispatch<128>(q, k, v, o, dO, m, l, dq, Dws, BH, T, scale, xv, ov, gv, stream); break;
     }
 }
 
 void launch_flash_bwd_dkdv_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                                 const uint16_t* dO, const float* m, const float* l,
                                 const float* Dws, uint16_t* dk, uint16_t* dv, int BH, int T,
-                                int d, float scale, hipStream_t stream) {
+                                int d, float scale, const HeadView& xv, const HeadView& ov,
+                                const HeadView& gv, hipStream_t stream) {
     switch (d) {
-        case 32: dkdv_dispatch<32>(q, k, v, dO, m, l, Dws, dk, dv, BH, T, scale, stream); break;
-        case 64: dkdv_dispatch<64>(q, k, v, dO, m, l, Dws, dk, dv, BH, T, scale, stream); break;
-        default: dkdv_dispatch<128>(q, k, v, dO, m, l, Dws, dk, dv, BH, T, scale, stream); break;
+        case 32: dkdv_dispatch<32>(q, k, v, dO, m, l, Dws, dk, dv, BH, T, scale, xv, ov, gv, stream); break;
+        case 64: dkdv_dispatch<64>(q, k, v, dO, m, l, Dws, dk, dv, BH, T, scale, xv, ov, gv, stream); break;
+        default: dkdv_dispatch<128>(q, k, v, dO, m, l, Dws, dk, dv, BH, T, scale, xv, ov, gv, stream); break;
     }
 }
 

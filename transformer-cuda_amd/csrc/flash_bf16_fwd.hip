@@ -128,7 +128,8 @@ template <int D, int NSUB>
 __global__ __launch_bounds__(kWave* kWaves) void flash_fwd_bf16_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, uint16_t* __restrict__ o, float* __restrict__ m_out,
-    float* __restrict__ l_out, int BH, int T, float scale, int nblk) {
+    float* __restrict__ l_out, int BH, int T, float scale, int nblk, HeadView xv,
+    HeadView ov) {
     using S = Swz<D>;
     __shared__ __attribute__((aligned(1024))) FwdSmem<D> sm;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
@@ -141,21 +142,22 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_fwd_bf16_kernel(
     const int q0 = blk * kBlock;
     const int qj0 = q0 + kSub * wave;                                     // sub-block 0
     const int qj1 = NSUB == 2 ? q0 + kSub * (2 * kWaves - 1 - wave) : qj0;  // sub-block 1
-    const size_t head_off = static_cast<size_t>(bh) * T * D;
-    const uint16_t* kh = k + head_off;
-    const uint16_t* vh = v + head_off;
+    const size_t xoff = xv.off(bh), ooff = ov.off(bh);  // q, k, v head / o head
+    const int xrs = xv.row, ors = ov.row;
+    const uint16_t* kh = k + xoff;
+    const uint16_t* vh = v + xoff;
     const float c = scale * kLog2e;
 
     bf16x8 qr0[D / 16], qr1[D / 16];
-    if constexpr (NSUB == 2) load_rowop<D>(qr0, q + head_off, qj0 + col, T, half);
-    load_rowop<D>(qr1, q + head_off, qj1 + col, T, half);
+    if constexpr (NSUB == 2) load_rowop<D>(qr0, q + xoff, qj0 + col, T, half, xrs);
+    load_rowop<D>(qr1, q + xoff, qj1 + col, T, half, xrs);
 
     const int kend = min(T, q0 + kBlock);
     const int ntile = (kend + kKeyTile - 1) / kKeyTile;
     const uint32_t k_lds = lds_addr(sm.k[0]);
     const uint32_t v_lds = lds_addr(sm.v[0]);
-    dma_tile<D>(kh, 0, T, k_lds, wave, lane);
-    dma_tile<D>(vh, 0, T, v_lds, wave, lane);
+    dma_tile<D>(kh, 0, T, k_lds, wave, lane, xrs);
+    dma_tile<D>(vh, 0, T, v_lds, wave, lane, xrs);
 
     // Lane read offsets within a tile (K row reads, V transposing reads).
     uint32_t koff[D / 16], voff[D / 32];
@@ -186,8 +188,8 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_fwd_bf16_kernel(
             __syncthreads();  // ... and every wave's; tile kt-1 is no longer read by anyone
             if (kt + 1 < ntile) {
                 const uint32_t nbuf = static_cast<uint32_t>((kt + 1) & 1) * S::kBytes;
-                dma_tile<D>(kh, (kt + 1) * kKeyTile, T, k_lds + nbuf, wave, lane);
-                dma_tile<D>(vh, (kt + 1) * kKeyTile, T, v_lds + nbuf, wave, lane);
+                dma_tile<D>(kh, (kt + 1) * kKeyTile, T, k_lds + nbuf, wave, lane, xrs);
+                dma_tile<D>(vh, (kt + 1) * kKeyTile, T, v_lds + nbuf, wave, lane, xrs);
             }
         }
         const uint32_t base = static_cast<uint32_t>(kt & 1) * S::kBytes +
@@ -213,7 +215,7 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_fwd_bf16_kernel(
         const SubState<D>& st = j == 0 ? st0 : st1;
         const int qi = (j == 0 ? qj0 : qj1) + col;
         if (qi < T) {
-            store_row<D>(o + head_off, qi, half, st.acc, 1.0f / st.l);  // l >= 1
+            store_row<D>(o + ooff, qi, half, st.acc, 1.0f / st.l, ors);  // l >= 1
             if (half == 0) {
                 const size_t r = static_cast<size_t>(bh) * T + qi;
                 // m = scale * max_j q.k; l relative to that maximum
@@ -226,32 +228,35 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_fwd_bf16_kernel(
 
 template <int D, int NSUB>
 void fwd_launch(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o,
-                float* m_out, float* l_out, int BH, int T, float scale, hipStream_t stream) {
+                float* m_out, float* l_out, int BH, int T, float scale, const HeadView& xv,
+                const HeadView& ov, hipStream_t stream) {
     constexpr int kBlock = kWaves * NSUB * kSub;
     const int nblk = (T + kBlock - 1) / kBlock;
     hipLaunchKernelGGL((flash_fwd_bf16_kernel<D, NSUB>), dim3(BH * nblk), dim3(kWave * kWaves),
-                       0, stream, q, k, v, o, m_out, l_out, BH, T, scale, nblk);
+                       0, stream, q, k, v, o, m_out, l_out, BH, T, scale, nblk, xv, ov);
 }
 
 template <int D>
 void fwd_dispatch(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o,
-                  float* m_out, float* l_out, int BH, int T, float scale, hipStream_t stream) {
+                  float* m_out, float* l_out, int BH, int T, float scale, const HeadView& xv,
+                  const HeadView& ov, hipStream_t stream) {
     // d = 128: one sub-block per wave fits two waves per SIMD (two sub-blocks do not)
     if (D >= 128 || use_single_subblock(BH, T))
-        fwd_launch<D, 1>(q, k, v, o, m_out, l_out, BH, T, scale, stream);
+        fwd_launch<D, 1>(q, k, v, o, m_out, l_out, BH, T, scale, xv, ov, stream);
     else
-        fwd_launch<D, 2>(q, k, v, o, m_out, l_out, BH, T, scale, stream);
+        fwd_launch<D, 2>(q, k, v, o, m_out, l_out, BH, T, scale, xv, ov, stream);
 }
 
 }  // namespace
 
 void launch_flash_fwd_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                            uint16_t* o, float* m_out, float* l_out, int BH, int T, int d,
-                           float scale, hipStream_t stream) {
+                           float scale, const HeadView& xv, const HeadView& ov,
+                           hipStream_t stream) {
     switch (d) {
-        case 32: fwd_dispatch<32>(q, k, v, o, m_out, l_out, BH, T, scale, stream); break;
-        case 64: fwd_dispatch<64>(q, k, v, o, m_out, l_out, BH, T, scale, stream); break;
-        default: fwd_dispatch<128>(q, k, v, o, m_out, l_out, BH, T, scale, stream); break;
+        case 32: fwd_dispatch<32>(q, k, v, o, m_out, l_out, BH, T, scale, xv, ov, stream); break;
+        case 64: fwd_dispatch<64>(q, k, v, o, m_out, l_out, BH, T, scale, xv, ov, stream); break;
+        default: fwd_dispatch<128>(q, k, v, o, m_out, l_out, BH, T, scale, xv, ov, stream); break;
     }
 }
 

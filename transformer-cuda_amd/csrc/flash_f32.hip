@@ -53,17 +53,17 @@ __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_ex
 template <int D>
 constexpr int kTileDma = kTile * (D >= 64 ? D / 64 : 1);
 
-// Copy rows [row0, row0 + 32) of a row-major (T, D) fp32 head into LDS rows of STRIDE
-// floats starting at byte address lds.  Rows past T are read from row T-1 (finite values;
+// Copy rows [row0, row0 + 32) of a head (T rows of D fp32, consecutive rows rs floats
+// apart) into LDS rows of STRIDE floats starting at byte address lds.  Rows past T are read from row T-1 (finite values;
 // every consumer masks them).  D = 32 uses the lower half-wave per row.
 template <int D, int STRIDE>
 __device__ __forceinline__ void dma_tile(const float* __restrict__ head, int row0, int T,
-                                         uint32_t lds, int lane) {
+                                         uint32_t lds, int lane, int rs) {
     constexpr int kSeg = D >= 64 ? D / 64 : 1;
     const uint32_t voff = static_cast<uint32_t>(lane) * 4u;
 #pragma unroll
     for (int r = 0; r < kTile; ++r) {
-        const float* rowp = head + static_cast<size_t>(min(row0 + r, T - 1)) * D;
+        const float* rowp = head + static_cast<size_t>(min(row0 + r, T - 1)) * rs;
 #pragma unroll
         for (int sg = 0; sg < kSeg; ++sg) {
             if (D >= 64 || lane < D) {
@@ -74,12 +74,13 @@ __device__ __forceinline__ void dma_tile(const float* __restrict__ head, int row
     }
 }
 
-// Lane (col, half) loads its row's half: dst[j] = src[row][half*D/2 + j], zeros if row >= T.
+// Lane (col, half) loads its row's half: dst[j] = src[row][half*D/2 + j], zeros if row >= T
+// (rows rs floats apart).
 template <int D>
 __device__ __forceinline__ void load_row_half(float (&dst)[D / 2], const float* __restrict__ head,
-                                              int row, int T, int half) {
+                                              int row, int T, int half, int rs) {
     if (row < T) {
-        const float* p = head + static_cast<size_t>(row) * D + half * (D / 2);
+        const float* p = head + static_cast<size_t>(row) * rs + half * (D / 2);
 #pragma unroll
         for (int j = 0; j < D / 2; j += 4) {
             const f32x4 x = *reinterpret_cast<const f32x4*>(p + j);
@@ -133,8 +134,8 @@ __device__ __forceinline__ void mma_cols(const float* lds, int col, int half, co
 // half)) of a row-major (T, D) tensor, row = this lane's row.  Four float4 per 32 columns.
 template <int D>
 __device__ __forceinline__ void store_acc_row(float* __restrict__ head, int row, int half,
-                                              const f32x16 (&acc)[D / 32], float mul) {
-    float* p = head + static_cast<size_t>(row) * D + 4 * half;
+                                              const f32x16 (&acc)[D / 32], float mul, int rs) {
+    float* p = head + static_cast<size_t>(row) * rs + 4 * half;
 #pragma unroll
     for (int dt = 0; dt < D / 32; ++dt) {
 #pragma unroll
@@ -176,10 +177,10 @@ __device__ __forceinline__ void put_part(float* part, const f32x16 (&x)[N], int 
 // two float4 stores (f0 is a multiple of 8, so the 8 elements are rows acc_row(8u..8u+7)).
 template <int D>
 __device__ __forceinline__ void store_slice8(float* __restrict__ head, int row, int half,
-                                             int f0, const float (&x)[8], float mul) {
+                                             int f0, const float (&x)[8], float mul, int rs) {
     const int i = f0 >> 4;
     const int u = (f0 & 15) >> 3;  // which 8 of the 16 accumulator rows
-    float* p = head + static_cast<size_t>(row) * D + i * 32 + 16 * u + 4 * half;
+    float* p = head + static_cast<size_t>(row) * rs + i * 32 + 16 * u + 4 * half;
     f32x4 a, b;
     a[0] = x[0] * mul; a[1] = x[1] * mul; a[2] = x[2] * mul; a[3] = x[3] * mul;
     b[0] = x[4] * mul; b[1] = x[5] * mul; b[2] = x[6] * mul; b[3] = x[7] * mul;
@@ -221,7 +222,8 @@ static_assert(sizeof(FwdLds<32>) >= (32 * 32 + 128) * 4, "partial exchange fits"
 
 template <int D>
 __device__ __forceinline__ void fwd_chunk(const float* __restrict__ kh,
-                                          const float* __restrict__ vh, int T, float c, int qb,
+                                          const float* __restrict__ vh, int T, int stride,
+                                          float c, int qb,
                                           int t0, int t1, const float (&qreg)[D / 2],
                                           FwdLds<D>& L, int lane, Fetch& fetch,
                                           f32x16 (&acc)[D / 32], float& m_raw, float& l_i) {
@@ -239,8 +241,8 @@ __device__ __forceinline__ void fwd_chunk(const float* __restrict__ kh,
         fetch.issue(lane);
         return;
     }
-    dma_tile<D, KS>(kh, t0 * kTile, T, lds_addr(L.k), lane);
-    dma_tile<D, VS>(vh, t0 * kTile, T, lds_addr(L.v), lane);
+    dma_tile<D, KS>(kh, t0 * kTile, T, lds_addr(L.k), lane, stride);
+    dma_tile<D, VS>(vh, t0 * kTile, T, lds_addr(L.v), lane, stride);
     fetch.issue(lane);
 
     for (int t = t0; t < t1; ++t) {
@@ -248,7 +250,7 @@ __device__ __forceinline__ void fwd_chunk(const float* __restrict__ kh,
         wait_vm<kTileDma<D>>();  // K tile t landed
         f32x16 s = mma_rows<D>(Ks + col * KS + half * (D / 2), qreg, f32x16{});
         wait_lds();
-        if (more) dma_tile<D, KS>(kh, (t + 1) * kTile, T, lds_addr(L.k), lane);
+        if (more) dma_tile<D, KS>(kh, (t + 1) * kTile, T, lds_addr(L.k), lane, stride);
         if (t == qb) {  // diagonal tile
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
@@ -280,7 +282,7 @@ __device__ __forceinline__ void fwd_chunk(const float* __restrict__ kh,
         }
         mma_cols<D, VS>(Vs, col, half, s, acc);
         wait_lds();
-        if (more) dma_tile<D, VS>(vh, (t + 1) * kTile, T, lds_addr(L.v), lane);
+        if (more) dma_tile<D, VS>(vh, (t + 1) * kTile, T, lds_addr(L.v), lane, stride);
     }
 }
 
@@ -288,7 +290,7 @@ template <int D>
 __global__ __launch_bounds__(kWave* kWaves) void flash_fwd_f32_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
     float* __restrict__ o, float* __restrict__ m_out, float* __restrict__ l_out, int BH, int T,
-    float scale, int nqb, QueueSlot* slot, int per_xcd) {
+    float scale, int nqb, QueueSlot* slot, int per_xcd, HeadView xv, HeadView ov) {
     __shared__ FwdLds<D> L[kWaves];
     __shared__ unsigned s_next;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
@@ -303,16 +305,16 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_fwd_f32_kernel(
         tq.decode(task, bh, rank);
         const int qb = nqb - 1 - rank;
         const int qi = qb * kTile + col;
-        const size_t head_off = static_cast<size_t>(bh) * T * D;
+        const size_t xoff = wave_uniform(xv.off(bh)), ooff = wave_uniform(ov.off(bh));
         int t0, t1;
         wave_range(qb + 1, wave, t0, t1);
 
         float qreg[D / 2];
-        load_row_half<D>(qreg, q + head_off, qi, T, half);
+        load_row_half<D>(qreg, q + xoff, qi, T, half, xv.row);
         Fetch fetch{wave == 0 ? &tq : nullptr, 0u};
         f32x16 acc[D / 32];
         float m_raw, l_i;
-        fwd_chunk<D>(k + head_off, v + head_off, T, c, qb, t0, t1, qreg, L[wave], lane, fetch,
+        fwd_chunk<D>(k + xoff, v + xoff, T, xv.row, c, qb, t0, t1, qreg, L[wave], lane, fetch,
                      acc, m_raw, l_i);
 
         // Merge: every wave publishes (acc, m, l) over its own tiles; then wave w reduces
@@ -347,7 +349,7 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_fwd_f32_kernel(
                     sum += reinterpret_cast<const float*>(&L[w])[(f0 + e) * kWave + lane] * aw[w];
                 x[e] = sum;
             }
-            if (qi < T) store_slice8<D>(o + head_off, qi, half, f0, x, 1.0f / l_tot);
+            if (qi < T) store_slice8<D>(o + ooff, qi, half, f0, x, 1.0f / l_tot, ov.row);
         }
         if (wave == 0 && half == 0 && qi < T) {
             // max_j scale*s_j = scale * max_j s_j exactly (rounding is monotone); l_tot >= 1
@@ -355,7 +357,7 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_fwd_f32_kernel(
             if (l_out != nullptr) l_out[static_cast<size_t>(bh) * T + qi] = l_tot;
         }
         __syncthreads();
-        task = s_next;
+        task = __builtin_amdgcn_readfirstlane(s_next);  // the same in every lane
     }
 }
 
@@ -395,7 +397,8 @@ struct DqLds {
 
 template <int D>
 __device__ __forceinline__ void dq_chunk(const float* __restrict__ kh,
-                                         const float* __restrict__ vh, int T, float c,
+                                         const float* __restrict__ vh, int T, int stride,
+                                         float c,
                                          float lse2, float Dval, int qb, int t0, int t1,
                                          const float (&qreg)[D / 2],
                                          const float (&doreg)[D / 2], DqLds<D>& L, int lane,
@@ -412,8 +415,8 @@ __device__ __forceinline__ void dq_chunk(const float* __restrict__ kh,
         fetch.issue(lane);
         return;
     }
-    dma_tile<D, KS>(kh, t0 * kTile, T, lds_addr(L.k), lane);
-    dma_tile<D, VS>(vh, t0 * kTile, T, lds_addr(L.v), lane);
+    dma_tile<D, KS>(kh, t0 * kTile, T, lds_addr(L.k), lane, stride);
+    dma_tile<D, VS>(vh, t0 * kTile, T, lds_addr(L.v), lane, stride);
     fetch.issue(lane);
 
     for (int t = t0; t < t1; ++t) {
@@ -422,7 +425,7 @@ __device__ __forceinline__ void dq_chunk(const float* __restrict__ kh,
         f32x16 dp = mma_rows<D>(Vs + col * VS + half * (D / 2), doreg, f32x16{});
         f32x16 s = mma_rows<D>(Ks + col * KS + half * (D / 2), qreg, f32x16{});
         wait_lds();
-        if (more) dma_tile<D, VS>(vh, (t + 1) * kTile, T, lds_addr(L.v), lane);
+        if (more) dma_tile<D, VS>(vh, (t + 1) * kTile, T, lds_addr(L.v), lane, stride);
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             float p = exp2_fast(fmaf(s[r], c, -lse2));
@@ -434,7 +437,7 @@ __device__ __forceinline__ void dq_chunk(const float* __restrict__ kh,
         mma_cols<D, KS>(Ks, col, half, s, part);
         add_into(acc, part);
         wait_lds();
-        if (more) dma_tile<D, KS>(kh, (t + 1) * kTile, T, lds_addr(L.k), lane);
+        if (more) dma_tile<D, KS>(kh, (t + 1) * kTile, T, lds_addr(L.k), lane, stride);
     }
 }
 
@@ -443,7 +446,8 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_bwd_dq_f32_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
     const float* __restrict__ o, const float* __restrict__ dO, const float* __restrict__ m,
     const float* __restrict__ l, float* __restrict__ dq, float* __restrict__ Dws, int BH,
-    int T, float scale, int nqb, QueueSlot* slot, int per_xcd) {
+    int T, float scale, int nqb, QueueSlot* slot, int per_xcd, HeadView xv, HeadView ov,
+    HeadView gv) {
     __shared__ DqLds<D> L[kWaves];
     __shared__ unsigned s_next;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
@@ -459,20 +463,21 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_bwd_dq_f32_kernel(
         const int qb = nqb - 1 - rank;
         const int qi = qb * kTile + col;
         const bool row_ok = qi < T;
-        const size_t head_off = static_cast<size_t>(bh) * T * D;
+        const size_t xoff = wave_uniform(xv.off(bh)), ooff = wave_uniform(ov.off(bh)),
+                     goff = wave_uniform(gv.off(bh));
         const size_t stat_off = static_cast<size_t>(bh) * T;
         int t0, t1;
         wave_range(qb + 1, wave, t0, t1);
 
         float qreg[D / 2];
         float doreg[D / 2];
-        load_row_half<D>(qreg, q + head_off, qi, T, half);
-        load_row_half<D>(doreg, dO + head_off, qi, T, half);
+        load_row_half<D>(qreg, q + xoff, qi, T, half, xv.row);
+        load_row_half<D>(doreg, dO + ooff, qi, T, half, ov.row);
         // D_i from this lane's half row of O, completed across the halves.
         float Dval;
         {
             float orow[D / 2];
-            load_row_half<D>(orow, o + head_off, qi, T, half);
+            load_row_half<D>(orow, o + ooff, qi, T, half, ov.row);
             float pd = 0.0f;
 #pragma unroll
             for (int j = 0; j < D / 2; ++j) pd = fmaf(doreg[j], orow[j], pd);
@@ -485,7 +490,7 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_bwd_dq_f32_kernel(
                    : INFINITY;
         Fetch fetch{wave == 0 ? &tq : nullptr, 0u};
         f32x16 acc[D / 32];
-        dq_chunk<D>(k + head_off, v + head_off, T, c, lse2, Dval, qb, t0, t1, qreg, doreg,
+        dq_chunk<D>(k + xoff, v + xoff, T, xv.row, c, lse2, Dval, qb, t0, t1, qreg, doreg,
                     L[wave], lane, fetch, acc);
 
         // Merge: every wave publishes its partial dQ; wave w sums (in wave order) and stores
@@ -505,11 +510,11 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_bwd_dq_f32_kernel(
                     sum += reinterpret_cast<const float*>(&L[w])[(f0 + e) * kWave + lane];
                 x[e] = sum;
             }
-            if (row_ok) store_slice8<D>(dq + head_off, qi, half, f0, x, scale);
+            if (row_ok) store_slice8<D>(dq + goff, qi, half, f0, x, scale, gv.row);
         }
         if (wave == 0 && half == 0 && row_ok) Dws[stat_off + qi] = Dval;
         __syncthreads();
-        task = s_next;
+        task = __builtin_amdgcn_readfirstlane(s_next);  // the same in every lane
     }
 }
 
@@ -536,7 +541,8 @@ __device__ __forceinline__ void dkdv_chunk(const float* __restrict__ qh,
                                            const float* __restrict__ m,
                                            const float* __restrict__ l,
                                            const float* __restrict__ Dws, size_t stat_off,
-                                           int T, float c, int kb, int t0, int t1,
+                                           int T, int qstride, int gstride, float c, int kb, int t0,
+                                           int t1,
                                            const float (&kreg)[D / 2],
                                            const float (&vreg)[D / 2], DkdvLds<D>& L, int lane,
                                            Fetch& fetch, f32x16 (&dk_acc)[D / 32],
@@ -565,8 +571,8 @@ __device__ __forceinline__ void dkdv_chunk(const float* __restrict__ qh,
         return Dws[stat_off + r];
     };
     St[half][col] = load_stat(t0 * kTile);
-    dma_tile<D, QS>(qh, t0 * kTile, T, lds_addr(L.q), lane);
-    dma_tile<D, GS>(doh, t0 * kTile, T, lds_addr(L.g), lane);
+    dma_tile<D, QS>(qh, t0 * kTile, T, lds_addr(L.q), lane, qstride);
+    dma_tile<D, GS>(doh, t0 * kTile, T, lds_addr(L.g), lane, gstride);
     fetch.issue(lane);
 
     for (int t = t0; t < t1; ++t) {
@@ -594,8 +600,8 @@ __device__ __forceinline__ void dkdv_chunk(const float* __restrict__ qh,
         wait_lds();
         if (more) {
             St[half][col] = st_n;
-            dma_tile<D, QS>(qh, (t + 1) * kTile, T, lds_addr(L.q), lane);
-            dma_tile<D, GS>(doh, (t + 1) * kTile, T, lds_addr(L.g), lane);
+            dma_tile<D, QS>(qh, (t + 1) * kTile, T, lds_addr(L.q), lane, qstride);
+            dma_tile<D, GS>(doh, (t + 1) * kTile, T, lds_addr(L.g), lane, gstride);
         }
     }
 }
@@ -605,7 +611,8 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_bwd_dkdv_f32_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
     const float* __restrict__ dO, const float* __restrict__ m, const float* __restrict__ l,
     const float* __restrict__ Dws, float* __restrict__ dk, float* __restrict__ dv, int BH,
-    int T, float scale, int nkb, QueueSlot* slot, int per_xcd) {
+    int T, float scale, int nkb, QueueSlot* slot, int per_xcd, HeadView xv, HeadView ov,
+    HeadView gv) {
     __shared__ DkdvLds<D> L[kWaves];
     __shared__ unsigned s_next;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
@@ -619,18 +626,19 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_bwd_dkdv_f32_kernel(
         int bh, kb;
         tq.decode(task, bh, kb);
         const int kj = kb * kTile + col;
-        const size_t head_off = static_cast<size_t>(bh) * T * D;
+        const size_t xoff = wave_uniform(xv.off(bh)), ooff = wave_uniform(ov.off(bh)),
+                     goff = wave_uniform(gv.off(bh));
         const size_t stat_off = static_cast<size_t>(bh) * T;
         int t0, t1;
         wave_range(nkb - kb, wave, t0, t1);
 
         float kreg[D / 2];
         float vreg[D / 2];
-        load_row_half<D>(kreg, k + head_off, kj, T, half);
-        load_row_half<D>(vreg, v + head_off, kj, T, half);
+        load_row_half<D>(kreg, k + xoff, kj, T, half, xv.row);
+        load_row_half<D>(vreg, v + xoff, kj, T, half, xv.row);
         Fetch fetch{wave == 0 ? &tq : nullptr, 0u};
         f32x16 dk_acc[D / 32], dv_acc[D / 32];
-        dkdv_chunk<D>(q + head_off, dO + head_off, m, l, Dws, stat_off, T, c, kb, kb + t0,
+        dkdv_chunk<D>(q + xoff, dO + ooff, m, l, Dws, stat_off, T, xv.row, ov.row, c, kb, kb + t0,
                       kb + t1, kreg, vreg, L[wave], lane, fetch, dk_acc, dv_acc);
 
         // Merge: every wave publishes its partial dK, dV; wave w sums (in wave order) and
@@ -654,14 +662,14 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_bwd_dkdv_f32_kernel(
             }
             if (kj < T) {
                 if (f0 < D / 2) {
-                    store_slice8<D>(dk + head_off, kj, half, f0, x, scale);
+                    store_slice8<D>(dk + goff, kj, half, f0, x, scale, gv.row);
                 } else {
-                    store_slice8<D>(dv + head_off, kj, half, f0 - D / 2, x, 1.0f);
+                    store_slice8<D>(dv + goff, kj, half, f0 - D / 2, x, 1.0f, gv.row);
                 }
             }
         }
         __syncthreads();
-        task = s_next;
+        task = __builtin_amdgcn_readfirstlane(s_next);  // the same in every lane
     }
 }
 
@@ -699,50 +707,53 @@ QueueSlot* queue_base(Family f) {
 
 template <int D>
 void fwd_dispatch(const float* q, const float* k, const float* v, float* o, float* m_out,
-                  float* l_out, int BH, int T, float scale, hipStream_t stream) {
+                  float* l_out, int BH, int T, float scale, const HeadView& xv,
+                  const HeadView& ov, hipStream_t stream) {
     const int nqb = (T + kTile - 1) / kTile;
     QueueSlot* slot = queue_base(Family::Fwd) + next_queue_slot(g_fwd_ticket);
     const int grid = persistent_grid(flash_fwd_f32_kernel<D>, kWave * kWaves, 0,
                                      static_cast<long long>(BH) * nqb);
     hipLaunchKernelGGL(flash_fwd_f32_kernel<D>, dim3(grid), dim3(kWave * kWaves), 0, stream, q, k, v, o,
-                       m_out, l_out, BH, T, scale, nqb, slot, (BH % kXcds) == 0 ? 1 : 0);
+                       m_out, l_out, BH, T, scale, nqb, slot, (BH % kXcds) == 0 ? 1 : 0, xv, ov);
 }
 
 template <int D>
 void dq_dispatch(const float* q, const float* k, const float* v, const float* o,
                  const float* dO, const float* m, const float* l, float* dq, float* Dws, int BH,
-                 int T, float scale, hipStream_t stream) {
+                 int T, float scale, const HeadView& xv, const HeadView& ov, const HeadView& gv,
+                 hipStream_t stream) {
     const int nqb = (T + kTile - 1) / kTile;
     QueueSlot* slot = queue_base(Family::Dq) + next_queue_slot(g_dq_ticket);
     const int grid = persistent_grid(flash_bwd_dq_f32_kernel<D>, kWave * kWaves, 0,
                                      static_cast<long long>(BH) * nqb);
     hipLaunchKernelGGL(flash_bwd_dq_f32_kernel<D>, dim3(grid), dim3(kWave * kWaves), 0, stream, q, k, v,
                        o, dO, m, l, dq, Dws, BH, T, scale, nqb, slot,
-                       (BH % kXcds) == 0 ? 1 : 0);
+                       (BH % kXcds) == 0 ? 1 : 0, xv, ov, gv);
 }
 
 template <int D>
 void dkdv_dispatch(const float* q, const float* k, const float* v, const float* dO,
                    const float* m, const float* l, const float* Dws, float* dk, float* dv,
-                   int BH, int T, float scale, hipStream_t stream) {
+                   int BH, int T, float scale, const HeadView& xv, const HeadView& ov,
+                   const HeadView& gv, hipStream_t stream) {
     const int nkb = (T + kTile - 1) / kTile;
     QueueSlot* slot = queue_base(Family::Dkdv) + next_queue_slot(g_dkdv_ticket);
     const int grid = persistent_grid(flash_bwd_dkdv_f32_kernel<D>, kWave * kWaves, 0,
                                      static_cast<long long>(BH) * nkb);
     hipLaunchKernelGGL(flash_bwd_dkdv_f32_kernel<D>, dim3(grid), dim3(kWave * kWaves), 0, stream, q, k,
                        v, dO, m, l, Dws, dk, dv, BH, T, scale, nkb, slot,
-                       (BH % kXcds) == 0 ? 1 : 0);
+                       (BH % kXcds) == 0 ? 1 : 0, xv, ov, gv);
 }
 
 }  // namespace
 
 void launch_flash_fwd_f32(const float* q, const float* k, const float* v, float* o,
                           float* m_out, float* l_out, int BH, int T, int d, float scale,
-                          hipStream_t stream) {
+                          const HeadView& xv, const HeadView& ov, hipStream_t stream) {
     switch (d) {
-        case 32: fwd_dispatch<32>(q, k, v, o, m_out, l_out, BH, T, scale, stream); break;
-        case 64: fwd_dispatch<64>(q, k, v, o, m_out, l_out, BH, T, scale, stream); break;
-        default: fwd_dispatch<128>(q, k, v, o, m_out, l_out, BH, T, scale, stream); break;
+        case 32: fwd_dispatch<32>(q, k, v, o, m_out, l_out, BH, T, scale, xv, ov, stream); break;
+        case 64: fwd_dispatch<64>(q, k, v, o, m_out, l_out, BH, T, scale, xv, ov, stream); break;
+        default: fwd_dispatch<128>(q, k, v, o, m_out, l_out, BH, T, scale, xv, ov, stream); break;
     }
 }
 
@@ -755,23 +766,24 @@ void launch_dot_do_o_f32(const float* dO, const float* O, float* D, int64_t rows
 
 void launch_flash_bwd_dq_f32(const float* q, const float* k, const float* v, const float* o,
                              const float* dO, const float* m, const float* l, float* dq,
-                             float* Dws, int BH, int T, int d, float scale,
-                             hipStream_t stream) {
+                             float* Dws, int BH, int T, int d, float scale, const HeadView& xv,
+                             const HeadView& ov, const HeadView& gv, hipStream_t stream) {
     switch (d) {
-        case 32: dq_dispatch<32>(q, k, v, o, dO, m, l, dq, Dws, BH, T, scale, stream); break;
-        case 64: dq_dispatch<64>(q, k, v, o, dO, m, l, dq, Dws, BH, T, scale, stream); break;
-        default: dq_dispatch<128>(q, k, v, o, dO, m, l, dq, Dws, BH, T, scale, stream); break;
+        case 32: dq_dispatch<32>(q, k, v, o, dO, m, l, dq, Dws, BH, T, scale, xv, ov, gv, stream); break;
+        case 64: dq_dispatch<64>(q, k, v, o, dO, m, l, dq, Dws, BH, T, scale, xv, ov, gv, stream); break;
+        default: dq_dispatch<128>(q, k, v, o, dO, m, l, dq, Dws, BH, T, scale, xv, ov, gv, stream); break;
     }
 }
 
 void launch_flash_bwd_dkdv_f32(const float* q, const float* k, const float* v,
                                const float* dO, const float* m, const float* l,
                                const float* Dws, float* dk, float* dv, int BH, int T, int d,
-                               float scale, hipStream_t stream) {
+                               float scale, const HeadView& xv, const HeadView& ov,
+                               const HeadView& gv, hipStream_t stream) {
     switch (d) {
-        case 32: dkdv_dispatch<32>(q, k, v, dO, m, l, Dws, dk, dv, BH, T, scale, stream); break;
-        case 64: dkdv_dispatch<64>(q, k, v, dO, m, l, Dws, dk, dv, BH, T, scale, stream); break;
-        default: dkdv_dispatch<128>(q, k, v, dO, m, l, Dws, dk, dv, BH, T, scale, stream); break;
+        case 32: dkdv_dispatch<32>(q, k, v, dO, m, l, Dws, dk, dv, BH, T, scale, xv, ov, gv, stream); break;
+        case 64: dkdv_dispatch<64>(q, k, v, dO, m, l, Dws, dk, dv, BH, T, scale, xv, ov, gv, stream); break;
+        default: dkdv_dispatch<128>(q, k, v, dO, m, l, Dws, dk, dv, BH, T, scale, xv, ov, gv, stream); break;
     }
 }
 

@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "device_common.hpp"
+
 namespace tcamd {
 
 enum class ElemType { F32, BF16 };
@@ -32,27 +34,35 @@ void launch_batched_gemm_f32(const float* A, const float* B, float* C, int M, in
 void launch_dot_do_o_f32(const float* dO, const float* O, float* D, int64_t rows, int d,
                          hipStream_t stream);
 
+// The flash kernels address their operands through HeadViews: xv for q, k, v (head-major,
+// or the packed QKV layout with q/k/v pointing at their column blocks), ov for o and dO
+// (head-major), gv for dq, dk, dv (head-major or packed like xv).
 void launch_flash_fwd_f32(const float* q, const float* k, const float* v, float* o,
                           float* m_out, float* l_out, int BH, int T, int d, float scale,
-                          hipStream_t stream);
+                          const HeadView& xv, const HeadView& ov, hipStream_t stream);
 void launch_flash_bwd_dq_f32(const float* q, const float* k, const float* v, const float* o,
                              const float* dO, const float* m, const float* l, float* dq,
-                             float* Dws, int BH, int T, int d, float scale, hipStream_t stream);
+                             float* Dws, int BH, int T, int d, float scale, const HeadView& xv,
+                             const HeadView& ov, const HeadView& gv, hipStream_t stream);
 void launch_flash_bwd_dkdv_f32(const float* q, const float* k, const float* v,
                                const float* dO, const float* m, const float* l,
                                const float* Dws, float* dk, float* dv, int BH, int T, int d,
-                               float scale, hipStream_t stream);
+                               float scale, const HeadView& xv, const HeadView& ov,
+                               const HeadView& gv, hipStream_t stream);
 
 void launch_flash_fwd_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                            uint16_t* o, float* m_out, float* l_out, int BH, int T, int d,
-                           float scale, hipStream_t stream);
+                           float scale, const HeadView& xv, const HeadView& ov,
+                           hipStream_t stream);
 void launch_flash_bwd_dq_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                               const uint16_t* o, const uint16_t* dO, const float* m,
                               const float* l, uint16_t* dq, float* Dws, int BH, int T, int d,
-                              float scale, hipStream_t stream);
+                              float scale, const HeadView& xv, const HeadView& ov,
+                              const HeadView& gv, hipStream_t stream);
 void launch_flash_bwd_dkdv_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                                 const uint16_t* dO, const float* m, const float* l,
                                 const float* Dws, uint16_t* dk, uint16_t* dv, int BH, int T,
-                                int d, float scale, hipStream_t stream);
+                                int d, float scale, const HeadView& xv, const HeadView& ov,
+                                const HeadView& gv, hipStream_t stream);
 
 }  // namespace tcamd

@@ -26,6 +26,14 @@ __device__ __forceinline__ void wait_vm() {
 }
 __device__ __forceinline__ void wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
+// A 64-bit value that is the same in every lane, moved to SGPRs (the copies take their base
+// address from SGPRs).
+__device__ __forceinline__ size_t wave_uniform(size_t v) {
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
+    return (static_cast<size_t>(hi) << 32) | lo;
+}
+
 // M0 carries the LDS address.  These asm statements are the only users of M0 in the kernels
 // (gfx9-class LDS instructions do not read it), so declaring it clobbered is exact; the
 // compiler's generic warning about clobbering a reserved register is silenced.

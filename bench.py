@@ -2,14 +2,21 @@
 """Causal multi-head attention fwd+bwd throughput on one MI355X (gfx950).
 
 One step is one pass of the hot path over one batch, every kernel launched through the
-C ABI (include/attn_capi.h) on torch's current stream:
+C ABI (include/attn_capi.h) on torch's current stream.  Default (--path packed), the
+MI355X form of the path: the split-transposes are fused into the attention kernels' tile
+copies and stores, so qkv (B,T,3C) is read and dqkv (B,T,3C) written directly:
+    attn_fwd_packed   qkv -> O (B,H,T,d), m, l                    reference model.cu:305-311
+    bwd_dq_packed     D = rowsum(dO*O), dQ -> dqkv[:, :, q block]  reference model.cu:609, 653
+    bwd_dkdv_packed   dK, dV -> dqkv[:, :, k and v blocks]         reference model.cu:609, 653
+--path split runs the reference's launcher sequence with separate split-transpose kernels:
     qkv (B,T,3C) --split-transpose--> q,k,v (B,H,T,d)             reference model.cu:305
     tiled forward          -> O, m, l                             reference model.cu:311
     backward stage 1       -> D = rowsum(dO*O), dQ                 reference model.cu:609
     backward stage 2       -> dK, dV                               reference model.cu:609
     dq,dk,dv --split-transpose backward--> dqkv (B,T,3C)          reference model.cu:653
-Inputs (qkv, dO) are synthetic N(0,1) from a fixed seed and resident in HBM before the
-timed region starts.
+Both produce bitwise the same O, m, l and dqkv (tests/test_gpu_packed.py).  Inputs (qkv,
+dO) are synthetic N(0,1) from a fixed seed and resident in HBM before the timed region
+starts.
 
 value = algorithmic FLOPs of causal attention fwd+bwd, 7*B*H*T^2*d (FlashAttention-2
 convention: fwd 2*B*H*T^2*d, bwd 5*B*H*T^2*d), divided by the wall-clock time of the K
@@ -23,8 +30,9 @@ roofline.traffic is the dominant kernel's measured HBM bytes per dispatch, read 
 profiles/hbm_traffic.md (rocprofv3 FETCH_SIZE and WRITE_SIZE of this same bench command,
 scaled by a device-copy calibration); null when that file has no row for the workload.
 
-secondary: the same step in bf16 at config 2's shape and at config 3, and the reference's
-materialised mode (full-square GEMMs + fused softmax, fp32, config 2) as a timed fwd+bwd.
+secondary: the same workload through the other path, the step in bf16 at config 2's shape
+and at config 3, and the reference's materialised mode (full-square GEMMs + fused softmax,
+fp32, config 2) as a timed fwd+bwd.
 
 cpu_baseline: the torch-CPU fp32 restatement of the reference attention
 (pytorch_src/model.py:43-52, forward + autograd backward) timed on this host on the same
@@ -61,8 +69,8 @@ CONFIG_NAMES = {
 METRIC = "causal attn fwd+bwd TFLOP/s & % MFMA peak, B8 H12 T1024 d64 fp32/bf16"
 
 # kernel -> algorithmic FLOP units (unit = B*H*T^2*d) or HBM bytes factor
-KERNELS = ("split_fwd", "attn_fwd", "bwd_dq", "bwd_dkdv", "split_bwd")
-FLOP_UNITS = {"attn_fwd": 2, "bwd_dq": 1, "bwd_dkdv": 4}
+FLOP_UNITS = {"attn_fwd": 2, "bwd_dq": 1, "bwd_dkdv": 4,
+              "attn_fwd_packed": 2, "bwd_dq_packed": 1, "bwd_dkdv_packed": 4}
 
 
 def parse_args():
@@ -74,6 +82,10 @@ def parse_args():
     ap.add_argument("--dtype", choices=["f32", "bf16"], default=None,
                     help="override the config's dtype")
     ap.add_argument("--seed", type=int, default=42)
+    ap.add_argument("--path", choices=["packed", "split"], default="packed",
+                    help="packed: attention reads qkv and writes dqkv directly (split-transposes "
+                         "fused into its tile copies); split: the reference's launcher sequence "
+                         "with separate split-transpose kernels")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="target CPU time of the cpu_baseline sample")
@@ -109,9 +121,10 @@ def load_lib():
 class PathRunner:
     """Device buffers of one workload and the launches of one step."""
 
-    def __init__(self, lib, B, H, T, d, dtype, seed, qk_scale):
+    def __init__(self, lib, B, H, T, d, dtype, seed, qk_scale, path="packed"):
         import torch
         self.lib, self.torch = lib, torch
+        self.path = path
         self.B, self.H, self.T, self.d = B, H, T, d
         self.C = H * d
         self.dtype = dtype
@@ -134,6 +147,18 @@ class PathRunner:
     def launches(self):
         L, a = self.lib, (self.B, self.H, self.T, self.d)
         B, H, T, d = a
+        if self.path == "packed":
+            # the split-transposes happen inside the attention kernels' tile copies/stores
+            return (
+                ("attn_fwd_packed", lambda: L.packed_causal_attention_forward(
+                    self.qkv, self.o, B, H, T, d, self.scale, self.m, self.l)),
+                ("bwd_dq_packed", lambda: L.packed_causal_attention_backward_dq(
+                    self.qkv, self.o, self.do, self.m, self.l, self.dqkv, self.ws, B, H, T, d,
+                    self.scale)),
+                ("bwd_dkdv_packed", lambda: L.packed_causal_attention_backward_dkdv(
+                    self.qkv, self.do, self.m, self.l, self.ws, self.dqkv, B, H, T, d,
+                    self.scale)),
+            )
         return (
             ("split_fwd", lambda: L.qkv_split_transpose_forward(
                 self.qkv, self.q, self.k, self.v, B, T, H, d)),
@@ -191,8 +216,23 @@ class PathRunner:
 
     def outputs_finite(self):
         torch = self.torch
-        return all(bool(torch.isfinite(t.float()).all()) for t in
-                   (self.o, self.dq, self.dk, self.dv, self.dqkv))
+        outs = (self.o, self.dqkv) if self.path == "packed" else (
+            self.o, self.dq, self.dk, self.dv, self.dqkv)
+        return all(bool(torch.isfinite(t.float()).all()) for t in outs)
+
+    def head_major_inputs(self):
+        """(q, k, v) as (B, H, T, d) views of qkv (the split-transpose's outputs)."""
+        B, H, T, d = self.B, self.H, self.T, self.d
+        x = self.qkv.view(B, T, 3, H, d).permute(2, 0, 3, 1, 4)
+        return x[0], x[1], x[2]
+
+    def head_major_grads(self):
+        """(dq, dk, dv) as (B, H, T, d) tensors, whichever path produced them."""
+        if self.path != "packed":
+            return self.dq, self.dk, self.dv
+        B, H, T, d = self.B, self.H, self.T, self.d
+        g = self.dqkv.view(B, T, 3, H, d).permute(2, 0, 3, 1, 4)
+        return g[0], g[1], g[2]
 
 
 def measured_traffic(config, dtype, kernel):
@@ -257,7 +297,8 @@ def cpu_baseline(runner, target_s):
     cores = torch.get_num_threads()
     B, H, T, d = runner.B, runner.H, runner.T, runner.d
     f = lambda t: t.float().cpu()
-    q, k, v, do = f(runner.q), f(runner.k), f(runner.v), f(runner.do)
+    q, k, v = (f(t).contiguous() for t in runner.head_major_inputs())
+    do = f(runner.do)
     # sample: whole (b, h) heads in groups of up to 8 slices of one batch row, cycling over
     # the workload's heads until about target_s of CPU time has been spent (the first pass
     # over each head also gives the GPU-vs-CPU difference)
@@ -270,7 +311,8 @@ def cpu_baseline(runner, target_s):
             groups.append((b, hs[0], hs[-1] + 1))
     ref.attention_fwd_bwd(q[:1, :1], k[:1, :1], v[:1, :1], do[:1, :1], runner.scale)  # warm-up
     errs = {n: 0.0 for n in ("o", "dq", "dk", "dv")}
-    got = {n: f(getattr(runner, n)) for n in ("o", "dq", "dk", "dv")}
+    dq_, dk_, dv_ = runner.head_major_grads()
+    got = {"o": f(runner.o), "dq": f(dq_), "dk": f(dk_), "dv": f(dv_)}
     n_eval, t_cpu, gi = 0, 0.0, 0
     while t_cpu < target_s and gi < 1000 * len(groups):
         b, h0, h1 = groups[gi % len(groups)]
@@ -301,14 +343,14 @@ def cpu_baseline(runner, target_s):
     }
 
 
-def secondary(lib, cfg, dtype, steps, seed):
+def secondary(lib, cfg, dtype, steps, seed, path="packed"):
     B, H, T, d, _, qk = CONFIGS[cfg]
-    r = PathRunner(lib, B, H, T, d, dtype, seed, qk)
+    r = PathRunner(lib, B, H, T, d, dtype, seed, qk, path)
     wall, per_kernel = r.timed(steps, 3)
     ms = wall / steps * 1e3
     tf = r.flops_total() / (ms * 1e-3) / 1e12
-    attn_ms = sum(per_kernel[n] for n in FLOP_UNITS)
-    out = {"config": cfg, "shape": f"B{B} H{H} T{T} d{d}", "dtype": dtype,
+    attn_ms = sum(ms_ for n, ms_ in per_kernel.items() if n in FLOP_UNITS)
+    out = {"config": cfg, "path": path, "shape": f"B{B} H{H} T{T} d{d}", "dtype": dtype,
            "ms_per_step": round(ms, 4), "tflops": round(tf, 2),
            "frac_mfma_peak": round(tf / PEAK_TFLOPS[dtype], 4),
            "attn_only_tflops": round(r.flops_total() / (attn_ms * 1e-3) / 1e12, 2),
@@ -370,12 +412,12 @@ def main():
     lib = load_lib()
     B, H, T, d, cdt, qk = CONFIGS[args.config]
     dtype = args.dtype or cdt
-    runner = PathRunner(lib, B, H, T, d, dtype, args.seed, qk)
+    runner = PathRunner(lib, B, H, T, d, dtype, args.seed, qk, args.path)
     wall, per_kernel = runner.timed(args.steps, args.warmup)
     ms = wall / args.steps * 1e3
     value = runner.flops_total() / (ms * 1e-3) / 1e12
     dom, roof = roofline_of(runner, per_kernel, args.config)
-    attn_ms = sum(per_kernel[n] for n in FLOP_UNITS)
+    attn_ms = sum(ms_ for n, ms_ in per_kernel.items() if n in FLOP_UNITS)
     props = torch.cuda.get_device_properties(0)
     line = {
         "metric": METRIC,
@@ -392,7 +434,7 @@ def main():
         "data": "synthetic N(0,1) qkv and dO from a fixed seed, resident in HBM",
         "config": {"workload": CONFIG_NAMES[args.config], "B": B, "H": H, "T": T,
                    "d_head": d, "causal": True,
-                   "step": "split_fwd + attn_fwd + bwd_dq + bwd_dkdv + split_bwd",
+                   "step": " + ".join(n for n, _ in runner.launches()),
                    "flops_per_step": runner.flops_total()},
         "frac_mfma_peak": round(value / PEAK_TFLOPS[dtype], 4),
         "attn_only_tflops": round(runner.flops_total() / (attn_ms * 1e-3) / 1e12, 3),
@@ -409,8 +451,10 @@ def main():
     del runner
     torch.cuda.empty_cache()
     if not args.no_secondary:
-        sec = [secondary(lib, args.config, "bf16", args.secondary_steps, args.seed)] \
-            if dtype != "bf16" else []
+        other = "split" if args.path == "packed" else "packed"
+        sec = [secondary(lib, args.config, dtype, args.secondary_steps, args.seed, other)]
+        if dtype != "bf16":
+            sec.append(secondary(lib, args.config, "bf16", args.secondary_steps, args.seed))
         sec.append(secondary(lib, "c3", "bf16", args.secondary_steps, args.seed))
         sec.append(materialized(lib, max(3, args.secondary_steps // 4), args.seed))
         line["secondary"] = sec

@@ -222,6 +222,16 @@ int attn_packed_causal_backward_f32(const float* qkv, const float* o, const floa
                                     const float* m_ptr, const float* l_ptr, float* dqkv,
                                     float* d_workspace, int B, int H, int T, int d_head,
                                     float scale, hipStream_t stream);
+/* The two stages of the packed backward (enqueued in this order by the call above): stage 1
+ * writes D into d_workspace and the q block of dqkv, stage 2 the k and v blocks. */
+int attn_packed_causal_backward_dq_f32(const float* qkv, const float* o, const float* do_ptr,
+                                       const float* m_ptr, const float* l_ptr, float* dqkv,
+                                       float* d_workspace, int B, int H, int T, int d_head,
+                                       float scale, hipStream_t stream);
+int attn_packed_causal_backward_dkdv_f32(const float* qkv, const float* do_ptr,
+                                         const float* m_ptr, const float* l_ptr,
+                                         const float* d_workspace, float* dqkv, int B, int H,
+                                         int T, int d_head, float scale, hipStream_t stream);
 int attn_packed_causal_forward_bf16(const attn_bf16* qkv, attn_bf16* out, int B, int H, int T,
                                     int d_head, float scale, float* m_out, float* l_out,
                                     hipStream_t stream);
@@ -230,6 +240,16 @@ int attn_packed_causal_backward_bf16(const attn_bf16* qkv, const attn_bf16* o,
                                      const float* l_ptr, attn_bf16* dqkv, float* d_workspace,
                                      int B, int H, int T, int d_head, float scale,
                                      hipStream_t stream);
+int attn_packed_causal_backward_dq_bf16(const attn_bf16* qkv, const attn_bf16* o,
+                                        const attn_bf16* do_ptr, const float* m_ptr,
+                                        const float* l_ptr, attn_bf16* dqkv, float* d_workspace,
+                                        int B, int H, int T, int d_head, float scale,
+                                        hipStream_t stream);
+int attn_packed_causal_backward_dkdv_bf16(const attn_bf16* qkv, const attn_bf16* do_ptr,
+                                          const float* m_ptr, const float* l_ptr,
+                                          const float* d_workspace, attn_bf16* dqkv, int B,
+                                          int H, int T, int d_head, float scale,
+                                          hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -58,6 +58,12 @@ SIGNATURES = {
     "attn_materialized_causal_forward_f32": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P],
     "attn_packed_causal_forward_f32": [_P, _P, _I, _I, _I, _I, _F, _P, _P, _P],
     "attn_packed_causal_backward_f32": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P],
+    "attn_packed_causal_backward_dq_f32":
+        [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P],
+    "attn_packed_causal_backward_dkdv_f32": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P],
+    "attn_packed_causal_backward_dq_bf16":
+        [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P],
+    "attn_packed_causal_backward_dkdv_bf16": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P],
     "attn_packed_causal_forward_bf16": [_P, _P, _I, _I, _I, _I, _F, _P, _P, _P],
     "attn_packed_causal_backward_bf16": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P],
     "attn_materialized_causal_backward_f32":
@@ -305,6 +311,34 @@ def packed_causal_attention_backward(qkv, o, dO, m, l, dqkv, workspace, B, H, T,
                _ptr(m, f32, r, "m"), _ptr(l, f32, r, "l"), _ptr(dqkv, dt, 3 * n, "dqkv"),
                _ptr(workspace, f32, r, "workspace"), B, H, T, d_head, float(scale),
                _stream(stream)), "packed_causal_attention_backward")
+
+
+def packed_causal_attention_backward_dq(qkv, o, dO, m, l, dqkv, workspace, B, H, T, d_head,
+                                        scale, stream=None):
+    """Stage 1 of the packed backward: D into workspace, dq into the q block of dqkv."""
+    torch = _torch()
+    bf = qkv.dtype == torch.bfloat16
+    n, r = B * H * T * d_head, B * H * T
+    dt, f32 = _dt(bf), _dt(False)
+    check(call("attn_packed_causal_backward_dq_" + ("bf16" if bf else "f32"),
+               _ptr(qkv, dt, 3 * n, "qkv"), _ptr(o, dt, n, "o"), _ptr(dO, dt, n, "dO"),
+               _ptr(m, f32, r, "m"), _ptr(l, f32, r, "l"), _ptr(dqkv, dt, 3 * n, "dqkv"),
+               _ptr(workspace, f32, r, "workspace"), B, H, T, d_head, float(scale),
+               _stream(stream)), "packed_causal_attention_backward_dq")
+
+
+def packed_causal_attention_backward_dkdv(qkv, dO, m, l, workspace, dqkv, B, H, T, d_head,
+                                          scale, stream=None):
+    """Stage 2 of the packed backward: dk, dv into the k and v blocks of dqkv."""
+    torch = _torch()
+    bf = qkv.dtype == torch.bfloat16
+    n, r = B * H * T * d_head, B * H * T
+    dt, f32 = _dt(bf), _dt(False)
+    check(call("attn_packed_causal_backward_dkdv_" + ("bf16" if bf else "f32"),
+               _ptr(qkv, dt, 3 * n, "qkv"), _ptr(dO, dt, n, "dO"), _ptr(m, f32, r, "m"),
+               _ptr(l, f32, r, "l"), _ptr(workspace, f32, r, "workspace"),
+               _ptr(dqkv, dt, 3 * n, "dqkv"), B, H, T, d_head, float(scale), _stream(stream)),
+          "packed_causal_attention_backward_dkdv")
 
 
 def attention_precompute_dot_do_o(dO, O, D, B, H, T, d_head, stream=None):

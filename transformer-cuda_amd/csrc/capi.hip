@@ -445,27 +445,66 @@ int attn_packed_causal_forward_f32(const float* qkv, float* out, int B, int H, i
     return launch_status();
 }
 
-int attn_packed_causal_backward_f32(const float* qkv, const float* o, const float* do_ptr,
-                                    const float* m_ptr, const float* l_ptr, float* dqkv,
-                                    float* d_workspace, int B, int H, int T, int d_head,
-                                    float scale, hipStream_t stream) {
-    if (qkv == nullptr || o == nullptr || do_ptr == nullptr || m_ptr == nullptr ||
-        l_ptr == nullptr || dqkv == nullptr || d_workspace == nullptr)
+namespace {
+// Shared checks of the packed-layout backward stages.
+int check_packed_bwd(const void* qkv, const void* dO, const void* m, const void* l,
+                     const void* dqkv, const void* ws, int B, int H, int T, int d,
+                     float scale) {
+    if (qkv == nullptr || dO == nullptr || m == nullptr || l == nullptr || dqkv == nullptr ||
+        ws == nullptr)
         return ATTN_ERROR_NULL_POINTER;
-    const int st = check_tiled(B, H, T, d_head, scale);
+    const int st = check_tiled(B, H, T, d, scale);
     if (st != ATTN_SUCCESS) return st;
-    if (!aligned16(qkv) || !aligned16(o) || !aligned16(do_ptr) || !aligned16(dqkv))
-        return ATTN_ERROR_MISALIGNED;
+    if (!aligned16(qkv) || !aligned16(dO) || !aligned16(dqkv)) return ATTN_ERROR_MISALIGNED;
+    return ATTN_SUCCESS;
+}
+}  // namespace
+
+int attn_packed_causal_backward_dq_f32(const float* qkv, const float* o, const float* do_ptr,
+                                       const float* m_ptr, const float* l_ptr, float* dqkv,
+                                       float* d_workspace, int B, int H, int T, int d_head,
+                                       float scale, hipStream_t stream) {
+    if (o == nullptr) return ATTN_ERROR_NULL_POINTER;
+    const int st = check_packed_bwd(qkv, do_ptr, m_ptr, l_ptr, dqkv, d_workspace, B, H, T,
+                                    d_head, scale);
+    if (st != ATTN_SUCCESS) return st;
+    if (!aligned16(o)) return ATTN_ERROR_MISALIGNED;
     const size_t C = static_cast<size_t>(H) * d_head;
     const tcamd::HeadView xv = tcamd::packed_qkv_view(H, T, d_head);
     const tcamd::HeadView hm = tcamd::head_major_view(H, T, d_head);
     clear_error();
     tcamd::launch_flash_bwd_dq_f32(qkv, qkv + C, qkv + 2 * C, o, do_ptr, m_ptr, l_ptr, dqkv,
                                    d_workspace, B * H, T, d_head, scale, xv, hm, xv, stream);
+    return launch_status();
+}
+
+int attn_packed_causal_backward_dkdv_f32(const float* qkv, const float* do_ptr,
+                                         const float* m_ptr, const float* l_ptr,
+                                         const float* d_workspace, float* dqkv, int B, int H,
+                                         int T, int d_head, float scale, hipStream_t stream) {
+    const int st = check_packed_bwd(qkv, do_ptr, m_ptr, l_ptr, dqkv, d_workspace, B, H, T,
+                                    d_head, scale);
+    if (st != ATTN_SUCCESS) return st;
+    const size_t C = static_cast<size_t>(H) * d_head;
+    const tcamd::HeadView xv = tcamd::packed_qkv_view(H, T, d_head);
+    const tcamd::HeadView hm = tcamd::head_major_view(H, T, d_head);
+    clear_error();
     tcamd::launch_flash_bwd_dkdv_f32(qkv, qkv + C, qkv + 2 * C, do_ptr, m_ptr, l_ptr,
                                      d_workspace, dqkv + C, dqkv + 2 * C, B * H, T, d_head,
                                      scale, xv, hm, xv, stream);
     return launch_status();
+}
+
+int attn_packed_causal_backward_f32(const float* qkv, const float* o, const float* do_ptr,
+                                    const float* m_ptr, const float* l_ptr, float* dqkv,
+                                    float* d_workspace, int B, int H, int T, int d_head,
+                                    float scale, hipStream_t stream) {
+    const int st = attn_packed_causal_backward_dq_f32(qkv, o, do_ptr, m_ptr, l_ptr, dqkv,
+                                                      d_workspace, B, H, T, d_head, scale,
+                                                      stream);
+    if (st != ATTN_SUCCESS) return st;
+    return attn_packed_causal_backward_dkdv_f32(qkv, do_ptr, m_ptr, l_ptr, d_workspace, dqkv, B,
+                                                H, T, d_head, scale, stream);
 }
 
 int attn_packed_causal_forward_bf16(const attn_bf16* qkv, attn_bf16* out, int B, int H, int T,
@@ -484,28 +523,54 @@ int attn_packed_causal_forward_bf16(const attn_bf16* qkv, attn_bf16* out, int B,
     return launch_status();
 }
 
-int attn_packed_causal_backward_bf16(const attn_bf16* qkv, const attn_bf16* o,
-                                     const attn_bf16* do_ptr, const float* m_ptr,
-                                     const float* l_ptr, attn_bf16* dqkv, float* d_workspace,
-                                     int B, int H, int T, int d_head, float scale,
-                                     hipStream_t stream) {
-    if (qkv == nullptr || o == nullptr || do_ptr == nullptr || m_ptr == nullptr ||
-        l_ptr == nullptr || dqkv == nullptr || d_workspace == nullptr)
-        return ATTN_ERROR_NULL_POINTER;
-    const int st = check_tiled(B, H, T, d_head, scale);
+int attn_packed_causal_backward_dq_bf16(const attn_bf16* qkv, const attn_bf16* o,
+                                        const attn_bf16* do_ptr, const float* m_ptr,
+                                        const float* l_ptr, attn_bf16* dqkv, float* d_workspace,
+                                        int B, int H, int T, int d_head, float scale,
+                                        hipStream_t stream) {
+    if (o == nullptr) return ATTN_ERROR_NULL_POINTER;
+    const int st = check_packed_bwd(qkv, do_ptr, m_ptr, l_ptr, dqkv, d_workspace, B, H, T,
+                                    d_head, scale);
     if (st != ATTN_SUCCESS) return st;
-    if (!aligned16(qkv) || !aligned16(o) || !aligned16(do_ptr) || !aligned16(dqkv))
-        return ATTN_ERROR_MISALIGNED;
+    if (!aligned16(o)) return ATTN_ERROR_MISALIGNED;
     const size_t C = static_cast<size_t>(H) * d_head;
     const tcamd::HeadView xv = tcamd::packed_qkv_view(H, T, d_head);
     const tcamd::HeadView hm = tcamd::head_major_view(H, T, d_head);
     clear_error();
     tcamd::launch_flash_bwd_dq_bf16(qkv, qkv + C, qkv + 2 * C, o, do_ptr, m_ptr, l_ptr, dqkv,
                                     d_workspace, B * H, T, d_head, scale, xv, hm, xv, stream);
+    return launch_status();
+}
+
+int attn_packed_causal_backward_dkdv_bf16(const attn_bf16* qkv, const attn_bf16* do_ptr,
+                                          const float* m_ptr, const float* l_ptr,
+                                          const float* d_workspace, attn_bf16* dqkv, int B,
+                                          int H, int T, int d_head, float scale,
+                                          hipStream_t stream) {
+    const int st = check_packed_bwd(qkv, do_ptr, m_ptr, l_ptr, dqkv, d_workspace, B, H, T,
+                                    d_head, scale);
+    if (st != ATTN_SUCCESS) return st;
+    const size_t C = static_cast<size_t>(H) * d_head;
+    const tcamd::HeadView xv = tcamd::packed_qkv_view(H, T, d_head);
+    const tcamd::HeadView hm = tcamd::head_major_view(H, T, d_head);
+    clear_error();
     tcamd::launch_flash_bwd_dkdv_bf16(qkv, qkv + C, qkv + 2 * C, do_ptr, m_ptr, l_ptr,
                                       d_workspace, dqkv + C, dqkv + 2 * C, B * H, T, d_head,
                                       scale, xv, hm, xv, stream);
     return launch_status();
+}
+
+int attn_packed_causal_backward_bf16(const attn_bf16* qkv, const attn_bf16* o,
+                                     const attn_bf16* do_ptr, const float* m_ptr,
+                                     const float* l_ptr, attn_bf16* dqkv, float* d_workspace,
+                                     int B, int H, int T, int d_head, float scale,
+                                     hipStream_t stream) {
+    const int st = attn_packed_causal_backward_dq_bf16(qkv, o, do_ptr, m_ptr, l_ptr, dqkv,
+                                                       d_workspace, B, H, T, d_head, scale,
+                                                       stream);
+    if (st != ATTN_SUCCESS) return st;
+    return attn_packed_causal_backward_dkdv_bf16(qkv, do_ptr, m_ptr, l_ptr, d_workspace, dqkv,
+                                                 B, H, T, d_head, scale, stream);
 }
 
 }  // extern "C"

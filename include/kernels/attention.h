@@ -164,3 +164,53 @@ inline void tiled_causal_attention_backward_bf16(
                                         d_workspace, B, H, T, d_head, scale, stream),
         "tiled_causal_attention_backward_bf16");
 }
+
+// ---- packed QKV layout (additions; no counterpart in the reference) -----------------------
+// Attention straight from the QKV projection's output qkv (B, T, 3*H*d_head), with the
+// gradient written straight into dqkv (B, T, 3*H*d_head): one launcher replaces
+// qkv_split_transpose_forward + tiled_causal_attention_forward (src/model.cu:305-311), the
+// other tiled_causal_attention_backward + qkv_split_transpose_backward (:609-615, 653).
+// Results are bitwise those of the unfused sequences; out, o, dO stay (B, H, T, d_head).
+
+inline void packed_causal_attention_forward(const float* qkv, float* out, int B, int H, int T,
+                                            int d_head, float scale, float* m_out = nullptr,
+                                            float* l_out = nullptr,
+                                            hipStream_t stream = nullptr) {
+    tcamd::check_status(
+        attn_packed_causal_forward_f32(qkv, out, B, H, T, d_head, scale, m_out, l_out, stream),
+        "packed_causal_attention_forward");
+}
+
+inline void packed_causal_attention_backward(const float* qkv, const float* o,
+                                             const float* do_ptr, const float* m_ptr,
+                                             const float* l_ptr, float* dqkv,
+                                             float* d_workspace, int B, int H, int T,
+                                             int d_head, float scale,
+                                             hipStream_t stream = nullptr) {
+    tcamd::check_status(attn_packed_causal_backward_f32(qkv, o, do_ptr, m_ptr, l_ptr, dqkv,
+                                                        d_workspace, B, H, T, d_head, scale,
+                                                        stream),
+                        "packed_causal_attention_backward");
+}
+
+inline void packed_causal_attention_forward_bf16(const attn_bf16* qkv, attn_bf16* out, int B,
+                                                 int H, int T, int d_head, float scale,
+                                                 float* m_out = nullptr,
+                                                 float* l_out = nullptr,
+                                                 hipStream_t stream = nullptr) {
+    tcamd::check_status(
+        attn_packed_causal_forward_bf16(qkv, out, B, H, T, d_head, scale, m_out, l_out, stream),
+        "packed_causal_attention_forward_bf16");
+}
+
+inline void packed_causal_attention_backward_bf16(const attn_bf16* qkv, const attn_bf16* o,
+                                                  const attn_bf16* do_ptr, const float* m_ptr,
+                                                  const float* l_ptr, attn_bf16* dqkv,
+                                                  float* d_workspace, int B, int H, int T,
+                                                  int d_head, float scale,
+                                                  hipStream_t stream = nullptr) {
+    tcamd::check_status(attn_packed_causal_backward_bf16(qkv, o, do_ptr, m_ptr, l_ptr, dqkv,
+                                                         d_workspace, B, H, T, d_head, scale,
+                                                         stream),
+                        "packed_causal_attention_backward_bf16");
+}

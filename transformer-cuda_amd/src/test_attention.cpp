@@ -9,11 +9,14 @@
 //   * Q = 0 at T not a multiple of the tile: P_ij = 1/(i+1), O_i = mean(v_0..v_i),
 //     m_i = 0, l_i = i+1;
 //   * QKV split followed by its backward is the identity (bitwise), head merge likewise;
+//   * the packed launchers (attention straight from qkv, gradient straight into dqkv) equal
+//     split + tiled + split-back bitwise;
 //   * an unsupported head dimension throws instead of silently doing nothing.
 // Exit status 0 iff every test passes.
 #include <cmath>
 #include <cstdio>
 #include <stdexcept>
+#include <utility>
 #include <vector>
 
 #include "common.h"
@@ -174,6 +177,46 @@ bool test_split_roundtrip() {
     return true;
 }
 
+bool test_packed_matches_split(int d, int T) {
+    std::printf("[Test] packed launchers == split + tiled + split-back, bitwise (T=%d, d=%d)...\n",
+                T, d);
+    const int B = 2, H = 3;
+    const size_t n = static_cast<size_t>(B) * H * T * d;
+    const size_t r = static_cast<size_t>(B) * H * T;
+    const float scale = 1.0f / std::sqrt(static_cast<float>(d));
+    std::vector<float> hqkv(3 * n), hdo(n);
+    uint32_t state = 777u + static_cast<uint32_t>(T);
+    auto next = [&state]() {
+        state = state * 1664525u + 1013904223u;
+        return static_cast<float>(static_cast<int>(state >> 9) % 2001 - 1000) / 700.0f;
+    };
+    for (auto& x : hqkv) x = next();
+    for (auto& x : hdo) x = next();
+    DevBuf qkv(3 * n), dO(n), q(n), k(n), v(n), o1(n), m1(r), l1(r), dq(n), dk(n), dv(n),
+        dqkv1(3 * n), ws1(r), o2(n), m2(r), l2(r), dqkv2(3 * n), ws2(r);
+    qkv.upload(hqkv);
+    dO.upload(hdo);
+    qkv_split_transpose_forward(qkv.p, q.p, k.p, v.p, B, T, H, d);
+    tiled_causal_attention_forward(q.p, k.p, v.p, o1.p, B, H, T, d, scale, m1.p, l1.p);
+    tiled_causal_attention_backward(q.p, k.p, v.p, o1.p, dO.p, m1.p, l1.p, dq.p, dk.p, dv.p,
+                                    ws1.p, B, H, T, d, scale);
+    qkv_split_transpose_backward(dq.p, dk.p, dv.p, dqkv1.p, B, T, H, d);
+    packed_causal_attention_forward(qkv.p, o2.p, B, H, T, d, scale, m2.p, l2.p);
+    packed_causal_attention_backward(qkv.p, o2.p, dO.p, m2.p, l2.p, dqkv2.p, ws2.p, B, H, T, d,
+                                     scale);
+    HIP_CHECK(hipDeviceSynchronize());
+    const std::pair<const DevBuf*, const DevBuf*> pairs[] = {
+        {&o1, &o2}, {&m1, &m2}, {&l1, &l2}, {&dqkv1, &dqkv2}, {&ws1, &ws2}};
+    const char* names[] = {"O", "m", "l", "dqkv", "D"};
+    for (int t = 0; t < 5; ++t) {
+        const auto a = pairs[t].first->download(), b = pairs[t].second->download();
+        for (size_t i = 0; i < a.size(); ++i)
+            EXPECT(std::isfinite(a[i]) && a[i] == b[i], "%s[%zu]: split %.9g, packed %.9g",
+                   names[t], i, a[i], b[i]);
+    }
+    return true;
+}
+
 bool test_bad_head_dim() {
     std::printf("[Test] unsupported d_head is an error, not a silent no-op...\n");
     DevBuf buf(1024);
@@ -200,6 +243,8 @@ int main() {
     test_zero_query(128, 33);
     test_zero_query(32, 257);
     test_split_roundtrip();
+    test_packed_matches_split(64, 77);
+    test_packed_matches_split(128, 130);
     test_bad_head_dim();
     if (g_failures == 0) {
         std::printf("All host tests passed.\n");

@@ -28,22 +28,39 @@ typedef short s16x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// A 64-row x D bf16 tile in LDS: row r, 16-byte chunk c at byte r*2D + 16*(c ^ swz(r)).
-// swz(r) = 2*(r%4) + (r/4)%2 (d >= 64): eight consecutive rows get eight distinct chunk
-// slots (conflict-free 16-byte row reads), and the 4 rows x 2 chunks that a 16-lane group
-// of a transposing read touches land in 8 distinct slots (conflict-free transposing reads).
-// swz depends on r % 8 only, so row offsets that are multiples of 8 commute with it.
+// A 64-row x D bf16 tile in LDS.  Rows are grouped in blocks of 8; row r, 16-byte chunk c
+// is at byte (r/8)*B + (r%8)*2D + 16*(c ^ swz(r)), where B = 8 rows + kPad bytes.
+//   * swz(r) = 2*(r%4) + (r/4)%2 (d >= 64) gives the 8 rows of a block 8 distinct chunk
+//     slots, and the 4 rows x 2 chunks that a 16-lane group of a transposing read touches
+//     (rows inside one block) 8 distinct slots.
+//   * The LDS serves 16 lanes of a 16-byte read per cycle (64 banks x 4 bytes), so a row
+//     read (lane i: row i, same chunk) covers 16 rows, i.e. two blocks; kPad = 128 bytes
+//     after each block (d >= 64) moves the second block's rows to the other half of the
+//     256-byte bank line, where they meet no slot of the first block.
+// Both the swizzle and the padding repeat every 8 rows, so a row offset that is a multiple
+// of 8 is a constant byte offset (rows()).
 template <int D>
 struct Swz {
     static constexpr int kCpr = D / 8;  // 16-byte chunks per row
     static constexpr int kRowBytes = 2 * D;
-    static constexpr int kBytes = kRowTile * kRowBytes;
-    static constexpr int kDma = kBytes / 1024;  // wave instructions per tile
+    static constexpr int kPad = D >= 64 ? 128 : 0;
+    static constexpr int kBlockData = 8 * kRowBytes;
+    static constexpr int kBlockBytes = kBlockData + kPad;
+    static constexpr int kBytes = (kRowTile / 8) * kBlockBytes;  // one tile
+    static constexpr int kDma = kRowTile * kRowBytes / 1024;     // wave instructions per tile
+    static_assert(kPad == 0 || kBlockData % 1024 == 0, "a copy instruction stays in a block");
+    // Byte offset of row n (a multiple of 8).
+    static constexpr uint32_t rows(int n) { return static_cast<uint32_t>((n / 8) * kBlockBytes); }
+    // Byte offset of the 1 KB that copy instruction i writes (tile bytes i*1024 ..).
+    static constexpr uint32_t dma_off(int i) {
+        return static_cast<uint32_t>((i * 1024 / kBlockData) * kBlockBytes + (i * 1024) % kBlockData);
+    }
     __device__ static int swz(int r) {
         return kCpr >= 8 ? 2 * (r & 3) + ((r >> 2) & 1) : (r & (kCpr - 1));
     }
     __device__ static uint32_t off(int r, int c) {
-        return static_cast<uint32_t>(r * kRowBytes + ((c ^ swz(r)) << 4));
+        return static_cast<uint32_t>((r >> 3) * kBlockBytes + (r & 7) * kRowBytes +
+                                     ((c ^ swz(r)) << 4));
     }
 };
 
@@ -62,8 +79,7 @@ __device__ __forceinline__ void dma_tile(const uint16_t* __restrict__ head, int 
         const int r = p / S::kCpr;
         const int c = (p % S::kCpr) ^ S::swz(r);
         const int gr = min(r, T - 1 - row0);
-        dma_dwordx4(base, lds + static_cast<uint32_t>(i * 1024),
-                    static_cast<uint32_t>(gr * rs * 2 + c * 16));
+        dma_dwordx4(base, lds + S::dma_off(i), static_cast<uint32_t>(gr * rs * 2 + c * 16));
     }
 }
 

@@ -52,16 +52,16 @@ using namespace bf16t;
 // K and V tiles of stage 1 (same shape as the forward's).
 template <int D>
 struct KvSmem {
-    uint16_t k[2][kRowTile * D];
-    uint16_t v[2][kRowTile * D];
+    uint16_t k[2][Swz<D>::kBytes / 2];
+    uint16_t v[2][Swz<D>::kBytes / 2];
 };
 
 // Q and dO tiles of stage 2, each with an extra 8-element column chunk per row that carries
 // the row's statistic (see dkdv_scores).
 template <int D>
 struct QgSmem {
-    uint16_t q[2][kRowTile * D];
-    uint16_t g[2][kRowTile * D];
+    uint16_t q[2][Swz<D>::kBytes / 2];
+    uint16_t g[2][Swz<D>::kBytes / 2];
     uint16_t qx[2][kRowTile * 8];  // row r: (-lse2)_hi, (-lse2)_lo, 0 x 6
     uint16_t gx[2][kRowTile * 8];  // row r: (-D)_hi, (-D)_lo, 0 x 6
 };
@@ -136,7 +136,6 @@ __device__ __forceinline__ void dq_half(int kb, const uint32_t (&ka)[D / 16],
                                         const uint32_t (&kta)[D / 32], DqSub<D>& sb0,
                                         DqSub<D>& sb1, int qj0, int qj1, int col, int half,
                                         float c) {
-    constexpr uint32_t RB = Swz<D>::kRowBytes;
     f32x16 s0 = f32x16{}, s1 = f32x16{}, p0 = f32x16{}, p1 = f32x16{};
 #pragma unroll
     for (int st = 0; st < D / 16; ++st) {
@@ -157,7 +156,7 @@ __device__ __forceinline__ void dq_half(int kb, const uint32_t (&ka)[D / 16],
     for (int dt = 0; dt < D / 32; ++dt) {
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-            const bf16x8 a = lds_tr(kta[dt] + 16u * u * RB, 8u * RB);
+            const bf16x8 a = lds_tr(kta[dt] + u * Swz<D>::rows(16), Swz<D>::rows(8));
             sb1.acc[dt] = mfma_32x32x16_bf16(a, d1[u], sb1.acc[dt]);
             if constexpr (BOTH) sb0.acc[dt] = mfma_32x32x16_bf16(a, d0[u], sb0.acc[dt]);
         }
@@ -226,7 +225,7 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_bwd_dq_bf16_kernel(
             }
         }
         const uint32_t base = static_cast<uint32_t>(kt & 1) * S::kBytes +
-                              static_cast<uint32_t>(hh & 1) * 32u * S::kRowBytes;
+                              static_cast<uint32_t>(hh & 1) * S::rows(32);
 #pragma unroll
         for (int st = 0; st < D / 16; ++st) {
             ka[st] = k_lds + base + roff[st];
@@ -293,7 +292,6 @@ __device__ __forceinline__ void dkdv_update(const HalfAddr<D>& a, f32x16& s, con
                                             f32x16 (&dk_acc)[D / 32],
                                             f32x16 (&dv_acc)[D / 32], int qb, int kj,
                                             int half) {
-    constexpr uint32_t RB = Swz<D>::kRowBytes;
 #pragma unroll
     for (int r = 0; r < 16; ++r) s[r] = exp2_fast(s[r]);
     if constexpr (MASK) {
@@ -310,9 +308,9 @@ __device__ __forceinline__ void dkdv_update(const HalfAddr<D>& a, f32x16& s, con
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
             dv_acc[dt] =
-                mfma_32x32x16_bf16(lds_tr(a.gt[dt] + 16u * u * RB, 8u * RB), pb[u], dv_acc[dt]);
+                mfma_32x32x16_bf16(lds_tr(a.gt[dt] + u * Swz<D>::rows(16), Swz<D>::rows(8)), pb[u], dv_acc[dt]);
             dk_acc[dt] =
-                mfma_32x32x16_bf16(lds_tr(a.qt[dt] + 16u * u * RB, 8u * RB), db[u], dk_acc[dt]);
+                mfma_32x32x16_bf16(lds_tr(a.qt[dt] + u * Swz<D>::rows(16), Swz<D>::rows(8)), db[u], dk_acc[dt]);
         }
     }
 }
@@ -327,7 +325,6 @@ __global__ __launch_bounds__(kWave* NW) void flash_bwd_dkdv_bf16_kernel(
     int nblk, HeadView xv, HeadView ov, HeadView gv) {
     using S = Swz<D>;
     constexpr int kBlock = NW * kSub;  // keys per workgroup
-    constexpr uint32_t RB = S::kRowBytes;
     __shared__ __attribute__((aligned(1024))) QgSmem<D> sm;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     const int lane = threadIdx.x & (kWave - 1);
@@ -422,7 +419,7 @@ __global__ __launch_bounds__(kWave* NW) void flash_bwd_dkdv_bf16_kernel(
         HalfAddr<D> a;
         const int kt = hh >> 1;
         const uint32_t base = static_cast<uint32_t>(kt & 1) * S::kBytes +
-                              static_cast<uint32_t>(hh & 1) * 32u * RB;
+                              static_cast<uint32_t>(hh & 1) * S::rows(32);
 #pragma unroll
         for (int st = 0; st < D / 16; ++st) {
             a.q[st] = q_lds + base + roff[st];
@@ -443,7 +440,7 @@ __global__ __launch_bounds__(kWave* NW) void flash_bwd_dkdv_bf16_kernel(
     auto half_addr_c = [&](auto buf, auto hsel) {
         HalfAddr<D> a;
         constexpr uint32_t base = static_cast<uint32_t>(decltype(buf)::value) * S::kBytes +
-                                  static_cast<uint32_t>(decltype(hsel)::value) * 32u * RB;
+                                  static_cast<uint32_t>(decltype(hsel)::value) * S::rows(32);
         constexpr uint32_t xbase = static_cast<uint32_t>(decltype(buf)::value * kRowTile +
                                                          decltype(hsel)::value * 32) * 16u;
 #pragma unroll

@@ -25,8 +25,9 @@
 // and the exported (m, l) are converted to it.
 //
 // Staging.  Tiles are copied HBM -> LDS with global_load_lds_dwordx4 (1 KB per wave
-// instruction) into rows whose 16-byte chunks are XOR-swizzled by row, so that both the row
-// reads of K and the transposing reads of V hit distinct banks.
+// instruction) into rows whose 16-byte chunks are XOR-swizzled by row, with padding after
+// every 8 rows, so that both the row reads of K and the transposing reads of V hit distinct
+// banks (bf16_tile.hpp).
 #include <math.h>
 
 #include "device_common.hpp"
@@ -43,9 +44,26 @@ constexpr float kRescaleLog2 = 8.0f;  // raise the running max only beyond p = 2
 
 template <int D>
 struct FwdSmem {
-    uint16_t k[2][kKeyTile * D];
-    uint16_t v[2][kKeyTile * D];
+    uint16_t k[2][Swz<D>::kBytes / 2];
+    uint16_t v[2][Swz<D>::kBytes / 2];
 };
+
+// Maximum and sum of a lane's 16 scores as balanced trees (dependency depth 3 and 4 instead
+// of 8 and 16 for a running reduction).
+__device__ __forceinline__ float max_tree16(const f32x16& s) {
+    const float a = fmaxf(fmaxf(s[0], s[1]), s[2]), b = fmaxf(fmaxf(s[3], s[4]), s[5]);
+    const float c = fmaxf(fmaxf(s[6], s[7]), s[8]), d = fmaxf(fmaxf(s[9], s[10]), s[11]);
+    const float e = fmaxf(fmaxf(s[12], s[13]), s[14]);
+    return fmaxf(fmaxf(fmaxf(a, b), c), fmaxf(fmaxf(d, e), s[15]));
+}
+__device__ __forceinline__ float sum_tree16(const f32x16& s) {
+    float t[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) t[i] = s[2 * i] + s[2 * i + 1];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) t[i] += t[i + 4];
+    return (t[0] + t[2]) + (t[1] + t[3]);
+}
 
 // Per-wave softmax state of one 32-query sub-block.
 template <int D>
@@ -66,9 +84,7 @@ __device__ __forceinline__ void softmax_step(f32x16& s, SubState<D>& st, bf16x8 
         for (int r = 0; r < 16; ++r)
             if (kb + acc_row(r, half) > qj + col) s[r] = -INFINITY;
     }
-    float mx = fmaxf(s[0], s[1]);
-#pragma unroll
-    for (int r = 2; r < 16; ++r) mx = fmaxf(mx, s[r]);
+    float mx = max_tree16(s);
     mx = xhalf_max(mx);
     st.m_true = fmaxf(st.m_true, mx);
     if (__builtin_amdgcn_ballot_w64((mx - st.m_used) * c > kRescaleLog2) != 0) {
@@ -80,13 +96,9 @@ __device__ __forceinline__ void softmax_step(f32x16& s, SubState<D>& st, bf16x8 
         st.m_used = m_new;
     }
     const float mc = st.m_used * c;
-    float rs = 0.0f;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        s[r] = exp2_fast(fmaf(s[r], c, -mc));
-        rs += s[r];
-    }
-    st.l += xhalf_sum(rs);
+    for (int r = 0; r < 16; ++r) s[r] = exp2_fast(fmaf(s[r], c, -mc));
+    st.l += xhalf_sum(sum_tree16(s));
     pb[0] = pack_b(s, 0);
     pb[1] = pack_b(s, 1);
 }
@@ -100,7 +112,6 @@ __device__ __forceinline__ void half_step(int kb, const uint32_t (&ka)[D / 16],
                                           const bf16x8 (&q1)[D / 16], SubState<D>& st0,
                                           SubState<D>& st1, int qj0, int qj1, int col, int half,
                                           float c) {
-    constexpr uint32_t RB = Swz<D>::kRowBytes;
     f32x16 s0 = f32x16{}, s1 = f32x16{};
 #pragma unroll
     for (int st = 0; st < D / 16; ++st) {
@@ -115,7 +126,7 @@ __device__ __forceinline__ void half_step(int kb, const uint32_t (&ka)[D / 16],
     for (int dt = 0; dt < D / 32; ++dt) {
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-            const bf16x8 a = lds_tr(va[dt] + 16u * u * RB, 8u * RB);
+            const bf16x8 a = lds_tr(va[dt] + u * Swz<D>::rows(16), Swz<D>::rows(8));
             st1.acc[dt] = mfma_32x32x16_bf16(a, p1[u], st1.acc[dt]);
             if constexpr (BOTH) st0.acc[dt] = mfma_32x32x16_bf16(a, p0[u], st0.acc[dt]);
         }
@@ -193,7 +204,7 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_fwd_bf16_kernel(
             }
         }
         const uint32_t base = static_cast<uint32_t>(kt & 1) * S::kBytes +
-                              static_cast<uint32_t>(hh & 1) * 32u * S::kRowBytes;
+                              static_cast<uint32_t>(hh & 1) * S::rows(32);
 #pragma unroll
         for (int st = 0; st < D / 16; ++st) ka[st] = k_lds + base + koff[st];
 #pragma unroll

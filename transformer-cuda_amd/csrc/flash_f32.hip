@@ -15,11 +15,12 @@
 //   * dK/dV compute S = Q K^T (keys = columns), so P and dS are the B operands of
 //     dV^T += dO^T P and dK^T += Q^T dS.
 //
-// Work decomposition.  A workgroup is ONE wavefront with private LDS tiles, so there is no
-// workgroup barrier anywhere.  The kernels are persistent: as many one-wave workgroups as
-// fit resident are launched, and each wave pulls (head, block) tasks heaviest first from a
-// per-XCD atomic queue (sched.hpp), which balances the very unequal causal blocks across
-// SIMDs and keeps a head's K/V in one XCD's L2.
+// Work decomposition.  The kernels are persistent: as many workgroups as fit resident are
+// launched, and each pulls (head, block) tasks heaviest first from a per-XCD atomic queue
+// (sched.hpp), which balances the very unequal causal blocks across CUs and keeps a head's
+// K/V in one XCD's L2.  A workgroup is four wavefronts, one per SIMD; the four split the
+// task's tiles into contiguous ranges, each with private LDS tiles, and merge their partial
+// results through LDS at the end of the task (the only workgroup barriers).
 //
 // Staging.  The 32-row tiles streamed over the sequence (K/V, or Q/dO) are copied from HBM
 // straight into LDS with global_load_lds (4 bytes per lane, one row segment of 64 floats
@@ -27,7 +28,8 @@
 // tensor has one LDS tile: the next tile's copy is issued as soon as the current tile's
 // last LDS read has returned, and waited for (vmcnt) just before its first read, so the
 // copy overlaps the other tensor's contraction and the softmax; a second resident wave on
-// the SIMD covers what remains.
+// the SIMD covers what remains.  In the dQ kernel a tile starts with the V contraction, so
+// the K copy issued at the end of the previous tile lands behind it.
 //
 // Summation.  The backward kernels accumulate each 32-row tile's contraction in a fresh
 // MFMA accumulator and add the tile totals into the running sum (two-level summation), so
@@ -188,13 +190,19 @@ __device__ __forceinline__ void store_slice8(float* __restrict__ head, int row, 
     *reinterpret_cast<f32x4*>(p + 8) = b;
 }
 
-// Work split of a task over the 4 waves of a workgroup (one per SIMD): wave w takes the
-// contiguous tile range [n*w/4, n*(w+1)/4) of the task's n tiles.
-constexpr int kWaves = 4;
+// Work split of a task over the NW waves of a workgroup: wave w takes the contiguous tile
+// range [n*w/NW, n*(w+1)/NW) of the task's n tiles, and the workgroup waits at the merge
+// for the wave with the most tiles.  The forward and dK/dV kernels use 4 waves (one per
+// SIMD); the dQ kernel uses 2, which halves that wait when a task's tiles do not split
+// evenly (its per-wave LDS tiles still leave room for two waves per SIMD).
+constexpr int kFwdWaves = 4, kDqWaves = 2, kDkdvWaves = 4;
+template <int NW>
 __device__ __forceinline__ void wave_range(int n, int wave, int& t0, int& t1) {
-    t0 = n * wave / kWaves;
-    t1 = n * (wave + 1) / kWaves;
+    t0 = n * wave / NW;
+    t1 = n * (wave + 1) / NW;
 }
+
+#define TCAMD_F32_KERNEL(NW) __global__ __launch_bounds__(kWave*(NW))
 
 // The next task is fetched by lane 0 of wave 0, right after that wave's first tile copies
 // are issued, so the atomic's round trip overlaps the chunk's work.
@@ -287,11 +295,11 @@ __device__ __forceinline__ void fwd_chunk(const float* __restrict__ kh,
 }
 
 template <int D>
-__global__ __launch_bounds__(kWave* kWaves) void flash_fwd_f32_kernel(
+TCAMD_F32_KERNEL(kFwdWaves) void flash_fwd_f32_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
     float* __restrict__ o, float* __restrict__ m_out, float* __restrict__ l_out, int BH, int T,
     float scale, int nqb, QueueSlot* slot, int per_xcd, HeadView xv, HeadView ov) {
-    __shared__ FwdLds<D> L[kWaves];
+    __shared__ FwdLds<D> L[kFwdWaves];
     __shared__ unsigned s_next;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     const int lane = threadIdx.x & (kWave - 1);
@@ -307,7 +315,7 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_fwd_f32_kernel(
         const int qi = qb * kTile + col;
         const size_t xoff = wave_uniform(xv.off(bh)), ooff = wave_uniform(ov.off(bh));
         int t0, t1;
-        wave_range(qb + 1, wave, t0, t1);
+        wave_range<kFwdWaves>(qb + 1, wave, t0, t1);
 
         float qreg[D / 2];
         load_row_half<D>(qreg, q + xoff, qi, T, half, xv.row);
@@ -326,26 +334,26 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_fwd_f32_kernel(
         part[D * 32 + kWave + lane] = l_i;
         if (wave == 0 && lane == 0) s_next = fetch.value;
         __syncthreads();
-        float mw[kWaves], m_tot = -INFINITY;
+        float mw[kFwdWaves], m_tot = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) {
+        for (int w = 0; w < kFwdWaves; ++w) {
             mw[w] = reinterpret_cast<const float*>(&L[w])[D * 32 + lane];
             m_tot = fmaxf(m_tot, mw[w]);
         }
-        float aw[kWaves], l_tot = 0.0f;
+        float aw[kFwdWaves], l_tot = 0.0f;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) {
+        for (int w = 0; w < kFwdWaves; ++w) {
             aw[w] = exp2_fast((mw[w] - m_tot) * c);  // 0 for an empty chunk
             l_tot += reinterpret_cast<const float*>(&L[w])[D * 32 + kWave + lane] * aw[w];
         }
 #pragma unroll 1
-        for (int f0 = wave * 8; f0 < NP; f0 += 8 * kWaves) {  // 8-element chunks, round robin
+        for (int f0 = wave * 8; f0 < NP; f0 += 8 * kFwdWaves) {  // 8-element chunks, round robin
             float x[8];
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 float sum = 0.0f;
 #pragma unroll
-                for (int w = 0; w < kWaves; ++w)
+                for (int w = 0; w < kFwdWaves; ++w)
                     sum += reinterpret_cast<const float*>(&L[w])[(f0 + e) * kWave + lane] * aw[w];
                 x[e] = sum;
             }
@@ -384,8 +392,8 @@ __global__ __launch_bounds__(256) void dot_do_o_f32_kernel(const float* __restri
 // --------------------------------------------------------------------------------------
 // Backward stage 1 (query-parallel): D = rowsum(dO*O) and
 //     dQ_i = scale * sum_j P_ij (dP_ij - D_i) k_j,   dP = dO V^T.
-// Task = query block qb; wave w runs key tiles [n*w/4, n*(w+1)/4) of the qb+1 tiles with
-// Q, dO in VGPRs and its own K/V LDS tiles; the four partial dQ are summed by wave 0.
+// Task = query block qb; wave w of the two runs key tiles [n*w/2, n*(w+1)/2) of the qb+1
+// tiles with Q, dO in VGPRs and its own K/V LDS tiles; the partial dQ are summed in LDS.
 // --------------------------------------------------------------------------------------
 template <int D>
 struct DqLds {
@@ -415,17 +423,24 @@ __device__ __forceinline__ void dq_chunk(const float* __restrict__ kh,
         fetch.issue(lane);
         return;
     }
-    dma_tile<D, KS>(kh, t0 * kTile, T, lds_addr(L.k), lane, stride);
+    // V before K: the V copy of a tile is always the older one in flight, so each tile
+    // starts with dP (V) while the K copy issued at the end of the previous tile lands.
     dma_tile<D, VS>(vh, t0 * kTile, T, lds_addr(L.v), lane, stride);
+    dma_tile<D, KS>(kh, t0 * kTile, T, lds_addr(L.k), lane, stride);
     fetch.issue(lane);
 
     for (int t = t0; t < t1; ++t) {
         const bool more = t + 1 < t1;
-        wait_vm<0>();  // K and V tiles t landed
+        wait_vm<kTileDma<D>>();  // V tile t landed (K tile t may still be in flight)
         f32x16 dp = mma_rows<D>(Vs + col * VS + half * (D / 2), doreg, f32x16{});
-        f32x16 s = mma_rows<D>(Ks + col * KS + half * (D / 2), qreg, f32x16{});
         wait_lds();
-        if (more) dma_tile<D, VS>(vh, (t + 1) * kTile, T, lds_addr(L.v), lane, stride);
+        if (more) {
+            dma_tile<D, VS>(vh, (t + 1) * kTile, T, lds_addr(L.v), lane, stride);
+            wait_vm<kTileDma<D>>();  // K tile t landed (V tile t+1 in flight)
+        } else {
+            wait_vm<0>();
+        }
+        f32x16 s = mma_rows<D>(Ks + col * KS + half * (D / 2), qreg, f32x16{});
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             float p = exp2_fast(fmaf(s[r], c, -lse2));
@@ -442,13 +457,13 @@ __device__ __forceinline__ void dq_chunk(const float* __restrict__ kh,
 }
 
 template <int D>
-__global__ __launch_bounds__(kWave* kWaves) void flash_bwd_dq_f32_kernel(
+TCAMD_F32_KERNEL(kDqWaves) void flash_bwd_dq_f32_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
     const float* __restrict__ o, const float* __restrict__ dO, const float* __restrict__ m,
     const float* __restrict__ l, float* __restrict__ dq, float* __restrict__ Dws, int BH,
     int T, float scale, int nqb, QueueSlot* slot, int per_xcd, HeadView xv, HeadView ov,
     HeadView gv) {
-    __shared__ DqLds<D> L[kWaves];
+    __shared__ DqLds<D> L[kDqWaves];
     __shared__ unsigned s_next;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     const int lane = threadIdx.x & (kWave - 1);
@@ -467,7 +482,7 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_bwd_dq_f32_kernel(
                      goff = wave_uniform(gv.off(bh));
         const size_t stat_off = static_cast<size_t>(bh) * T;
         int t0, t1;
-        wave_range(qb + 1, wave, t0, t1);
+        wave_range<kDqWaves>(qb + 1, wave, t0, t1);
 
         float qreg[D / 2];
         float doreg[D / 2];
@@ -494,19 +509,19 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_bwd_dq_f32_kernel(
                     L[wave], lane, fetch, acc);
 
         // Merge: every wave publishes its partial dQ; wave w sums (in wave order) and stores
-        // the 8-element chunks w, w+4, ... of the flat accumulator.
+        // the 8-element chunks w, w+2, ... of the flat accumulator.
         constexpr int NP = D / 2;
         put_part(reinterpret_cast<float*>(&L[wave]), acc, lane);
         if (wave == 0 && lane == 0) s_next = fetch.value;
         __syncthreads();
 #pragma unroll 1
-        for (int f0 = wave * 8; f0 < NP; f0 += 8 * kWaves) {  // 8-element chunks, round robin
+        for (int f0 = wave * 8; f0 < NP; f0 += 8 * kDqWaves) {  // 8-element chunks, round robin
             float x[8];
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 float sum = reinterpret_cast<const float*>(&L[0])[(f0 + e) * kWave + lane];
 #pragma unroll
-                for (int w = 1; w < kWaves; ++w)
+                for (int w = 1; w < kDqWaves; ++w)
                     sum += reinterpret_cast<const float*>(&L[w])[(f0 + e) * kWave + lane];
                 x[e] = sum;
             }
@@ -607,13 +622,13 @@ __device__ __forceinline__ void dkdv_chunk(const float* __restrict__ qh,
 }
 
 template <int D>
-__global__ __launch_bounds__(kWave* kWaves) void flash_bwd_dkdv_f32_kernel(
+TCAMD_F32_KERNEL(kDkdvWaves) void flash_bwd_dkdv_f32_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
     const float* __restrict__ dO, const float* __restrict__ m, const float* __restrict__ l,
     const float* __restrict__ Dws, float* __restrict__ dk, float* __restrict__ dv, int BH,
     int T, float scale, int nkb, QueueSlot* slot, int per_xcd, HeadView xv, HeadView ov,
     HeadView gv) {
-    __shared__ DkdvLds<D> L[kWaves];
+    __shared__ DkdvLds<D> L[kDkdvWaves];
     __shared__ unsigned s_next;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     const int lane = threadIdx.x & (kWave - 1);
@@ -630,7 +645,7 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_bwd_dkdv_f32_kernel(
                      goff = wave_uniform(gv.off(bh));
         const size_t stat_off = static_cast<size_t>(bh) * T;
         int t0, t1;
-        wave_range(nkb - kb, wave, t0, t1);
+        wave_range<kDkdvWaves>(nkb - kb, wave, t0, t1);
 
         float kreg[D / 2];
         float vreg[D / 2];
@@ -650,13 +665,13 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_bwd_dkdv_f32_kernel(
         if (wave == 0 && lane == 0) s_next = fetch.value;
         __syncthreads();
 #pragma unroll 1
-        for (int f0 = wave * 8; f0 < NP; f0 += 8 * kWaves) {  // 8-element chunks, round robin
+        for (int f0 = wave * 8; f0 < NP; f0 += 8 * kDkdvWaves) {  // 8-element chunks, round robin
             float x[8];
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 float sum = reinterpret_cast<const float*>(&L[0])[(f0 + e) * kWave + lane];
 #pragma unroll
-                for (int w = 1; w < kWaves; ++w)
+                for (int w = 1; w < kDkdvWaves; ++w)
                     sum += reinterpret_cast<const float*>(&L[w])[(f0 + e) * kWave + lane];
                 x[e] = sum;
             }
@@ -711,9 +726,9 @@ void fwd_dispatch(const float* q, const float* k, const float* v, float* o, floa
                   const HeadView& ov, hipStream_t stream) {
     const int nqb = (T + kTile - 1) / kTile;
     QueueSlot* slot = queue_base(Family::Fwd) + next_queue_slot(g_fwd_ticket);
-    const int grid = persistent_grid(flash_fwd_f32_kernel<D>, kWave * kWaves, 0,
+    const int grid = persistent_grid(flash_fwd_f32_kernel<D>, kWave * kFwdWaves, 0,
                                      static_cast<long long>(BH) * nqb);
-    hipLaunchKernelGGL(flash_fwd_f32_kernel<D>, dim3(grid), dim3(kWave * kWaves), 0, stream, q, k, v, o,
+    hipLaunchKernelGGL(flash_fwd_f32_kernel<D>, dim3(grid), dim3(kWave * kFwdWaves), 0, stream, q, k, v, o,
                        m_out, l_out, BH, T, scale, nqb, slot, (BH % kXcds) == 0 ? 1 : 0, xv, ov);
 }
 
@@ -724,9 +739,9 @@ void dq_dispatch(const float* q, const float* k, const float* v, const float* o,
                  hipStream_t stream) {
     const int nqb = (T + kTile - 1) / kTile;
     QueueSlot* slot = queue_base(Family::Dq) + next_queue_slot(g_dq_ticket);
-    const int grid = persistent_grid(flash_bwd_dq_f32_kernel<D>, kWave * kWaves, 0,
+    const int grid = persistent_grid(flash_bwd_dq_f32_kernel<D>, kWave * kDqWaves, 0,
                                      static_cast<long long>(BH) * nqb);
-    hipLaunchKernelGGL(flash_bwd_dq_f32_kernel<D>, dim3(grid), dim3(kWave * kWaves), 0, stream, q, k, v,
+    hipLaunchKernelGGL(flash_bwd_dq_f32_kernel<D>, dim3(grid), dim3(kWave * kDqWaves), 0, stream, q, k, v,
                        o, dO, m, l, dq, Dws, BH, T, scale, nqb, slot,
                        (BH % kXcds) == 0 ? 1 : 0, xv, ov, gv);
 }
@@ -738,9 +753,9 @@ void dkdv_dispatch(const float* q, const float* k, const float* v, const float* 
                    const HeadView& gv, hipStream_t stream) {
     const int nkb = (T + kTile - 1) / kTile;
     QueueSlot* slot = queue_base(Family::Dkdv) + next_queue_slot(g_dkdv_ticket);
-    const int grid = persistent_grid(flash_bwd_dkdv_f32_kernel<D>, kWave * kWaves, 0,
+    const int grid = persistent_grid(flash_bwd_dkdv_f32_kernel<D>, kWave * kDkdvWaves, 0,
                                      static_cast<long long>(BH) * nkb);
-    hipLaunchKernelGGL(flash_bwd_dkdv_f32_kernel<D>, dim3(grid), dim3(kWave * kWaves), 0, stream, q, k,
+    hipLaunchKernelGGL(flash_bwd_dkdv_f32_kernel<D>, dim3(grid), dim3(kWave * kDkdvWaves), 0, stream, q, k,
                        v, dO, m, l, Dws, dk, dv, BH, T, scale, nkb, slot,
                        (BH % kXcds) == 0 ? 1 : 0, xv, ov, gv);
 }

@@ -251,6 +251,49 @@ int attn_packed_causal_backward_dkdv_bf16(const attn_bf16* qkv, const attn_bf16*
                                           int H, int T, int d_head, float scale,
                                           hipStream_t stream);
 
+/* ------------------------------------------------------------------------------------------
+ * Fused layout: packed QKV in, merged heads out.  As the packed entry points above, but the
+ * attention output `out` / `o` and its gradient `do_ptr` are in the (B, T, H*d_head) layout of
+ * head_merge_transpose_forward's output (include/kernels/attention.cuh:91-105): one launch
+ * replaces split-transpose -> tiled forward -> head merge, and the backward reads the
+ * out-projection's input gradient directly (no head_merge_transpose_backward).  Results are
+ * bitwise those of the packed entry points followed / preceded by the head merge.  No
+ * counterpart in the reference: a fused form of its src/model.cu:305-336 and :602-653.
+ * ------------------------------------------------------------------------------------------ */
+int attn_fused_causal_forward_f32(const float* qkv, float* out, int B, int H, int T,
+                                  int d_head, float scale, float* m_out, float* l_out,
+                                  hipStream_t stream);
+int attn_fused_causal_backward_f32(const float* qkv, const float* o, const float* do_ptr,
+                                   const float* m_ptr, const float* l_ptr, float* dqkv,
+                                   float* d_workspace, int B, int H, int T, int d_head,
+                                   float scale, hipStream_t stream);
+int attn_fused_causal_backward_dq_f32(const float* qkv, const float* o, const float* do_ptr,
+                                      const float* m_ptr, const float* l_ptr, float* dqkv,
+                                      float* d_workspace, int B, int H, int T, int d_head,
+                                      float scale, hipStream_t stream);
+int attn_fused_causal_backward_dkdv_f32(const float* qkv, const float* do_ptr,
+                                        const float* m_ptr, const float* l_ptr,
+                                        const float* d_workspace, float* dqkv, int B, int H,
+                                        int T, int d_head, float scale, hipStream_t stream);
+int attn_fused_causal_forward_bf16(const attn_bf16* qkv, attn_bf16* out, int B, int H, int T,
+                                   int d_head, float scale, float* m_out, float* l_out,
+                                   hipStream_t stream);
+int attn_fused_causal_backward_bf16(const attn_bf16* qkv, const attn_bf16* o,
+                                    const attn_bf16* do_ptr, const float* m_ptr,
+                                    const float* l_ptr, attn_bf16* dqkv, float* d_workspace,
+                                    int B, int H, int T, int d_head, float scale,
+                                    hipStream_t stream);
+int attn_fused_causal_backward_dq_bf16(const attn_bf16* qkv, const attn_bf16* o,
+                                       const attn_bf16* do_ptr, const float* m_ptr,
+                                       const float* l_ptr, attn_bf16* dqkv, float* d_workspace,
+                                       int B, int H, int T, int d_head, float scale,
+                                       hipStream_t stream);
+int attn_fused_causal_backward_dkdv_bf16(const attn_bf16* qkv, const attn_bf16* do_ptr,
+                                         const float* m_ptr, const float* l_ptr,
+                                         const float* d_workspace, attn_bf16* dqkv, int B,
+                                         int H, int T, int d_head, float scale,
+                                         hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -214,3 +214,49 @@ inline void packed_causal_attention_backward_bf16(const attn_bf16* qkv, const at
                                                          stream),
                         "packed_causal_attention_backward_bf16");
 }
+
+// ---- fused layout: packed QKV in, merged heads out (additions; no counterpart) ----------
+// As the packed launchers, with the attention output and its gradient in the (B, T, H*d_head)
+// layout of head_merge_transpose_forward's output: the forward also replaces the head merge
+// at src/model.cu:336, the backward the head_merge_transpose_backward at :602.
+
+inline void fused_causal_attention_forward(const float* qkv, float* out, int B, int H, int T,
+                                           int d_head, float scale, float* m_out = nullptr,
+                                           float* l_out = nullptr,
+                                           hipStream_t stream = nullptr) {
+    tcamd::check_status(
+        attn_fused_causal_forward_f32(qkv, out, B, H, T, d_head, scale, m_out, l_out, stream),
+        "fused_causal_attention_forward");
+}
+
+inline void fused_causal_attention_backward(const float* qkv, const float* o,
+                                            const float* do_ptr, const float* m_ptr,
+                                            const float* l_ptr, float* dqkv, float* d_workspace,
+                                            int B, int H, int T, int d_head, float scale,
+                                            hipStream_t stream = nullptr) {
+    tcamd::check_status(attn_fused_causal_backward_f32(qkv, o, do_ptr, m_ptr, l_ptr, dqkv,
+                                                       d_workspace, B, H, T, d_head, scale,
+                                                       stream),
+                        "fused_causal_attention_backward");
+}
+
+inline void fused_causal_attention_forward_bf16(const attn_bf16* qkv, attn_bf16* out, int B,
+                                                int H, int T, int d_head, float scale,
+                                                float* m_out = nullptr, float* l_out = nullptr,
+                                                hipStream_t stream = nullptr) {
+    tcamd::check_status(
+        attn_fused_causal_forward_bf16(qkv, out, B, H, T, d_head, scale, m_out, l_out, stream),
+        "fused_causal_attention_forward_bf16");
+}
+
+inline void fused_causal_attention_backward_bf16(const attn_bf16* qkv, const attn_bf16* o,
+                                                 const attn_bf16* do_ptr, const float* m_ptr,
+                                                 const float* l_ptr, attn_bf16* dqkv,
+                                                 float* d_workspace, int B, int H, int T,
+                                                 int d_head, float scale,
+                                                 hipStream_t stream = nullptr) {
+    tcamd::check_status(attn_fused_causal_backward_bf16(qkv, o, do_ptr, m_ptr, l_ptr, dqkv,
+                                                        d_workspace, B, H, T, d_head, scale,
+                                                        stream),
+                        "fused_causal_attention_backward_bf16");
+}

@@ -66,6 +66,14 @@ SIGNATURES = {
     "attn_packed_causal_backward_dkdv_bf16": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P],
     "attn_packed_causal_forward_bf16": [_P, _P, _I, _I, _I, _I, _F, _P, _P, _P],
     "attn_packed_causal_backward_bf16": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P],
+    "attn_fused_causal_forward_f32": [_P, _P, _I, _I, _I, _I, _F, _P, _P, _P],
+    "attn_fused_causal_backward_f32": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P],
+    "attn_fused_causal_backward_dq_f32": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P],
+    "attn_fused_causal_backward_dkdv_f32": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P],
+    "attn_fused_causal_forward_bf16": [_P, _P, _I, _I, _I, _I, _F, _P, _P, _P],
+    "attn_fused_causal_backward_bf16": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P],
+    "attn_fused_causal_backward_dq_bf16": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P],
+    "attn_fused_causal_backward_dkdv_bf16": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P],
     "attn_materialized_causal_backward_f32":
         [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P],
     "attn_tiled_causal_forward_f32": [_P, _P, _P, _P, _I, _I, _I, _I, _F, _P, _P, _P],
@@ -281,64 +289,93 @@ def tiled_causal_attention_forward(q, k, v, out, B, H, T, d_head, scale, m_out=N
           "tiled_causal_attention_forward")
 
 
+def _qkv_forward(family, qkv, out, B, H, T, d_head, scale, m_out, l_out, stream):
+    torch = _torch()
+    bf = qkv.dtype == torch.bfloat16
+    n, r = B * H * T * d_head, B * H * T
+    dt, f32 = _dt(bf), _dt(False)
+    check(call(f"attn_{family}_causal_forward_" + ("bf16" if bf else "f32"),
+               _ptr(qkv, dt, 3 * n, "qkv"), _ptr(out, dt, n, "out"), B, H, T, d_head,
+               float(scale), _ptr(m_out, f32, r, "m_out"), _ptr(l_out, f32, r, "l_out"),
+               _stream(stream)), f"{family}_causal_attention_forward")
+
+
+def _qkv_backward(family, stage, qkv, o, dO, m, l, dqkv, workspace, B, H, T, d_head, scale,
+                  stream):
+    torch = _torch()
+    bf = qkv.dtype == torch.bfloat16
+    n, r = B * H * T * d_head, B * H * T
+    dt, f32 = _dt(bf), _dt(False)
+    name = f"attn_{family}_causal_backward{stage}_" + ("bf16" if bf else "f32")
+    if stage == "_dkdv":
+        args = (_ptr(qkv, dt, 3 * n, "qkv"), _ptr(dO, dt, n, "dO"), _ptr(m, f32, r, "m"),
+                _ptr(l, f32, r, "l"), _ptr(workspace, f32, r, "workspace"),
+                _ptr(dqkv, dt, 3 * n, "dqkv"))
+    else:
+        args = (_ptr(qkv, dt, 3 * n, "qkv"), _ptr(o, dt, n, "o"), _ptr(dO, dt, n, "dO"),
+                _ptr(m, f32, r, "m"), _ptr(l, f32, r, "l"), _ptr(dqkv, dt, 3 * n, "dqkv"),
+                _ptr(workspace, f32, r, "workspace"))
+    check(call(name, *args, B, H, T, d_head, float(scale), _stream(stream)),
+          f"{family}_causal_attention_backward{stage}")
+
+
 def packed_causal_attention_forward(qkv, out, B, H, T, d_head, scale, m_out=None,
                                     l_out=None, stream=None):
     """Attention straight from the QKV projection's packed output qkv (B, T, 3*H*d): the
     split-transpose (include/kernels/attention.cuh:5-11) happens in the kernels' tile
     copies.  out (B, H, T, d); fp32 or bf16 by the tensors' dtype."""
-    torch = _torch()
-    bf = qkv.dtype == torch.bfloat16
-    n = B * H * T * d_head
-    r = B * H * T
-    dt, f32 = _dt(bf), _dt(False)
-    name = "attn_packed_causal_forward_" + ("bf16" if bf else "f32")
-    check(call(name, _ptr(qkv, dt, 3 * n, "qkv"), _ptr(out, dt, n, "out"), B, H, T, d_head,
-               float(scale), _ptr(m_out, f32, r, "m_out"), _ptr(l_out, f32, r, "l_out"),
-               _stream(stream)), "packed_causal_attention_forward")
+    _qkv_forward("packed", qkv, out, B, H, T, d_head, scale, m_out, l_out, stream)
 
 
 def packed_causal_attention_backward(qkv, o, dO, m, l, dqkv, workspace, B, H, T, d_head, scale,
                                      stream=None):
     """Backward from the packed qkv, writing dq, dk, dv straight into dqkv (B, T, 3*H*d), the
     layout qkv_split_transpose_backward (include/kernels/attention.cuh:13-19) produces."""
-    torch = _torch()
-    bf = qkv.dtype == torch.bfloat16
-    n = B * H * T * d_head
-    r = B * H * T
-    dt, f32 = _dt(bf), _dt(False)
-    name = "attn_packed_causal_backward_" + ("bf16" if bf else "f32")
-    check(call(name, _ptr(qkv, dt, 3 * n, "qkv"), _ptr(o, dt, n, "o"), _ptr(dO, dt, n, "dO"),
-               _ptr(m, f32, r, "m"), _ptr(l, f32, r, "l"), _ptr(dqkv, dt, 3 * n, "dqkv"),
-               _ptr(workspace, f32, r, "workspace"), B, H, T, d_head, float(scale),
-               _stream(stream)), "packed_causal_attention_backward")
+    _qkv_backward("packed", "", qkv, o, dO, m, l, dqkv, workspace, B, H, T, d_head, scale,
+                  stream)
 
 
 def packed_causal_attention_backward_dq(qkv, o, dO, m, l, dqkv, workspace, B, H, T, d_head,
                                         scale, stream=None):
     """Stage 1 of the packed backward: D into workspace, dq into the q block of dqkv."""
-    torch = _torch()
-    bf = qkv.dtype == torch.bfloat16
-    n, r = B * H * T * d_head, B * H * T
-    dt, f32 = _dt(bf), _dt(False)
-    check(call("attn_packed_causal_backward_dq_" + ("bf16" if bf else "f32"),
-               _ptr(qkv, dt, 3 * n, "qkv"), _ptr(o, dt, n, "o"), _ptr(dO, dt, n, "dO"),
-               _ptr(m, f32, r, "m"), _ptr(l, f32, r, "l"), _ptr(dqkv, dt, 3 * n, "dqkv"),
-               _ptr(workspace, f32, r, "workspace"), B, H, T, d_head, float(scale),
-               _stream(stream)), "packed_causal_attention_backward_dq")
+    _qkv_backward("packed", "_dq", qkv, o, dO, m, l, dqkv, workspace, B, H, T, d_head, scale,
+                  stream)
 
 
 def packed_causal_attention_backward_dkdv(qkv, dO, m, l, workspace, dqkv, B, H, T, d_head,
                                           scale, stream=None):
     """Stage 2 of the packed backward: dk, dv into the k and v blocks of dqkv."""
-    torch = _torch()
-    bf = qkv.dtype == torch.bfloat16
-    n, r = B * H * T * d_head, B * H * T
-    dt, f32 = _dt(bf), _dt(False)
-    check(call("attn_packed_causal_backward_dkdv_" + ("bf16" if bf else "f32"),
-               _ptr(qkv, dt, 3 * n, "qkv"), _ptr(dO, dt, n, "dO"), _ptr(m, f32, r, "m"),
-               _ptr(l, f32, r, "l"), _ptr(workspace, f32, r, "workspace"),
-               _ptr(dqkv, dt, 3 * n, "dqkv"), B, H, T, d_head, float(scale), _stream(stream)),
-          "packed_causal_attention_backward_dkdv")
+    _qkv_backward("packed", "_dkdv", qkv, None, dO, m, l, dqkv, workspace, B, H, T, d_head,
+                  scale, stream)
+
+
+def fused_causal_attention_forward(qkv, out, B, H, T, d_head, scale, m_out=None, l_out=None,
+                                   stream=None):
+    """As packed_causal_attention_forward, with out in the merged-heads layout (B, T, H*d)
+    that head_merge_transpose_forward (include/kernels/attention.cuh:91-97) produces."""
+    _qkv_forward("fused", qkv, out, B, H, T, d_head, scale, m_out, l_out, stream)
+
+
+def fused_causal_attention_backward(qkv, o, dO, m, l, dqkv, workspace, B, H, T, d_head, scale,
+                                    stream=None):
+    """As packed_causal_attention_backward, with o and dO in the merged-heads layout
+    (B, T, H*d) (dO as head_merge_transpose_backward's input, attention.cuh:99-105)."""
+    _qkv_backward("fused", "", qkv, o, dO, m, l, dqkv, workspace, B, H, T, d_head, scale,
+                  stream)
+
+
+def fused_causal_attention_backward_dq(qkv, o, dO, m, l, dqkv, workspace, B, H, T, d_head,
+                                       scale, stream=None):
+    """Stage 1 of the fused backward."""
+    _qkv_backward("fused", "_dq", qkv, o, dO, m, l, dqkv, workspace, B, H, T, d_head, scale,
+                  stream)
+
+
+def fused_causal_attention_backward_dkdv(qkv, dO, m, l, workspace, dqkv, B, H, T, d_head,
+                                         scale, stream=None):
+    """Stage 2 of the fused backward."""
+    _qkv_backward("fused", "_dkdv", qkv, None, dO, m, l, dqkv, workspace, B, H, T, d_head,
+                  scale, stream)
 
 
 def attention_precompute_dot_do_o(dO, O, D, B, H, T, d_head, stream=None):

@@ -80,7 +80,128 @@ int split_common(const void* rm, ElemType rm_t, void* q, void* k, void* v, ElemT
     return launch_status();
 }
 
+// ---- packed-QKV implementations (shared by the packed and fused entry points) ----------
+// q, k, v are read from qkv (B, T, 3C) and dq, dk, dv written into dqkv; o and dO are
+// head-major (B, H, T, d) or, `merged`, in the (B, T, C) layout of the head merge.
+
+void flash_fwd(const float* q, const float* k, const float* v, float* o, float* m, float* l,
+               int BH, int T, int d, float scale, const tcamd::HeadView& xv,
+               const tcamd::HeadView& ov, hipStream_t s) {
+    tcamd::launch_flash_fwd_f32(q, k, v, o, m, l, BH, T, d, scale, xv, ov, s);
+}
+void flash_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o, float* m,
+               float* l, int BH, int T, int d, float scale, const tcamd::HeadView& xv,
+               const tcamd::HeadView& ov, hipStream_t s) {
+    tcamd::launch_flash_fwd_bf16(q, k, v, o, m, l, BH, T, d, scale, xv, ov, s);
+}
+void flash_dq(const float* q, const float* k, const float* v, const float* o, const float* dO,
+              const float* m, const float* l, float* dq, float* ws, int BH, int T, int d,
+              float scale, const tcamd::HeadView& xv, const tcamd::HeadView& ov,
+              const tcamd::HeadView& gv, hipStream_t s) {
+    tcamd::launch_flash_bwd_dq_f32(q, k, v, o, dO, m, l, dq, ws, BH, T, d, scale, xv, ov, gv, s);
+}
+void flash_dq(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* o,
+              const uint16_t* dO, const float* m, const float* l, uint16_t* dq, float* ws,
+              int BH, int T, int d, float scale, const tcamd::HeadView& xv,
+              const tcamd::HeadView& ov, const tcamd::HeadView& gv, hipStream_t s) {
+    tcamd::launch_flash_bwd_dq_bf16(q, k, v, o, dO, m, l, dq, ws, BH, T, d, scale, xv, ov, gv, s);
+}
+void flash_dkdv(const float* q, const float* k, const float* v, const float* dO, const float* m,
+                const float* l, const float* ws, float* dk, float* dv, int BH, int T, int d,
+                float scale, const tcamd::HeadView& xv, const tcamd::HeadView& ov,
+                const tcamd::HeadView& gv, hipStream_t s) {
+    tcamd::launch_flash_bwd_dkdv_f32(q, k, v, dO, m, l, ws, dk, dv, BH, T, d, scale, xv, ov, gv,
+                                     s);
+}
+void flash_dkdv(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* dO,
+                const float* m, const float* l, const float* ws, uint16_t* dk, uint16_t* dv,
+                int BH, int T, int d, float scale, const tcamd::HeadView& xv,
+                const tcamd::HeadView& ov, const tcamd::HeadView& gv, hipStream_t s) {
+    tcamd::launch_flash_bwd_dkdv_bf16(q, k, v, dO, m, l, ws, dk, dv, BH, T, d, scale, xv, ov, gv,
+                                      s);
+}
+
+tcamd::HeadView out_view(int H, int T, int d, bool merged) {
+    return merged ? tcamd::merged_view(H, T, d) : tcamd::head_major_view(H, T, d);
+}
+
+// The qkv row stride 3*H*d is an int in the kernels.
+int check_packed(int B, int H, int T, int d, float scale) {
+    const int st = check_tiled(B, H, T, d, scale);
+    if (st != ATTN_SUCCESS) return st;
+    if (3LL * H * d > kInt32Max) return ATTN_ERROR_INVALID_DIM;
+    return ATTN_SUCCESS;
+}
+
+template <typename E>
+int packed_forward(const E* qkv, E* out, int B, int H, int T, int d, float scale, float* m_out,
+                   float* l_out, bool merged, hipStream_t stream) {
+    if (qkv == nullptr || out == nullptr) return ATTN_ERROR_NULL_POINTER;
+    const int st = check_packed(B, H, T, d, scale);
+    if (st != ATTN_SUCCESS) return st;
+    if (!aligned16(qkv) || !aligned16(out)) return ATTN_ERROR_MISALIGNED;
+    const size_t C = static_cast<size_t>(H) * d;
+    clear_error();
+    flash_fwd(qkv, qkv + C, qkv + 2 * C, out, m_out, l_out, B * H, T, d, scale,
+              tcamd::packed_qkv_view(H, T, d), out_view(H, T, d, merged), stream);
+    return launch_status();
+}
+
+// Shared checks of the packed-layout backward stages.
+int check_packed_bwd(const void* qkv, const void* dO, const void* m, const void* l,
+                     const void* dqkv, const void* ws, int B, int H, int T, int d,
+                     float scale) {
+    if (qkv == nullptr || dO == nullptr || m == nullptr || l == nullptr || dqkv == nullptr ||
+        ws == nullptr)
+        return ATTN_ERROR_NULL_POINTER;
+    const int st = check_packed(B, H, T, d, scale);
+    if (st != ATTN_SUCCESS) return st;
+    if (!aligned16(qkv) || !aligned16(dO) || !aligned16(dqkv)) return ATTN_ERROR_MISALIGNED;
+    return ATTN_SUCCESS;
+}
+
+template <typename E>
+int packed_backward_dq(const E* qkv, const E* o, const E* dO, const float* m, const float* l,
+                       E* dqkv, float* ws, int B, int H, int T, int d, float scale, bool merged,
+                       hipStream_t stream) {
+    if (o == nullptr) return ATTN_ERROR_NULL_POINTER;
+    const int st = check_packed_bwd(qkv, dO, m, l, dqkv, ws, B, H, T, d, scale);
+    if (st != ATTN_SUCCESS) return st;
+    if (!aligned16(o)) return ATTN_ERROR_MISALIGNED;
+    const size_t C = static_cast<size_t>(H) * d;
+    const tcamd::HeadView xv = tcamd::packed_qkv_view(H, T, d);
+    clear_error();
+    flash_dq(qkv, qkv + C, qkv + 2 * C, o, dO, m, l, dqkv, ws, B * H, T, d, scale, xv,
+             out_view(H, T, d, merged), xv, stream);
+    return launch_status();
+}
+
+template <typename E>
+int packed_backward_dkdv(const E* qkv, const E* dO, const float* m, const float* l,
+                         const float* ws, E* dqkv, int B, int H, int T, int d, float scale,
+                         bool merged, hipStream_t stream) {
+    const int st = check_packed_bwd(qkv, dO, m, l, dqkv, ws, B, H, T, d, scale);
+    if (st != ATTN_SUCCESS) return st;
+    const size_t C = static_cast<size_t>(H) * d;
+    const tcamd::HeadView xv = tcamd::packed_qkv_view(H, T, d);
+    clear_error();
+    flash_dkdv(qkv, qkv + C, qkv + 2 * C, dO, m, l, ws, dqkv + C, dqkv + 2 * C, B * H, T, d,
+               scale, xv, out_view(H, T, d, merged), xv, stream);
+    return launch_status();
+}
+
+template <typename E>
+int packed_backward(const E* qkv, const E* o, const E* dO, const float* m, const float* l,
+                    E* dqkv, float* ws, int B, int H, int T, int d, float scale, bool merged,
+                    hipStream_t stream) {
+    const int st = packed_backward_dq(qkv, o, dO, m, l, dqkv, ws, B, H, T, d, scale, merged,
+                                      stream);
+    if (st != ATTN_SUCCESS) return st;
+    return packed_backward_dkdv(qkv, dO, m, l, ws, dqkv, B, H, T, d, scale, merged, stream);
+}
+
 }  // namespace
+
 
 extern "C" {
 
@@ -432,145 +553,115 @@ int attn_tiled_causal_backward_bf16(const attn_bf16* q, const attn_bf16* k,
 int attn_packed_causal_forward_f32(const float* qkv, float* out, int B, int H, int T,
                                    int d_head, float scale, float* m_out, float* l_out,
                                    hipStream_t stream) {
-    if (qkv == nullptr || out == nullptr) return ATTN_ERROR_NULL_POINTER;
-    const int st = check_tiled(B, H, T, d_head, scale);
-    if (st != ATTN_SUCCESS) return st;
-    if (!aligned16(qkv) || !aligned16(out)) return ATTN_ERROR_MISALIGNED;
-    const size_t C = static_cast<size_t>(H) * d_head;
-    const tcamd::HeadView xv = tcamd::packed_qkv_view(H, T, d_head);
-    const tcamd::HeadView hm = tcamd::head_major_view(H, T, d_head);
-    clear_error();
-    tcamd::launch_flash_fwd_f32(qkv, qkv + C, qkv + 2 * C, out, m_out, l_out, B * H, T, d_head,
-                                scale, xv, hm, stream);
-    return launch_status();
+    return packed_forward(qkv, out, B, H, T, d_head, scale, m_out, l_out, false, stream);
 }
-
-namespace {
-// Shared checks of the packed-layout backward stages.
-int check_packed_bwd(const void* qkv, const void* dO, const void* m, const void* l,
-                     const void* dqkv, const void* ws, int B, int H, int T, int d,
-                     float scale) {
-    if (qkv == nullptr || dO == nullptr || m == nullptr || l == nullptr || dqkv == nullptr ||
-        ws == nullptr)
-        return ATTN_ERROR_NULL_POINTER;
-    const int st = check_tiled(B, H, T, d, scale);
-    if (st != ATTN_SUCCESS) return st;
-    if (!aligned16(qkv) || !aligned16(dO) || !aligned16(dqkv)) return ATTN_ERROR_MISALIGNED;
-    return ATTN_SUCCESS;
-}
-}  // namespace
-
 int attn_packed_causal_backward_dq_f32(const float* qkv, const float* o, const float* do_ptr,
                                        const float* m_ptr, const float* l_ptr, float* dqkv,
                                        float* d_workspace, int B, int H, int T, int d_head,
                                        float scale, hipStream_t stream) {
-    if (o == nullptr) return ATTN_ERROR_NULL_POINTER;
-    const int st = check_packed_bwd(qkv, do_ptr, m_ptr, l_ptr, dqkv, d_workspace, B, H, T,
-                                    d_head, scale);
-    if (st != ATTN_SUCCESS) return st;
-    if (!aligned16(o)) return ATTN_ERROR_MISALIGNED;
-    const size_t C = static_cast<size_t>(H) * d_head;
-    const tcamd::HeadView xv = tcamd::packed_qkv_view(H, T, d_head);
-    const tcamd::HeadView hm = tcamd::head_major_view(H, T, d_head);
-    clear_error();
-    tcamd::launch_flash_bwd_dq_f32(qkv, qkv + C, qkv + 2 * C, o, do_ptr, m_ptr, l_ptr, dqkv,
-                                   d_workspace, B * H, T, d_head, scale, xv, hm, xv, stream);
-    return launch_status();
+    return packed_backward_dq(qkv, o, do_ptr, m_ptr, l_ptr, dqkv, d_workspace, B, H, T, d_head,
+                              scale, false, stream);
 }
-
 int attn_packed_causal_backward_dkdv_f32(const float* qkv, const float* do_ptr,
                                          const float* m_ptr, const float* l_ptr,
                                          const float* d_workspace, float* dqkv, int B, int H,
                                          int T, int d_head, float scale, hipStream_t stream) {
-    const int st = check_packed_bwd(qkv, do_ptr, m_ptr, l_ptr, dqkv, d_workspace, B, H, T,
-                                    d_head, scale);
-    if (st != ATTN_SUCCESS) return st;
-    const size_t C = static_cast<size_t>(H) * d_head;
-    const tcamd::HeadView xv = tcamd::packed_qkv_view(H, T, d_head);
-    const tcamd::HeadView hm = tcamd::head_major_view(H, T, d_head);
-    clear_error();
-    tcamd::launch_flash_bwd_dkdv_f32(qkv, qkv + C, qkv + 2 * C, do_ptr, m_ptr, l_ptr,
-                                     d_workspace, dqkv + C, dqkv + 2 * C, B * H, T, d_head,
-                                     scale, xv, hm, xv, stream);
-    return launch_status();
+    return packed_backward_dkdv(qkv, do_ptr, m_ptr, l_ptr, d_workspace, dqkv, B, H, T, d_head,
+                                scale, false, stream);
 }
-
 int attn_packed_causal_backward_f32(const float* qkv, const float* o, const float* do_ptr,
                                     const float* m_ptr, const float* l_ptr, float* dqkv,
                                     float* d_workspace, int B, int H, int T, int d_head,
                                     float scale, hipStream_t stream) {
-    const int st = attn_packed_causal_backward_dq_f32(qkv, o, do_ptr, m_ptr, l_ptr, dqkv,
-                                                      d_workspace, B, H, T, d_head, scale,
-                                                      stream);
-    if (st != ATTN_SUCCESS) return st;
-    return attn_packed_causal_backward_dkdv_f32(qkv, do_ptr, m_ptr, l_ptr, d_workspace, dqkv, B,
-                                                H, T, d_head, scale, stream);
+    return packed_backward(qkv, o, do_ptr, m_ptr, l_ptr, dqkv, d_workspace, B, H, T, d_head,
+                           scale, false, stream);
 }
-
 int attn_packed_causal_forward_bf16(const attn_bf16* qkv, attn_bf16* out, int B, int H, int T,
                                     int d_head, float scale, float* m_out, float* l_out,
                                     hipStream_t stream) {
-    if (qkv == nullptr || out == nullptr) return ATTN_ERROR_NULL_POINTER;
-    const int st = check_tiled(B, H, T, d_head, scale);
-    if (st != ATTN_SUCCESS) return st;
-    if (!aligned16(qkv) || !aligned16(out)) return ATTN_ERROR_MISALIGNED;
-    const size_t C = static_cast<size_t>(H) * d_head;
-    const tcamd::HeadView xv = tcamd::packed_qkv_view(H, T, d_head);
-    const tcamd::HeadView hm = tcamd::head_major_view(H, T, d_head);
-    clear_error();
-    tcamd::launch_flash_fwd_bf16(qkv, qkv + C, qkv + 2 * C, out, m_out, l_out, B * H, T, d_head,
-                                 scale, xv, hm, stream);
-    return launch_status();
+    return packed_forward(qkv, out, B, H, T, d_head, scale, m_out, l_out, false, stream);
 }
-
 int attn_packed_causal_backward_dq_bf16(const attn_bf16* qkv, const attn_bf16* o,
                                         const attn_bf16* do_ptr, const float* m_ptr,
                                         const float* l_ptr, attn_bf16* dqkv, float* d_workspace,
                                         int B, int H, int T, int d_head, float scale,
                                         hipStream_t stream) {
-    if (o == nullptr) return ATTN_ERROR_NULL_POINTER;
-    const int st = check_packed_bwd(qkv, do_ptr, m_ptr, l_ptr, dqkv, d_workspace, B, H, T,
-                                    d_head, scale);
-    if (st != ATTN_SUCCESS) return st;
-    if (!aligned16(o)) return ATTN_ERROR_MISALIGNED;
-    const size_t C = static_cast<size_t>(H) * d_head;
-    const tcamd::HeadView xv = tcamd::packed_qkv_view(H, T, d_head);
-    const tcamd::HeadView hm = tcamd::head_major_view(H, T, d_head);
-    clear_error();
-    tcamd::launch_flash_bwd_dq_bf16(qkv, qkv + C, qkv + 2 * C, o, do_ptr, m_ptr, l_ptr, dqkv,
-                                    d_workspace, B * H, T, d_head, scale, xv, hm, xv, stream);
-    return launch_status();
+    return packed_backward_dq(qkv, o, do_ptr, m_ptr, l_ptr, dqkv, d_workspace, B, H, T, d_head,
+                              scale, false, stream);
 }
-
 int attn_packed_causal_backward_dkdv_bf16(const attn_bf16* qkv, const attn_bf16* do_ptr,
                                           const float* m_ptr, const float* l_ptr,
                                           const float* d_workspace, attn_bf16* dqkv, int B,
                                           int H, int T, int d_head, float scale,
                                           hipStream_t stream) {
-    const int st = check_packed_bwd(qkv, do_ptr, m_ptr, l_ptr, dqkv, d_workspace, B, H, T,
-                                    d_head, scale);
-    if (st != ATTN_SUCCESS) return st;
-    const size_t C = static_cast<size_t>(H) * d_head;
-    const tcamd::HeadView xv = tcamd::packed_qkv_view(H, T, d_head);
-    const tcamd::HeadView hm = tcamd::head_major_view(H, T, d_head);
-    clear_error();
-    tcamd::launch_flash_bwd_dkdv_bf16(qkv, qkv + C, qkv + 2 * C, do_ptr, m_ptr, l_ptr,
-                                      d_workspace, dqkv + C, dqkv + 2 * C, B * H, T, d_head,
-                                      scale, xv, hm, xv, stream);
-    return launch_status();
+    return packed_backward_dkdv(qkv, do_ptr, m_ptr, l_ptr, d_workspace, dqkv, B, H, T, d_head,
+                                scale, false, stream);
 }
-
 int attn_packed_causal_backward_bf16(const attn_bf16* qkv, const attn_bf16* o,
                                      const attn_bf16* do_ptr, const float* m_ptr,
                                      const float* l_ptr, attn_bf16* dqkv, float* d_workspace,
                                      int B, int H, int T, int d_head, float scale,
                                      hipStream_t stream) {
-    const int st = attn_packed_causal_backward_dq_bf16(qkv, o, do_ptr, m_ptr, l_ptr, dqkv,
-                                                       d_workspace, B, H, T, d_head, scale,
-                                                       stream);
-    if (st != ATTN_SUCCESS) return st;
-    return attn_packed_causal_backward_dkdv_bf16(qkv, do_ptr, m_ptr, l_ptr, d_workspace, dqkv,
-                                                 B, H, T, d_head, scale, stream);
+    return packed_backward(qkv, o, do_ptr, m_ptr, l_ptr, dqkv, d_workspace, B, H, T, d_head,
+                           scale, false, stream);
+}
+
+// ---- fused: packed QKV in, heads merged out (split-transpose and head merge fused) -------
+
+int attn_fused_causal_forward_f32(const float* qkv, float* out, int B, int H, int T,
+                                  int d_head, float scale, float* m_out, float* l_out,
+                                  hipStream_t stream) {
+    return packed_forward(qkv, out, B, H, T, d_head, scale, m_out, l_out, true, stream);
+}
+int attn_fused_causal_backward_dq_f32(const float* qkv, const float* o, const float* do_ptr,
+                                      const float* m_ptr, const float* l_ptr, float* dqkv,
+                                      float* d_workspace, int B, int H, int T, int d_head,
+                                      float scale, hipStream_t stream) {
+    return packed_backward_dq(qkv, o, do_ptr, m_ptr, l_ptr, dqkv, d_workspace, B, H, T, d_head,
+                              scale, true, stream);
+}
+int attn_fused_causal_backward_dkdv_f32(const float* qkv, const float* do_ptr,
+                                        const float* m_ptr, const float* l_ptr,
+                                        const float* d_workspace, float* dqkv, int B, int H,
+                                        int T, int d_head, float scale, hipStream_t stream) {
+    return packed_backward_dkdv(qkv, do_ptr, m_ptr, l_ptr, d_workspace, dqkv, B, H, T, d_head,
+                                scale, true, stream);
+}
+int attn_fused_causal_backward_f32(const float* qkv, const float* o, const float* do_ptr,
+                                   const float* m_ptr, const float* l_ptr, float* dqkv,
+                                   float* d_workspace, int B, int H, int T, int d_head,
+                                   float scale, hipStream_t stream) {
+    return packed_backward(qkv, o, do_ptr, m_ptr, l_ptr, dqkv, d_workspace, B, H, T, d_head,
+                           scale, true, stream);
+}
+int attn_fused_causal_forward_bf16(const attn_bf16* qkv, attn_bf16* out, int B, int H, int T,
+                                   int d_head, float scale, float* m_out, float* l_out,
+                                   hipStream_t stream) {
+    return packed_forward(qkv, out, B, H, T, d_head, scale, m_out, l_out, true, stream);
+}
+int attn_fused_causal_backward_dq_bf16(const attn_bf16* qkv, const attn_bf16* o,
+                                       const attn_bf16* do_ptr, const float* m_ptr,
+                                       const float* l_ptr, attn_bf16* dqkv, float* d_workspace,
+                                       int B, int H, int T, int d_head, float scale,
+                                       hipStream_t stream) {
+    return packed_backward_dq(qkv, o, do_ptr, m_ptr, l_ptr, dqkv, d_workspace, B, H, T, d_head,
+                              scale, true, stream);
+}
+int attn_fused_causal_backward_dkdv_bf16(const attn_bf16* qkv, const attn_bf16* do_ptr,
+                                         const float* m_ptr, const float* l_ptr,
+                                         const float* d_workspace, attn_bf16* dqkv, int B,
+                                         int H, int T, int d_head, float scale,
+                                         hipStream_t stream) {
+    return packed_backward_dkdv(qkv, do_ptr, m_ptr, l_ptr, d_workspace, dqkv, B, H, T, d_head,
+                                scale, true, stream);
+}
+int attn_fused_causal_backward_bf16(const attn_bf16* qkv, const attn_bf16* o,
+                                    const attn_bf16* do_ptr, const float* m_ptr,
+                                    const float* l_ptr, attn_bf16* dqkv, float* d_workspace,
+                                    int B, int H, int T, int d_head, float scale,
+                                    hipStream_t stream) {
+    return packed_backward(qkv, o, do_ptr, m_ptr, l_ptr, dqkv, d_workspace, B, H, T, d_head,
+                           scale, true, stream);
 }
 
 }  // extern "C"

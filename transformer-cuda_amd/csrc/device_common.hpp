@@ -56,7 +56,8 @@ __device__ __forceinline__ float xhalf_sum(float x) {
 // Where head bh = b*H + h of a (B, H, T, d) operand lives: element (t, e) is at
 // off(bh) + t*row + e.  Head-major tensors (B, H, T, d): batch = H*T*d, head = T*d, row = d.
 // The packed QKV layout (B, T, 3*H*d), pointer advanced to the q, k or v column block:
-// batch = 3*H*T*d, head = d, row = 3*H*d.
+// batch = 3*H*T*d, head = d, row = 3*H*d.  The merged-heads layout (B, T, H*d) of the
+// attention output: batch = H*T*d, head = d, row = H*d.
 struct HeadView {
     long long batch;
     long long head;
@@ -71,6 +72,9 @@ inline HeadView head_major_view(int H, int T, int d) {
 }
 inline HeadView packed_qkv_view(int H, int T, int d) {
     return HeadView{3LL * H * T * d, d, 3 * H * d, H};
+}
+inline HeadView merged_view(int H, int T, int d) {
+    return HeadView{static_cast<long long>(H) * T * d, d, H * d, H};
 }
 
 // fp32 -> bf16 bits, round to nearest even (v_cvt_pk_bf16_f32 on gfx950).

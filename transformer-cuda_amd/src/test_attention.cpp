@@ -10,7 +10,8 @@
 //     m_i = 0, l_i = i+1;
 //   * QKV split followed by its backward is the identity (bitwise), head merge likewise;
 //   * the packed launchers (attention straight from qkv, gradient straight into dqkv) equal
-//     split + tiled + split-back bitwise;
+//     split + tiled + split-back bitwise, and the fused launchers (output and its gradient in
+//     the merged-heads layout) equal them with the head merge applied;
 //   * an unsupported head dimension throws instead of silently doing nothing.
 // Exit status 0 iff every test passes.
 #include <cmath>
@@ -178,7 +179,7 @@ bool test_split_roundtrip() {
 }
 
 bool test_packed_matches_split(int d, int T) {
-    std::printf("[Test] packed launchers == split + tiled + split-back, bitwise (T=%d, d=%d)...\n",
+    std::printf("[Test] packed / fused launchers == split + tiled + split-back, bitwise (T=%d, d=%d)...\n",
                 T, d);
     const int B = 2, H = 3;
     const size_t n = static_cast<size_t>(B) * H * T * d;
@@ -205,10 +206,21 @@ bool test_packed_matches_split(int d, int T) {
     packed_causal_attention_backward(qkv.p, o2.p, dO.p, m2.p, l2.p, dqkv2.p, ws2.p, B, H, T, d,
                                      scale);
     HIP_CHECK(hipDeviceSynchronize());
+    // Fused: O written in the merged-heads layout, dO read from it (the head merge is a
+    // permutation, so the comparison is bitwise too).
+    DevBuf om(n), dOm(n), m3(r), l3(r), dqkv3(3 * n), ws3(r), om_ref(n);
+    head_merge_transpose_forward(dO.p, dOm.p, B, H, T, d);
+    head_merge_transpose_forward(o1.p, om_ref.p, B, H, T, d);
+    fused_causal_attention_forward(qkv.p, om.p, B, H, T, d, scale, m3.p, l3.p);
+    fused_causal_attention_backward(qkv.p, om.p, dOm.p, m3.p, l3.p, dqkv3.p, ws3.p, B, H, T, d,
+                                    scale);
+    HIP_CHECK(hipDeviceSynchronize());
     const std::pair<const DevBuf*, const DevBuf*> pairs[] = {
-        {&o1, &o2}, {&m1, &m2}, {&l1, &l2}, {&dqkv1, &dqkv2}, {&ws1, &ws2}};
-    const char* names[] = {"O", "m", "l", "dqkv", "D"};
-    for (int t = 0; t < 5; ++t) {
+        {&o1, &o2}, {&m1, &m2}, {&l1, &l2}, {&dqkv1, &dqkv2}, {&ws1, &ws2},
+        {&om_ref, &om}, {&m1, &m3}, {&l1, &l3}, {&dqkv1, &dqkv3}, {&ws1, &ws3}};
+    const char* names[] = {"O", "m", "l", "dqkv", "D",
+                           "fused O", "fused m", "fused l", "fused dqkv", "fused D"};
+    for (int t = 0; t < 10; ++t) {
         const auto a = pairs[t].first->download(), b = pairs[t].second->download();
         for (size_t i = 0; i < a.size(); ++i)
             EXPECT(std::isfinite(a[i]) && a[i] == b[i], "%s[%zu]: split %.9g, packed %.9g",

@@ -34,6 +34,12 @@ secondary: the same workload through the other path, the step in bf16 at config 
 and at config 3, and the reference's materialised mode (full-square GEMMs + fused softmax,
 fp32, config 2) as a timed fwd+bwd.
 
+training_step: BASELINE config 5, the reference's GPT-2-small training step (L12 C768 H12
+T1024 B8 V50257, fp32, forward + backward + fused clip/AdamW) through the harness of
+libtcamd_gpt, once per attention mode (fused: this build's path; tiled_split: the
+reference's tiled launcher sequence; materialized: the reference's default): tokens/s and
+the share of the step in the attention launches.
+
 cpu_baseline: the torch-CPU fp32 restatement of the reference attention
 (pytorch_src/model.py:43-52, forward + autograd backward) timed on this host on the same
 inputs, which also gives a max-abs parity figure for the GPU result.
@@ -92,6 +98,9 @@ def parse_args():
     ap.add_argument("--no-secondary", action="store_true",
                     help="skip the bf16 secondary measurements")
     ap.add_argument("--secondary-steps", type=int, default=20)
+    ap.add_argument("--gpt-steps", type=int, default=5,
+                    help="timed steps of the config-5 training-step harness per attention "
+                         "mode (0 skips it)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="instead of the bench: run 10 plain device copies of MIB MiB (the "
                          "known-size kernel that scales rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -396,6 +405,66 @@ def materialized(lib, steps, seed):
     return out_d
 
 
+# the reference's GPT-2-small training step (fp32, AdamW).
+GPT_C5 = dict(V=50257, T=1024, C=768, L=12, H=12, d_ff=3072, B=8)
+
+
+def gpt_training_step(mode, steps, warmup, seed):
+    """Config 5 through the GPT training-step harness (libtcamd_gpt: the reference's
+    TransformerModel forward/backward + fused clip/AdamW, rocBLAS GEMMs) with the attention
+    of every block in `mode`: tokens/s of the whole step (forward, backward, optimizer) and
+    the share of the step spent in the attention launches (HIP events around them)."""
+    import numpy as np
+    import torch
+    import __graft_entry__
+    gpt = __graft_entry__.load_gpt()
+    c = GPT_C5
+    cfg = gpt.default_config(c["V"], c["T"], c["C"], c["L"], c["H"], c["d_ff"], c["B"], mode)
+    model = gpt.GPT(cfg)
+    rng = np.random.default_rng(seed)
+    flat = (rng.standard_normal(model.n_params, dtype=np.float32) * 0.02).astype(np.float32)
+    off = 0  # LayerNorm gamma 1, beta and biases 0 (src/model.cu:219-241)
+    for name, shape in gpt.param_layout(c["V"], c["T"], c["C"], c["L"], c["d_ff"]):
+        n = int(np.prod(shape))
+        leaf = name.split(".")[-1]
+        if leaf.endswith("_g"):
+            flat[off:off + n] = 1.0
+        elif leaf.endswith("_b"):
+            flat[off:off + n] = 0.0
+        off += n
+    model.set_parameters(flat)
+    del flat
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    tokens = torch.randint(0, c["V"], (c["B"], c["T"]), generator=g, dtype=torch.int32).cuda()
+    targets = torch.randint(0, c["V"], (c["B"], c["T"]), generator=g, dtype=torch.int32).cuda()
+    loss = torch.zeros(1, device="cuda:0")
+    for _ in range(warmup):
+        model.forward_backward(tokens, targets, loss)
+        model.optimizer_step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        model.forward_backward(tokens, targets, loss)
+        model.optimizer_step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) / steps * 1e3
+    model.set_attention_timing(True)
+    model.forward_backward(tokens, targets, loss)
+    model.optimizer_step()
+    attn_ms = model.last_attention_ms()
+    torch.cuda.synchronize()
+    out = {"config": "c5", "workload": "GPT-2-small training step (BASELINE config 5)",
+           "attention": mode, "dtype": "f32", "ms_per_step": round(ms, 3),
+           "tokens_per_s": round(c["B"] * c["T"] / (ms * 1e-3), 1),
+           "attention_ms": round(attn_ms, 3),
+           "attention_share": round(attn_ms / ms, 4),
+           "loss": round(float(loss.item()), 5), "finite": bool(math.isfinite(loss.item())),
+           "params": model.n_params}
+    model.close()
+    torch.cuda.empty_cache()
+    return out
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -458,6 +527,9 @@ def main():
         sec.append(secondary(lib, "c3", "bf16", args.secondary_steps, args.seed))
         sec.append(materialized(lib, max(3, args.secondary_steps // 4), args.seed))
         line["secondary"] = sec
+    if args.gpt_steps > 0:
+        line["training_step"] = [gpt_training_step(m, args.gpt_steps, 2, args.seed)
+                                 for m in ("fused", "tiled_split", "materialized")]
     print(json.dumps(line), flush=True)
     return 0
 

@@ -113,3 +113,94 @@ def layer0_attention_tensors(B=4, T=64, C=128, L=2, H=4, d_ff=512, V=256, seed=4
     out["dv"] = cap["v"].grad.detach().contiguous().numpy()
     out["loss"] = float(loss.item())
     return out
+
+
+# ---- the flat-buffer training step (checker of the GPT harness, libtcamd_gpt) -------------
+
+def flat_layout(V, T, C, L, d_ff):
+    """(name, shape) of the reference's flat parameter buffer in order (src/model.cu:185-217):
+    weights stored (in, out), row-major."""
+    out = [("tok_emb", (V, C)), ("pos_emb", (T, C))]
+    for i in range(L):
+        out += [(f"l{i}.ln1_g", (C,)), (f"l{i}.ln1_b", (C,)), (f"l{i}.qkv_w", (C, 3 * C)),
+                (f"l{i}.qkv_b", (3 * C,)), (f"l{i}.proj_w", (C, C)), (f"l{i}.proj_b", (C,)),
+                (f"l{i}.ln2_g", (C,)), (f"l{i}.ln2_b", (C,)), (f"l{i}.ffn1_w", (C, d_ff)),
+                (f"l{i}.ffn1_b", (d_ff,)), (f"l{i}.ffn2_w", (d_ff, C)),
+                (f"l{i}.ffn2_b", (C,))]
+    out += [("lnf_g", (C,)), ("lnf_b", (C,)), ("head_w", (C, V))]
+    return out
+
+
+def _tensor_map(model: TinyGPT):
+    """name -> (module parameter, stored transposed?) for flat_layout's names."""
+    m = {"tok_emb": (model.tok_emb.weight, False), "pos_emb": (model.pos_emb.weight, False),
+         "lnf_g": (model.ln_f.weight, False), "lnf_b": (model.ln_f.bias, False),
+         "head_w": (model.head.weight, True)}
+    for i, blk in enumerate(model.blocks):
+        m.update({f"l{i}.ln1_g": (blk.ln_1.weight, False), f"l{i}.ln1_b": (blk.ln_1.bias, False),
+                  f"l{i}.qkv_w": (blk.attn.qkv_proj.weight, True),
+                  f"l{i}.qkv_b": (blk.attn.qkv_proj.bias, False),
+                  f"l{i}.proj_w": (blk.attn.out_proj.weight, True),
+                  f"l{i}.proj_b": (blk.attn.out_proj.bias, False),
+                  f"l{i}.ln2_g": (blk.ln_2.weight, False), f"l{i}.ln2_b": (blk.ln_2.bias, False),
+                  f"l{i}.ffn1_w": (blk.ffn_1.weight, True), f"l{i}.ffn1_b": (blk.ffn_1.bias, False),
+                  f"l{i}.ffn2_w": (blk.ffn_2.weight, True),
+                  f"l{i}.ffn2_b": (blk.ffn_2.bias, False)})
+    return m
+
+
+def model_from_flat(flat, V, T, C, L, H, d_ff, eps=1e-5, dtype=torch.float64) -> TinyGPT:
+    """A TinyGPT whose parameters are the flat buffer's (nn.Linear holds (out, in))."""
+    model = TinyGPT(V, T, C, L, H, d_ff, eps).to(dtype)
+    tm = _tensor_map(model)
+    off = 0
+    with torch.no_grad():
+        for name, shape in flat_layout(V, T, C, L, d_ff):
+            n = int(torch.tensor(shape).prod())
+            x = torch.as_tensor(flat[off:off + n], dtype=dtype).view(shape)
+            p, tr = tm[name]
+            p.copy_(x.t() if tr else x)
+            off += n
+    assert off == len(flat)
+    return model
+
+
+def flat_from_model(model: TinyGPT, V, T, C, L, d_ff, grads=False):
+    """The model's parameters (or their .grad) in the flat layout, as a float64 numpy array."""
+    tm = _tensor_map(model)
+    parts = []
+    for name, _ in flat_layout(V, T, C, L, d_ff):
+        p, tr = tm[name]
+        x = (p.grad if grads else p).detach()
+        parts.append((x.t() if tr else x).contiguous().reshape(-1).double().numpy())
+    import numpy as np
+    return np.concatenate(parts)
+
+
+def training_step_grads(flat, tokens, targets, V, T, C, L, H, d_ff, eps=1e-5):
+    """Mean cross-entropy and its gradient for every parameter, in fp64 on the CPU:
+    (loss, flat gradient)."""
+    model = model_from_flat(flat, V, T, C, L, H, d_ff, eps)
+    _, loss = model(torch.as_tensor(tokens, dtype=torch.long),
+                    torch.as_tensor(targets, dtype=torch.long))
+    loss.backward()
+    return float(loss.item()), flat_from_model(model, V, T, C, L, d_ff, grads=True)
+
+
+def clip_adamw(params, grads, m, v, step, lr=3e-4, beta1=0.9, beta2=0.999, eps=1e-8,
+               weight_decay=0.01, max_norm=1.0):
+    """The reference's fused optimizer step (src/optimizer.cu:117-154) in fp64 numpy: scale
+    the gradient by max_norm/||g|| when ||g|| > max_norm, Adam moments with bias correction,
+    decoupled weight decay on the old parameter.  Returns (params, m, v)."""
+    import numpy as np
+    g = np.asarray(grads, np.float64)
+    norm = float(np.sqrt((g * g).sum()))
+    if norm > max_norm and norm > 1e-6:
+        g = g * (max_norm / norm)
+    m = beta1 * np.asarray(m, np.float64) + (1 - beta1) * g
+    v = beta2 * np.asarray(v, np.float64) + (1 - beta2) * g * g
+    mh = m / (1 - beta1 ** step)
+    vh = v / (1 - beta2 ** step)
+    p = np.asarray(params, np.float64)
+    p = p - lr * (mh / (np.sqrt(vh) + eps) + weight_decay * p)
+    return p, m, v

@@ -53,6 +53,9 @@ int gpt_set_parameters(gpt_model* model, const float* host, long long n);
 int gpt_get_parameters(const gpt_model* model, float* host, long long n);
 int gpt_get_gradients(const gpt_model* model, float* host, long long n);
 
+/* The logits (B*T, V) of the last forward (synchronous copy). */
+int gpt_get_logits(const gpt_model* model, float* host, long long n);
+
 /* Forward + backward for tokens / targets (device int32, B*T each): the mean loss into
  * *loss_dev (device float) and every parameter gradient (overwritten). */
 int gpt_forward_backward(gpt_model* model, const int* tokens, const int* targets,

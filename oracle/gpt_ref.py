@@ -177,14 +177,22 @@ def flat_from_model(model: TinyGPT, V, T, C, L, d_ff, grads=False):
     return np.concatenate(parts)
 
 
+def training_step_outputs(flat, tokens, targets, V, T, C, L, H, d_ff, eps=1e-5):
+    """Logits (B*T, V), mean cross-entropy and its gradient for every parameter, in fp64 on
+    the CPU: the tensors the reference's parity audit dumps (src/parity_audit.cu:64-89)."""
+    model = model_from_flat(flat, V, T, C, L, H, d_ff, eps)
+    logits, loss = model(torch.as_tensor(tokens, dtype=torch.long),
+                         torch.as_tensor(targets, dtype=torch.long))
+    loss.backward()
+    return (logits.detach().reshape(-1, V).numpy(), float(loss.item()),
+            flat_from_model(model, V, T, C, L, d_ff, grads=True))
+
+
 def training_step_grads(flat, tokens, targets, V, T, C, L, H, d_ff, eps=1e-5):
     """Mean cross-entropy and its gradient for every parameter, in fp64 on the CPU:
     (loss, flat gradient)."""
-    model = model_from_flat(flat, V, T, C, L, H, d_ff, eps)
-    _, loss = model(torch.as_tensor(tokens, dtype=torch.long),
-                    torch.as_tensor(targets, dtype=torch.long))
-    loss.backward()
-    return float(loss.item()), flat_from_model(model, V, T, C, L, d_ff, grads=True)
+    _, loss, grads = training_step_outputs(flat, tokens, targets, V, T, C, L, H, d_ff, eps)
+    return loss, grads
 
 
 def clip_adamw(params, grads, m, v, step, lr=3e-4, beta1=0.9, beta2=0.999, eps=1e-8,

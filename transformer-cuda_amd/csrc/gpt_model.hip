@@ -203,10 +203,11 @@ int check_config(const gpt_config& c) {
         c.num_heads <= 0 || c.d_ff <= 0 || c.batch_size <= 0)
         return ATTN_ERROR_INVALID_DIM;
     if (c.d_model % c.num_heads != 0) return ATTN_ERROR_INVALID_DIM;
-    const int d = c.d_model / c.num_heads;
-    if (d != 32 && d != 64 && d != 128) return ATTN_ERROR_UNSUPPORTED_HEAD_DIM;
     if (c.attention_mode < GPT_ATTN_FUSED || c.attention_mode > GPT_ATTN_MATERIALIZED)
         return ATTN_ERROR_INVALID_VALUE;
+    const int d = c.d_model / c.num_heads;  // the materialised mode takes any head dimension
+    if (c.attention_mode != GPT_ATTN_MATERIALIZED && d != 32 && d != 64 && d != 128)
+        return ATTN_ERROR_UNSUPPORTED_HEAD_DIM;
     const long long rows = static_cast<long long>(c.batch_size) * c.max_seq_len;
     if (rows * c.vocab_size > 2147483647LL * 8 || rows > 2147483647LL)
         return ATTN_ERROR_INVALID_DIM;
@@ -431,6 +432,16 @@ int gpt_get_gradients(const gpt_model* m, float* host, long long n) {
     if (m == nullptr || host == nullptr) return ATTN_ERROR_NULL_POINTER;
     if (n != m->n_params) return ATTN_ERROR_INVALID_DIM;
     return hipMemcpy(host, m->grads, n * sizeof(float), hipMemcpyDeviceToHost) == hipSuccess
+               ? ATTN_SUCCESS
+               : ATTN_ERROR_LAUNCH;
+}
+
+int gpt_get_logits(const gpt_model* m, float* host, long long n) {
+    if (m == nullptr || host == nullptr) return ATTN_ERROR_NULL_POINTER;
+    const long long want =
+        static_cast<long long>(m->cfg.batch_size) * m->cfg.max_seq_len * m->cfg.vocab_size;
+    if (n != want) return ATTN_ERROR_INVALID_DIM;
+    return hipMemcpy(host, m->logits, n * sizeof(float), hipMemcpyDeviceToHost) == hipSuccess
                ? ATTN_SUCCESS
                : ATTN_ERROR_LAUNCH;
 }

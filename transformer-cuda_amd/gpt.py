@@ -49,6 +49,7 @@ SIGNATURES = {
     "gpt_set_parameters": ([_P, _P, _L], _I),
     "gpt_get_parameters": ([_P, _P, _L], _I),
     "gpt_get_gradients": ([_P, _P, _L], _I),
+    "gpt_get_logits": ([_P, _P, _L], _I),
     "gpt_forward_backward": ([_P, _P, _P, _P, _P], _I),
     "gpt_optimizer_step": ([_P, _P], _I),
     "gpt_set_attention_timing": ([_P, _I], _I),
@@ -118,6 +119,12 @@ class GPT:
     def gradients(self) -> np.ndarray:
         out = np.empty(self.n_params, np.float32)
         check(_lib.gpt_get_gradients(self._h, out.ctypes.data, out.size), "gpt_get_gradients")
+        return out
+
+    def logits(self) -> np.ndarray:
+        c = self.cfg
+        out = np.empty(c.batch_size * c.max_seq_len * c.vocab_size, np.float32)
+        check(_lib.gpt_get_logits(self._h, out.ctypes.data, out.size), "gpt_get_logits")
         return out
 
     def forward_backward(self, tokens, targets, loss, stream=None):

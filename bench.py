@@ -101,6 +101,8 @@ def parse_args():
     ap.add_argument("--gpt-steps", type=int, default=5,
                     help="timed steps of the config-5 training-step harness per attention "
                          "mode (0 skips it)")
+    ap.add_argument("--gpt-modes", default="fused,tiled_split,materialized",
+                    help="attention modes of the training-step measurement (comma separated)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="instead of the bench: run 10 plain device copies of MIB MiB (the "
                          "known-size kernel that scales rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -529,7 +531,7 @@ def main():
         line["secondary"] = sec
     if args.gpt_steps > 0:
         line["training_step"] = [gpt_training_step(m, args.gpt_steps, 2, args.seed)
-                                 for m in ("fused", "tiled_split", "materialized")]
+                                 for m in args.gpt_modes.split(",")]
     print(json.dumps(line), flush=True)
     return 0
 

@@ -51,30 +51,121 @@ constexpr float kLog2e = 1.4426950408889634f;
 // exp(scale*s - m) = 2^(s*c - m*log2 e) with c = scale*log2 e folded into one FMA.
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// DMA instructions that copy one 32-row tile of a (T, D) head into LDS.
-template <int D>
-constexpr int kTileDma = kTile * (D >= 64 ? D / 64 : 1);
-
-// Copy rows [row0, row0 + 32) of a head (T rows of D fp32, consecutive rows rs floats
-// apart) into LDS rows of STRIDE floats starting at byte address lds.  Rows past T are read from row T-1 (finite values;
-// every consumer masks them).  D = 32 uses the lower half-wave per row.
+// A 32-row tile of a (T, D) head copied into LDS rows of STRIDE floats with 16-byte copies:
+// copy instruction i writes LDS bytes [1024 i, 1024 i + 1024) of the tile, lane l the 16
+// bytes at 1024 i + 16 l, i.e. byte b of row r with (r, b) = divmod(1024 i + 16 l, 4 STRIDE).
+// Lanes that land on a row's padding copy the row's first 16 bytes there (never read);
+// lanes past the tile's end, in the last instruction only, are off.  In a partial last tile
+// (rows at or beyond T) those rows read the last 16 bytes of row T - 1 instead: every read
+// stays inside the head and the padding rows hold finite values, which the kernels mask.
 template <int D, int STRIDE>
-__device__ __forceinline__ void dma_tile(const float* __restrict__ head, int row0, int T,
-                                         uint32_t lds, int lane, int rs) {
-    constexpr int kSeg = D >= 64 ? D / 64 : 1;
-    const uint32_t voff = static_cast<uint32_t>(lane) * 4u;
+struct TileShape {
+    static constexpr int kRowBytes = 4 * STRIDE;
+    static constexpr int kBytes = kTile * kRowBytes;
+    static constexpr int kInst = (kBytes + 1023) / 1024;
+    static_assert(STRIDE % 4 == 0 && D % 4 == 0, "16-byte chunks");
+    // Row r and source byte (0 for padding) of lane `lane` in instruction i.
+    __device__ static void row_byte(int i, int lane, int& r, int& b) {
+        const int o = 1024 * i + 16 * lane;
+        r = o / kRowBytes;
+        b = o - r * kRowBytes;
+        if (b >= 4 * D) b = 0;
+    }
+    __device__ static bool active(int i, int lane) {
+        return i + 1 < kInst || 1024 * i + 16 * lane < kBytes;
+    }
+    // Largest in-bounds offset from row0 when the tile is partial.
+    __device__ static uint32_t last(int row0, int T, int rs) {
+        return static_cast<uint32_t>((T - 1 - row0) * rs * 4 + 4 * D - 16);
+    }
+};
+
+// Copy plan for one row stride rs: voff[i] is the lane's source byte offset from the tile's
+// first row, the same for every tile, so a whole tile costs no VALU.
+template <int D, int STRIDE>
+struct TileCopy : TileShape<D, STRIDE> {
+    using S = TileShape<D, STRIDE>;
+    uint32_t voff[S::kInst];
+
+    __device__ void init(int lane, int rs) {
 #pragma unroll
-    for (int r = 0; r < kTile; ++r) {
-        const float* rowp = head + static_cast<size_t>(min(row0 + r, T - 1)) * rs;
-#pragma unroll
-        for (int sg = 0; sg < kSeg; ++sg) {
-            if (D >= 64 || lane < D) {
-                dma_dword(rowp + sg * 64, lds + static_cast<uint32_t>((r * STRIDE + sg * 64) * 4),
-                          voff);
-            }
+        for (int i = 0; i < S::kInst; ++i) {
+            int r, b;
+            S::row_byte(i, lane, r, b);
+            voff[i] = static_cast<uint32_t>(r * rs * 4 + b);
         }
     }
-}
+    // Copy rows [row0, row0 + kTile) of a head (rows rs floats apart; rs is the init's) into
+    // the tile at LDS byte address lds.
+    __device__ void copy(const float* __restrict__ head, int row0, int T, uint32_t lds, int lane,
+                         int rs) const {
+        const float* base = head + static_cast<size_t>(row0) * rs;
+        const bool whole = row0 + kTile <= T;
+        const uint32_t last = S::last(row0, T, rs);
+#pragma unroll
+        for (int i = 0; i < S::kInst; ++i)
+            if (S::active(i, lane))
+                dma_dwordx4(base, lds + static_cast<uint32_t>(1024 * i),
+                            whole ? voff[i] : min(voff[i], last));
+    }
+};
+
+// Copy plan for any row stride: rb[i] = r | (b / 16) << 24, and every copy forms
+// r * 4 rs + b = mul_u24(rb, 4 rs) + (rb >> 20) (bits 20-23 are zero) in two VALU
+// instructions.  One plan serves two tiles whose rows are strided differently.  The two
+// instructions are asm so that the optimiser cannot hoist them out of the tile loop into one
+// register per instruction and stride.
+template <int D, int STRIDE>
+struct TileCopyAnyStride : TileShape<D, STRIDE> {
+    using S = TileShape<D, STRIDE>;
+    static_assert(kTile < (1 << 20) && S::kRowBytes / 16 < 256, "fields of rb");
+    uint32_t rb[S::kInst];
+
+    __device__ void init(int lane) {
+#pragma unroll
+        for (int i = 0; i < S::kInst; ++i) {
+            int r, b;
+            S::row_byte(i, lane, r, b);
+            rb[i] = static_cast<uint32_t>(r) | static_cast<uint32_t>(b / 16) << 24;
+        }
+    }
+    __device__ static uint32_t offset(uint32_t p, uint32_t rs4) {
+        uint32_t off, t;
+        asm volatile(
+            "v_lshrrev_b32 %1, 20, %2\n\t"
+            "v_mad_u32_u24 %0, %2, %3, %1"
+            : "=v"(off), "=&v"(t)
+            : "v"(p), "s"(rs4));
+        return off;
+    }
+    __device__ void copy(const float* __restrict__ head, int row0, int T, uint32_t lds, int lane,
+                         int rs) const {
+        const float* base = head + static_cast<size_t>(row0) * rs;
+        const uint32_t rs4 = static_cast<uint32_t>(rs) * 4u;
+        if (row0 + kTile <= T) {
+#pragma unroll
+            for (int i = 0; i < S::kInst; ++i)
+                if (S::active(i, lane))
+                    dma_dwordx4(base, lds + static_cast<uint32_t>(1024 * i), offset(rb[i], rs4));
+        } else {
+            const uint32_t last = S::last(row0, T, rs);
+#pragma unroll
+            for (int i = 0; i < S::kInst; ++i)
+                if (S::active(i, lane))
+                    dma_dwordx4(base, lds + static_cast<uint32_t>(1024 * i),
+                                min(offset(rb[i], rs4), last));
+        }
+    }
+};
+
+// Copy instructions per tile (every tile of the kernels has kTile rows of D + 4 or D + 8
+// floats; both give the same count).
+template <int D>
+constexpr int kTileDma = TileShape<D, D + 4>::kInst;
+static_assert(TileShape<32, 36>::kInst == TileShape<32, 40>::kInst &&
+              TileShape<64, 68>::kInst == TileShape<64, 72>::kInst &&
+              TileShape<128, 132>::kInst == TileShape<128, 136>::kInst,
+              "the copy waits count one instruction total per tile");
 
 // Lane (col, half) loads its row's half: dst[j] = src[row][half*D/2 + j], zeros if row >= T
 // (rows rs floats apart).
@@ -234,6 +325,8 @@ __device__ __forceinline__ void fwd_chunk(const float* __restrict__ kh,
                                           float c, int qb,
                                           int t0, int t1, const float (&qreg)[D / 2],
                                           FwdLds<D>& L, int lane, Fetch& fetch,
+                                          const TileCopy<D, FwdLds<D>::KS>& kc,
+                                          const TileCopy<D, FwdLds<D>::VS>& vc,
                                           f32x16 (&acc)[D / 32], float& m_raw, float& l_i) {
     constexpr int KS = FwdLds<D>::KS;
     constexpr int VS = FwdLds<D>::VS;
@@ -249,8 +342,8 @@ __device__ __forceinline__ void fwd_chunk(const float* __restrict__ kh,
         fetch.issue(lane);
         return;
     }
-    dma_tile<D, KS>(kh, t0 * kTile, T, lds_addr(L.k), lane, stride);
-    dma_tile<D, VS>(vh, t0 * kTile, T, lds_addr(L.v), lane, stride);
+    kc.copy(kh, t0 * kTile, T, lds_addr(L.k), lane, stride);
+    vc.copy(vh, t0 * kTile, T, lds_addr(L.v), lane, stride);
     fetch.issue(lane);
 
     for (int t = t0; t < t1; ++t) {
@@ -258,7 +351,7 @@ __device__ __forceinline__ void fwd_chunk(const float* __restrict__ kh,
         wait_vm<kTileDma<D>>();  // K tile t landed
         f32x16 s = mma_rows<D>(Ks + col * KS + half * (D / 2), qreg, f32x16{});
         wait_lds();
-        if (more) dma_tile<D, KS>(kh, (t + 1) * kTile, T, lds_addr(L.k), lane, stride);
+        if (more) kc.copy(kh, (t + 1) * kTile, T, lds_addr(L.k), lane, stride);
         if (t == qb) {  // diagonal tile
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
@@ -290,7 +383,7 @@ __device__ __forceinline__ void fwd_chunk(const float* __restrict__ kh,
         }
         mma_cols<D, VS>(Vs, col, half, s, acc);
         wait_lds();
-        if (more) dma_tile<D, VS>(vh, (t + 1) * kTile, T, lds_addr(L.v), lane, stride);
+        if (more) vc.copy(vh, (t + 1) * kTile, T, lds_addr(L.v), lane, stride);
     }
 }
 
@@ -307,6 +400,10 @@ TCAMD_F32_KERNEL(kFwdWaves) void flash_fwd_f32_kernel(
     const int half = lane >> 5;
     const float c = scale * kLog2e;
     const TaskQueue tq = TaskQueue::bind(slot, BH, nqb, per_xcd != 0);
+    TileCopy<D, FwdLds<D>::KS> kc;
+    TileCopy<D, FwdLds<D>::VS> vc;
+    kc.init(lane, xv.row);
+    vc.init(lane, xv.row);
     unsigned task = tq.first();
     while (task < tq.n_tasks) {
         int bh, rank;
@@ -323,7 +420,7 @@ TCAMD_F32_KERNEL(kFwdWaves) void flash_fwd_f32_kernel(
         f32x16 acc[D / 32];
         float m_raw, l_i;
         fwd_chunk<D>(k + xoff, v + xoff, T, xv.row, c, qb, t0, t1, qreg, L[wave], lane, fetch,
-                     acc, m_raw, l_i);
+                     kc, vc, acc, m_raw, l_i);
 
         // Merge: every wave publishes (acc, m, l) over its own tiles; then wave w reduces
         // and stores the 8-element chunks w, w+4, ... of the flat accumulator.
@@ -410,7 +507,8 @@ __device__ __forceinline__ void dq_chunk(const float* __restrict__ kh,
                                          float lse2, float Dval, int qb, int t0, int t1,
                                          const float (&qreg)[D / 2],
                                          const float (&doreg)[D / 2], DqLds<D>& L, int lane,
-                                         Fetch& fetch, f32x16 (&acc)[D / 32]) {
+                                         Fetch& fetch, const TileCopy<D, DqLds<D>::KS>& kc,
+                                         f32x16 (&acc)[D / 32]) {
     constexpr int KS = DqLds<D>::KS;
     constexpr int VS = DqLds<D>::VS;
     const float* Ks = L.k;
@@ -425,8 +523,8 @@ __device__ __forceinline__ void dq_chunk(const float* __restrict__ kh,
     }
     // V before K: the V copy of a tile is always the older one in flight, so each tile
     // starts with dP (V) while the K copy issued at the end of the previous tile lands.
-    dma_tile<D, VS>(vh, t0 * kTile, T, lds_addr(L.v), lane, stride);
-    dma_tile<D, KS>(kh, t0 * kTile, T, lds_addr(L.k), lane, stride);
+    kc.copy(vh, t0 * kTile, T, lds_addr(L.v), lane, stride);
+    kc.copy(kh, t0 * kTile, T, lds_addr(L.k), lane, stride);
     fetch.issue(lane);
 
     for (int t = t0; t < t1; ++t) {
@@ -435,7 +533,7 @@ __device__ __forceinline__ void dq_chunk(const float* __restrict__ kh,
         f32x16 dp = mma_rows<D>(Vs + col * VS + half * (D / 2), doreg, f32x16{});
         wait_lds();
         if (more) {
-            dma_tile<D, VS>(vh, (t + 1) * kTile, T, lds_addr(L.v), lane, stride);
+            kc.copy(vh, (t + 1) * kTile, T, lds_addr(L.v), lane, stride);
             wait_vm<kTileDma<D>>();  // K tile t landed (V tile t+1 in flight)
         } else {
             wait_vm<0>();
@@ -452,7 +550,7 @@ __device__ __forceinline__ void dq_chunk(const float* __restrict__ kh,
         mma_cols<D, KS>(Ks, col, half, s, part);
         add_into(acc, part);
         wait_lds();
-        if (more) dma_tile<D, KS>(kh, (t + 1) * kTile, T, lds_addr(L.k), lane, stride);
+        if (more) kc.copy(kh, (t + 1) * kTile, T, lds_addr(L.k), lane, stride);
     }
 }
 
@@ -471,6 +569,9 @@ TCAMD_F32_KERNEL(kDqWaves) void flash_bwd_dq_f32_kernel(
     const int half = lane >> 5;
     const float c = scale * kLog2e;
     const TaskQueue tq = TaskQueue::bind(slot, BH, nqb, per_xcd != 0);
+    static_assert(DqLds<D>::KS == DqLds<D>::VS, "K and V tiles share one copy plan");
+    TileCopy<D, DqLds<D>::KS> kc;
+    kc.init(lane, xv.row);
     unsigned task = tq.first();
     while (task < tq.n_tasks) {
         int bh, rank;
@@ -506,7 +607,7 @@ TCAMD_F32_KERNEL(kDqWaves) void flash_bwd_dq_f32_kernel(
         Fetch fetch{wave == 0 ? &tq : nullptr, 0u};
         f32x16 acc[D / 32];
         dq_chunk<D>(k + xoff, v + xoff, T, xv.row, c, lse2, Dval, qb, t0, t1, qreg, doreg,
-                    L[wave], lane, fetch, acc);
+                    L[wave], lane, fetch, kc, acc);
 
         // Merge: every wave publishes its partial dQ; wave w sums (in wave order) and stores
         // the 8-element chunks w, w+2, ... of the flat accumulator.
@@ -560,7 +661,9 @@ __device__ __forceinline__ void dkdv_chunk(const float* __restrict__ qh,
                                            int t1,
                                            const float (&kreg)[D / 2],
                                            const float (&vreg)[D / 2], DkdvLds<D>& L, int lane,
-                                           Fetch& fetch, f32x16 (&dk_acc)[D / 32],
+                                           Fetch& fetch,
+                                           const TileCopyAnyStride<D, DkdvLds<D>::QS>& tc,
+                                           f32x16 (&dk_acc)[D / 32],
                                            f32x16 (&dv_acc)[D / 32]) {
     constexpr int QS = DkdvLds<D>::QS;
     constexpr int GS = DkdvLds<D>::GS;
@@ -586,8 +689,8 @@ __device__ __forceinline__ void dkdv_chunk(const float* __restrict__ qh,
         return Dws[stat_off + r];
     };
     St[half][col] = load_stat(t0 * kTile);
-    dma_tile<D, QS>(qh, t0 * kTile, T, lds_addr(L.q), lane, qstride);
-    dma_tile<D, GS>(doh, t0 * kTile, T, lds_addr(L.g), lane, gstride);
+    tc.copy(qh, t0 * kTile, T, lds_addr(L.q), lane, qstride);
+    tc.copy(doh, t0 * kTile, T, lds_addr(L.g), lane, gstride);
     fetch.issue(lane);
 
     for (int t = t0; t < t1; ++t) {
@@ -615,8 +718,8 @@ __device__ __forceinline__ void dkdv_chunk(const float* __restrict__ qh,
         wait_lds();
         if (more) {
             St[half][col] = st_n;
-            dma_tile<D, QS>(qh, (t + 1) * kTile, T, lds_addr(L.q), lane, qstride);
-            dma_tile<D, GS>(doh, (t + 1) * kTile, T, lds_addr(L.g), lane, gstride);
+            tc.copy(qh, (t + 1) * kTile, T, lds_addr(L.q), lane, qstride);
+            tc.copy(doh, (t + 1) * kTile, T, lds_addr(L.g), lane, gstride);
         }
     }
 }
@@ -636,6 +739,9 @@ TCAMD_F32_KERNEL(kDkdvWaves) void flash_bwd_dkdv_f32_kernel(
     const int half = lane >> 5;
     const float c = scale * kLog2e;
     const TaskQueue tq = TaskQueue::bind(slot, BH, nkb, per_xcd != 0);
+    static_assert(DkdvLds<D>::QS == DkdvLds<D>::GS, "Q and dO tiles share one copy plan");
+    TileCopyAnyStride<D, DkdvLds<D>::QS> tc;
+    tc.init(lane);
     unsigned task = tq.first();
     while (task < tq.n_tasks) {
         int bh, kb;
@@ -654,7 +760,7 @@ TCAMD_F32_KERNEL(kDkdvWaves) void flash_bwd_dkdv_f32_kernel(
         Fetch fetch{wave == 0 ? &tq : nullptr, 0u};
         f32x16 dk_acc[D / 32], dv_acc[D / 32];
         dkdv_chunk<D>(q + xoff, dO + ooff, m, l, Dws, stat_off, T, xv.row, ov.row, c, kb, kb + t0,
-                      kb + t1, kreg, vreg, L[wave], lane, fetch, dk_acc, dv_acc);
+                      kb + t1, kreg, vreg, L[wave], lane, fetch, tc, dk_acc, dv_acc);
 
         // Merge: every wave publishes its partial dK, dV; wave w sums (in wave order) and
         // stores the 8-element chunks w, w+4, ... of the concatenated (dK, dV) accumulators.

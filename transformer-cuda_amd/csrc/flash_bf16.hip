@@ -66,6 +66,35 @@ struct QgSmem {
     uint16_t gx[2][kRowTile * 8];  // row r: (-D)_hi, (-D)_lo, 0 x 6
 };
 
+// x as the bf16 pair (hi, lo), hi + lo = x to ~2^-16 relative, packed into one dword.
+__device__ __forceinline__ uint32_t split_bf16x2(float x) {
+    const uint16_t hi = f32_to_bf16_bits(x);
+    const uint16_t lo = f32_to_bf16_bits(x - bf16_bits_to_f32(hi));
+    return static_cast<uint32_t>(hi) | (static_cast<uint32_t>(lo) << 16);
+}
+
+// The B or A operand (1, 1, 0, ...) of a contraction step that adds a per-row statistic
+// (hi, lo) to a product: lanes of k-group 1 hold zeros.
+__device__ __forceinline__ bf16x8 ones_pair(int half) {
+    bf16x8 one = bf16x8{};
+    if (half == 0) {
+        one[0] = static_cast<__bf16>(1.0f);
+        one[1] = static_cast<__bf16>(1.0f);
+    }
+    return one;
+}
+
+// The statistic chunk (x_hi, x_lo, 0, ...) of a lane's row (zeros in k-group 1).
+__device__ __forceinline__ bf16x8 stat_chunk(float x, int half) {
+    u16x8 v = u16x8{};
+    if (half == 0) {
+        const uint32_t p = split_bf16x2(x);
+        v[0] = static_cast<uint16_t>(p);
+        v[1] = static_cast<uint16_t>(p >> 16);
+    }
+    return __builtin_bit_cast(bf16x8, v);
+}
+
 // ---------------------------------------------------------------------------------------
 // Stage 1: D and dQ.
 // ---------------------------------------------------------------------------------------
@@ -73,21 +102,22 @@ struct QgSmem {
 // One 32-query sub-block of a wave.
 template <int D>
 struct DqSub {
-    bf16x8 q[D / 16];    // Q row of query col (B operand over d)
+    bf16x8 q[D / 16];    // c * Q row of query col (B operand over d)
     bf16x8 g[D / 16];    // dO row
+    bf16x8 xs, xd;       // statistic chunks: -lse2 (-1e30 for padded queries: P = 0), -D
     f32x16 acc[D / 32];  // dQ^T
-    float lse2;          // +inf for padded queries: P = 0
-    float dlt;           // D = rowsum(dO * O)
 };
 
-// qh: this head's q (rows xrs apart); oh, gh: its o and dO (rows ors apart).
+// qh: this head's q (rows xrs apart); oh, gh: its o and dO (rows ors apart).  Q is held
+// pre-multiplied by c = scale*log2 e and rounded to bf16 (one extra rounding, ~2^-9
+// relative per element), so that the scores come out in the log2 domain.
 template <int D>
 __device__ __forceinline__ void dq_init(DqSub<D>& sb, const uint16_t* __restrict__ qh,
                                         const uint16_t* __restrict__ oh,
                                         const uint16_t* __restrict__ gh,
                                         const float* __restrict__ m, const float* __restrict__ l,
                                         float* __restrict__ Dws, int xrs, int ors,
-                                        size_t stat_off, int qi, int T, int half) {
+                                        size_t stat_off, int qi, int T, int half, float c) {
     load_rowop<D>(sb.q, qh, qi, T, half, xrs);
     load_rowop<D>(sb.g, gh, qi, T, half, ors);
     bf16x8 orow[D / 16];
@@ -99,50 +129,62 @@ __device__ __forceinline__ void dq_init(DqSub<D>& sb, const uint16_t* __restrict
         for (int e = 0; e < 8; ++e)
             part = fmaf(static_cast<float>(sb.g[j][e]), static_cast<float>(orow[j][e]), part);
     }
-    sb.dlt = xhalf_sum(part);
-    sb.lse2 = INFINITY;
-    if (qi < T) {
-        if (half == 0) Dws[stat_off + qi] = sb.dlt;
-        sb.lse2 = m[stat_off + qi] * kLog2e + log2f(l[stat_off + qi]);
+#pragma unroll
+    for (int j = 0; j < D / 16; ++j) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sb.q[j][e] = static_cast<__bf16>(static_cast<float>(sb.q[j][e]) * c);
     }
+    const float dlt = xhalf_sum(part);
+    float nl = -1e30f;
+    if (qi < T) {
+        if (half == 0) Dws[stat_off + qi] = dlt;
+        nl = -(m[stat_off + qi] * kLog2e + log2f(l[stat_off + qi]));
+    }
+    sb.xs = stat_chunk(nl, half);
+    sb.xd = stat_chunk(-dlt, half);
 #pragma unroll
     for (int dt = 0; dt < D / 32; ++dt) sb.acc[dt] = f32x16{};
 }
 
-// s = S^T, dp = dP^T of keys kb.. (rows) x queries qj + col (columns) -> dS^T as the two B
-// operands of dQ^T += K^T dS^T.  Keys past the query get P = 0.
-template <int D>
-__device__ __forceinline__ void dq_ds(f32x16& s, const f32x16& dp, const DqSub<D>& sb,
-                                      bf16x8 (&db)[2], int kb, int qj, int col, int half,
-                                      float c) {
+// s = S'^T = K (cQ)^T - lse2, dp = dP'^T = V dO^T - D of keys kb.. (rows) x queries qj + col
+// (columns) -> dS^T = 2^s o dp as the two B operands of dQ^T += K^T dS^T.  Keys past the
+// query get P = 0.
+__device__ __forceinline__ void dq_ds(f32x16& s, const f32x16& dp, bf16x8 (&db)[2], int kb,
+                                      int qj, int col, int half) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) s[r] = exp2_fast(fmaf(s[r], c, -sb.lse2));
+    for (int r = 0; r < 16; ++r) s[r] = exp2_fast(s[r]);
     if (kb + 31 > qj) {  // the half tile crosses the diagonal of this sub-block
 #pragma unroll
         for (int r = 0; r < 16; ++r)
             if (kb + acc_row(r, half) > qj + col) s[r] = 0.0f;
     }
 #pragma unroll
-    for (int r = 0; r < 16; ++r) s[r] *= dp[r] - sb.dlt;
+    for (int r = 0; r < 16; ++r) s[r] *= dp[r];
     db[0] = pack_b(s, 0);
     db[1] = pack_b(s, 1);
 }
 
 // One 32-key half tile for sub-block 1, and sub-block 0 too when BOTH.  ka/va: this lane's
 // row-read addresses in the K / V tile; kta: transposing-read addresses in the K tile.
+// -lse2 and -D enter S^T and dP^T as one more contraction step: the A operand `one`
+// (1, 1, 0, ...) times the sub-block's statistic chunks (hi, lo, 0, ...).
 template <int D, bool BOTH>
 __device__ __forceinline__ void dq_half(int kb, const uint32_t (&ka)[D / 16],
                                         const uint32_t (&va)[D / 16],
-                                        const uint32_t (&kta)[D / 32], DqSub<D>& sb0,
-                                        DqSub<D>& sb1, int qj0, int qj1, int col, int half,
-                                        float c) {
-    f32x16 s0 = f32x16{}, s1 = f32x16{}, p0 = f32x16{}, p1 = f32x16{};
+                                        const uint32_t (&kta)[D / 32], const bf16x8& one,
+                                        DqSub<D>& sb0, DqSub<D>& sb1, int qj0, int qj1, int col,
+                                        int half) {
+    f32x16 s0, s1, p0, p1;
+    s1 = mfma_32x32x16_bf16(one, sb1.xs, f32x16{});
+    if constexpr (BOTH) s0 = mfma_32x32x16_bf16(one, sb0.xs, f32x16{});
 #pragma unroll
     for (int st = 0; st < D / 16; ++st) {
         const bf16x8 a = lds_b128(ka[st]);
         s1 = mfma_32x32x16_bf16(a, sb1.q[st], s1);
         if constexpr (BOTH) s0 = mfma_32x32x16_bf16(a, sb0.q[st], s0);
     }
+    p1 = mfma_32x32x16_bf16(one, sb1.xd, f32x16{});
+    if constexpr (BOTH) p0 = mfma_32x32x16_bf16(one, sb0.xd, f32x16{});
 #pragma unroll
     for (int st = 0; st < D / 16; ++st) {
         const bf16x8 a = lds_b128(va[st]);
@@ -150,8 +192,8 @@ __device__ __forceinline__ void dq_half(int kb, const uint32_t (&ka)[D / 16],
         if constexpr (BOTH) p0 = mfma_32x32x16_bf16(a, sb0.g[st], p0);
     }
     bf16x8 d0[2], d1[2];
-    dq_ds<D>(s1, p1, sb1, d1, kb, qj1, col, half, c);
-    if constexpr (BOTH) dq_ds<D>(s0, p0, sb0, d0, kb, qj0, col, half, c);
+    dq_ds(s1, p1, d1, kb, qj1, col, half);
+    if constexpr (BOTH) dq_ds(s0, p0, d0, kb, qj0, col, half);
 #pragma unroll
     for (int dt = 0; dt < D / 32; ++dt) {
 #pragma unroll
@@ -200,10 +242,11 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_bwd_dq_bf16_kernel(
 
     DqSub<D> sb0, sb1;
     dq_init<D>(sb1, q + xoff, o + ooff, dO + ooff, m, l, Dws, xrs, ors, stat_off, qj1 + col, T,
-               half);
+               half, c);
     if constexpr (NSUB == 2)
         dq_init<D>(sb0, q + xoff, o + ooff, dO + ooff, m, l, Dws, xrs, ors, stat_off, qj0 + col,
-                   T, half);
+                   T, half, c);
+    const bf16x8 one = ones_pair(half);
 
     uint32_t roff[D / 16], troff[D / 32];
     lane_offsets<D>(lane, roff, troff);
@@ -237,11 +280,11 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_bwd_dq_bf16_kernel(
     int hh = 0;
     for (; hh < hA; ++hh) {
         tile_sync(hh);
-        dq_half<D, true>(32 * hh, ka, va, kta, sb0, sb1, qj0, qj1, col, half, c);
+        dq_half<D, true>(32 * hh, ka, va, kta, one, sb0, sb1, qj0, qj1, col, half);
     }
     for (; hh < hB; ++hh) {
         tile_sync(hh);
-        dq_half<D, false>(32 * hh, ka, va, kta, sb0, sb1, qj0, qj1, col, half, c);
+        dq_half<D, false>(32 * hh, ka, va, kta, one, sb0, sb1, qj0, qj1, col, half);
     }
     for (; hh < hend; ++hh) tile_sync(hh);
 
@@ -261,13 +304,6 @@ struct HalfAddr {
     uint32_t qt[D / 32], gt[D / 32];  // transposing reads, head-dim tile dt
     uint32_t qx, gx;                  // statistic chunks of row col
 };
-
-// x as the bf16 pair (hi, lo), hi + lo = x to ~2^-16 relative, packed into one dword.
-__device__ __forceinline__ uint32_t split_bf16x2(float x) {
-    const uint16_t hi = f32_to_bf16_bits(x);
-    const uint16_t lo = f32_to_bf16_bits(x - bf16_bits_to_f32(hi));
-    return static_cast<uint32_t>(hi) | (static_cast<uint32_t>(lo) << 16);
-}
 
 // S' = Q (cK)^T - lse2 and dP' = dO V^T - D of one half tile.  The statistics ride in the
 // products: a fifth 16-wide contraction step multiplies the row's chunk (hi, lo, 0, ...)
@@ -373,11 +409,7 @@ __global__ __launch_bounds__(kWave* NW) void flash_bwd_dkdv_bf16_kernel(
             *reinterpret_cast<u16x8*>(&sm.gx[b][lane * 8]) = z;
         }
     }
-    bf16x8 one = bf16x8{};
-    if (half == 0) {
-        one[0] = static_cast<__bf16>(1.0f);
-        one[1] = static_cast<__bf16>(1.0f);
-    }
+    const bf16x8 one = ones_pair(half);
 
     bf16x8 kr[D / 16], vr[D / 16];
     load_rowop<D>(kr, k + xoff, kj, T, half, xrs);

@@ -294,6 +294,41 @@ int attn_fused_causal_backward_dkdv_bf16(const attn_bf16* qkv, const attn_bf16* 
                                          int H, int T, int d_head, float scale,
                                          hipStream_t stream);
 
+/* ------------------------------------------------------------------------------------------
+ * fp32 on bf16 matrix cores.  The fp32 entry points above run the fp32 MFMA (157 TFLOP/s
+ * peak on MI355X); these compute the same fp32 attention on the bf16 MFMA (16x the rate):
+ * every fp32 operand x is carried as three bf16 planes x_0 + x_1 + x_2 (24 significant
+ * bits, all of fp32's) and every product a*b as the six plane products a_i*b_j, i + j <= 2
+ * (what is left out is below 2^-23 |a*b|, about one fp32 rounding), accumulated in fp32.
+ * Inputs, outputs and statistics are fp32 with the meaning of the packed / fused entry
+ * points.  d_head 32 or 64.
+ *
+ * `planes` is caller-owned device memory of attn_f32x3_workspace_bytes(B, H, T, d_head)
+ * bytes (16-byte aligned) for the planes of k, v, q and dO.  The forward writes those of k
+ * and v; a backward with kv_planes_ready = 1 reuses them (the caller guarantees that qkv and
+ * the workspace are unchanged since that forward), with 0 it splits k and v again.  The
+ * backward's d_workspace is the B*H*T floats of D, as in the other backward entry points.
+ * No counterpart in the reference (an MI355X-specific form of
+ * src/kernels/attention.cu:518-1012).
+ * ------------------------------------------------------------------------------------------ */
+size_t attn_f32x3_workspace_bytes(int B, int H, int T, int d_head);
+int attn_packed_causal_forward_f32x3(const float* qkv, float* out, int B, int H, int T,
+                                     int d_head, float scale, float* m_out, float* l_out,
+                                     void* planes, hipStream_t stream);
+int attn_fused_causal_forward_f32x3(const float* qkv, float* out, int B, int H, int T,
+                                    int d_head, float scale, float* m_out, float* l_out,
+                                    void* planes, hipStream_t stream);
+int attn_packed_causal_backward_f32x3(const float* qkv, const float* o, const float* do_ptr,
+                                      const float* m_ptr, const float* l_ptr, float* dqkv,
+                                      float* d_workspace, int B, int H, int T, int d_head,
+                                      float scale, void* planes, int kv_planes_ready,
+                                      hipStream_t stream);
+int attn_fused_causal_backward_f32x3(const float* qkv, const float* o, const float* do_ptr,
+                                     const float* m_ptr, const float* l_ptr, float* dqkv,
+                                     float* d_workspace, int B, int H, int T, int d_head,
+                                     float scale, void* planes, int kv_planes_ready,
+                                     hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,226 @@
+"""fp32 attention on the bf16 matrix cores (the *_f32x3 entry points: every fp32 operand as
+three bf16 planes, every product as six plane products) against the restated reference
+(torch fp32 on the CPU, pytorch_src/model.py:43-52) at the reference gate, max-abs <= 1e-5
+(scripts/compare_parity.py:108-116), with the distance to fp64 of this path, of the fp32
+MFMA path and of torch fp32 printed side by side."""
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import default_scale, max_abs
+from oracle import attention_ref as ref
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+
+
+def heads(qkv, B, H, T, d):
+    """q, k, v (B, H, T, d) of a packed (B, T, 3C) tensor (reference map attention.cu:40-47)."""
+    x = qkv.reshape(B, T, 3, H, d).permute(2, 0, 3, 1, 4)
+    return x[0].contiguous(), x[1].contiguous(), x[2].contiguous()
+
+
+def planes(lib, B, H, T, d):
+    n = lib.f32x3_workspace_bytes(B, H, T, d)
+    return torch.empty(n, dtype=torch.uint8, device="cuda:0")
+
+
+def x3_forward(lib, qkv, B, H, T, d, scale, merged=False):
+    shape = (B, T, H * d) if merged else (B, H, T, d)
+    o = torch.full(shape, float("nan"), device="cuda:0")
+    m = torch.full((B, H, T), float("nan"), device="cuda:0")
+    l = torch.full_like(m, float("nan"))
+    ws = planes(lib, B, H, T, d)
+    f = lib.fused_causal_attention_forward_f32x3 if merged else \
+        lib.packed_causal_attention_forward_f32x3
+    f(qkv, o, B, H, T, d, scale, ws, m, l)
+    torch.cuda.synchronize()
+    if merged:
+        o = o.reshape(B, T, H, d).permute(0, 2, 1, 3).contiguous()
+    return o.cpu(), m.cpu(), l.cpu()
+
+
+def mfma_forward(lib, qkv, B, H, T, d, scale):
+    o = torch.empty((B, H, T, d), device="cuda:0")
+    m = torch.empty((B, H, T), device="cuda:0")
+    l = torch.empty_like(m)
+    lib.packed_causal_attention_forward(qkv, o, B, H, T, d, scale, m, l)
+    torch.cuda.synchronize()
+    return o.cpu(), m.cpu(), l.cpu()
+
+
+SHAPES = [(1, 1, 1, 64), (2, 3, 17, 32), (1, 2, 100, 64), (2, 2, 257, 32), (2, 4, 640, 64),
+          (1, 2, 1000, 64)]
+
+
+@pytest.mark.parametrize("B,H,T,d", SHAPES)
+@pytest.mark.parametrize("merged", [False, True])
+def test_forward_vs_oracle(lib, B, H, T, d, merged):
+    g = torch.Generator(device="cpu").manual_seed(T * 5 + d)
+    qkv = torch.randn((B, T, 3 * H * d), generator=g)
+    scale = default_scale(d)
+    o, m, l = x3_forward(lib, qkv.to("cuda:0"), B, H, T, d, scale, merged)
+    q, k, v = heads(qkv, B, H, T, d)
+    want = ref.attention_fwd_bwd(q, k, v, torch.zeros_like(q), scale, dtype=torch.float32,
+                                 with_grad=False)
+    assert max_abs(o.numpy(), want.o.numpy()) <= TOL
+    lse = (m + torch.log(l)).numpy()
+    assert max_abs(lse, want.lse.numpy()) <= TOL
+    assert max_abs(m.numpy(), want.m.numpy()) <= TOL
+
+
+def test_forward_config2_against_fp64(lib):
+    """BASELINE config 2 (B8 H12 T1024 d64, seed 42): within the gate of torch fp32, and as
+    close to fp64 as the fp32 MFMA path."""
+    B, H, T, d = 8, 12, 1024, 64
+    g = torch.Generator(device="cpu").manual_seed(42)
+    qkv = torch.randn((B, T, 3 * H * d), generator=g)
+    dev = qkv.to("cuda:0")
+    o, m, l = x3_forward(lib, dev, B, H, T, d, 0.125)
+    o32, m32, l32 = mfma_forward(lib, dev, B, H, T, d, 0.125)
+    q, k, v = heads(qkv, B, H, T, d)
+    want = ref.attention_fwd_bwd(q, k, v, torch.zeros_like(q), 0.125, dtype=torch.float32,
+                                 with_grad=False)
+    w64 = ref.attention_fwd_bwd(q, k, v, torch.zeros_like(q), 0.125, dtype=torch.float64,
+                                with_grad=False)
+    e = {"x3": max_abs(o.numpy(), w64.o.numpy()), "mfma_f32": max_abs(o32.numpy(), w64.o.numpy()),
+         "torch_f32": max_abs(want.o.numpy(), w64.o.numpy())}
+    print("config2 O max-abs to fp64:", {k: f"{x:.2e}" for k, x in e.items()})
+    assert max_abs(o.numpy(), want.o.numpy()) <= TOL
+    assert max_abs((m + torch.log(l)).numpy(), want.lse.numpy()) <= TOL
+    assert e["x3"] <= 2 * max(e["mfma_f32"], e["torch_f32"])
+
+
+def test_forward_closed_forms(lib):
+    """V = 1 gives O = 1; Q = 0 gives the prefix mean of V and LSE = ln(i + 1)."""
+    B, H, T, d = 1, 2, 300, 64
+    g = torch.Generator(device="cpu").manual_seed(3)
+    qkv = torch.randn((B, T, 3 * H * d), generator=g)
+    C = H * d
+    ones = qkv.clone()
+    ones[..., 2 * C:] = 1.0
+    o, _, _ = x3_forward(lib, ones.to("cuda:0"), B, H, T, d, 0.125)
+    assert max_abs(o.numpy(), np.ones_like(o.numpy())) <= 1e-6
+    zq = qkv.clone()
+    zq[..., :C] = 0.0
+    o, m, l = x3_forward(lib, zq.to("cuda:0"), B, H, T, d, 0.125)
+    _, _, v = heads(zq, B, H, T, d)
+    prefix = torch.cumsum(v.double(), 2) / torch.arange(1, T + 1, dtype=torch.float64).view(1, 1, T, 1)
+    assert max_abs(o.numpy(), prefix.numpy()) <= 1e-5
+    lse = (m + torch.log(l)).double().numpy()
+    assert max_abs(lse, np.log(np.arange(1, T + 1))[None, None, :]) <= 1e-5
+
+
+def test_workspace_and_validation(lib):
+    B, H, T, d = 2, 3, 40, 64
+    assert lib.f32x3_workspace_bytes(B, H, T, d) == 4 * 3 * B * H * T * d * 2
+    assert lib.f32x3_workspace_bytes(0, H, T, d) == 0
+    qkv = torch.zeros((B, T, 3 * H * d), device="cuda:0")
+    o = torch.empty((B, H, T, d), device="cuda:0")
+    ws = planes(lib, B, H, T, d)
+    st = lib.call("attn_packed_causal_forward_f32x3", qkv.data_ptr(), o.data_ptr(), B, H, T,
+                  128, 0.1, None, None, ws.data_ptr(), None)
+    assert st == 2  # d_head 128: unsupported on this path
+    st = lib.call("attn_packed_causal_forward_f32x3", qkv.data_ptr(), o.data_ptr(), B, H, T, d,
+                  0.1, None, None, None, None)
+    assert st == 3  # planes NULL
+    with pytest.raises(ValueError):
+        lib.packed_causal_attention_forward_f32x3(qkv, o, B, H, T, d, 0.1, ws[:100])
+
+
+def x3_fwd_bwd(lib, qkv, do, B, H, T, d, scale, merged=False, kv_ready=True):
+    """Forward then backward on the GPU; returns head-major o, m, l and dq, dk, dv, D."""
+    shape = (B, T, H * d) if merged else (B, H, T, d)
+    o = torch.full(shape, float("nan"), device="cuda:0")
+    m = torch.full((B, H, T), float("nan"), device="cuda:0")
+    l = torch.full_like(m, float("nan"))
+    ws = planes(lib, B, H, T, d)
+    fwd = lib.fused_causal_attention_forward_f32x3 if merged else \
+        lib.packed_causal_attention_forward_f32x3
+    bwd = lib.fused_causal_attention_backward_f32x3 if merged else \
+        lib.packed_causal_attention_backward_f32x3
+    fwd(qkv, o, B, H, T, d, scale, ws, m, l)
+    if not kv_ready:
+        ws.fill_(0)  # the backward must split k and v itself
+    if merged:
+        do = do.permute(0, 2, 1, 3).reshape(B, T, H * d).contiguous()
+    dqkv = torch.full_like(qkv, float("nan"))
+    D = torch.full_like(m, float("nan"))
+    bwd(qkv, o, do, m, l, dqkv, D, B, H, T, d, scale, ws, kv_ready)
+    torch.cuda.synchronize()
+    if merged:
+        o = o.reshape(B, T, H, d).permute(0, 2, 1, 3).contiguous()
+    dq, dk, dv = heads(dqkv.cpu(), B, H, T, d)
+    return {"o": o.cpu(), "m": m.cpu(), "l": l.cpu(), "dq": dq, "dk": dk, "dv": dv,
+            "D": D.cpu()}
+
+
+BWD_SHAPES = [(1, 1, 1, 64), (2, 3, 17, 32), (1, 2, 100, 64), (2, 2, 257, 32),
+              (2, 4, 640, 64), (1, 1, 1000, 64)]
+
+
+@pytest.mark.parametrize("B,H,T,d", BWD_SHAPES)
+@pytest.mark.parametrize("merged,kv_ready", [(False, True), (True, True), (False, False)])
+def test_backward_vs_oracle(lib, B, H, T, d, merged, kv_ready):
+    g = torch.Generator(device="cpu").manual_seed(T * 3 + d)
+    qkv = torch.randn((B, T, 3 * H * d), generator=g)
+    do = torch.randn((B, H, T, d), generator=g)
+    scale = default_scale(d)
+    got = x3_fwd_bwd(lib, qkv.to("cuda:0"), do.to("cuda:0"), B, H, T, d, scale, merged,
+                     kv_ready)
+    q, k, v = heads(qkv, B, H, T, d)
+    want = ref.attention_fwd_bwd(q, k, v, do, scale, dtype=torch.float32)
+    for n in ("o", "dq", "dk", "dv"):
+        e = max_abs(got[n].numpy(), getattr(want, n).numpy())
+        assert e <= TOL, f"{n}: max-abs {e:.3e} > {TOL}"
+    D = (do.double() * want.o.double()).sum(-1)
+    assert max_abs(got["D"].numpy(), D.numpy()) <= TOL
+
+
+def test_backward_config2_against_fp64(lib):
+    """every gradient within the gate of torch fp32 and as close to fp64
+    as the fp32 MFMA path's."""
+    B, H, T, d = 8, 12, 1024, 64
+    g = torch.Generator(device="cpu").manual_seed(42)
+    qkv = torch.randn((B, T, 3 * H * d), generator=g)
+    do = torch.randn((B, H, T, d), generator=g)
+    dev, ddev = qkv.to("cuda:0"), do.to("cuda:0")
+    got = x3_fwd_bwd(lib, dev, ddev, B, H, T, d, 0.125)
+    o = torch.empty((B, H, T, d), device="cuda:0")
+    m = torch.empty((B, H, T), device="cuda:0")
+    l = torch.empty_like(m)
+    lib.packed_causal_attention_forward(dev, o, B, H, T, d, 0.125, m, l)
+    dqkv = torch.empty_like(dev)
+    D = torch.empty_like(m)
+    lib.packed_causal_attention_backward(dev, o, ddev, m, l, dqkv, D, B, H, T, d, 0.125)
+    torch.cuda.synchronize()
+    mf = dict(zip(("dq", "dk", "dv"), heads(dqkv.cpu(), B, H, T, d)))
+    mf["o"] = o.cpu()
+    q, k, v = heads(qkv, B, H, T, d)
+    want = ref.attention_fwd_bwd(q, k, v, do, 0.125, dtype=torch.float32)
+    w64 = ref.attention_fwd_bwd(q, k, v, do, 0.125, dtype=torch.float64)
+    for n in ("o", "dq", "dk", "dv"):
+        w = getattr(w64, n).numpy()
+        e = (max_abs(got[n].numpy(), w), max_abs(mf[n].numpy(), w),
+             max_abs(getattr(want, n).numpy(), w))
+        print(f"config2 {n} max-abs to fp64 (x3, mfma f32, torch f32): "
+              f"{e[0]:.2e} {e[1]:.2e} {e[2]:.2e}")
+        assert max_abs(got[n].numpy(), getattr(want, n).numpy()) <= TOL
+        assert e[0] <= 2 * max(e[1], e[2])
+
+
+def test_backward_reference_kat(lib):
+    """The reference's known-answer input (tests/test_kernels.cu:245-268: q = k = 0.1,
+    v = 1, dO = 0.5, T = 8, d = 32): O = 1, dQ = dK = 0, dV_j = 0.5 sum_{i>=j} 1/(i+1)."""
+    B, H, T, d = 1, 1, 8, 32
+    qkv = torch.full((B, T, 3 * H * d), 0.1)
+    qkv[..., 2 * d:] = 1.0
+    do = torch.full((B, H, T, d), 0.5)
+    got = x3_fwd_bwd(lib, qkv.to("cuda:0"), do.to("cuda:0"), B, H, T, d, 1 / np.sqrt(d))
+    np.testing.assert_allclose(got["o"].numpy(), 1.0, atol=1e-6)
+    np.testing.assert_allclose(got["dq"].numpy(), 0.0, atol=1e-6)
+    np.testing.assert_allclose(got["dk"].numpy(), 0.0, atol=1e-6)
+    want = np.array([sum(0.5 / (i + 1) for i in range(j, T)) for j in range(T)])
+    np.testing.assert_allclose(got["dv"][0, 0].numpy(), np.repeat(want[:, None], d, 1),
+                               rtol=1e-6)

@@ -91,6 +91,12 @@ SIGNATURES = {
         [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P],
     "attn_tiled_causal_backward_dkdv_bf16":
         [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P],
+    "attn_packed_causal_forward_f32x3": [_P, _P, _I, _I, _I, _I, _F, _P, _P, _P, _P],
+    "attn_fused_causal_forward_f32x3": [_P, _P, _I, _I, _I, _I, _F, _P, _P, _P, _P],
+    "attn_packed_causal_backward_f32x3":
+        [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P, _I, _P],
+    "attn_fused_causal_backward_f32x3":
+        [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P, _I, _P],
 }
 
 for _name, _args in SIGNATURES.items():
@@ -101,6 +107,8 @@ _lib.attn_status_string.argtypes = [_I]
 _lib.attn_status_string.restype = ctypes.c_char_p
 _lib.attn_version.argtypes = []
 _lib.attn_version.restype = ctypes.c_int
+_lib.attn_f32x3_workspace_bytes.argtypes = [_I, _I, _I, _I]
+_lib.attn_f32x3_workspace_bytes.restype = ctypes.c_size_t
 
 
 def raw():
@@ -376,6 +384,69 @@ def fused_causal_attention_backward_dkdv(qkv, dO, m, l, workspace, dqkv, B, H, T
     """Stage 2 of the fused backward."""
     _qkv_backward("fused", "_dkdv", qkv, None, dO, m, l, dqkv, workspace, B, H, T, d_head,
                   scale, stream)
+
+
+def f32x3_workspace_bytes(B, H, T, d_head):
+    """Bytes of the plane workspace of the *_f32x3 entry points (include/attn_capi.h)."""
+    return int(_lib.attn_f32x3_workspace_bytes(B, H, T, d_head))
+
+
+def _planes_ptr(planes, B, H, T, d_head):
+    need = f32x3_workspace_bytes(B, H, T, d_head)
+    if planes is not None and planes.numel() * planes.element_size() < need:
+        raise ValueError(f"planes: needs {need} bytes")
+    return _ptr(planes, None, None, "planes")
+
+
+def _qkv_forward_f32x3(family, qkv, out, B, H, T, d_head, scale, planes, m_out, l_out,
+                       stream):
+    n, r = B * H * T * d_head, B * H * T
+    f32 = _dt(False)
+    check(call(f"attn_{family}_causal_forward_f32x3", _ptr(qkv, f32, 3 * n, "qkv"),
+               _ptr(out, f32, n, "out"), B, H, T, d_head, float(scale),
+               _ptr(m_out, f32, r, "m_out"), _ptr(l_out, f32, r, "l_out"),
+               _planes_ptr(planes, B, H, T, d_head), _stream(stream)),
+          f"{family}_causal_attention_forward_f32x3")
+
+
+def packed_causal_attention_forward_f32x3(qkv, out, B, H, T, d_head, scale, planes, m_out=None,
+                                          l_out=None, stream=None):
+    """packed_causal_attention_forward for fp32 on the bf16 matrix cores (operands as three
+    bf16 planes in `planes`, f32x3_workspace_bytes bytes)."""
+    _qkv_forward_f32x3("packed", qkv, out, B, H, T, d_head, scale, planes, m_out, l_out, stream)
+
+
+def fused_causal_attention_forward_f32x3(qkv, out, B, H, T, d_head, scale, planes, m_out=None,
+                                         l_out=None, stream=None):
+    """fused_causal_attention_forward for fp32 on the bf16 matrix cores."""
+    _qkv_forward_f32x3("fused", qkv, out, B, H, T, d_head, scale, planes, m_out, l_out, stream)
+
+
+def _qkv_backward_f32x3(family, qkv, o, dO, m, l, dqkv, workspace, B, H, T, d_head, scale,
+                        planes, kv_planes_ready, stream):
+    n, r = B * H * T * d_head, B * H * T
+    f32 = _dt(False)
+    check(call(f"attn_{family}_causal_backward_f32x3", _ptr(qkv, f32, 3 * n, "qkv"),
+               _ptr(o, f32, n, "o"), _ptr(dO, f32, n, "dO"), _ptr(m, f32, r, "m"),
+               _ptr(l, f32, r, "l"), _ptr(dqkv, f32, 3 * n, "dqkv"),
+               _ptr(workspace, f32, r, "workspace"), B, H, T, d_head, float(scale),
+               _planes_ptr(planes, B, H, T, d_head), 1 if kv_planes_ready else 0,
+               _stream(stream)), f"{family}_causal_attention_backward_f32x3")
+
+
+def packed_causal_attention_backward_f32x3(qkv, o, dO, m, l, dqkv, workspace, B, H, T, d_head,
+                                           scale, planes, kv_planes_ready=False, stream=None):
+    """packed_causal_attention_backward for fp32 on the bf16 matrix cores; kv_planes_ready
+    reuses the k/v planes the forward left in `planes` (qkv unchanged since)."""
+    _qkv_backward_f32x3("packed", qkv, o, dO, m, l, dqkv, workspace, B, H, T, d_head, scale,
+                        planes, kv_planes_ready, stream)
+
+
+def fused_causal_attention_backward_f32x3(qkv, o, dO, m, l, dqkv, workspace, B, H, T, d_head,
+                                          scale, planes, kv_planes_ready=False, stream=None):
+    """fused_causal_attention_backward for fp32 on the bf16 matrix cores."""
+    _qkv_backward_f32x3("fused", qkv, o, dO, m, l, dqkv, workspace, B, H, T, d_head, scale,
+                        planes, kv_planes_ready, stream)
 
 
 def attention_precompute_dot_do_o(dO, O, D, B, H, T, d_head, stream=None):

@@ -39,15 +39,15 @@ __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_ex
 //     256-byte bank line, where they meet no slot of the first block.
 // Both the swizzle and the padding repeat every 8 rows, so a row offset that is a multiple
 // of 8 is a constant byte offset (rows()).
-template <int D>
+template <int D, int ROWS = kRowTile>
 struct Swz {
     static constexpr int kCpr = D / 8;  // 16-byte chunks per row
     static constexpr int kRowBytes = 2 * D;
     static constexpr int kPad = D >= 64 ? 128 : 0;
     static constexpr int kBlockData = 8 * kRowBytes;
     static constexpr int kBlockBytes = kBlockData + kPad;
-    static constexpr int kBytes = (kRowTile / 8) * kBlockBytes;  // one tile
-    static constexpr int kDma = kRowTile * kRowBytes / 1024;     // wave instructions per tile
+    static constexpr int kBytes = (ROWS / 8) * kBlockBytes;  // one tile of ROWS rows
+    static constexpr int kDma = ROWS * kRowBytes / 1024;     // wave instructions per tile
     static_assert(kPad == 0 || kBlockData % 1024 == 0, "a copy instruction stays in a block");
     // Byte offset of row n (a multiple of 8).
     static constexpr uint32_t rows(int n) { return static_cast<uint32_t>((n / 8) * kBlockBytes); }
@@ -64,14 +64,14 @@ struct Swz {
     }
 };
 
-// Wave `wave` of NW issues its share of the copy of rows [row0, row0 + 64) of a head (T rows
-// of D bf16, consecutive rows rs elements apart) into the tile at LDS byte address lds.
+// Wave `wave` of NW issues its share of the copy of rows [row0, row0 + ROWS) of a head (T
+// rows of D bf16, consecutive rows rs elements apart) into the tile at LDS byte address lds.
 // Rows past T are read from row T-1 (finite values; every consumer masks or zero-weights
 // them).
-template <int D, int NW = kWaves>
+template <int D, int NW = kWaves, int ROWS = kRowTile>
 __device__ __forceinline__ void dma_tile(const uint16_t* __restrict__ head, int row0, int T,
                                          uint32_t lds, int wave, int lane, int rs) {
-    using S = Swz<D>;
+    using S = Swz<D, ROWS>;
     const uint16_t* base = head + static_cast<size_t>(row0) * rs;
 #pragma unroll
     for (int i = wave; i < S::kDma; i += NW) {
@@ -123,6 +123,113 @@ __device__ __forceinline__ void store_row(uint16_t* __restrict__ head, int row, 
             o[2] = f32_to_bf16_bits(acc[dt][4 * g + 2] * mul);
             o[3] = f32_to_bf16_bits(acc[dt][4 * g + 3] * mul);
             *reinterpret_cast<u16x4*>(p + dt * 32 + 8 * g) = o;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------
+// fp32 operands as bf16 planes.  An fp32 value x is carried as NP bf16 values (planes)
+// x_0 + x_1 + ... with x_0 = bf16(x), x_i = bf16(x - x_0 - ... - x_{i-1}) (round to nearest
+// even).  NP = 1 is the bf16 path itself.  NP = 3 keeps 3 x 8 significant bits, all of
+// fp32's 24, and a product a*b is taken as the six plane products a_i*b_j with i + j <= 2;
+// the three left out are below 2^-23 |a*b| together, about one fp32 rounding.
+// ---------------------------------------------------------------------------------------
+
+// c + A*B over planes, the small products first.
+template <int NP>
+__device__ __forceinline__ f32x16 mma_planes(const bf16x8 (&a)[NP], const bf16x8 (&b)[NP],
+                                             f32x16 c) {
+    static_assert(NP == 1 || NP == 3, "1 or 3 planes");
+    if constexpr (NP == 1) {
+        return mfma_32x32x16_bf16(a[0], b[0], c);
+    } else {
+        c = mfma_32x32x16_bf16(a[2], b[0], c);
+        c = mfma_32x32x16_bf16(a[1], b[1], c);
+        c = mfma_32x32x16_bf16(a[0], b[2], c);
+        c = mfma_32x32x16_bf16(a[1], b[0], c);
+        c = mfma_32x32x16_bf16(a[0], b[1], c);
+        return mfma_32x32x16_bf16(a[0], b[0], c);
+    }
+}
+
+// The planes of 8 fp32 values.
+template <int NP>
+__device__ __forceinline__ void split_planes(const float (&x)[8], bf16x8 (&p)[NP]) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        float r = x[e];
+#pragma unroll
+        for (int i = 0; i < NP; ++i) {
+            const __bf16 h = static_cast<__bf16>(r);
+            p[i][e] = h;
+            if (i + 1 < NP) r -= static_cast<float>(h);
+        }
+    }
+}
+
+// pack_b over planes: accumulator rows acc_row(8u .. 8u+7, half) as NP B operands.
+template <int NP>
+__device__ __forceinline__ void pack_planes(const f32x16& x, int u, bf16x8 (&p)[NP]) {
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = x[8 * u + e];
+    split_planes<NP>(v, p);
+}
+
+// load_rowop over planes: dst[s][i] = chunk s of plane i of row `row`; plane i lies
+// pstride elements after plane i-1.
+template <int D, int NP>
+__device__ __forceinline__ void load_rowop_planes(bf16x8 (&dst)[D / 16][NP],
+                                                  const uint16_t* __restrict__ head,
+                                                  size_t pstride, int row, int T, int half,
+                                                  int rs) {
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+        bf16x8 t[D / 16];
+        load_rowop<D>(t, head + i * pstride, row, T, half, rs);
+#pragma unroll
+        for (int st = 0; st < D / 16; ++st) dst[st][i] = t[st];
+    }
+}
+
+// load_rowop_planes from fp32 rows: the planes of row `row` of an fp32 head (rows rs
+// floats apart), split in registers.
+template <int D, int NP>
+__device__ __forceinline__ void load_rowop_split(bf16x8 (&dst)[D / 16][NP],
+                                                 const float* __restrict__ head, int row, int T,
+                                                 int half, int rs) {
+#pragma unroll
+    for (int st = 0; st < D / 16; ++st) {
+        float x[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        if (row < T) {
+            const float* p = head + static_cast<size_t>(row) * rs + 16 * st + 8 * half;
+            const f32x4 a = *reinterpret_cast<const f32x4*>(p);
+            const f32x4 b = *reinterpret_cast<const f32x4*>(p + 4);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                x[e] = a[e];
+                x[e + 4] = b[e];
+            }
+        }
+        split_planes<NP>(x, dst[st]);
+    }
+}
+
+// store_row in fp32.
+template <int D>
+__device__ __forceinline__ void store_row(float* __restrict__ head, int row, int half,
+                                          const f32x16 (&acc)[D / 32], float mul, int rs) {
+    float* p = head + static_cast<size_t>(row) * rs + 4 * half;
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            f32x4 o;
+            o[0] = acc[dt][4 * g + 0] * mul;
+            o[1] = acc[dt][4 * g + 1] * mul;
+            o[2] = acc[dt][4 * g + 2] * mul;
+            o[3] = acc[dt][4 * g + 3] * mul;
+            *reinterpret_cast<f32x4*>(p + dt * 32 + 8 * g) = o;
         }
     }
 }

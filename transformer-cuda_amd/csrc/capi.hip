@@ -200,6 +200,81 @@ int packed_backward(const E* qkv, const E* o, const E* dO, const float* m, const
     return packed_backward_dkdv(qkv, dO, m, l, ws, dqkv, B, H, T, d, scale, merged, stream);
 }
 
+// ---- fp32 on bf16 MFMAs: operands as three bf16 planes in a caller workspace -------------
+// Workspace: four tensors (q, k, v, dO) x three planes x N = B*H*T*d bf16, head-major.
+
+constexpr int kPlaneTensors = 4;
+constexpr int kPlanes = 3;
+
+size_t plane_elems(int B, int H, int T, int d) {
+    return static_cast<size_t>(B) * H * T * d;
+}
+uint16_t* plane_tensor(void* planes, size_t N, int tensor) {
+    return static_cast<uint16_t*>(planes) + static_cast<size_t>(tensor) * kPlanes * N;
+}
+
+int check_f32x3(int B, int H, int T, int d, float scale) {
+    const int st = check_packed(B, H, T, d, scale);
+    if (st != ATTN_SUCCESS) return st;
+    if (d != 32 && d != 64) return ATTN_ERROR_UNSUPPORTED_HEAD_DIM;
+    return ATTN_SUCCESS;
+}
+
+// k and v of qkv (B, T, 3C) into their planes (tensors 1 and 2 of the workspace).
+void split_kv_planes(const float* qkv, void* planes, int B, int H, int T, int d,
+                     hipStream_t stream) {
+    const size_t N = plane_elems(B, H, T, d), C = static_cast<size_t>(H) * d;
+    const tcamd::HeadView xv = tcamd::packed_qkv_view(H, T, d);
+    for (int t = 1; t < 3; ++t)
+        tcamd::launch_split_planes(qkv + t * C, xv, plane_tensor(planes, N, t), N, B * H, T, d,
+                                   stream);
+}
+
+int packed_forward_f32x3(const float* qkv, float* out, int B, int H, int T, int d, float scale,
+                         float* m_out, float* l_out, void* planes, bool merged,
+                         hipStream_t stream) {
+    if (qkv == nullptr || out == nullptr || planes == nullptr) return ATTN_ERROR_NULL_POINTER;
+    const int st = check_f32x3(B, H, T, d, scale);
+    if (st != ATTN_SUCCESS) return st;
+    if (!aligned16(qkv) || !aligned16(out) || !aligned16(planes)) return ATTN_ERROR_MISALIGNED;
+    const size_t N = plane_elems(B, H, T, d);
+    clear_error();
+    split_kv_planes(qkv, planes, B, H, T, d, stream);
+    tcamd::launch_flash_fwd_f32x3(qkv, tcamd::packed_qkv_view(H, T, d),
+                                  plane_tensor(planes, N, 1), plane_tensor(planes, N, 2), N, out,
+                                  m_out, l_out, B * H, T, d, scale,
+                                  tcamd::head_major_view(H, T, d), out_view(H, T, d, merged),
+                                  stream);
+    return launch_status();
+}
+
+int packed_backward_f32x3(const float* qkv, const float* o, const float* dO, const float* m,
+                          const float* l, float* dqkv, float* ws, int B, int H, int T, int d,
+                          float scale, void* planes, int kv_ready, bool merged,
+                          hipStream_t stream) {
+    if (o == nullptr || planes == nullptr) return ATTN_ERROR_NULL_POINTER;
+    int st = check_packed_bwd(qkv, dO, m, l, dqkv, ws, B, H, T, d, scale);
+    if (st != ATTN_SUCCESS) return st;
+    st = check_f32x3(B, H, T, d, scale);
+    if (st != ATTN_SUCCESS) return st;
+    if (!aligned16(o) || !aligned16(planes)) return ATTN_ERROR_MISALIGNED;
+    const size_t N = plane_elems(B, H, T, d), C = static_cast<size_t>(H) * d;
+    const tcamd::HeadView xv = tcamd::packed_qkv_view(H, T, d);
+    const tcamd::HeadView hv = tcamd::head_major_view(H, T, d);
+    const tcamd::HeadView ov = out_view(H, T, d, merged);
+    clear_error();
+    if (!kv_ready) split_kv_planes(qkv, planes, B, H, T, d, stream);
+    tcamd::launch_split_planes(qkv, xv, plane_tensor(planes, N, 0), N, B * H, T, d, stream);
+    tcamd::launch_split_planes(dO, ov, plane_tensor(planes, N, 3), N, B * H, T, d, stream);
+    tcamd::launch_flash_bwd_dq_f32x3(qkv, xv, plane_tensor(planes, N, 1),
+                                     plane_tensor(planes, N, 2), hv, N, o, dO, ov, m, l, dqkv,
+                                     xv, ws, B * H, T, d, scale, stream);
+    tcamd::launch_flash_bwd_dkdv_f32x3(plane_tensor(planes, N, 0), plane_tensor(planes, N, 3),
+                                       hv, N, qkv + C, qkv + 2 * C, xv, m, l, ws, dqkv + C,
+                                       dqkv + 2 * C, xv, B * H, T, d, scale, stream);
+    return launch_status();
+}
+
 }  // namespace
 
 
@@ -662,6 +737,47 @@ int attn_fused_causal_backward_bf16(const attn_bf16* qkv, const attn_bf16* o,
                                     hipStream_t stream) {
     return packed_backward(qkv, o, do_ptr, m_ptr, l_ptr, dqkv, d_workspace, B, H, T, d_head,
                            scale, true, stream);
+}
+
+
+// ---- fp32 on bf16 MFMAs (three bf16 planes per operand) --------------------------------
+
+size_t attn_f32x3_workspace_bytes(int B, int H, int T, int d_head) {
+    if (B <= 0 || H <= 0 || T <= 0 || d_head <= 0) return 0;
+    return static_cast<size_t>(kPlaneTensors) * kPlanes * plane_elems(B, H, T, d_head) *
+           sizeof(uint16_t);
+}
+
+int attn_packed_causal_forward_f32x3(const float* qkv, float* out, int B, int H, int T,
+                                     int d_head, float scale, float* m_out, float* l_out,
+                                     void* planes, hipStream_t stream) {
+    return packed_forward_f32x3(qkv, out, B, H, T, d_head, scale, m_out, l_out, planes, false,
+                                stream);
+}
+
+int attn_fused_causal_forward_f32x3(const float* qkv, float* out, int B, int H, int T,
+                                    int d_head, float scale, float* m_out, float* l_out,
+                                    void* planes, hipStream_t stream) {
+    return packed_forward_f32x3(qkv, out, B, H, T, d_head, scale, m_out, l_out, planes, true,
+                                stream);
+}
+
+int attn_packed_causal_backward_f32x3(const float* qkv, const float* o, const float* do_ptr,
+                                      const float* m_ptr, const float* l_ptr, float* dqkv,
+                                      float* d_workspace, int B, int H, int T, int d_head,
+                                      float scale, void* planes, int kv_planes_ready,
+                                      hipStream_t stream) {
+    return packed_backward_f32x3(qkv, o, do_ptr, m_ptr, l_ptr, dqkv, d_workspace, B, H, T,
+                                 d_head, scale, planes, kv_planes_ready, false, stream);
+}
+
+int attn_fused_causal_backward_f32x3(const float* qkv, const float* o, const float* do_ptr,
+                                     const float* m_ptr, const float* l_ptr, float* dqkv,
+                                     float* d_workspace, int B, int H, int T, int d_head,
+                                     float scale, void* planes, int kv_planes_ready,
+                                     hipStream_t stream) {
+    return packed_backward_f32x3(qkv, o, do_ptr, m_ptr, l_ptr, dqkv, d_workspace, B, H, T,
+                                 d_head, scale, planes, kv_planes_ready, true, stream);
 }
 
 }  // extern "C"

@@ -1,35 +1,41 @@
-// flash_bf16.hip - tiled causal attention backward, bf16 fast path, on
-// v_mfma_f32_32x32x16_bf16 with fp32 accumulation (the forward is in flash_bf16_fwd.hip).
+// flash_bf16.hip - tiled causal attention backward on v_mfma_f32_32x32x16_bf16 with fp32
+// accumulation (the forward is in flash_bf16_fwd.hip), for bf16 operands (NP = 1) and for
+// fp32 operands carried as NP = 3 bf16 planes (bf16_tile.hpp).
 //
 // Algorithm: the reference's analytical backward (src/kernels/attention.cu:626-955) in the
 // split form of the fp32 path: stage 1 (query-parallel) writes D = rowsum(dO * O) and dQ,
 // stage 2 (key-parallel) dK and dV, both recomputing P = 2^(s*c - lse2) from the forward's
-// statistics (lse2 = m*log2 e + log2 l, the log2-domain log-sum-exp).  P and dS are rounded
-// to bf16 as MFMA operands; dQ/dK/dV are rounded once, at the store.
+// statistics (lse2 = m*log2 e + log2 l, the log2-domain log-sum-exp).  P and dS are MFMA
+// operands in NP planes (NP = 1: rounded to bf16); dQ/dK/dV are stored in bf16 (NP = 1,
+// rounded once) or fp32 (NP = 3).
 //
-// Both stages use the forward's staging: 64-row tiles copied HBM -> LDS with
+// Both stages use the forward's staging: tiles copied HBM -> LDS with
 // global_load_lds_dwordx4 into XOR-swizzled rows, double buffered and shared by the 4 waves
-// of a workgroup.  A product that contracts over the head dimension reads its A operand as
-// 16-byte row reads of a tile and its B operand from VGPRs; a product that contracts over
-// the sequence reads its A operand with ds_read_tr16_b64 from the same row-major tile and
-// takes its B operand (P or dS, rounded to bf16) straight from the accumulator of the
-// score product, whose rows are the contracted positions.
+// of a workgroup (NP planes per tile).  A product that contracts over the head dimension
+// reads its A operand as 16-byte row reads of a tile and its B operand from VGPRs; a
+// product that contracts over the sequence reads its A operand with ds_read_tr16_b64 from
+// the same row-major tile and takes its B operand (P or dS) straight from the accumulator of
+// the score product, whose rows are the contracted positions.  With NP = 3 the tiles come
+// from plane tensors in HBM and the register operands are split from the fp32 rows.
 //
-// Stage 1, per 32-key half tile and 32-query sub-block (d = 64: 12 MFMAs):
-//   S^T  = K Q^T      A = K rows,  B = Q (VGPRs)
-//   dP^T = V dO^T     A = V rows,  B = dO (VGPRs)
-//   dS^T = P^T o (dP^T - D)        lane l holds query l%32: lse2 and D are per lane
-//   dQ^T += K^T dS^T  A = K^T (transposing reads of the K tile), B = dS^T
-// A workgroup owns 256 queries (d <= 64; wave w: sub-blocks w and 7-w, as the forward) or
-// 128 (d = 128, one sub-block per wave, for registers).
+// Stage 1, per 32-key half tile and 32-query sub-block (d = 64, NP = 1: 14 MFMAs):
+//   S'^T = K (cQ)^T - lse2   A = K rows, B = c*Q (VGPRs), plus one contraction step
+//   dP'^T = V dO^T - D       A = V rows, B = dO (VGPRs), plus one contraction step
+//   dS^T = 2^S'^T o dP'^T    lane l holds query l%32
+//   dQ^T += K^T dS^T         A = K^T (transposing reads of the K tile), B = dS^T
+// The per-query -lse2 and -D enter the products as one more 16-wide contraction step: the
+// A operand (1, 1, 0, ...) times a statistic chunk (hi, lo, 0, ...) (NP = 3: three ones and
+// three terms).  A workgroup owns 256 queries (d <= 64; wave w: sub-blocks w and 7-w, as the
+// forward) or 128 (one sub-block per wave: d = 128, small grids).  NP = 3 streams 32-key
+// tiles, so that the double-buffered K and V planes leave room for two workgroups per CU.
 //
-// Stage 2, per 32-query half tile and a wave's 32 keys (d = 64: 18 MFMAs):
+// Stage 2, per 32-query half tile and a wave's 32 keys (d = 64, NP = 1: 18 MFMAs):
 //   S  = Q K^T        A = Q rows,  B = K (VGPRs)
 //   dP = dO V^T       A = dO rows, B = V (VGPRs)
 //   dS = P o (dP - D)              -lse2 and -D enter S and dP as one more contraction step
-//                                  over a per-row (hi, lo) bf16 chunk (see dkdv_scores); K is
-//                                  held pre-multiplied by c = scale*log2 e, so P = 2^S
-//                                  needs no per-element multiply
+//                                  over a per-row statistic chunk held in LDS (see
+//                                  dkdv_scores); K is held pre-multiplied by
+//                                  c = scale*log2 e, so P = 2^S needs no per-element multiply
 //   dV^T += dO^T P    A = dO^T (transposing reads), B = P
 //   dK^T += Q^T dS    A = Q^T (transposing reads),  B = dS
 // A workgroup owns 128 keys; query tiles start at the workgroup's first key, and wave w
@@ -49,50 +55,110 @@ namespace {
 
 using namespace bf16t;
 
-// K and V tiles of stage 1 (same shape as the forward's).
-template <int D>
+// Element types: register-operand rows (bf16 or fp32) and outputs.
+template <int NP>
+using InT = std::conditional_t<NP == 1, uint16_t, float>;
+template <int NP>
+using OutT = std::conditional_t<NP == 1, uint16_t, float>;
+
+// Terms of a statistic chunk: (hi, lo) carries 16 significant bits, enough next to bf16
+// operands; fp32 operands take three.
+template <int NP>
+constexpr int kStatTerms = NP == 1 ? 2 : 3;
+
+// Key rows per stage-1 tile.
+template <int NP>
+constexpr int kKeyTileDq = NP == 1 ? kRowTile : 32;
+
+// K and V tiles of stage 1 (as the forward's), NP planes each.
+template <int D, int NP>
 struct KvSmem {
-    uint16_t k[2][Swz<D>::kBytes / 2];
-    uint16_t v[2][Swz<D>::kBytes / 2];
+    uint16_t k[2][NP][Swz<D, kKeyTileDq<NP>>::kBytes / 2];
+    uint16_t v[2][NP][Swz<D, kKeyTileDq<NP>>::kBytes / 2];
 };
 
-// Q and dO tiles of stage 2, each with an extra 8-element column chunk per row that carries
+// Q and dO tiles of stage 2 (NP planes each), and per row an 8-element chunk that carries
 // the row's statistic (see dkdv_scores).
-template <int D>
+template <int D, int NP>
 struct QgSmem {
-    uint16_t q[2][Swz<D>::kBytes / 2];
-    uint16_t g[2][Swz<D>::kBytes / 2];
-    uint16_t qx[2][kRowTile * 8];  // row r: (-lse2)_hi, (-lse2)_lo, 0 x 6
-    uint16_t gx[2][kRowTile * 8];  // row r: (-D)_hi, (-D)_lo, 0 x 6
+    uint16_t q[2][NP][Swz<D>::kBytes / 2];
+    uint16_t g[2][NP][Swz<D>::kBytes / 2];
+    uint16_t qx[2][kRowTile * 8];  // row r: the terms of -lse2, then zeros
+    uint16_t gx[2][kRowTile * 8];  // row r: the terms of -D, then zeros
 };
 
-// x as the bf16 pair (hi, lo), hi + lo = x to ~2^-16 relative, packed into one dword.
-__device__ __forceinline__ uint32_t split_bf16x2(float x) {
-    const uint16_t hi = f32_to_bf16_bits(x);
-    const uint16_t lo = f32_to_bf16_bits(x - bf16_bits_to_f32(hi));
-    return static_cast<uint32_t>(hi) | (static_cast<uint32_t>(lo) << 16);
+// The terms of x: x_0 = bf16(x), x_i = bf16(x - x_0 - ... - x_{i-1}).
+template <int NP>
+__device__ __forceinline__ u16x4 stat_terms(float x) {
+    u16x4 v = u16x4{};
+#pragma unroll
+    for (int i = 0; i < kStatTerms<NP>; ++i) {
+        v[i] = f32_to_bf16_bits(x);
+        x -= bf16_bits_to_f32(v[i]);
+    }
+    return v;
 }
 
-// The B or A operand (1, 1, 0, ...) of a contraction step that adds a per-row statistic
-// (hi, lo) to a product: lanes of k-group 1 hold zeros.
-__device__ __forceinline__ bf16x8 ones_pair(int half) {
+// The B or A operand (1, 1, [1,] 0, ...) of a contraction step that adds a per-row
+// statistic chunk to a product: lanes of k-group 1 hold zeros.
+template <int NP>
+__device__ __forceinline__ bf16x8 ones_chunk(int half) {
     bf16x8 one = bf16x8{};
     if (half == 0) {
-        one[0] = static_cast<__bf16>(1.0f);
-        one[1] = static_cast<__bf16>(1.0f);
+#pragma unroll
+        for (int i = 0; i < kStatTerms<NP>; ++i) one[i] = static_cast<__bf16>(1.0f);
     }
     return one;
 }
 
-// The statistic chunk (x_hi, x_lo, 0, ...) of a lane's row (zeros in k-group 1).
+// The statistic chunk (terms of x, 0, ...) of a lane's row (zeros in k-group 1).
+template <int NP>
 __device__ __forceinline__ bf16x8 stat_chunk(float x, int half) {
     u16x8 v = u16x8{};
     if (half == 0) {
-        const uint32_t p = split_bf16x2(x);
-        v[0] = static_cast<uint16_t>(p);
-        v[1] = static_cast<uint16_t>(p >> 16);
+        const u16x4 t = stat_terms<NP>(x);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = t[i];
     }
     return __builtin_bit_cast(bf16x8, v);
+}
+
+// A register operand over the head dimension: the NP planes of row `row` of a head (rows rs
+// elements apart; zeros if row >= T), times `mul` first when SCALE (NP = 1: the bf16 value
+// times mul, rounded to bf16 again; NP = 3: the fp32 value times mul, then split).
+template <int D, int NP, bool SCALE>
+__device__ __forceinline__ void load_operand(bf16x8 (&dst)[D / 16][NP],
+                                             const InT<NP>* __restrict__ head, int row, int T,
+                                             int half, int rs, float mul) {
+    if constexpr (NP == 1) {
+        bf16x8 t[D / 16];
+        load_rowop<D>(t, head, row, T, half, rs);
+#pragma unroll
+        for (int st = 0; st < D / 16; ++st) {
+            if constexpr (SCALE) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    t[st][e] = static_cast<__bf16>(static_cast<float>(t[st][e]) * mul);
+            }
+            dst[st][0] = t[st];
+        }
+    } else {
+#pragma unroll
+        for (int st = 0; st < D / 16; ++st) {
+            float x[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            if (row < T) {
+                const float* p = head + static_cast<size_t>(row) * rs + 16 * st + 8 * half;
+                const f32x4 a = *reinterpret_cast<const f32x4*>(p);
+                const f32x4 b = *reinterpret_cast<const f32x4*>(p + 4);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    x[e] = SCALE ? a[e] * mul : a[e];
+                    x[e + 4] = SCALE ? b[e] * mul : b[e];
+                }
+            }
+            split_planes<NP>(x, dst[st]);
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------------------
@@ -100,56 +166,69 @@ __device__ __forceinline__ bf16x8 stat_chunk(float x, int half) {
 // ---------------------------------------------------------------------------------------
 
 // One 32-query sub-block of a wave.
-template <int D>
+template <int D, int NP>
 struct DqSub {
-    bf16x8 q[D / 16];    // c * Q row of query col (B operand over d)
-    bf16x8 g[D / 16];    // dO row
-    bf16x8 xs, xd;       // statistic chunks: -lse2 (-1e30 for padded queries: P = 0), -D
-    f32x16 acc[D / 32];  // dQ^T
+    bf16x8 q[D / 16][NP];  // c * Q row of query col (B operand over d)
+    bf16x8 g[D / 16][NP];  // dO row
+    bf16x8 xs, xd;         // statistic chunks: -lse2 (-1e30 for padded queries: P = 0), -D
+    f32x16 acc[D / 32];    // dQ^T
 };
 
-// qh: this head's q (rows xrs apart); oh, gh: its o and dO (rows ors apart).  Q is held
-// pre-multiplied by c = scale*log2 e and rounded to bf16 (one extra rounding, ~2^-9
-// relative per element), so that the scores come out in the log2 domain.
-template <int D>
-__device__ __forceinline__ void dq_init(DqSub<D>& sb, const uint16_t* __restrict__ qh,
-                                        const uint16_t* __restrict__ oh,
-                                        const uint16_t* __restrict__ gh,
+// qh: this head's q (rows qrs apart); oh, gh: its o and dO (rows ors apart).  Q is held
+// pre-multiplied by c = scale*log2 e (NP = 1: rounded to bf16, one extra rounding of ~2^-9
+// relative per element; NP = 3: in fp32, then split), so that the scores come out in the
+// log2 domain.  D = rowsum(dO o O) in fp32 from the stored O and dO.
+template <int D, int NP>
+__device__ __forceinline__ void dq_init(DqSub<D, NP>& sb, const InT<NP>* __restrict__ qh,
+                                        const InT<NP>* __restrict__ oh,
+                                        const InT<NP>* __restrict__ gh,
                                         const float* __restrict__ m, const float* __restrict__ l,
-                                        float* __restrict__ Dws, int xrs, int ors,
+                                        float* __restrict__ Dws, int qrs, int ors,
                                         size_t stat_off, int qi, int T, int half, float c) {
-    load_rowop<D>(sb.q, qh, qi, T, half, xrs);
-    load_rowop<D>(sb.g, gh, qi, T, half, ors);
-    bf16x8 orow[D / 16];
-    load_rowop<D>(orow, oh, qi, T, half, ors);
+    load_operand<D, NP, false>(sb.g, gh, qi, T, half, ors, 1.0f);
     float part = 0.0f;
+    if constexpr (NP == 1) {
+        bf16x8 orow[D / 16];
+        load_rowop<D>(orow, oh, qi, T, half, ors);
 #pragma unroll
-    for (int j = 0; j < D / 16; ++j) {
+        for (int j = 0; j < D / 16; ++j) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-            part = fmaf(static_cast<float>(sb.g[j][e]), static_cast<float>(orow[j][e]), part);
+            for (int e = 0; e < 8; ++e)
+                part = fmaf(static_cast<float>(sb.g[j][0][e]), static_cast<float>(orow[j][e]),
+                            part);
+        }
+    } else if (qi < T) {
+        const float* gp = gh + static_cast<size_t>(qi) * ors;
+        const float* op = oh + static_cast<size_t>(qi) * ors;
+#pragma unroll
+        for (int j = 0; j < D / 16; ++j) {
+#pragma unroll
+            for (int e = 0; e < 8; e += 4) {
+                const f32x4 a = *reinterpret_cast<const f32x4*>(gp + 16 * j + 8 * half + e);
+                const f32x4 b = *reinterpret_cast<const f32x4*>(op + 16 * j + 8 * half + e);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) part = fmaf(a[i], b[i], part);
+            }
+        }
     }
-#pragma unroll
-    for (int j = 0; j < D / 16; ++j) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) sb.q[j][e] = static_cast<__bf16>(static_cast<float>(sb.q[j][e]) * c);
-    }
+    load_operand<D, NP, true>(sb.q, qh, qi, T, half, qrs, c);
     const float dlt = xhalf_sum(part);
     float nl = -1e30f;
     if (qi < T) {
         if (half == 0) Dws[stat_off + qi] = dlt;
         nl = -(m[stat_off + qi] * kLog2e + log2f(l[stat_off + qi]));
     }
-    sb.xs = stat_chunk(nl, half);
-    sb.xd = stat_chunk(-dlt, half);
+    sb.xs = stat_chunk<NP>(nl, half);
+    sb.xd = stat_chunk<NP>(-dlt, half);
 #pragma unroll
     for (int dt = 0; dt < D / 32; ++dt) sb.acc[dt] = f32x16{};
 }
 
 // s = S'^T = K (cQ)^T - lse2, dp = dP'^T = V dO^T - D of keys kb.. (rows) x queries qj + col
-// (columns) -> dS^T = 2^s o dp as the two B operands of dQ^T += K^T dS^T.  Keys past the
-// query get P = 0.
-__device__ __forceinline__ void dq_ds(f32x16& s, const f32x16& dp, bf16x8 (&db)[2], int kb,
+// (columns) -> dS^T = 2^s o dp as the two B operands (NP planes each) of dQ^T += K^T dS^T.
+// Keys past the query get P = 0.
+template <int NP>
+__device__ __forceinline__ void dq_ds(f32x16& s, const f32x16& dp, bf16x8 (&db)[2][NP], int kb,
                                       int qj, int col, int half) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) s[r] = exp2_fast(s[r]);
@@ -160,93 +239,128 @@ __device__ __forceinline__ void dq_ds(f32x16& s, const f32x16& dp, bf16x8 (&db)[
     }
 #pragma unroll
     for (int r = 0; r < 16; ++r) s[r] *= dp[r];
-    db[0] = pack_b(s, 0);
-    db[1] = pack_b(s, 1);
+    pack_planes<NP>(s, 0, db[0]);
+    pack_planes<NP>(s, 1, db[1]);
 }
 
 // One 32-key half tile for sub-block 1, and sub-block 0 too when BOTH.  ka/va: this lane's
-// row-read addresses in the K / V tile; kta: transposing-read addresses in the K tile.
-// -lse2 and -D enter S^T and dP^T as one more contraction step: the A operand `one`
-// (1, 1, 0, ...) times the sub-block's statistic chunks (hi, lo, 0, ...).
-template <int D, bool BOTH>
+// row-read addresses in plane 0 of the K / V tile; kta: transposing-read addresses in plane
+// 0 of the K tile; plane i lies i tile sizes further.  -lse2 and -D enter S^T and dP^T as
+// one more contraction step: the A operand `one` times the sub-block's statistic chunks.
+template <int D, bool BOTH, int NP>
 __device__ __forceinline__ void dq_half(int kb, const uint32_t (&ka)[D / 16],
                                         const uint32_t (&va)[D / 16],
                                         const uint32_t (&kta)[D / 32], const bf16x8& one,
-                                        DqSub<D>& sb0, DqSub<D>& sb1, int qj0, int qj1, int col,
-                                        int half) {
+                                        DqSub<D, NP>& sb0, DqSub<D, NP>& sb1, int qj0, int qj1,
+                                        int col, int half) {
+    constexpr uint32_t kPlane = Swz<D, kKeyTileDq<NP>>::kBytes;
     f32x16 s0, s1, p0, p1;
     s1 = mfma_32x32x16_bf16(one, sb1.xs, f32x16{});
     if constexpr (BOTH) s0 = mfma_32x32x16_bf16(one, sb0.xs, f32x16{});
 #pragma unroll
     for (int st = 0; st < D / 16; ++st) {
-        const bf16x8 a = lds_b128(ka[st]);
-        s1 = mfma_32x32x16_bf16(a, sb1.q[st], s1);
-        if constexpr (BOTH) s0 = mfma_32x32x16_bf16(a, sb0.q[st], s0);
+        bf16x8 a[NP];
+#pragma unroll
+        for (int i = 0; i < NP; ++i) a[i] = lds_b128(ka[st] + i * kPlane);
+        s1 = mma_planes<NP>(a, sb1.q[st], s1);
+        if constexpr (BOTH) s0 = mma_planes<NP>(a, sb0.q[st], s0);
     }
     p1 = mfma_32x32x16_bf16(one, sb1.xd, f32x16{});
     if constexpr (BOTH) p0 = mfma_32x32x16_bf16(one, sb0.xd, f32x16{});
 #pragma unroll
     for (int st = 0; st < D / 16; ++st) {
-        const bf16x8 a = lds_b128(va[st]);
-        p1 = mfma_32x32x16_bf16(a, sb1.g[st], p1);
-        if constexpr (BOTH) p0 = mfma_32x32x16_bf16(a, sb0.g[st], p0);
+        bf16x8 a[NP];
+#pragma unroll
+        for (int i = 0; i < NP; ++i) a[i] = lds_b128(va[st] + i * kPlane);
+        p1 = mma_planes<NP>(a, sb1.g[st], p1);
+        if constexpr (BOTH) p0 = mma_planes<NP>(a, sb0.g[st], p0);
     }
-    bf16x8 d0[2], d1[2];
-    dq_ds(s1, p1, d1, kb, qj1, col, half);
-    if constexpr (BOTH) dq_ds(s0, p0, d0, kb, qj0, col, half);
+    bf16x8 d0[2][NP], d1[2][NP];
+    dq_ds<NP>(s1, p1, d1, kb, qj1, col, half);
+    if constexpr (BOTH) dq_ds<NP>(s0, p0, d0, kb, qj0, col, half);
 #pragma unroll
     for (int dt = 0; dt < D / 32; ++dt) {
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-            const bf16x8 a = lds_tr(kta[dt] + u * Swz<D>::rows(16), Swz<D>::rows(8));
-            sb1.acc[dt] = mfma_32x32x16_bf16(a, d1[u], sb1.acc[dt]);
-            if constexpr (BOTH) sb0.acc[dt] = mfma_32x32x16_bf16(a, d0[u], sb0.acc[dt]);
+            bf16x8 a[NP];
+#pragma unroll
+            for (int i = 0; i < NP; ++i)
+                a[i] = lds_tr(kta[dt] + i * kPlane + u * Swz<D>::rows(16), Swz<D>::rows(8));
+            sb1.acc[dt] = mma_planes<NP>(a, d1[u], sb1.acc[dt]);
+            if constexpr (BOTH) sb0.acc[dt] = mma_planes<NP>(a, d0[u], sb0.acc[dt]);
         }
     }
 }
 
+// Operands of one stage-1 launch.  q, o, dO: register-operand rows (views qv, ov); k, v:
+// plane 0 of the K / V tile sources (view kv, planes pstride elements apart); dq: output
+// rows (view gv).
+template <int NP>
+struct DqArgs {
+    const InT<NP> *q, *o, *dO;
+    const uint16_t *k, *v;
+    const float *m, *l;
+    OutT<NP>* dq;
+    float* Dws;
+    int BH, T;
+    float scale;
+    HeadView qv, kv, ov, gv;
+    size_t pstride;
+};
+
 // NSUB = 2: 256 queries per workgroup, wave w owns sub-blocks w (0) and 7-w (1).
 // NSUB = 1: 128 queries per workgroup, wave w owns sub-block w (1).
-template <int D, int NSUB>
-__global__ __launch_bounds__(kWave* kWaves) void flash_bwd_dq_bf16_kernel(
-    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
-    const uint16_t* __restrict__ v, const uint16_t* __restrict__ o,
-    const uint16_t* __restrict__ dO, const float* __restrict__ m, const float* __restrict__ l,
-    uint16_t* __restrict__ dq, float* __restrict__ Dws, int BH, int T, float scale, int nblk,
-    HeadView xv, HeadView ov, HeadView gv) {
-    using S = Swz<D>;
+template <int D, int NSUB, int NP>
+__global__ __launch_bounds__(kWave* kWaves) void flash_bwd_dq_bf16_kernel(DqArgs<NP> a,
+                                                                         int nblk) {
+    constexpr int KT = kKeyTileDq<NP>;
+    constexpr int kHalves = KT / 32;
+    using S = Swz<D, KT>;
+    constexpr uint32_t kBuf = NP * S::kBytes;  // one K (or V) buffer: NP plane tiles
     constexpr int kBlock = kWaves * NSUB * kSub;
-    __shared__ __attribute__((aligned(1024))) KvSmem<D> sm;
+    __shared__ __attribute__((aligned(1024))) KvSmem<D, NP> sm;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     const int lane = threadIdx.x & (kWave - 1);
     const int col = lane & 31;
     const int half = lane >> 5;
+    const int T = a.T;
     int bh, blk;
-    map_block(blockIdx.x, BH, nblk, true, bh, blk);
+    map_block(blockIdx.x, a.BH, nblk, true, bh, blk);
     const int q0 = blk * kBlock;
     const int qj0 = q0 + kSub * wave;
     const int qj1 = NSUB == 2 ? q0 + kSub * (2 * kWaves - 1 - wave) : qj0;
-    const size_t xoff = xv.off(bh), ooff = ov.off(bh), goff = gv.off(bh);
-    const int xrs = xv.row, ors = ov.row, grs = gv.row;
+    const size_t qoff = a.qv.off(bh), koff = a.kv.off(bh), ooff = a.ov.off(bh),
+                 goff = a.gv.off(bh);
+    const int krs = a.kv.row;
     const size_t stat_off = static_cast<size_t>(bh) * T;
-    const uint16_t* kh = k + xoff;
-    const uint16_t* vh = v + xoff;
-    const float c = scale * kLog2e;
+    const uint16_t* kh = a.k + koff;
+    const uint16_t* vh = a.v + koff;
+    const float c = a.scale * kLog2e;
 
     const int kend = min(T, q0 + kBlock);
-    const int ntile = (kend + kRowTile - 1) / kRowTile;
-    const uint32_t k_lds = lds_addr(sm.k[0]);
-    const uint32_t v_lds = lds_addr(sm.v[0]);
-    dma_tile<D>(kh, 0, T, k_lds, wave, lane, xrs);
-    dma_tile<D>(vh, 0, T, v_lds, wave, lane, xrs);
+    const int ntile = (kend + KT - 1) / KT;
+    const uint32_t k_lds = lds_addr(sm.k[0][0]);
+    const uint32_t v_lds = lds_addr(sm.v[0][0]);
+    // Tile kt of K and V (every plane) into buffer kt % 2.
+    auto copy_tile = [&](int kt) {
+        const uint32_t buf = static_cast<uint32_t>(kt & 1) * kBuf;
+#pragma unroll
+        for (int i = 0; i < NP; ++i) {
+            dma_tile<D, kWaves, KT>(kh + i * a.pstride, kt * KT, T, k_lds + buf + i * S::kBytes,
+                                    wave, lane, krs);
+            dma_tile<D, kWaves, KT>(vh + i * a.pstride, kt * KT, T, v_lds + buf + i * S::kBytes,
+                                    wave, lane, krs);
+        }
+    };
+    copy_tile(0);
 
-    DqSub<D> sb0, sb1;
-    dq_init<D>(sb1, q + xoff, o + ooff, dO + ooff, m, l, Dws, xrs, ors, stat_off, qj1 + col, T,
-               half, c);
+    DqSub<D, NP> sb0, sb1;
+    dq_init<D, NP>(sb1, a.q + qoff, a.o + ooff, a.dO + ooff, a.m, a.l, a.Dws, a.qv.row,
+                   a.ov.row, stat_off, qj1 + col, T, half, c);
     if constexpr (NSUB == 2)
-        dq_init<D>(sb0, q + xoff, o + ooff, dO + ooff, m, l, Dws, xrs, ors, stat_off, qj0 + col,
-                   T, half, c);
-    const bf16x8 one = ones_pair(half);
+        dq_init<D, NP>(sb0, a.q + qoff, a.o + ooff, a.dO + ooff, a.m, a.l, a.Dws, a.qv.row,
+                       a.ov.row, stat_off, qj0 + col, T, half, c);
+    const bf16x8 one = ones_chunk<NP>(half);
 
     uint32_t roff[D / 16], troff[D / 32];
     lane_offsets<D>(lane, roff, troff);
@@ -254,21 +368,17 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_bwd_dq_bf16_kernel(
     const int nhalf_t = (T + 31) / 32;
     const int hA = NSUB == 2 ? min(qj0 / 32 + 1, nhalf_t) : 0;
     const int hB = min(qj1 / 32 + 1, nhalf_t);
-    const int hend = 2 * ntile;
+    const int hend = kHalves * ntile;
     uint32_t ka[D / 16], va[D / 16], kta[D / 32];
     auto tile_sync = [&](int hh) {
-        const int kt = hh >> 1;
-        if ((hh & 1) == 0) {
+        const int kt = hh / kHalves;
+        if (hh % kHalves == 0) {
             wait_vm<0>();     // this wave's copies of tile kt landed ...
             __syncthreads();  // ... and every wave's; tile kt-1 is no longer read by anyone
-            if (kt + 1 < ntile) {
-                const uint32_t nbuf = static_cast<uint32_t>((kt + 1) & 1) * S::kBytes;
-                dma_tile<D>(kh, (kt + 1) * kRowTile, T, k_lds + nbuf, wave, lane, xrs);
-                dma_tile<D>(vh, (kt + 1) * kRowTile, T, v_lds + nbuf, wave, lane, xrs);
-            }
+            if (kt + 1 < ntile) copy_tile(kt + 1);
         }
-        const uint32_t base = static_cast<uint32_t>(kt & 1) * S::kBytes +
-                              static_cast<uint32_t>(hh & 1) * S::rows(32);
+        const uint32_t base = static_cast<uint32_t>(kt & 1) * kBuf +
+                              static_cast<uint32_t>(hh % kHalves) * S::rows(32);
 #pragma unroll
         for (int st = 0; st < D / 16; ++st) {
             ka[st] = k_lds + base + roff[st];
@@ -280,24 +390,25 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_bwd_dq_bf16_kernel(
     int hh = 0;
     for (; hh < hA; ++hh) {
         tile_sync(hh);
-        dq_half<D, true>(32 * hh, ka, va, kta, one, sb0, sb1, qj0, qj1, col, half);
+        dq_half<D, true, NP>(32 * hh, ka, va, kta, one, sb0, sb1, qj0, qj1, col, half);
     }
     for (; hh < hB; ++hh) {
         tile_sync(hh);
-        dq_half<D, false>(32 * hh, ka, va, kta, one, sb0, sb1, qj0, qj1, col, half);
+        dq_half<D, false, NP>(32 * hh, ka, va, kta, one, sb0, sb1, qj0, qj1, col, half);
     }
     for (; hh < hend; ++hh) tile_sync(hh);
 
-    if (qj1 + col < T) store_row<D>(dq + goff, qj1 + col, half, sb1.acc, scale, grs);
+    if (qj1 + col < T) store_row<D>(a.dq + goff, qj1 + col, half, sb1.acc, a.scale, a.gv.row);
     if constexpr (NSUB == 2)
-        if (qj0 + col < T) store_row<D>(dq + goff, qj0 + col, half, sb0.acc, scale, grs);
+        if (qj0 + col < T) store_row<D>(a.dq + goff, qj0 + col, half, sb0.acc, a.scale, a.gv.row);
 }
 
 // ---------------------------------------------------------------------------------------
 // Stage 2: dK, dV.
 // ---------------------------------------------------------------------------------------
 
-// Per-lane operands of one 32-query half tile of stage 2.
+// Per-lane operands of one 32-query half tile of stage 2 (plane 0; plane i lies i tile
+// sizes further).
 template <int D>
 struct HalfAddr {
     uint32_t q[D / 16], g[D / 16];    // row reads, chunk step st
@@ -306,28 +417,40 @@ struct HalfAddr {
 };
 
 // S' = Q (cK)^T - lse2 and dP' = dO V^T - D of one half tile.  The statistics ride in the
-// products: a fifth 16-wide contraction step multiplies the row's chunk (hi, lo, 0, ...)
-// by the B operand `one` = (1, 1, 0, ...) (lanes of k-group 1 hold zeros), so that
+// products: one more 16-wide contraction step multiplies the row's chunk (terms, 0, ...)
+// by the B operand `one` = (1, 1, [1,] 0, ...) (lanes of k-group 1 hold zeros), so that
 // 2^S' = P and P o dP' = dS need no per-row values in VGPRs.
-template <int D>
-__device__ __forceinline__ void dkdv_scores(const HalfAddr<D>& a, const bf16x8 (&kr)[D / 16],
-                                            const bf16x8 (&vr)[D / 16], const bf16x8& one,
+template <int D, int NP>
+__device__ __forceinline__ void dkdv_scores(const HalfAddr<D>& a, const bf16x8 (&kr)[D / 16][NP],
+                                            const bf16x8 (&vr)[D / 16][NP], const bf16x8& one,
                                             f32x16& s, f32x16& dp) {
+    constexpr uint32_t kPlane = Swz<D>::kBytes;
     s = mfma_32x32x16_bf16(lds_b128(a.qx), one, f32x16{});
 #pragma unroll
-    for (int st = 0; st < D / 16; ++st) s = mfma_32x32x16_bf16(lds_b128(a.q[st]), kr[st], s);
+    for (int st = 0; st < D / 16; ++st) {
+        bf16x8 x[NP];
+#pragma unroll
+        for (int i = 0; i < NP; ++i) x[i] = lds_b128(a.q[st] + i * kPlane);
+        s = mma_planes<NP>(x, kr[st], s);
+    }
     dp = mfma_32x32x16_bf16(lds_b128(a.gx), one, f32x16{});
 #pragma unroll
-    for (int st = 0; st < D / 16; ++st) dp = mfma_32x32x16_bf16(lds_b128(a.g[st]), vr[st], dp);
+    for (int st = 0; st < D / 16; ++st) {
+        bf16x8 x[NP];
+#pragma unroll
+        for (int i = 0; i < NP; ++i) x[i] = lds_b128(a.g[st] + i * kPlane);
+        dp = mma_planes<NP>(x, vr[st], dp);
+    }
 }
 
 // P = 2^S' (0 where the query precedes the key, on the diagonal half tile) and
 // dS = P o dP'; dV^T += dO^T P, dK^T += Q^T dS.
-template <int D, bool MASK>
+template <int D, bool MASK, int NP>
 __device__ __forceinline__ void dkdv_update(const HalfAddr<D>& a, f32x16& s, const f32x16& dp,
                                             f32x16 (&dk_acc)[D / 32],
                                             f32x16 (&dv_acc)[D / 32], int qb, int kj,
                                             int half) {
+    constexpr uint32_t kPlane = Swz<D>::kBytes;
 #pragma unroll
     for (int r = 0; r < 16; ++r) s[r] = exp2_fast(s[r]);
     if constexpr (MASK) {
@@ -335,65 +458,96 @@ __device__ __forceinline__ void dkdv_update(const HalfAddr<D>& a, f32x16& s, con
         for (int r = 0; r < 16; ++r)
             if (qb + acc_row(r, half) < kj) s[r] = 0.0f;
     }
-    const bf16x8 pb[2] = {pack_b(s, 0), pack_b(s, 1)};
+    bf16x8 pb[2][NP], db[2][NP];
+    pack_planes<NP>(s, 0, pb[0]);
+    pack_planes<NP>(s, 1, pb[1]);
 #pragma unroll
     for (int r = 0; r < 16; ++r) s[r] *= dp[r];
-    const bf16x8 db[2] = {pack_b(s, 0), pack_b(s, 1)};
+    pack_planes<NP>(s, 0, db[0]);
+    pack_planes<NP>(s, 1, db[1]);
 #pragma unroll
     for (int dt = 0; dt < D / 32; ++dt) {
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-            dv_acc[dt] =
-                mfma_32x32x16_bf16(lds_tr(a.gt[dt] + u * Swz<D>::rows(16), Swz<D>::rows(8)), pb[u], dv_acc[dt]);
-            dk_acc[dt] =
-                mfma_32x32x16_bf16(lds_tr(a.qt[dt] + u * Swz<D>::rows(16), Swz<D>::rows(8)), db[u], dk_acc[dt]);
+            bf16x8 g[NP], q[NP];
+#pragma unroll
+            for (int i = 0; i < NP; ++i) {
+                g[i] = lds_tr(a.gt[dt] + i * kPlane + u * Swz<D>::rows(16), Swz<D>::rows(8));
+                q[i] = lds_tr(a.qt[dt] + i * kPlane + u * Swz<D>::rows(16), Swz<D>::rows(8));
+            }
+            dv_acc[dt] = mma_planes<NP>(g, pb[u], dv_acc[dt]);
+            dk_acc[dt] = mma_planes<NP>(q, db[u], dk_acc[dt]);
         }
     }
 }
 
+// Operands of one stage-2 launch.  q, dO: plane 0 of the Q / dO tile sources (views qv,
+// gtv; planes pstride elements apart); k, v: register-operand rows (view kv); dk, dv:
+// output rows (view gv).
+template <int NP>
+struct DkdvArgs {
+    const uint16_t *q, *dO;
+    const InT<NP> *k, *v;
+    const float *m, *l, *Dws;
+    OutT<NP> *dk, *dv;
+    int BH, T;
+    float scale;
+    HeadView qv, gtv, kv, gv;
+    size_t pstride;
+};
+
 // NW waves per workgroup; wave w owns keys k0 + 32w ...
-template <int D, int NW>
-__global__ __launch_bounds__(kWave* NW) void flash_bwd_dkdv_bf16_kernel(
-    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
-    const uint16_t* __restrict__ v, const uint16_t* __restrict__ dO,
-    const float* __restrict__ m, const float* __restrict__ l, const float* __restrict__ Dws,
-    uint16_t* __restrict__ dk, uint16_t* __restrict__ dv, int BH, int T, float scale,
-    int nblk, HeadView xv, HeadView ov, HeadView gv) {
+template <int D, int NW, int NP>
+__global__ __launch_bounds__(kWave* NW) void flash_bwd_dkdv_bf16_kernel(DkdvArgs<NP> a,
+                                                                       int nblk) {
     using S = Swz<D>;
-    constexpr int kBlock = NW * kSub;  // keys per workgroup
-    __shared__ __attribute__((aligned(1024))) QgSmem<D> sm;
+    constexpr uint32_t kBuf = NP * S::kBytes;  // one Q (or dO) buffer: NP plane tiles
+    constexpr int kBlock = NW * kSub;          // keys per workgroup
+    __shared__ __attribute__((aligned(1024))) QgSmem<D, NP> sm;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     const int lane = threadIdx.x & (kWave - 1);
     const int col = lane & 31;
     const int half = lane >> 5;
+    const int T = a.T;
     int bh, blk;
-    map_block(blockIdx.x, BH, nblk, false, bh, blk);  // block 0 sees every query
+    map_block(blockIdx.x, a.BH, nblk, false, bh, blk);  // block 0 sees every query
     const int k0 = blk * kBlock;
     const int kw = k0 + kSub * wave;
     const int kj = kw + col;
-    const size_t xoff = xv.off(bh), ooff = ov.off(bh), goff = gv.off(bh);
-    const int xrs = xv.row, ors = ov.row, grs = gv.row;
+    const size_t qoff = a.qv.off(bh), gtoff = a.gtv.off(bh), koff = a.kv.off(bh),
+                 goff = a.gv.off(bh);
+    const int qrs = a.qv.row, grs = a.gtv.row;
     const size_t stat_off = static_cast<size_t>(bh) * T;
-    const uint16_t* qh = q + xoff;
-    const uint16_t* gh = dO + ooff;
-    const float c = scale * kLog2e;
+    const uint16_t* qh = a.q + qoff;
+    const uint16_t* gh = a.dO + gtoff;
+    const float c = a.scale * kLog2e;
 
     const int t0 = k0 / kRowTile;
     const int ntile = (T + kRowTile - 1) / kRowTile;
-    const uint32_t q_lds = lds_addr(sm.q[0]);
-    const uint32_t g_lds = lds_addr(sm.g[0]);
+    const uint32_t q_lds = lds_addr(sm.q[0][0]);
+    const uint32_t g_lds = lds_addr(sm.g[0][0]);
     const uint32_t qx_lds = lds_addr(sm.qx[0]);
     const uint32_t gx_lds = lds_addr(sm.gx[0]);
-    dma_tile<D, NW>(qh, t0 * kRowTile, T, q_lds, wave, lane, xrs);
-    dma_tile<D, NW>(gh, t0 * kRowTile, T, g_lds, wave, lane, ors);
+    // Tile kt of Q and dO (every plane) into buffer kt % 2.
+    auto copy_tile = [&](int kt) {
+        const uint32_t buf = static_cast<uint32_t>(kt & 1) * kBuf;
+#pragma unroll
+        for (int i = 0; i < NP; ++i) {
+            dma_tile<D, NW>(qh + i * a.pstride, kt * kRowTile, T, q_lds + buf + i * S::kBytes,
+                            wave, lane, qrs);
+            dma_tile<D, NW>(gh + i * a.pstride, kt * kRowTile, T, g_lds + buf + i * S::kBytes,
+                            wave, lane, grs);
+        }
+    };
+    copy_tile(t0);
     // Wave 0 stages the statistics of a tile through VGPRs: lane i holds query 64t + i.
     float st_m = 0.0f, st_l = 1.0f, st_d = 0.0f;
     auto load_stats = [&](int t) {
         const int r = t * kRowTile + lane;
         if (r < T) {
-            st_m = m[stat_off + r];
-            st_l = l[stat_off + r];
-            st_d = Dws[stat_off + r];
+            st_m = a.m[stat_off + r];
+            st_l = a.l[stat_off + r];
+            st_d = a.Dws[stat_off + r];
         } else {
             st_m = -INFINITY;  // padded query: P = 0 (see tile_sync)
             st_l = 1.0f;
@@ -409,17 +563,14 @@ __global__ __launch_bounds__(kWave* NW) void flash_bwd_dkdv_bf16_kernel(
             *reinterpret_cast<u16x8*>(&sm.gx[b][lane * 8]) = z;
         }
     }
-    const bf16x8 one = ones_pair(half);
+    const bf16x8 one = ones_chunk<NP>(half);
 
-    bf16x8 kr[D / 16], vr[D / 16];
-    load_rowop<D>(kr, k + xoff, kj, T, half, xrs);
-    // c*K rounded to bf16 (one extra rounding, ~2^-9 relative per element; the score error it
-    // causes is a random sum over d, ~1e-3 in log2 units for unit-variance inputs)
-#pragma unroll
-    for (int st = 0; st < D / 16; ++st)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) kr[st][e] = static_cast<__bf16>(static_cast<float>(kr[st][e]) * c);
-    load_rowop<D>(vr, v + xoff, kj, T, half, xrs);
+    // c*K (NP = 1: rounded to bf16, one extra rounding of ~2^-9 relative per element; the
+    // score error it causes is a random sum over d, ~1e-3 in log2 units for unit-variance
+    // inputs.  NP = 3: in fp32, then split) and V.
+    bf16x8 kr[D / 16][NP], vr[D / 16][NP];
+    load_operand<D, NP, true>(kr, a.k + koff, kj, T, half, a.kv.row, c);
+    load_operand<D, NP, false>(vr, a.v + koff, kj, T, half, a.kv.row, 1.0f);
     f32x16 dk_acc[D / 32], dv_acc[D / 32];
 #pragma unroll
     for (int dt = 0; dt < D / 32; ++dt) {
@@ -433,81 +584,80 @@ __global__ __launch_bounds__(kWave* NW) void flash_bwd_dkdv_bf16_kernel(
     // Tile kt: wait for its copies, publish its statistics, barrier, start the next copy.
     auto tile_sync = [&](int kt) {
         wait_vm<0>();  // this wave's copies (and statistics loads) of tile kt landed
-        if (wave == 0) {  // -lse2 (-1e30 for padded queries: P = 0) and -D as bf16 pairs
+        if (wave == 0) {  // the terms of -lse2 (-1e30 for padded queries: P = 0) and of -D
             const float nl = st_m == -INFINITY ? -1e30f : -(st_m * kLog2e + log2f(st_l));
-            *reinterpret_cast<uint32_t*>(&sm.qx[kt & 1][lane * 8]) = split_bf16x2(nl);
-            *reinterpret_cast<uint32_t*>(&sm.gx[kt & 1][lane * 8]) = split_bf16x2(-st_d);
+            *reinterpret_cast<u16x4*>(&sm.qx[kt & 1][lane * 8]) = stat_terms<NP>(nl);
+            *reinterpret_cast<u16x4*>(&sm.gx[kt & 1][lane * 8]) = stat_terms<NP>(-st_d);
         }
         __syncthreads();  // every wave's copies landed; tile kt-1 is no longer read
         if (kt + 1 < ntile) {
             if (wave == 0) load_stats(kt + 1);
-            const uint32_t nbuf = static_cast<uint32_t>((kt + 1) & 1) * S::kBytes;
-            dma_tile<D, NW>(qh, (kt + 1) * kRowTile, T, q_lds + nbuf, wave, lane, xrs);
-            dma_tile<D, NW>(gh, (kt + 1) * kRowTile, T, g_lds + nbuf, wave, lane, ors);
+            copy_tile(kt + 1);
         }
     };
     // Operand addresses of half tile hh (queries 32*hh ..).
     auto half_addr = [&](int hh) {
-        HalfAddr<D> a;
+        HalfAddr<D> h;
         const int kt = hh >> 1;
-        const uint32_t base = static_cast<uint32_t>(kt & 1) * S::kBytes +
+        const uint32_t base = static_cast<uint32_t>(kt & 1) * kBuf +
                               static_cast<uint32_t>(hh & 1) * S::rows(32);
 #pragma unroll
         for (int st = 0; st < D / 16; ++st) {
-            a.q[st] = q_lds + base + roff[st];
-            a.g[st] = g_lds + base + roff[st];
+            h.q[st] = q_lds + base + roff[st];
+            h.g[st] = g_lds + base + roff[st];
         }
 #pragma unroll
         for (int dt = 0; dt < D / 32; ++dt) {
-            a.qt[dt] = q_lds + base + troff[dt];
-            a.gt[dt] = g_lds + base + troff[dt];
+            h.qt[dt] = q_lds + base + troff[dt];
+            h.gt[dt] = g_lds + base + troff[dt];
         }
         const uint32_t xrow = static_cast<uint32_t>(((kt & 1) * kRowTile + (hh & 1) * 32 + col) * 16);
-        a.qx = qx_lds + xrow;
-        a.gx = gx_lds + xrow;
-        return a;
+        h.qx = qx_lds + xrow;
+        h.gx = gx_lds + xrow;
+        return h;
     };
     // The same with the buffer parity and half a compile-time constant: every address is a
     // lane offset plus an immediate.
     auto half_addr_c = [&](auto buf, auto hsel) {
-        HalfAddr<D> a;
-        constexpr uint32_t base = static_cast<uint32_t>(decltype(buf)::value) * S::kBytes +
+        HalfAddr<D> h;
+        constexpr uint32_t base = static_cast<uint32_t>(decltype(buf)::value) * kBuf +
                                   static_cast<uint32_t>(decltype(hsel)::value) * S::rows(32);
         constexpr uint32_t xbase = static_cast<uint32_t>(decltype(buf)::value * kRowTile +
                                                          decltype(hsel)::value * 32) * 16u;
 #pragma unroll
         for (int st = 0; st < D / 16; ++st) {
-            a.q[st] = roff[st] + (q_lds + base);
-            a.g[st] = roff[st] + (g_lds + base);
+            h.q[st] = roff[st] + (q_lds + base);
+            h.g[st] = roff[st] + (g_lds + base);
         }
 #pragma unroll
         for (int dt = 0; dt < D / 32; ++dt) {
-            a.qt[dt] = troff[dt] + (q_lds + base);
-            a.gt[dt] = troff[dt] + (g_lds + base);
+            h.qt[dt] = troff[dt] + (q_lds + base);
+            h.gt[dt] = troff[dt] + (g_lds + base);
         }
-        a.qx = soff + (qx_lds + xbase);
-        a.gx = soff + (gx_lds + xbase);
-        return a;
+        h.qx = soff + (qx_lds + xbase);
+        h.gx = soff + (gx_lds + xbase);
+        return h;
     };
     // Both half tiles of tile kt (held in buffer `buf`), no diagonal.
     auto pair_c = [&](int kt, auto buf) {
         const HalfAddr<D> a0 = half_addr_c(buf, std::integral_constant<int, 0>{});
         const HalfAddr<D> a1 = half_addr_c(buf, std::integral_constant<int, 1>{});
         f32x16 s0, dp0, s1, dp1;
-        dkdv_scores<D>(a0, kr, vr, one, s0, dp0);
-        dkdv_scores<D>(a1, kr, vr, one, s1, dp1);
-        dkdv_update<D, false>(a0, s0, dp0, dk_acc, dv_acc, 64 * kt, kj, half);
-        dkdv_update<D, false>(a1, s1, dp1, dk_acc, dv_acc, 64 * kt + 32, kj, half);
+        dkdv_scores<D, NP>(a0, kr, vr, one, s0, dp0);
+        dkdv_scores<D, NP>(a1, kr, vr, one, s1, dp1);
+        dkdv_update<D, false, NP>(a0, s0, dp0, dk_acc, dv_acc, 64 * kt, kj, half);
+        dkdv_update<D, false, NP>(a1, s1, dp1, dk_acc, dv_acc, 64 * kt + 32, kj, half);
     };
     // Both half tiles of tile kt; the first is the diagonal one when MASK0.  The score
     // products of the second half tile are issued before the first half tile's softmax.
     auto pair = [&](int kt, auto mask0) {
         const HalfAddr<D> a0 = half_addr(2 * kt), a1 = half_addr(2 * kt + 1);
         f32x16 s0, dp0, s1, dp1;
-        dkdv_scores<D>(a0, kr, vr, one, s0, dp0);
-        dkdv_scores<D>(a1, kr, vr, one, s1, dp1);
-        dkdv_update<D, decltype(mask0)::value>(a0, s0, dp0, dk_acc, dv_acc, 64 * kt, kj, half);
-        dkdv_update<D, false>(a1, s1, dp1, dk_acc, dv_acc, 64 * kt + 32, kj, half);
+        dkdv_scores<D, NP>(a0, kr, vr, one, s0, dp0);
+        dkdv_scores<D, NP>(a1, kr, vr, one, s1, dp1);
+        dkdv_update<D, decltype(mask0)::value, NP>(a0, s0, dp0, dk_acc, dv_acc, 64 * kt, kj,
+                                                   half);
+        dkdv_update<D, false, NP>(a1, s1, dp1, dk_acc, dv_acc, 64 * kt + 32, kj, half);
     };
 
     // Half tiles before hstart (= kw/32, the one holding the wave's first key) hold only
@@ -521,8 +671,8 @@ __global__ __launch_bounds__(kWave* NW) void flash_bwd_dkdv_bf16_kernel(
         if (hstart & 1) {  // only its second half tile, the diagonal one
             const HalfAddr<D> a1 = half_addr(hstart);
             f32x16 s1, dp1;
-            dkdv_scores<D>(a1, kr, vr, one, s1, dp1);
-            dkdv_update<D, true>(a1, s1, dp1, dk_acc, dv_acc, 32 * hstart, kj, half);
+            dkdv_scores<D, NP>(a1, kr, vr, one, s1, dp1);
+            dkdv_update<D, true, NP>(a1, s1, dp1, dk_acc, dv_acc, 32 * hstart, kj, half);
         } else {
             pair(kt, std::true_type{});
         }
@@ -548,46 +698,35 @@ __global__ __launch_bounds__(kWave* NW) void flash_bwd_dkdv_bf16_kernel(
     }
 
     if (kj < T) {
-        store_row<D>(dk + goff, kj, half, dk_acc, scale, grs);
-        store_row<D>(dv + goff, kj, half, dv_acc, 1.0f, grs);
+        store_row<D>(a.dk + goff, kj, half, dk_acc, a.scale, a.gv.row);
+        store_row<D>(a.dv + goff, kj, half, dv_acc, 1.0f, a.gv.row);
     }
 }
 
-template <int D, int NSUB>
-void dq_launch(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* o,
-               const uint16_t* dO, const float* m, const float* l, uint16_t* dq, float* Dws,
-               int BH, int T, float scale, const HeadView& xv, const HeadView& ov,
-               const HeadView& gv, hipStream_t stream) {
+template <int D, int NSUB, int NP>
+void dq_launch(const DqArgs<NP>& a, hipStream_t stream) {
     constexpr int kBlock = kWaves * NSUB * kSub;
-    const int nblk = (T + kBlock - 1) / kBlock;
-    hipLaunchKernelGGL((flash_bwd_dq_bf16_kernel<D, NSUB>), dim3(BH * nblk),
-                       dim3(kWave * kWaves), 0, stream, q, k, v, o, dO, m, l, dq, Dws, BH, T,
-                       scale, nblk, xv, ov, gv);
+    const int nblk = (a.T + kBlock - 1) / kBlock;
+    hipLaunchKernelGGL((flash_bwd_dq_bf16_kernel<D, NSUB, NP>), dim3(a.BH * nblk),
+                       dim3(kWave * kWaves), 0, stream, a, nblk);
 }
 
-template <int D>
-void dq_dispatch(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* o,
-                 const uint16_t* dO, const float* m, const float* l, uint16_t* dq, float* Dws,
-                 int BH, int T, float scale, const HeadView& xv, const HeadView& ov,
-                 const HeadView& gv, hipStream_t stream) {
+template <int D, int NP>
+void dq_dispatch(const DqArgs<NP>& a, hipStream_t stream) {
     // d = 128 holds one sub-block per wave (registers)
-    if (D >= 128 || use_single_subblock(BH, T))
-        dq_launch<D, 1>(q, k, v, o, dO, m, l, dq, Dws, BH, T, scale, xv, ov, gv, stream);
+    if (D >= 128 || use_single_subblock(a.BH, a.T))
+        dq_launch<D, 1, NP>(a, stream);
     else
-        dq_launch<D, (D >= 128 ? 1 : 2)>(q, k, v, o, dO, m, l, dq, Dws, BH, T, scale, xv, ov, gv,
-                                         stream);
+        dq_launch<D, (D >= 128 ? 1 : 2), NP>(a, stream);
 }
 
-template <int D>
-void dkdv_dispatch(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* dO,
-                   const float* m, const float* l, const float* Dws, uint16_t* dk, uint16_t* dv,
-                   int BH, int T, float scale, const HeadView& xv, const HeadView& ov,
-                   const HeadView& gv, hipStream_t stream) {
+template <int D, int NP>
+void dkdv_dispatch(const DkdvArgs<NP>& a, hipStream_t stream) {
     constexpr int NW = kWaves;
     constexpr int kBlock = NW * kSub;
-    const int nblk = (T + kBlock - 1) / kBlock;
-    hipLaunchKernelGGL((flash_bwd_dkdv_bf16_kernel<D, NW>), dim3(BH * nblk), dim3(kWave * NW), 0,
-                       stream, q, k, v, dO, m, l, Dws, dk, dv, BH, T, scale, nblk, xv, ov, gv);
+    const int nblk = (a.T + kBlock - 1) / kBlock;
+    hipLaunchKernelGGL((flash_bwd_dkdv_bf16_kernel<D, NW, NP>), dim3(a.BH * nblk),
+                       dim3(kWave * NW), 0, stream, a, nblk);
 }
 
 }  // namespace
@@ -597,10 +736,11 @@ void launch_flash_bwd_dq_bf16(const uint16_t* q, const uint16_t* k, const uint16
                               const float* l, uint16_t* dq, float* Dws, int BH, int T, int d,
                               float scale, const HeadView& xv, const HeadView& ov,
                               const HeadView& gv, hipStream_t stream) {
+    const DqArgs<1> a{q, o, dO, k, v, m, l, dq, Dws, BH, T, scale, xv, xv, ov, gv, 0};
     switch (d) {
-        case 32: dq_dispatch<32>(q, k, v, o, dO, m, l, dq, Dws, BH, T, scale, xv, ov, gv, stream); break;
-        case 64: dq_dispatch<64>(q, k, v, o, dO, m, l, dq, Dws, BH, T, scale, xv, ov, gv, stream); break;
-        default: dq_dispatch<128>(q, k, v, o, dO, m, l, dq, Dws, BH, T, scale, xv, ov, gv, stream); break;
+        case 32: dq_dispatch<32, 1>(a, stream); break;
+        case 64: dq_dispatch<64, 1>(a, stream); break;
+        default: dq_dispatch<128, 1>(a, stream); break;
     }
 }
 
@@ -609,11 +749,37 @@ void launch_flash_bwd_dkdv_bf16(const uint16_t* q, const uint16_t* k, const uint
                                 const float* Dws, uint16_t* dk, uint16_t* dv, int BH, int T,
                                 int d, float scale, const HeadView& xv, const HeadView& ov,
                                 const HeadView& gv, hipStream_t stream) {
+    const DkdvArgs<1> a{q, dO, k, v, m, l, Dws, dk, dv, BH, T, scale, xv, ov, xv, gv, 0};
     switch (d) {
-        case 32: dkdv_dispatch<32>(q, k, v, dO, m, l, Dws, dk, dv, BH, T, scale, xv, ov, gv, stream); break;
-        case 64: dkdv_dispatch<64>(q, k, v, dO, m, l, Dws, dk, dv, BH, T, scale, xv, ov, gv, stream); break;
-        default: dkdv_dispatch<128>(q, k, v, dO, m, l, Dws, dk, dv, BH, T, scale, xv, ov, gv, stream); break;
+        case 32: dkdv_dispatch<32, 1>(a, stream); break;
+        case 64: dkdv_dispatch<64, 1>(a, stream); break;
+        default: dkdv_dispatch<128, 1>(a, stream); break;
     }
+}
+
+void launch_flash_bwd_dq_f32x3(const float* q, const HeadView& qv, const uint16_t* k,
+                               const uint16_t* v, const HeadView& kv, size_t pstride,
+                               const float* o, const float* dO, const HeadView& ov,
+                               const float* m, const float* l, float* dq, const HeadView& gv,
+                               float* Dws, int BH, int T, int d, float scale,
+                               hipStream_t stream) {
+    const DqArgs<3> a{q, o, dO, k, v, m, l, dq, Dws, BH, T, scale, qv, kv, ov, gv, pstride};
+    if (d == 32)
+        dq_dispatch<32, 3>(a, stream);
+    else
+        dq_dispatch<64, 3>(a, stream);
+}
+
+void launch_flash_bwd_dkdv_f32x3(const uint16_t* q, const uint16_t* dO, const HeadView& tv,
+                                 size_t pstride, const float* k, const float* v,
+                                 const HeadView& kv, const float* m, const float* l,
+                                 const float* Dws, float* dk, float* dv, const HeadView& gv,
+                                 int BH, int T, int d, float scale, hipStream_t stream) {
+    const DkdvArgs<3> a{q, dO, k, v, m, l, Dws, dk, dv, BH, T, scale, tv, tv, kv, gv, pstride};
+    if (d == 32)
+        dkdv_dispatch<32, 3>(a, stream);
+    else
+        dkdv_dispatch<64, 3>(a, stream);
 }
 
 }  // namespace tcamd

@@ -30,6 +30,8 @@
 // banks (bf16_tile.hpp).
 #include <math.h>
 
+#include <type_traits>
+
 #include "device_common.hpp"
 #include "bf16_tile.hpp"
 #include "launch.hpp"
@@ -39,13 +41,17 @@ namespace {
 
 using namespace bf16t;
 
-constexpr int kKeyTile = kRowTile;    // keys per LDS tile
+// Keys per LDS tile: 64 for bf16; 32 for three planes, whose double-buffered K and V tiles
+// then take 55 KB at d = 64 (two workgroups per CU) instead of 110 KB.
+template <int NP>
+constexpr int kKeyTile = NP == 1 ? kRowTile : 32;
 constexpr float kRescaleLog2 = 8.0f;  // raise the running max only beyond p = 2^8
 
-template <int D>
+// Double-buffered K and V tiles, NP planes each.
+template <int D, int NP>
 struct FwdSmem {
-    uint16_t k[2][Swz<D>::kBytes / 2];
-    uint16_t v[2][Swz<D>::kBytes / 2];
+    uint16_t k[2][NP][Swz<D, kKeyTile<NP>>::kBytes / 2];
+    uint16_t v[2][NP][Swz<D, kKeyTile<NP>>::kBytes / 2];
 };
 
 // Maximum and sum of a lane's 16 scores as balanced trees (dependency depth 3 and 4 instead
@@ -75,9 +81,9 @@ struct SubState {
 };
 
 // Masks S^T for keys kb.. against queries qj + col, runs the online-softmax update of `st`,
-// and packs P as the two B operands of the PV products.
-template <int D>
-__device__ __forceinline__ void softmax_step(f32x16& s, SubState<D>& st, bf16x8 (&pb)[2],
+// and packs P as the two B operands (NP planes each) of the PV products.
+template <int D, int NP>
+__device__ __forceinline__ void softmax_step(f32x16& s, SubState<D>& st, bf16x8 (&pb)[2][NP],
                                              int kb, int qj, int col, int half, float c) {
     if (kb + 31 > qj) {  // the half tile crosses the diagonal of this sub-block
 #pragma unroll
@@ -99,50 +105,67 @@ __device__ __forceinline__ void softmax_step(f32x16& s, SubState<D>& st, bf16x8 
 #pragma unroll
     for (int r = 0; r < 16; ++r) s[r] = exp2_fast(fmaf(s[r], c, -mc));
     st.l += xhalf_sum(sum_tree16(s));
-    pb[0] = pack_b(s, 0);
-    pb[1] = pack_b(s, 1);
+    pack_planes<NP>(s, 0, pb[0]);
+    pack_planes<NP>(s, 1, pb[1]);
 }
 
 // One 32-key half tile (keys kb..kb+31, tile rows 32h..) for sub-block 1, and sub-block 0
-// too when BOTH.  ka[st] / va[dt]: this lane's LDS read addresses in the current tiles for
-// the K chunk of step st and the V^T fragment of head-dim tile dt (half 0, keys 0..).
-template <int D, bool BOTH>
+// too when BOTH.  ka[st] / va[dt]: this lane's LDS read addresses in plane 0 of the current
+// tiles for the K chunk of step st and the V^T fragment of head-dim tile dt (half 0, keys
+// 0..); plane i lies i tile sizes further.
+template <int D, bool BOTH, int NP>
 __device__ __forceinline__ void half_step(int kb, const uint32_t (&ka)[D / 16],
-                                          const uint32_t (&va)[D / 32], const bf16x8 (&q0)[D / 16],
-                                          const bf16x8 (&q1)[D / 16], SubState<D>& st0,
+                                          const uint32_t (&va)[D / 32],
+                                          const bf16x8 (&q0)[D / 16][NP],
+                                          const bf16x8 (&q1)[D / 16][NP], SubState<D>& st0,
                                           SubState<D>& st1, int qj0, int qj1, int col, int half,
                                           float c) {
+    constexpr uint32_t kPlane = Swz<D, kKeyTile<NP>>::kBytes;
     f32x16 s0 = f32x16{}, s1 = f32x16{};
 #pragma unroll
     for (int st = 0; st < D / 16; ++st) {
-        const bf16x8 a = lds_b128(ka[st]);
-        s1 = mfma_32x32x16_bf16(a, q1[st], s1);
-        if constexpr (BOTH) s0 = mfma_32x32x16_bf16(a, q0[st], s0);
+        bf16x8 a[NP];
+#pragma unroll
+        for (int i = 0; i < NP; ++i) a[i] = lds_b128(ka[st] + i * kPlane);
+        s1 = mma_planes<NP>(a, q1[st], s1);
+        if constexpr (BOTH) s0 = mma_planes<NP>(a, q0[st], s0);
     }
-    bf16x8 p0[2], p1[2];
-    softmax_step<D>(s1, st1, p1, kb, qj1, col, half, c);
-    if constexpr (BOTH) softmax_step<D>(s0, st0, p0, kb, qj0, col, half, c);
+    bf16x8 p0[2][NP], p1[2][NP];
+    softmax_step<D, NP>(s1, st1, p1, kb, qj1, col, half, c);
+    if constexpr (BOTH) softmax_step<D, NP>(s0, st0, p0, kb, qj0, col, half, c);
 #pragma unroll
     for (int dt = 0; dt < D / 32; ++dt) {
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-            const bf16x8 a = lds_tr(va[dt] + u * Swz<D>::rows(16), Swz<D>::rows(8));
-            st1.acc[dt] = mfma_32x32x16_bf16(a, p1[u], st1.acc[dt]);
-            if constexpr (BOTH) st0.acc[dt] = mfma_32x32x16_bf16(a, p0[u], st0.acc[dt]);
+            bf16x8 a[NP];
+#pragma unroll
+            for (int i = 0; i < NP; ++i)
+                a[i] = lds_tr(va[dt] + i * kPlane + u * Swz<D>::rows(16), Swz<D>::rows(8));
+            st1.acc[dt] = mma_planes<NP>(a, p1[u], st1.acc[dt]);
+            if constexpr (BOTH) st0.acc[dt] = mma_planes<NP>(a, p0[u], st0.acc[dt]);
         }
     }
 }
 
+// Output element type: bf16 for the bf16 path, fp32 for fp32 operands carried as planes.
+template <int NP>
+using OutT = std::conditional_t<NP == 1, uint16_t, float>;
+
 // NSUB = 2: 256 queries per workgroup, wave w owns sub-blocks w (0) and 7-w (1).
 // NSUB = 1: 128 queries per workgroup, wave w owns sub-block w (1) (small grids).
-template <int D, int NSUB>
+// k, v: plane 0 of NP bf16 planes, pstride elements apart (xv addresses a plane).  NP = 1:
+// q is bf16 like k; NP = 3: Q comes from the fp32 tensor qf (view qv) and is split here.
+template <int D, int NSUB, int NP>
 __global__ __launch_bounds__(kWave* kWaves) void flash_fwd_bf16_kernel(
-    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
-    const uint16_t* __restrict__ v, uint16_t* __restrict__ o, float* __restrict__ m_out,
-    float* __restrict__ l_out, int BH, int T, float scale, int nblk, HeadView xv,
-    HeadView ov) {
-    using S = Swz<D>;
-    __shared__ __attribute__((aligned(1024))) FwdSmem<D> sm;
+    const uint16_t* __restrict__ q, const float* __restrict__ qf,
+    const uint16_t* __restrict__ k, const uint16_t* __restrict__ v, OutT<NP>* __restrict__ o,
+    float* __restrict__ m_out, float* __restrict__ l_out, int BH, int T, float scale, int nblk,
+    HeadView xv, HeadView qv, HeadView ov, size_t pstride) {
+    constexpr int KT = kKeyTile<NP>;
+    constexpr int kHalves = KT / 32;  // 32-key half tiles per tile
+    using S = Swz<D, KT>;
+    constexpr uint32_t kBuf = NP * S::kBytes;  // one K (or V) buffer: NP plane tiles
+    __shared__ __attribute__((aligned(1024))) FwdSmem<D, NP> sm;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     const int lane = threadIdx.x & (kWave - 1);
     const int col = lane & 31;
@@ -159,16 +182,33 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_fwd_bf16_kernel(
     const uint16_t* vh = v + xoff;
     const float c = scale * kLog2e;
 
-    bf16x8 qr0[D / 16], qr1[D / 16];
-    if constexpr (NSUB == 2) load_rowop<D>(qr0, q + xoff, qj0 + col, T, half, xrs);
-    load_rowop<D>(qr1, q + xoff, qj1 + col, T, half, xrs);
+    bf16x8 qr0[D / 16][NP], qr1[D / 16][NP];
+    if constexpr (NP == 1) {
+        if constexpr (NSUB == 2)
+            load_rowop_planes<D, NP>(qr0, q + xoff, pstride, qj0 + col, T, half, xrs);
+        load_rowop_planes<D, NP>(qr1, q + xoff, pstride, qj1 + col, T, half, xrs);
+    } else {
+        const float* qh = qf + qv.off(bh);
+        if constexpr (NSUB == 2) load_rowop_split<D, NP>(qr0, qh, qj0 + col, T, half, qv.row);
+        load_rowop_split<D, NP>(qr1, qh, qj1 + col, T, half, qv.row);
+    }
 
     const int kend = min(T, q0 + kBlock);
-    const int ntile = (kend + kKeyTile - 1) / kKeyTile;
-    const uint32_t k_lds = lds_addr(sm.k[0]);
-    const uint32_t v_lds = lds_addr(sm.v[0]);
-    dma_tile<D>(kh, 0, T, k_lds, wave, lane, xrs);
-    dma_tile<D>(vh, 0, T, v_lds, wave, lane, xrs);
+    const int ntile = (kend + KT - 1) / KT;
+    const uint32_t k_lds = lds_addr(sm.k[0][0]);
+    const uint32_t v_lds = lds_addr(sm.v[0][0]);
+    // Tile kt of K and V (every plane) into buffer kt % 2.
+    auto copy_tile = [&](int kt) {
+        const uint32_t buf = static_cast<uint32_t>(kt & 1) * kBuf;
+#pragma unroll
+        for (int i = 0; i < NP; ++i) {
+            dma_tile<D, kWaves, KT>(kh + i * pstride, kt * KT, T, k_lds + buf + i * S::kBytes,
+                                    wave, lane, xrs);
+            dma_tile<D, kWaves, KT>(vh + i * pstride, kt * KT, T, v_lds + buf + i * S::kBytes,
+                                    wave, lane, xrs);
+        }
+    };
+    copy_tile(0);
 
     // Lane read offsets within a tile (K row reads, V transposing reads).
     uint32_t koff[D / 16], voff[D / 32];
@@ -184,27 +224,23 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_fwd_bf16_kernel(
     st0.m_true = st1.m_true = -INFINITY;
     st0.l = st1.l = 0.0f;
 
-    // Half tiles hh = 0 .. 2*ntile-1 (keys 32*hh ..).  Sub-block w is active for
+    // Half tiles hh = 0 .. kHalves*ntile-1 (keys 32*hh ..).  Sub-block w is active for
     // hh < hA, sub-block 7-w for hh < hB; every wave takes part in every tile's barrier and
     // copy.  Three straight loops keep the accumulators out of any control-flow join.
     const int nhalf_t = (T + 31) / 32;
     const int hA = NSUB == 2 ? min(qj0 / 32 + 1, nhalf_t) : 0;
     const int hB = min(qj1 / 32 + 1, nhalf_t);
-    const int hend = 2 * ntile;
+    const int hend = kHalves * ntile;
     uint32_t ka[D / 16], va[D / 32];
     auto tile_sync = [&](int hh) {
-        const int kt = hh >> 1;
-        if ((hh & 1) == 0) {
+        const int kt = hh / kHalves;
+        if (hh % kHalves == 0) {
             wait_vm<0>();     // this wave's copies of tile kt landed ...
             __syncthreads();  // ... and every wave's; tile kt-1 is no longer read by anyone
-            if (kt + 1 < ntile) {
-                const uint32_t nbuf = static_cast<uint32_t>((kt + 1) & 1) * S::kBytes;
-                dma_tile<D>(kh, (kt + 1) * kKeyTile, T, k_lds + nbuf, wave, lane, xrs);
-                dma_tile<D>(vh, (kt + 1) * kKeyTile, T, v_lds + nbuf, wave, lane, xrs);
-            }
+            if (kt + 1 < ntile) copy_tile(kt + 1);
         }
-        const uint32_t base = static_cast<uint32_t>(kt & 1) * S::kBytes +
-                              static_cast<uint32_t>(hh & 1) * S::rows(32);
+        const uint32_t base = static_cast<uint32_t>(kt & 1) * kBuf +
+                              static_cast<uint32_t>(hh % kHalves) * S::rows(32);
 #pragma unroll
         for (int st = 0; st < D / 16; ++st) ka[st] = k_lds + base + koff[st];
 #pragma unroll
@@ -213,11 +249,11 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_fwd_bf16_kernel(
     int hh = 0;
     for (; hh < hA; ++hh) {
         tile_sync(hh);
-        half_step<D, true>(32 * hh, ka, va, qr0, qr1, st0, st1, qj0, qj1, col, half, c);
+        half_step<D, true, NP>(32 * hh, ka, va, qr0, qr1, st0, st1, qj0, qj1, col, half, c);
     }
     for (; hh < hB; ++hh) {
         tile_sync(hh);
-        half_step<D, false>(32 * hh, ka, va, qr0, qr1, st0, st1, qj0, qj1, col, half, c);
+        half_step<D, false, NP>(32 * hh, ka, va, qr0, qr1, st0, st1, qj0, qj1, col, half, c);
     }
     for (; hh < hend; ++hh) tile_sync(hh);
 
@@ -237,25 +273,36 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_fwd_bf16_kernel(
     }
 }
 
-template <int D, int NSUB>
-void fwd_launch(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o,
-                float* m_out, float* l_out, int BH, int T, float scale, const HeadView& xv,
-                const HeadView& ov, hipStream_t stream) {
+// Operands of one forward launch.
+template <int NP>
+struct FwdArgs {
+    const uint16_t* q;  // bf16 (NP = 1)
+    const float* qf;    // fp32 (NP = 3)
+    const uint16_t *k, *v;
+    OutT<NP>* o;
+    float *m_out, *l_out;
+    int BH, T;
+    float scale;
+    HeadView xv, qv, ov;
+    size_t pstride;
+};
+
+template <int D, int NSUB, int NP>
+void fwd_launch(const FwdArgs<NP>& a, hipStream_t stream) {
     constexpr int kBlock = kWaves * NSUB * kSub;
-    const int nblk = (T + kBlock - 1) / kBlock;
-    hipLaunchKernelGGL((flash_fwd_bf16_kernel<D, NSUB>), dim3(BH * nblk), dim3(kWave * kWaves),
-                       0, stream, q, k, v, o, m_out, l_out, BH, T, scale, nblk, xv, ov);
+    const int nblk = (a.T + kBlock - 1) / kBlock;
+    hipLaunchKernelGGL((flash_fwd_bf16_kernel<D, NSUB, NP>), dim3(a.BH * nblk),
+                       dim3(kWave * kWaves), 0, stream, a.q, a.qf, a.k, a.v, a.o, a.m_out,
+                       a.l_out, a.BH, a.T, a.scale, nblk, a.xv, a.qv, a.ov, a.pstride);
 }
 
-template <int D>
-void fwd_dispatch(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o,
-                  float* m_out, float* l_out, int BH, int T, float scale, const HeadView& xv,
-                  const HeadView& ov, hipStream_t stream) {
+template <int D, int NP>
+void fwd_dispatch(const FwdArgs<NP>& a, hipStream_t stream) {
     // d = 128: one sub-block per wave fits two waves per SIMD (two sub-blocks do not)
-    if (D >= 128 || use_single_subblock(BH, T))
-        fwd_launch<D, 1>(q, k, v, o, m_out, l_out, BH, T, scale, xv, ov, stream);
+    if (D >= 128 || use_single_subblock(a.BH, a.T))
+        fwd_launch<D, 1, NP>(a, stream);
     else
-        fwd_launch<D, 2>(q, k, v, o, m_out, l_out, BH, T, scale, xv, ov, stream);
+        fwd_launch<D, (D >= 128 ? 1 : 2), NP>(a, stream);
 }
 
 }  // namespace
@@ -264,11 +311,23 @@ void launch_flash_fwd_bf16(const uint16_t* q, const uint16_t* k, const uint16_t*
                            uint16_t* o, float* m_out, float* l_out, int BH, int T, int d,
                            float scale, const HeadView& xv, const HeadView& ov,
                            hipStream_t stream) {
+    const FwdArgs<1> a{q, nullptr, k, v, o, m_out, l_out, BH, T, scale, xv, xv, ov, 0};
     switch (d) {
-        case 32: fwd_dispatch<32>(q, k, v, o, m_out, l_out, BH, T, scale, xv, ov, stream); break;
-        case 64: fwd_dispatch<64>(q, k, v, o, m_out, l_out, BH, T, scale, xv, ov, stream); break;
-        default: fwd_dispatch<128>(q, k, v, o, m_out, l_out, BH, T, scale, xv, ov, stream); break;
+        case 32: fwd_dispatch<32, 1>(a, stream); break;
+        case 64: fwd_dispatch<64, 1>(a, stream); break;
+        default: fwd_dispatch<128, 1>(a, stream); break;
     }
+}
+
+void launch_flash_fwd_f32x3(const float* q, const HeadView& qv, const uint16_t* k,
+                            const uint16_t* v, size_t pstride, float* o, float* m_out,
+                            float* l_out, int BH, int T, int d, float scale, const HeadView& xv,
+                            const HeadView& ov, hipStream_t stream) {
+    const FwdArgs<3> a{nullptr, q, k, v, o, m_out, l_out, BH, T, scale, xv, qv, ov, pstride};
+    if (d == 32)
+        fwd_dispatch<32, 3>(a, stream);
+    else
+        fwd_dispatch<64, 3>(a, stream);
 }
 
 }  // namespace tcamd

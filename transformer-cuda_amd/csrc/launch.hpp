@@ -65,4 +65,33 @@ void launch_flash_bwd_dkdv_bf16(const uint16_t* q, const uint16_t* k, const uint
                                 int d, float scale, const HeadView& xv, const HeadView& ov,
                                 const HeadView& gv, hipStream_t stream);
 
+// An fp32 (B*H, T, d) view (d % 8 == 0, rows 16-byte aligned) as three head-major bf16
+// planes (hi, mid, lo) at dst, dst + pstride, dst + 2 pstride.
+void launch_split_planes(const float* src, const HeadView& sv, uint16_t* dst, size_t pstride,
+                         int BH, int T, int d, hipStream_t stream);
+
+// fp32 attention on bf16 MFMAs: every fp32 operand carried as three bf16 planes (hi, mid,
+// lo; bf16_tile.hpp), products as six plane products.  Q is read in fp32 (view qv) and
+// split in registers; k and v point at plane 0 of planes pstride elements apart, each plane
+// addressed by xv; O is fp32.  d = 32 or 64.
+void launch_flash_fwd_f32x3(const float* q, const HeadView& qv, const uint16_t* k,
+                            const uint16_t* v, size_t pstride, float* o, float* m_out,
+                            float* l_out, int BH, int T, int d, float scale, const HeadView& xv,
+                            const HeadView& ov, hipStream_t stream);
+// Stage 1 (D and dQ): q, o, dO fp32 rows (views qv, ov), k and v plane tensors (view kv);
+// dq fp32 (view gv).
+void launch_flash_bwd_dq_f32x3(const float* q, const HeadView& qv, const uint16_t* k,
+                               const uint16_t* v, const HeadView& kv, size_t pstride,
+                               const float* o, const float* dO, const HeadView& ov,
+                               const float* m, const float* l, float* dq, const HeadView& gv,
+                               float* Dws, int BH, int T, int d, float scale,
+                               hipStream_t stream);
+// Stage 2 (dK, dV): q and dO plane tensors (view tv), k and v fp32 rows (view kv); dk, dv
+// fp32 (view gv).
+void launch_flash_bwd_dkdv_f32x3(const uint16_t* q, const uint16_t* dO, const HeadView& tv,
+                                 size_t pstride, const float* k, const float* v,
+                                 const HeadView& kv, const float* m, const float* l,
+                                 const float* Dws, float* dk, float* dv, const HeadView& gv,
+                                 int BH, int T, int d, float scale, hipStream_t stream);
+
 }  // namespace tcamd

@@ -2,9 +2,16 @@
 """Causal multi-head attention fwd+bwd throughput on one MI355X (gfx950).
 
 One step is one pass of the hot path over one batch, every kernel launched through the
-C ABI (include/attn_capi.h) on torch's current stream.  Default (--path packed), the
-MI355X form of the path: the split-transposes are fused into the attention kernels' tile
-copies and stores, so qkv (B,T,3C) is read and dqkv (B,T,3C) written directly:
+C ABI (include/attn_capi.h) on torch's current stream.  fp32 default (--path x3): fp32
+attention on the bf16 matrix cores, every fp32 operand carried as three bf16 planes (24
+significant bits) and every product as six plane products accumulated in fp32 (the
+*_f32x3 entry points; fp64 distance equal to the fp32 MFMA path's, tests/test_gpu_f32x3.py):
+    attn_fwd_x3       planes of k, v; qkv -> O (B,H,T,d), m, l     reference model.cu:305-311
+    bwd_dq_x3         planes of q, dO; D, dQ -> dqkv[:, :, q]      reference model.cu:609, 653
+    bwd_dkdv_x3       dK, dV -> dqkv[:, :, k and v blocks]         reference model.cu:609, 653
+bf16 default and --path packed (fp32 on the fp32 MFMA): the split-transposes are fused into
+the attention kernels' tile copies and stores, so qkv (B,T,3C) is read and dqkv (B,T,3C)
+written directly:
     attn_fwd_packed   qkv -> O (B,H,T,d), m, l                    reference model.cu:305-311
     bwd_dq_packed     D = rowsum(dO*O), dQ -> dqkv[:, :, q block]  reference model.cu:609, 653
     bwd_dkdv_packed   dK, dV -> dqkv[:, :, k and v blocks]         reference model.cu:609, 653
@@ -14,7 +21,7 @@ copies and stores, so qkv (B,T,3C) is read and dqkv (B,T,3C) written directly:
     backward stage 1       -> D = rowsum(dO*O), dQ                 reference model.cu:609
     backward stage 2       -> dK, dV                               reference model.cu:609
     dq,dk,dv --split-transpose backward--> dqkv (B,T,3C)          reference model.cu:653
-Both produce bitwise the same O, m, l and dqkv (tests/test_gpu_packed.py).  Inputs (qkv,
+packed and split produce bitwise the same O, m, l and dqkv (tests/test_gpu_packed.py).  Inputs (qkv,
 dO) are synthetic N(0,1) from a fixed seed and resident in HBM before the timed region
 starts.
 
@@ -25,14 +32,18 @@ duration, measured with HIP events recorded on the launch stream around every ke
 every timed step) against its algorithmic FLOPs:
     forward 2 units, backward dK/dV 4 units (S recompute, dP, dV, dK), backward dQ 1 unit
     (dQ; its S and dP recomputes duplicate work already counted), unit = B*H*T^2*d.
+For the x3 path the roofline is the bf16 MFMA's: achieved = 6 x the algorithmic FLOPs (six
+bf16 plane products per fp32 product) per second against the bf16 peak, with the fp32
+equivalent (algorithmic FLOPs against the fp32 peak) beside it.
 The split-transpose kernels are HBM-bound: 6*B*T*C*elem_bytes algorithmic bytes each.
 roofline.traffic is the dominant kernel's measured HBM bytes per dispatch, read from
 profiles/hbm_traffic.md (rocprofv3 FETCH_SIZE and WRITE_SIZE of this same bench command,
 scaled by a device-copy calibration); null when that file has no row for the workload.
 
-secondary: the same workload through the other path, the step in bf16 at config 2's shape
-and at config 3, and the reference's materialised mode (full-square GEMMs + fused softmax,
-fp32, config 2) as a timed fwd+bwd.
+secondary: the same workload through the other paths (fp32: the fp32 MFMA path, packed and
+the reference's split sequence), the step in bf16 at config 2's shape and at config 3, and
+the reference's materialised mode (full-square GEMMs + fused softmax, fp32, config 2) as a
+timed fwd+bwd.
 
 training_step: BASELINE config 5, the reference's GPT-2-small training step (L12 C768 H12
 T1024 B8 V50257, fp32, forward + backward + fused clip/AdamW) through the harness of
@@ -76,7 +87,9 @@ METRIC = "causal attn fwd+bwd TFLOP/s & % MFMA peak, B8 H12 T1024 d64 fp32/bf16"
 
 # kernel -> algorithmic FLOP units (unit = B*H*T^2*d) or HBM bytes factor
 FLOP_UNITS = {"attn_fwd": 2, "bwd_dq": 1, "bwd_dkdv": 4,
-              "attn_fwd_packed": 2, "bwd_dq_packed": 1, "bwd_dkdv_packed": 4}
+              "attn_fwd_packed": 2, "bwd_dq_packed": 1, "bwd_dkdv_packed": 4,
+              "attn_fwd_x3": 2, "bwd_dq_x3": 1, "bwd_dkdv_x3": 4}
+X3_PRODUCTS = 6  # bf16 plane products per fp32 product on the x3 path
 
 
 def parse_args():
@@ -88,10 +101,12 @@ def parse_args():
     ap.add_argument("--dtype", choices=["f32", "bf16"], default=None,
                     help="override the config's dtype")
     ap.add_argument("--seed", type=int, default=42)
-    ap.add_argument("--path", choices=["packed", "split"], default="packed",
-                    help="packed: attention reads qkv and writes dqkv directly (split-transposes "
-                         "fused into its tile copies); split: the reference's launcher sequence "
-                         "with separate split-transpose kernels")
+    ap.add_argument("--path", choices=["x3", "packed", "split"], default=None,
+                    help="x3 (fp32 default): fp32 on the bf16 MFMA as three bf16 planes; "
+                         "packed (bf16 default; fp32 on the fp32 MFMA): attention reads qkv and "
+                         "writes dqkv directly (split-transposes fused into its tile copies); "
+                         "split: the reference's launcher sequence with separate "
+                         "split-transpose kernels")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="target CPU time of the cpu_baseline sample")
@@ -154,10 +169,27 @@ class PathRunner:
         st = lambda: torch.empty((B, H, T), device=dev, dtype=torch.float32)
         self.m, self.l, self.ws = st(), st(), st()
         self.dqkv = torch.empty_like(self.qkv)
+        if path == "x3":
+            if dtype != "f32":
+                raise ValueError("the x3 path computes fp32 attention")
+            self.planes = torch.empty(lib.f32x3_workspace_bytes(B, H, T, d), device=dev,
+                                      dtype=torch.uint8)
 
     def launches(self):
         L, a = self.lib, (self.B, self.H, self.T, self.d)
         B, H, T, d = a
+        if self.path == "x3":
+            # stage 1 splits q and dO into planes; the k, v planes come from the forward
+            return (
+                ("attn_fwd_x3", lambda: L.packed_causal_attention_forward_f32x3(
+                    self.qkv, self.o, B, H, T, d, self.scale, self.planes, self.m, self.l)),
+                ("bwd_dq_x3", lambda: L.packed_causal_attention_backward_dq_f32x3(
+                    self.qkv, self.o, self.do, self.m, self.l, self.dqkv, self.ws, B, H, T, d,
+                    self.scale, self.planes, True)),
+                ("bwd_dkdv_x3", lambda: L.causal_attention_backward_dkdv_f32x3(
+                    self.qkv, self.m, self.l, self.ws, self.dqkv, B, H, T, d, self.scale,
+                    self.planes)),
+            )
         if self.path == "packed":
             # the split-transposes happen inside the attention kernels' tile copies/stores
             return (
@@ -227,7 +259,7 @@ class PathRunner:
 
     def outputs_finite(self):
         torch = self.torch
-        outs = (self.o, self.dqkv) if self.path == "packed" else (
+        outs = (self.o, self.dqkv) if self.path in ("packed", "x3") else (
             self.o, self.dq, self.dk, self.dv, self.dqkv)
         return all(bool(torch.isfinite(t.float()).all()) for t in outs)
 
@@ -239,7 +271,7 @@ class PathRunner:
 
     def head_major_grads(self):
         """(dq, dk, dv) as (B, H, T, d) tensors, whichever path produced them."""
-        if self.path != "packed":
+        if self.path == "split":
             return self.dq, self.dk, self.dv
         B, H, T, d = self.B, self.H, self.T, self.d
         g = self.dqkv.view(B, T, 3, H, d).permute(2, 0, 3, 1, 4)
@@ -269,7 +301,16 @@ def roofline_of(runner, per_kernel, config):
     name = max(per_kernel, key=per_kernel.get)
     amount, kind = runner.kernel_work(name)
     sec = per_kernel[name] * 1e-3
-    if kind == "flop":
+    extra = {}
+    if kind == "flop" and runner.path == "x3":
+        alg = amount / sec / 1e12
+        achieved = X3_PRODUCTS * alg
+        peak = PEAK_TFLOPS["bf16"]
+        bound, unit = "mfma", "TFLOP/s"
+        extra = {"mfma_type": "bf16 (fp32 operands as three bf16 planes, six products each)",
+                 "fp32_equivalent": {"achieved": round(alg, 3), "peak": PEAK_TFLOPS["f32"],
+                                     "frac": round(alg / PEAK_TFLOPS["f32"], 4)}}
+    elif kind == "flop":
         achieved = amount / sec / 1e12
         peak = PEAK_TFLOPS[runner.dtype]
         bound, unit = "mfma", "TFLOP/s"
@@ -277,9 +318,9 @@ def roofline_of(runner, per_kernel, config):
         achieved = amount / sec / 1e9
         peak = PEAK_HBM_GBS
         bound, unit = "hbm", "GB/s"
-    return name, {"bound": bound, "achieved": round(achieved, 3), "peak": peak, "unit": unit,
-                  "frac": round(achieved / peak, 4),
-                  "traffic": measured_traffic(config, runner.dtype, name)}
+    return name, dict({"bound": bound, "achieved": round(achieved, 3), "peak": peak,
+                       "unit": unit, "frac": round(achieved / peak, 4),
+                       "traffic": measured_traffic(config, runner.dtype, name)}, **extra)
 
 
 def kernel_table(runner, per_kernel):
@@ -290,6 +331,9 @@ def kernel_table(runner, per_kernel):
             rate = amount / (ms * 1e-3) / 1e12
             out[name] = {"ms": round(ms, 4), "tflops": round(rate, 2),
                          "frac_mfma": round(rate / PEAK_TFLOPS[runner.dtype], 4)}
+            if runner.path == "x3":
+                out[name]["frac_bf16_mfma_executed"] = round(
+                    X3_PRODUCTS * rate / PEAK_TFLOPS["bf16"], 4)
         else:
             rate = amount / (ms * 1e-3) / 1e9
             out[name] = {"ms": round(ms, 4), "gbs": round(rate, 1),
@@ -483,13 +527,19 @@ def main():
     lib = load_lib()
     B, H, T, d, cdt, qk = CONFIGS[args.config]
     dtype = args.dtype or cdt
-    runner = PathRunner(lib, B, H, T, d, dtype, args.seed, qk, args.path)
+    path = args.path or ("x3" if dtype == "f32" and d <= 64 else "packed")
+    runner = PathRunner(lib, B, H, T, d, dtype, args.seed, qk, path)
     wall, per_kernel = runner.timed(args.steps, args.warmup)
     ms = wall / args.steps * 1e3
     value = runner.flops_total() / (ms * 1e-3) / 1e12
     dom, roof = roofline_of(runner, per_kernel, args.config)
     attn_ms = sum(ms_ for n, ms_ in per_kernel.items() if n in FLOP_UNITS)
     props = torch.cuda.get_device_properties(0)
+    if path == "x3":
+        line_x3 = {"frac_bf16_mfma_executed": round(X3_PRODUCTS * value / PEAK_TFLOPS["bf16"],
+                                                    4)}
+    else:
+        line_x3 = {}
     line = {
         "metric": METRIC,
         "value": round(value, 3),
@@ -502,6 +552,7 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": dtype,
+        "path": path,
         "data": "synthetic N(0,1) qkv and dO from a fixed seed, resident in HBM",
         "config": {"workload": CONFIG_NAMES[args.config], "B": B, "H": H, "T": T,
                    "d_head": d, "causal": True,
@@ -509,6 +560,12 @@ def main():
                    "flops_per_step": runner.flops_total()},
         "frac_mfma_peak": round(value / PEAK_TFLOPS[dtype], 4),
         "attn_only_tflops": round(runner.flops_total() / (attn_ms * 1e-3) / 1e12, 3),
+        "arithmetic": (("fp32 operands as three bf16 planes (24 significant bits) on the bf16 "
+                        "MFMA, six plane products per fp32 product, fp32 accumulation; "
+                        "frac_mfma_peak is against the fp32 MFMA peak, "
+                        "frac_bf16_mfma_executed against the bf16 peak")
+                       if path == "x3" else f"{dtype} MFMA, fp32 accumulation"),
+        **line_x3,
         "roofline": dict(roof, kernel=dom),
         "kernels": kernel_table(runner, per_kernel),
         "finite": runner.outputs_finite(),
@@ -522,8 +579,9 @@ def main():
     del runner
     torch.cuda.empty_cache()
     if not args.no_secondary:
-        other = "split" if args.path == "packed" else "packed"
-        sec = [secondary(lib, args.config, dtype, args.secondary_steps, args.seed, other)]
+        others = {"x3": ["packed", "split"], "packed": ["split"], "split": ["packed"]}[path]
+        sec = [secondary(lib, args.config, dtype, args.secondary_steps, args.seed, o)
+               for o in others]
         if dtype != "bf16":
             sec.append(secondary(lib, args.config, "bf16", args.secondary_steps, args.seed))
         sec.append(secondary(lib, "c3", "bf16", args.secondary_steps, args.seed))

@@ -328,6 +328,24 @@ int attn_fused_causal_backward_f32x3(const float* qkv, const float* o, const flo
                                      float* d_workspace, int B, int H, int T, int d_head,
                                      float scale, void* planes, int kv_planes_ready,
                                      hipStream_t stream);
+/* The two stages of those backwards.  Stage 1 writes the planes of q and dO (and of k, v
+ * unless kv_planes_ready), D and dQ; stage 2 (one function for both layouts: it reads dO
+ * only through its planes) writes dK and dV from the planes stage 1 left in `planes`. */
+int attn_packed_causal_backward_dq_f32x3(const float* qkv, const float* o,
+                                         const float* do_ptr, const float* m_ptr,
+                                         const float* l_ptr, float* dqkv, float* d_workspace,
+                                         int B, int H, int T, int d_head, float scale,
+                                         void* planes, int kv_planes_ready,
+                                         hipStream_t stream);
+int attn_fused_causal_backward_dq_f32x3(const float* qkv, const float* o, const float* do_ptr,
+                                        const float* m_ptr, const float* l_ptr, float* dqkv,
+                                        float* d_workspace, int B, int H, int T, int d_head,
+                                        float scale, void* planes, int kv_planes_ready,
+                                        hipStream_t stream);
+int attn_causal_backward_dkdv_f32x3(const float* qkv, const float* m_ptr, const float* l_ptr,
+                                    const float* d_workspace, float* dqkv, int B, int H, int T,
+                                    int d_head, float scale, const void* planes,
+                                    hipStream_t stream);
 
 #ifdef __cplusplus
 }

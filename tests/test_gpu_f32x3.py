@@ -224,3 +224,31 @@ def test_backward_reference_kat(lib):
     want = np.array([sum(0.5 / (i + 1) for i in range(j, T)) for j in range(T)])
     np.testing.assert_allclose(got["dv"][0, 0].numpy(), np.repeat(want[:, None], d, 1),
                                rtol=1e-6)
+
+
+@pytest.mark.parametrize("merged", [False, True])
+def test_staged_backward_equals_one_call(lib, merged):
+    """Stage 1 (planes of q and dO, D, dQ) then stage 2 (dK, dV) give bitwise the one-call
+    backward's results."""
+    B, H, T, d = 2, 3, 300, 64
+    g = torch.Generator(device="cpu").manual_seed(9)
+    qkv = torch.randn((B, T, 3 * H * d), generator=g).to("cuda:0")
+    do = torch.randn((B, H, T, d), generator=g).to("cuda:0")
+    if merged:
+        do = do.permute(0, 2, 1, 3).reshape(B, T, H * d).contiguous()
+    shape = (B, T, H * d) if merged else (B, H, T, d)
+    o = torch.empty(shape, device="cuda:0")
+    m = torch.empty((B, H, T), device="cuda:0")
+    l = torch.empty_like(m)
+    ws = planes(lib, B, H, T, d)
+    fam = "fused" if merged else "packed"
+    getattr(lib, f"{fam}_causal_attention_forward_f32x3")(qkv, o, B, H, T, d, 0.125, ws, m, l)
+    one, D1 = torch.full_like(qkv, float("nan")), torch.full_like(m, float("nan"))
+    getattr(lib, f"{fam}_causal_attention_backward_f32x3")(qkv, o, do, m, l, one, D1, B, H, T,
+                                                          d, 0.125, ws, True)
+    two, D2 = torch.full_like(qkv, float("nan")), torch.full_like(m, float("nan"))
+    getattr(lib, f"{fam}_causal_attention_backward_dq_f32x3")(qkv, o, do, m, l, two, D2, B, H,
+                                                             T, d, 0.125, ws, True)
+    lib.causal_attention_backward_dkdv_f32x3(qkv, m, l, D2, two, B, H, T, d, 0.125, ws)
+    torch.cuda.synchronize()
+    assert torch.equal(one, two) and torch.equal(D1, D2)

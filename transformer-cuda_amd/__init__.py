@@ -97,6 +97,11 @@ SIGNATURES = {
         [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P, _I, _P],
     "attn_fused_causal_backward_f32x3":
         [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P, _I, _P],
+    "attn_packed_causal_backward_dq_f32x3":
+        [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P, _I, _P],
+    "attn_fused_causal_backward_dq_f32x3":
+        [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P, _I, _P],
+    "attn_causal_backward_dkdv_f32x3": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P, _P],
 }
 
 for _name, _args in SIGNATURES.items():
@@ -423,10 +428,10 @@ def fused_causal_attention_forward_f32x3(qkv, out, B, H, T, d_head, scale, plane
 
 
 def _qkv_backward_f32x3(family, qkv, o, dO, m, l, dqkv, workspace, B, H, T, d_head, scale,
-                        planes, kv_planes_ready, stream):
+                        planes, kv_planes_ready, stream, stage=""):
     n, r = B * H * T * d_head, B * H * T
     f32 = _dt(False)
-    check(call(f"attn_{family}_causal_backward_f32x3", _ptr(qkv, f32, 3 * n, "qkv"),
+    check(call(f"attn_{family}_causal_backward{stage}_f32x3", _ptr(qkv, f32, 3 * n, "qkv"),
                _ptr(o, f32, n, "o"), _ptr(dO, f32, n, "dO"), _ptr(m, f32, r, "m"),
                _ptr(l, f32, r, "l"), _ptr(dqkv, f32, 3 * n, "dqkv"),
                _ptr(workspace, f32, r, "workspace"), B, H, T, d_head, float(scale),
@@ -447,6 +452,34 @@ def fused_causal_attention_backward_f32x3(qkv, o, dO, m, l, dqkv, workspace, B, 
     """fused_causal_attention_backward for fp32 on the bf16 matrix cores."""
     _qkv_backward_f32x3("fused", qkv, o, dO, m, l, dqkv, workspace, B, H, T, d_head, scale,
                         planes, kv_planes_ready, stream)
+
+
+def packed_causal_attention_backward_dq_f32x3(qkv, o, dO, m, l, dqkv, workspace, B, H, T,
+                                              d_head, scale, planes, kv_planes_ready=False,
+                                              stream=None):
+    """Stage 1 of packed_causal_attention_backward_f32x3 (planes of q and dO, D, dQ)."""
+    _qkv_backward_f32x3("packed", qkv, o, dO, m, l, dqkv, workspace, B, H, T, d_head, scale,
+                        planes, kv_planes_ready, stream, "_dq")
+
+
+def fused_causal_attention_backward_dq_f32x3(qkv, o, dO, m, l, dqkv, workspace, B, H, T,
+                                             d_head, scale, planes, kv_planes_ready=False,
+                                             stream=None):
+    """Stage 1 of fused_causal_attention_backward_f32x3."""
+    _qkv_backward_f32x3("fused", qkv, o, dO, m, l, dqkv, workspace, B, H, T, d_head, scale,
+                        planes, kv_planes_ready, stream, "_dq")
+
+
+def causal_attention_backward_dkdv_f32x3(qkv, m, l, workspace, dqkv, B, H, T, d_head, scale,
+                                         planes, stream=None):
+    """Stage 2 of the *_f32x3 backwards (dK, dV from the planes stage 1 wrote)."""
+    n, r = B * H * T * d_head, B * H * T
+    f32 = _dt(False)
+    check(call("attn_causal_backward_dkdv_f32x3", _ptr(qkv, f32, 3 * n, "qkv"),
+               _ptr(m, f32, r, "m"), _ptr(l, f32, r, "l"), _ptr(workspace, f32, r, "workspace"),
+               _ptr(dqkv, f32, 3 * n, "dqkv"), B, H, T, d_head, float(scale),
+               _planes_ptr(planes, B, H, T, d_head), _stream(stream)),
+          "causal_attention_backward_dkdv_f32x3")
 
 
 def attention_precompute_dot_do_o(dO, O, D, B, H, T, d_head, stream=None):

@@ -248,31 +248,60 @@ int packed_forward_f32x3(const float* qkv, float* out, int B, int H, int T, int 
     return launch_status();
 }
 
-int packed_backward_f32x3(const float* qkv, const float* o, const float* dO, const float* m,
-                          const float* l, float* dqkv, float* ws, int B, int H, int T, int d,
-                          float scale, void* planes, int kv_ready, bool merged,
-                          hipStream_t stream) {
+// Stage 1: the planes of q and dO (and of k, v unless kv_ready), then D and dQ.
+int packed_backward_dq_f32x3(const float* qkv, const float* o, const float* dO, const float* m,
+                             const float* l, float* dqkv, float* ws, int B, int H, int T, int d,
+                             float scale, void* planes, int kv_ready, bool merged,
+                             hipStream_t stream) {
     if (o == nullptr || planes == nullptr) return ATTN_ERROR_NULL_POINTER;
     int st = check_packed_bwd(qkv, dO, m, l, dqkv, ws, B, H, T, d, scale);
     if (st != ATTN_SUCCESS) return st;
     st = check_f32x3(B, H, T, d, scale);
     if (st != ATTN_SUCCESS) return st;
     if (!aligned16(o) || !aligned16(planes)) return ATTN_ERROR_MISALIGNED;
-    const size_t N = plane_elems(B, H, T, d), C = static_cast<size_t>(H) * d;
+    const size_t N = plane_elems(B, H, T, d);
     const tcamd::HeadView xv = tcamd::packed_qkv_view(H, T, d);
-    const tcamd::HeadView hv = tcamd::head_major_view(H, T, d);
     const tcamd::HeadView ov = out_view(H, T, d, merged);
     clear_error();
     if (!kv_ready) split_kv_planes(qkv, planes, B, H, T, d, stream);
     tcamd::launch_split_planes(qkv, xv, plane_tensor(planes, N, 0), N, B * H, T, d, stream);
     tcamd::launch_split_planes(dO, ov, plane_tensor(planes, N, 3), N, B * H, T, d, stream);
     tcamd::launch_flash_bwd_dq_f32x3(qkv, xv, plane_tensor(planes, N, 1),
-                                     plane_tensor(planes, N, 2), hv, N, o, dO, ov, m, l, dqkv,
-                                     xv, ws, B * H, T, d, scale, stream);
-    tcamd::launch_flash_bwd_dkdv_f32x3(plane_tensor(planes, N, 0), plane_tensor(planes, N, 3),
-                                       hv, N, qkv + C, qkv + 2 * C, xv, m, l, ws, dqkv + C,
-                                       dqkv + 2 * C, xv, B * H, T, d, scale, stream);
+                                     plane_tensor(planes, N, 2), tcamd::head_major_view(H, T, d),
+                                     N, o, dO, ov, m, l, dqkv, xv, ws, B * H, T, d, scale,
+                                     stream);
     return launch_status();
+}
+
+// Stage 2: dK and dV from the planes of q and dO that stage 1 wrote.
+int packed_backward_dkdv_f32x3(const float* qkv, const float* m, const float* l,
+                               const float* ws, float* dqkv, int B, int H, int T, int d,
+                               float scale, const void* planes, hipStream_t stream) {
+    if (qkv == nullptr || m == nullptr || l == nullptr || ws == nullptr || dqkv == nullptr ||
+        planes == nullptr)
+        return ATTN_ERROR_NULL_POINTER;
+    const int st = check_f32x3(B, H, T, d, scale);
+    if (st != ATTN_SUCCESS) return st;
+    if (!aligned16(qkv) || !aligned16(dqkv) || !aligned16(planes)) return ATTN_ERROR_MISALIGNED;
+    const size_t N = plane_elems(B, H, T, d), C = static_cast<size_t>(H) * d;
+    const tcamd::HeadView xv = tcamd::packed_qkv_view(H, T, d);
+    void* pl = const_cast<void*>(planes);
+    clear_error();
+    tcamd::launch_flash_bwd_dkdv_f32x3(plane_tensor(pl, N, 0), plane_tensor(pl, N, 3),
+                                       tcamd::head_major_view(H, T, d), N, qkv + C, qkv + 2 * C,
+                                       xv, m, l, ws, dqkv + C, dqkv + 2 * C, xv, B * H, T, d,
+                                       scale, stream);
+    return launch_status();
+}
+
+int packed_backward_f32x3(const float* qkv, const float* o, const float* dO, const float* m,
+                          const float* l, float* dqkv, float* ws, int B, int H, int T, int d,
+                          float scale, void* planes, int kv_ready, bool merged,
+                          hipStream_t stream) {
+    const int st = packed_backward_dq_f32x3(qkv, o, dO, m, l, dqkv, ws, B, H, T, d, scale,
+                                            planes, kv_ready, merged, stream);
+    if (st != ATTN_SUCCESS) return st;
+    return packed_backward_dkdv_f32x3(qkv, m, l, ws, dqkv, B, H, T, d, scale, planes, stream);
 }
 
 }  // namespace
@@ -778,6 +807,33 @@ int attn_fused_causal_backward_f32x3(const float* qkv, const float* o, const flo
                                      hipStream_t stream) {
     return packed_backward_f32x3(qkv, o, do_ptr, m_ptr, l_ptr, dqkv, d_workspace, B, H, T,
                                  d_head, scale, planes, kv_planes_ready, true, stream);
+}
+
+int attn_packed_causal_backward_dq_f32x3(const float* qkv, const float* o,
+                                         const float* do_ptr, const float* m_ptr,
+                                         const float* l_ptr, float* dqkv, float* d_workspace,
+                                         int B, int H, int T, int d_head, float scale,
+                                         void* planes, int kv_planes_ready,
+                                         hipStream_t stream) {
+    return packed_backward_dq_f32x3(qkv, o, do_ptr, m_ptr, l_ptr, dqkv, d_workspace, B, H, T,
+                                    d_head, scale, planes, kv_planes_ready, false, stream);
+}
+
+int attn_fused_causal_backward_dq_f32x3(const float* qkv, const float* o, const float* do_ptr,
+                                        const float* m_ptr, const float* l_ptr, float* dqkv,
+                                        float* d_workspace, int B, int H, int T, int d_head,
+                                        float scale, void* planes, int kv_planes_ready,
+                                        hipStream_t stream) {
+    return packed_backward_dq_f32x3(qkv, o, do_ptr, m_ptr, l_ptr, dqkv, d_workspace, B, H, T,
+                                    d_head, scale, planes, kv_planes_ready, true, stream);
+}
+
+int attn_causal_backward_dkdv_f32x3(const float* qkv, const float* m_ptr, const float* l_ptr,
+                                    const float* d_workspace, float* dqkv, int B, int H, int T,
+                                    int d_head, float scale, const void* planes,
+                                    hipStream_t stream) {
+    return packed_backward_dkdv_f32x3(qkv, m_ptr, l_ptr, d_workspace, dqkv, B, H, T, d_head,
+                                      scale, planes, stream);
 }
 
 }  // extern "C"

@@ -66,9 +66,12 @@ using OutT = std::conditional_t<NP == 1, uint16_t, float>;
 template <int NP>
 constexpr int kStatTerms = NP == 1 ? 2 : 3;
 
-// Key rows per stage-1 tile.
+// Key rows per stage-1 tile and query rows per stage-2 tile: NP = 3 streams 32-row tiles, so
+// that the double-buffered planes leave room for two workgroups per CU.
 template <int NP>
 constexpr int kKeyTileDq = NP == 1 ? kRowTile : 32;
+template <int NP>
+constexpr int kQueryTile = NP == 1 ? kRowTile : 32;
 
 // K and V tiles of stage 1 (as the forward's), NP planes each.
 template <int D, int NP>
@@ -81,10 +84,11 @@ struct KvSmem {
 // the row's statistic (see dkdv_scores).
 template <int D, int NP>
 struct QgSmem {
-    uint16_t q[2][NP][Swz<D>::kBytes / 2];
-    uint16_t g[2][NP][Swz<D>::kBytes / 2];
-    uint16_t qx[2][kRowTile * 8];  // row r: the terms of -lse2, then zeros
-    uint16_t gx[2][kRowTile * 8];  // row r: the terms of -D, then zeros
+    static constexpr int KT = kQueryTile<NP>;
+    uint16_t q[2][NP][Swz<D, KT>::kBytes / 2];
+    uint16_t g[2][NP][Swz<D, KT>::kBytes / 2];
+    uint16_t qx[2][KT * 8];  // row r: the terms of -lse2, then zeros
+    uint16_t gx[2][KT * 8];  // row r: the terms of -D, then zeros
 };
 
 // The terms of x: x_0 = bf16(x), x_i = bf16(x - x_0 - ... - x_{i-1}).
@@ -424,7 +428,7 @@ template <int D, int NP>
 __device__ __forceinline__ void dkdv_scores(const HalfAddr<D>& a, const bf16x8 (&kr)[D / 16][NP],
                                             const bf16x8 (&vr)[D / 16][NP], const bf16x8& one,
                                             f32x16& s, f32x16& dp) {
-    constexpr uint32_t kPlane = Swz<D>::kBytes;
+    constexpr uint32_t kPlane = Swz<D, kQueryTile<NP>>::kBytes;
     s = mfma_32x32x16_bf16(lds_b128(a.qx), one, f32x16{});
 #pragma unroll
     for (int st = 0; st < D / 16; ++st) {
@@ -450,7 +454,7 @@ __device__ __forceinline__ void dkdv_update(const HalfAddr<D>& a, f32x16& s, con
                                             f32x16 (&dk_acc)[D / 32],
                                             f32x16 (&dv_acc)[D / 32], int qb, int kj,
                                             int half) {
-    constexpr uint32_t kPlane = Swz<D>::kBytes;
+    constexpr uint32_t kPlane = Swz<D, kQueryTile<NP>>::kBytes;
 #pragma unroll
     for (int r = 0; r < 16; ++r) s[r] = exp2_fast(s[r]);
     if constexpr (MASK) {
@@ -458,25 +462,57 @@ __device__ __forceinline__ void dkdv_update(const HalfAddr<D>& a, f32x16& s, con
         for (int r = 0; r < 16; ++r)
             if (qb + acc_row(r, half) < kj) s[r] = 0.0f;
     }
-    bf16x8 pb[2][NP], db[2][NP];
-    pack_planes<NP>(s, 0, pb[0]);
-    pack_planes<NP>(s, 1, pb[1]);
+    if constexpr (NP == 1) {
+        bf16x8 pb[2][NP], db[2][NP];
+        pack_planes<NP>(s, 0, pb[0]);
+        pack_planes<NP>(s, 1, pb[1]);
 #pragma unroll
-    for (int r = 0; r < 16; ++r) s[r] *= dp[r];
-    pack_planes<NP>(s, 0, db[0]);
-    pack_planes<NP>(s, 1, db[1]);
+        for (int r = 0; r < 16; ++r) s[r] *= dp[r];
+        pack_planes<NP>(s, 0, db[0]);
+        pack_planes<NP>(s, 1, db[1]);
 #pragma unroll
-    for (int dt = 0; dt < D / 32; ++dt) {
+        for (int dt = 0; dt < D / 32; ++dt) {
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                bf16x8 g[NP], q[NP];
+#pragma unroll
+                for (int i = 0; i < NP; ++i) {
+                    g[i] = lds_tr(a.gt[dt] + i * kPlane + u * Swz<D>::rows(16), Swz<D>::rows(8));
+                    q[i] = lds_tr(a.qt[dt] + i * kPlane + u * Swz<D>::rows(16), Swz<D>::rows(8));
+                }
+                dv_acc[dt] = mma_planes<NP>(g, pb[u], dv_acc[dt]);
+                dk_acc[dt] = mma_planes<NP>(q, db[u], dk_acc[dt]);
+            }
+        }
+    } else {
+        // Planes of P, then of dS, one 16-row half at a time: fewer live registers.
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-            bf16x8 g[NP], q[NP];
+            bf16x8 pb[NP];
+            pack_planes<NP>(s, u, pb);
 #pragma unroll
-            for (int i = 0; i < NP; ++i) {
-                g[i] = lds_tr(a.gt[dt] + i * kPlane + u * Swz<D>::rows(16), Swz<D>::rows(8));
-                q[i] = lds_tr(a.qt[dt] + i * kPlane + u * Swz<D>::rows(16), Swz<D>::rows(8));
+            for (int dt = 0; dt < D / 32; ++dt) {
+                bf16x8 g[NP];
+#pragma unroll
+                for (int i = 0; i < NP; ++i)
+                    g[i] = lds_tr(a.gt[dt] + i * kPlane + u * Swz<D>::rows(16), Swz<D>::rows(8));
+                dv_acc[dt] = mma_planes<NP>(g, pb, dv_acc[dt]);
             }
-            dv_acc[dt] = mma_planes<NP>(g, pb[u], dv_acc[dt]);
-            dk_acc[dt] = mma_planes<NP>(q, db[u], dk_acc[dt]);
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[r] *= dp[r];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            bf16x8 db[NP];
+            pack_planes<NP>(s, u, db);
+#pragma unroll
+            for (int dt = 0; dt < D / 32; ++dt) {
+                bf16x8 q[NP];
+#pragma unroll
+                for (int i = 0; i < NP; ++i)
+                    q[i] = lds_tr(a.qt[dt] + i * kPlane + u * Swz<D>::rows(16), Swz<D>::rows(8));
+                dk_acc[dt] = mma_planes<NP>(q, db, dk_acc[dt]);
+            }
         }
     }
 }
@@ -498,9 +534,10 @@ struct DkdvArgs {
 
 // NW waves per workgroup; wave w owns keys k0 + 32w ...
 template <int D, int NW, int NP>
-__global__ __launch_bounds__(kWave* NW) void flash_bwd_dkdv_bf16_kernel(DkdvArgs<NP> a,
+__global__ __launch_bounds__(kWave* NW, NP == 1 ? 1 : 2) void flash_bwd_dkdv_bf16_kernel(DkdvArgs<NP> a,
                                                                        int nblk) {
-    using S = Swz<D>;
+    constexpr int KT = kQueryTile<NP>;
+    using S = Swz<D, KT>;
     constexpr uint32_t kBuf = NP * S::kBytes;  // one Q (or dO) buffer: NP plane tiles
     constexpr int kBlock = NW * kSub;          // keys per workgroup
     __shared__ __attribute__((aligned(1024))) QgSmem<D, NP> sm;
@@ -522,8 +559,8 @@ __global__ __launch_bounds__(kWave* NW) void flash_bwd_dkdv_bf16_kernel(DkdvArgs
     const uint16_t* gh = a.dO + gtoff;
     const float c = a.scale * kLog2e;
 
-    const int t0 = k0 / kRowTile;
-    const int ntile = (T + kRowTile - 1) / kRowTile;
+    const int t0 = k0 / KT;
+    const int ntile = (T + KT - 1) / KT;
     const uint32_t q_lds = lds_addr(sm.q[0][0]);
     const uint32_t g_lds = lds_addr(sm.g[0][0]);
     const uint32_t qx_lds = lds_addr(sm.qx[0]);
@@ -533,17 +570,17 @@ __global__ __launch_bounds__(kWave* NW) void flash_bwd_dkdv_bf16_kernel(DkdvArgs
         const uint32_t buf = static_cast<uint32_t>(kt & 1) * kBuf;
 #pragma unroll
         for (int i = 0; i < NP; ++i) {
-            dma_tile<D, NW>(qh + i * a.pstride, kt * kRowTile, T, q_lds + buf + i * S::kBytes,
-                            wave, lane, qrs);
-            dma_tile<D, NW>(gh + i * a.pstride, kt * kRowTile, T, g_lds + buf + i * S::kBytes,
-                            wave, lane, grs);
+            dma_tile<D, NW, KT>(qh + i * a.pstride, kt * KT, T, q_lds + buf + i * S::kBytes,
+                                wave, lane, qrs);
+            dma_tile<D, NW, KT>(gh + i * a.pstride, kt * KT, T, g_lds + buf + i * S::kBytes,
+                                wave, lane, grs);
         }
     };
     copy_tile(t0);
-    // Wave 0 stages the statistics of a tile through VGPRs: lane i holds query 64t + i.
+    // Wave 0 stages the statistics of a tile through VGPRs: lane i < KT holds query KT*t + i.
     float st_m = 0.0f, st_l = 1.0f, st_d = 0.0f;
     auto load_stats = [&](int t) {
-        const int r = t * kRowTile + lane;
+        const int r = t * KT + lane;
         if (r < T) {
             st_m = a.m[stat_off + r];
             st_l = a.l[stat_off + r];
@@ -554,7 +591,7 @@ __global__ __launch_bounds__(kWave* NW) void flash_bwd_dkdv_bf16_kernel(DkdvArgs
             st_d = 0.0f;
         }
     };
-    if (wave == 0) {
+    if (wave == 0 && lane < KT) {
         load_stats(t0);
         const u16x8 z = u16x8{};  // the constant zeros of the statistic chunks
 #pragma unroll
@@ -584,14 +621,14 @@ __global__ __launch_bounds__(kWave* NW) void flash_bwd_dkdv_bf16_kernel(DkdvArgs
     // Tile kt: wait for its copies, publish its statistics, barrier, start the next copy.
     auto tile_sync = [&](int kt) {
         wait_vm<0>();  // this wave's copies (and statistics loads) of tile kt landed
-        if (wave == 0) {  // the terms of -lse2 (-1e30 for padded queries: P = 0) and of -D
+        if (wave == 0 && lane < KT) {  // terms of -lse2 (-1e30 for padded queries: P = 0), -D
             const float nl = st_m == -INFINITY ? -1e30f : -(st_m * kLog2e + log2f(st_l));
             *reinterpret_cast<u16x4*>(&sm.qx[kt & 1][lane * 8]) = stat_terms<NP>(nl);
             *reinterpret_cast<u16x4*>(&sm.gx[kt & 1][lane * 8]) = stat_terms<NP>(-st_d);
         }
         __syncthreads();  // every wave's copies landed; tile kt-1 is no longer read
         if (kt + 1 < ntile) {
-            if (wave == 0) load_stats(kt + 1);
+            if (wave == 0 && lane < KT) load_stats(kt + 1);
             copy_tile(kt + 1);
         }
     };
@@ -611,7 +648,7 @@ __global__ __launch_bounds__(kWave* NW) void flash_bwd_dkdv_bf16_kernel(DkdvArgs
             h.qt[dt] = q_lds + base + troff[dt];
             h.gt[dt] = g_lds + base + troff[dt];
         }
-        const uint32_t xrow = static_cast<uint32_t>(((kt & 1) * kRowTile + (hh & 1) * 32 + col) * 16);
+        const uint32_t xrow = static_cast<uint32_t>(((kt & 1) * KT + (hh & 1) * 32 + col) * 16);
         h.qx = qx_lds + xrow;
         h.gx = gx_lds + xrow;
         return h;
@@ -622,7 +659,7 @@ __global__ __launch_bounds__(kWave* NW) void flash_bwd_dkdv_bf16_kernel(DkdvArgs
         HalfAddr<D> h;
         constexpr uint32_t base = static_cast<uint32_t>(decltype(buf)::value) * kBuf +
                                   static_cast<uint32_t>(decltype(hsel)::value) * S::rows(32);
-        constexpr uint32_t xbase = static_cast<uint32_t>(decltype(buf)::value * kRowTile +
+        constexpr uint32_t xbase = static_cast<uint32_t>(decltype(buf)::value * KT +
                                                          decltype(hsel)::value * 32) * 16u;
 #pragma unroll
         for (int st = 0; st < D / 16; ++st) {
@@ -660,6 +697,45 @@ __global__ __launch_bounds__(kWave* NW) void flash_bwd_dkdv_bf16_kernel(DkdvArgs
         dkdv_update<D, false, NP>(a1, s1, dp1, dk_acc, dv_acc, 64 * kt + 32, kj, half);
     };
 
+    if constexpr (KT == 32) {
+        // One 32-query tile per step.  Tiles before tstart (= kw/32, the one holding the
+        // wave's first key, the only one it masks) hold only queries that precede every key
+        // of the wave; a wave whose keys start past T computes nothing.  Every wave takes
+        // part in every tile's barrier and copies.
+        auto step = [&](int kt, auto mask) {
+            HalfAddr<D> h;
+            const uint32_t base = static_cast<uint32_t>(kt & 1) * kBuf;
+#pragma unroll
+            for (int st = 0; st < D / 16; ++st) {
+                h.q[st] = q_lds + base + roff[st];
+                h.g[st] = g_lds + base + roff[st];
+            }
+#pragma unroll
+            for (int dt = 0; dt < D / 32; ++dt) {
+                h.qt[dt] = q_lds + base + troff[dt];
+                h.gt[dt] = g_lds + base + troff[dt];
+            }
+            const uint32_t xrow = static_cast<uint32_t>(((kt & 1) * KT + col) * 16);
+            h.qx = qx_lds + xrow;
+            h.gx = gx_lds + xrow;
+            f32x16 s1, dp1;
+            dkdv_scores<D, NP>(h, kr, vr, one, s1, dp1);
+            dkdv_update<D, decltype(mask)::value, NP>(h, s1, dp1, dk_acc, dv_acc, KT * kt, kj,
+                                                      half);
+        };
+        const int tstart = kw < T ? kw / KT : ntile;
+        int kt = t0;
+        for (; kt < tstart; ++kt) tile_sync(kt);
+        if (kt < ntile) {
+            tile_sync(kt);
+            step(kt, std::true_type{});
+            ++kt;
+        }
+        for (; kt < ntile; ++kt) {
+            tile_sync(kt);
+            step(kt, std::false_type{});
+        }
+    } else {
     // Half tiles before hstart (= kw/32, the one holding the wave's first key) hold only
     // queries that precede every key of the wave; a wave whose keys start past T computes
     // nothing.  Every wave takes part in every tile's barrier and copies.
@@ -695,6 +771,8 @@ __global__ __launch_bounds__(kWave* NW) void flash_bwd_dkdv_bf16_kernel(DkdvArgs
     if (kt < ntile) {
         tile_sync(kt);
         pair_c(kt, B0{});
+    }
+
     }
 
     if (kj < T) {

@@ -6,8 +6,8 @@ C ABI (include/attn_capi.h) on torch's current stream.  fp32 default (--path x3)
 attention on the bf16 matrix cores, every fp32 operand carried as three bf16 planes (24
 significant bits) and every product as six plane products accumulated in fp32 (the
 *_f32x3 entry points; fp64 distance equal to the fp32 MFMA path's, tests/test_gpu_f32x3.py):
-    attn_fwd_x3       planes of k, v; qkv -> O (B,H,T,d), m, l     reference model.cu:305-311
-    bwd_dq_x3         planes of q, dO; D, dQ -> dqkv[:, :, q]      reference model.cu:609, 653
+    attn_fwd_x3       planes of q, k, v; qkv -> O (B,H,T,d), m, l  reference model.cu:305-311
+    bwd_dq_x3         D, dQ -> dqkv[:, :, q], planes of dO         reference model.cu:609, 653
     bwd_dkdv_x3       dK, dV -> dqkv[:, :, k and v blocks]         reference model.cu:609, 653
 bf16 default and --path packed (fp32 on the fp32 MFMA): the split-transposes are fused into
 the attention kernels' tile copies and stores, so qkv (B,T,3C) is read and dqkv (B,T,3C)
@@ -179,7 +179,7 @@ class PathRunner:
         L, a = self.lib, (self.B, self.H, self.T, self.d)
         B, H, T, d = a
         if self.path == "x3":
-            # stage 1 splits q and dO into planes; the k, v planes come from the forward
+            # the forward splits k, v (and writes the planes of q), stage 1 writes those of dO
             return (
                 ("attn_fwd_x3", lambda: L.packed_causal_attention_forward_f32x3(
                     self.qkv, self.o, B, H, T, d, self.scale, self.planes, self.m, self.l)),

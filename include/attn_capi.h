@@ -304,9 +304,9 @@ int attn_fused_causal_backward_dkdv_bf16(const attn_bf16* qkv, const attn_bf16* 
  * points.  d_head 32 or 64.
  *
  * `planes` is caller-owned device memory of attn_f32x3_workspace_bytes(B, H, T, d_head)
- * bytes (16-byte aligned) for the planes of k, v, q and dO.  The forward writes those of k
- * and v; a backward with kv_planes_ready = 1 reuses them (the caller guarantees that qkv and
- * the workspace are unchanged since that forward), with 0 it splits k and v again.  The
+ * bytes (16-byte aligned) for the planes of q, k, v and dO.  The forward writes those of q,
+ * k and v; a backward with kv_planes_ready = 1 reuses them (the caller guarantees that qkv
+ * and the workspace are unchanged since that forward), with 0 it splits q, k and v again.  The
  * backward's d_workspace is the B*H*T floats of D, as in the other backward entry points.
  * No counterpart in the reference (an MI355X-specific form of
  * src/kernels/attention.cu:518-1012).
@@ -328,9 +328,9 @@ int attn_fused_causal_backward_f32x3(const float* qkv, const float* o, const flo
                                      float* d_workspace, int B, int H, int T, int d_head,
                                      float scale, void* planes, int kv_planes_ready,
                                      hipStream_t stream);
-/* The two stages of those backwards.  Stage 1 writes the planes of q and dO (and of k, v
- * unless kv_planes_ready), D and dQ; stage 2 (one function for both layouts: it reads dO
- * only through its planes) writes dK and dV from the planes stage 1 left in `planes`. */
+/* The two stages of those backwards.  Stage 1 writes the planes of dO (and of q, k, v unless
+ * kv_planes_ready), D and dQ; stage 2 (one function for both layouts: it reads dO only
+ * through its planes) writes dK and dV from the planes in `planes`. */
 int attn_packed_causal_backward_dq_f32x3(const float* qkv, const float* o,
                                          const float* do_ptr, const float* m_ptr,
                                          const float* l_ptr, float* dqkv, float* d_workspace,

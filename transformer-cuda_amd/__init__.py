@@ -442,7 +442,7 @@ def _qkv_backward_f32x3(family, qkv, o, dO, m, l, dqkv, workspace, B, H, T, d_he
 def packed_causal_attention_backward_f32x3(qkv, o, dO, m, l, dqkv, workspace, B, H, T, d_head,
                                            scale, planes, kv_planes_ready=False, stream=None):
     """packed_causal_attention_backward for fp32 on the bf16 matrix cores; kv_planes_ready
-    reuses the k/v planes the forward left in `planes` (qkv unchanged since)."""
+    reuses the q/k/v planes the forward left in `planes` (qkv unchanged since)."""
     _qkv_backward_f32x3("packed", qkv, o, dO, m, l, dqkv, workspace, B, H, T, d_head, scale,
                         planes, kv_planes_ready, stream)
 
@@ -457,7 +457,7 @@ def fused_causal_attention_backward_f32x3(qkv, o, dO, m, l, dqkv, workspace, B, 
 def packed_causal_attention_backward_dq_f32x3(qkv, o, dO, m, l, dqkv, workspace, B, H, T,
                                               d_head, scale, planes, kv_planes_ready=False,
                                               stream=None):
-    """Stage 1 of packed_causal_attention_backward_f32x3 (planes of q and dO, D, dQ)."""
+    """Stage 1 of packed_causal_attention_backward_f32x3 (D, dQ, planes of dO)."""
     _qkv_backward_f32x3("packed", qkv, o, dO, m, l, dqkv, workspace, B, H, T, d_head, scale,
                         planes, kv_planes_ready, stream, "_dq")
 

@@ -215,6 +215,23 @@ __device__ __forceinline__ void load_rowop_split(bf16x8 (&dst)[D / 16][NP],
     }
 }
 
+// The planes of a row operand (as load_rowop_planes / load_rowop_split give them) back to
+// NP head-major plane tensors (rows D elements apart, planes pstride elements apart); rows
+// at or beyond T are skipped.
+template <int D, int NP>
+__device__ __forceinline__ void store_planes(uint16_t* __restrict__ head, size_t pstride,
+                                             const bf16x8 (&x)[D / 16][NP], int row, int T,
+                                             int half) {
+    if (row >= T) return;
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+        uint16_t* p = head + i * pstride + static_cast<size_t>(row) * D + 8 * half;
+#pragma unroll
+        for (int st = 0; st < D / 16; ++st)
+            *reinterpret_cast<u16x8*>(p + 16 * st) = __builtin_bit_cast(u16x8, x[st][i]);
+    }
+}
+
 // store_row in fp32.
 template <int D>
 __device__ __forceinline__ void store_row(float* __restrict__ head, int row, int half,

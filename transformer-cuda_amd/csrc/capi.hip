@@ -241,14 +241,15 @@ int packed_forward_f32x3(const float* qkv, float* out, int B, int H, int T, int 
     clear_error();
     split_kv_planes(qkv, planes, B, H, T, d, stream);
     tcamd::launch_flash_fwd_f32x3(qkv, tcamd::packed_qkv_view(H, T, d),
-                                  plane_tensor(planes, N, 1), plane_tensor(planes, N, 2), N, out,
-                                  m_out, l_out, B * H, T, d, scale,
-                                  tcamd::head_major_view(H, T, d), out_view(H, T, d, merged),
-                                  stream);
+                                  plane_tensor(planes, N, 1), plane_tensor(planes, N, 2), N,
+                                  plane_tensor(planes, N, 0), out, m_out, l_out, B * H, T, d,
+                                  scale, tcamd::head_major_view(H, T, d),
+                                  out_view(H, T, d, merged), stream);
     return launch_status();
 }
 
-// Stage 1: the planes of q and dO (and of k, v unless kv_ready), then D and dQ.
+// Stage 1: the planes of q, k, v unless the forward's are ready; D and dQ, writing the
+// planes of dO.
 int packed_backward_dq_f32x3(const float* qkv, const float* o, const float* dO, const float* m,
                              const float* l, float* dqkv, float* ws, int B, int H, int T, int d,
                              float scale, void* planes, int kv_ready, bool merged,
@@ -263,13 +264,14 @@ int packed_backward_dq_f32x3(const float* qkv, const float* o, const float* dO, 
     const tcamd::HeadView xv = tcamd::packed_qkv_view(H, T, d);
     const tcamd::HeadView ov = out_view(H, T, d, merged);
     clear_error();
-    if (!kv_ready) split_kv_planes(qkv, planes, B, H, T, d, stream);
-    tcamd::launch_split_planes(qkv, xv, plane_tensor(planes, N, 0), N, B * H, T, d, stream);
-    tcamd::launch_split_planes(dO, ov, plane_tensor(planes, N, 3), N, B * H, T, d, stream);
+    if (!kv_ready) {
+        split_kv_planes(qkv, planes, B, H, T, d, stream);
+        tcamd::launch_split_planes(qkv, xv, plane_tensor(planes, N, 0), N, B * H, T, d, stream);
+    }
     tcamd::launch_flash_bwd_dq_f32x3(qkv, xv, plane_tensor(planes, N, 1),
                                      plane_tensor(planes, N, 2), tcamd::head_major_view(H, T, d),
-                                     N, o, dO, ov, m, l, dqkv, xv, ws, B * H, T, d, scale,
-                                     stream);
+                                     N, plane_tensor(planes, N, 3), o, dO, ov, m, l, dqkv, xv, ws,
+                                     B * H, T, d, scale, stream);
     return launch_status();
 }
 

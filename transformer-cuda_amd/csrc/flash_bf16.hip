@@ -310,6 +310,7 @@ struct DqArgs {
     float scale;
     HeadView qv, kv, ov, gv;
     size_t pstride;
+    uint16_t* gp;  // dO planes out (NP = 3; laid out as k's), or null
 };
 
 // NSUB = 2: 256 queries per workgroup, wave w owns sub-blocks w (0) and 7-w (1).
@@ -364,6 +365,13 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_bwd_dq_bf16_kernel(DqArgs
     if constexpr (NSUB == 2)
         dq_init<D, NP>(sb0, a.q + qoff, a.o + ooff, a.dO + ooff, a.m, a.l, a.Dws, a.qv.row,
                        a.ov.row, stat_off, qj0 + col, T, half, c);
+    if constexpr (NP > 1) {
+        if (a.gp != nullptr) {
+            store_planes<D, NP>(a.gp + koff, a.pstride, sb1.g, qj1 + col, T, half);
+            if constexpr (NSUB == 2)
+                store_planes<D, NP>(a.gp + koff, a.pstride, sb0.g, qj0 + col, T, half);
+        }
+    }
     const bf16x8 one = ones_chunk<NP>(half);
 
     uint32_t roff[D / 16], troff[D / 32];
@@ -814,7 +822,7 @@ void launch_flash_bwd_dq_bf16(const uint16_t* q, const uint16_t* k, const uint16
                               const float* l, uint16_t* dq, float* Dws, int BH, int T, int d,
                               float scale, const HeadView& xv, const HeadView& ov,
                               const HeadView& gv, hipStream_t stream) {
-    const DqArgs<1> a{q, o, dO, k, v, m, l, dq, Dws, BH, T, scale, xv, xv, ov, gv, 0};
+    const DqArgs<1> a{q, o, dO, k, v, m, l, dq, Dws, BH, T, scale, xv, xv, ov, gv, 0, nullptr};
     switch (d) {
         case 32: dq_dispatch<32, 1>(a, stream); break;
         case 64: dq_dispatch<64, 1>(a, stream); break;
@@ -837,11 +845,12 @@ void launch_flash_bwd_dkdv_bf16(const uint16_t* q, const uint16_t* k, const uint
 
 void launch_flash_bwd_dq_f32x3(const float* q, const HeadView& qv, const uint16_t* k,
                                const uint16_t* v, const HeadView& kv, size_t pstride,
-                               const float* o, const float* dO, const HeadView& ov,
-                               const float* m, const float* l, float* dq, const HeadView& gv,
-                               float* Dws, int BH, int T, int d, float scale,
-                               hipStream_t stream) {
-    const DqArgs<3> a{q, o, dO, k, v, m, l, dq, Dws, BH, T, scale, qv, kv, ov, gv, pstride};
+                               uint16_t* do_planes, const float* o, const float* dO,
+                               const HeadView& ov, const float* m, const float* l, float* dq,
+                               const HeadView& gv, float* Dws, int BH, int T, int d,
+                               float scale, hipStream_t stream) {
+    const DqArgs<3> a{q,  o,     dO, k,  v,  m,  l,  dq,      Dws,
+                      BH, T, scale, qv, kv, ov, gv, pstride, do_planes};
     if (d == 32)
         dq_dispatch<32, 3>(a, stream);
     else

@@ -154,13 +154,14 @@ using OutT = std::conditional_t<NP == 1, uint16_t, float>;
 // NSUB = 2: 256 queries per workgroup, wave w owns sub-blocks w (0) and 7-w (1).
 // NSUB = 1: 128 queries per workgroup, wave w owns sub-block w (1) (small grids).
 // k, v: plane 0 of NP bf16 planes, pstride elements apart (xv addresses a plane).  NP = 1:
-// q is bf16 like k; NP = 3: Q comes from the fp32 tensor qf (view qv) and is split here.
+// q is bf16 like k; NP = 3: Q comes from the fp32 tensor qf (view qv) and is split here,
+// and its planes are written to qp (laid out as k's) when qp is not null.
 template <int D, int NSUB, int NP>
 __global__ __launch_bounds__(kWave* kWaves) void flash_fwd_bf16_kernel(
     const uint16_t* __restrict__ q, const float* __restrict__ qf,
     const uint16_t* __restrict__ k, const uint16_t* __restrict__ v, OutT<NP>* __restrict__ o,
     float* __restrict__ m_out, float* __restrict__ l_out, int BH, int T, float scale, int nblk,
-    HeadView xv, HeadView qv, HeadView ov, size_t pstride) {
+    HeadView xv, HeadView qv, HeadView ov, size_t pstride, uint16_t* __restrict__ qp) {
     constexpr int KT = kKeyTile<NP>;
     constexpr int kHalves = KT / 32;  // 32-key half tiles per tile
     using S = Swz<D, KT>;
@@ -191,6 +192,10 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_fwd_bf16_kernel(
         const float* qh = qf + qv.off(bh);
         if constexpr (NSUB == 2) load_rowop_split<D, NP>(qr0, qh, qj0 + col, T, half, qv.row);
         load_rowop_split<D, NP>(qr1, qh, qj1 + col, T, half, qv.row);
+        if (qp != nullptr) {
+            if constexpr (NSUB == 2) store_planes<D, NP>(qp + xoff, pstride, qr0, qj0 + col, T, half);
+            store_planes<D, NP>(qp + xoff, pstride, qr1, qj1 + col, T, half);
+        }
     }
 
     const int kend = min(T, q0 + kBlock);
@@ -285,6 +290,7 @@ struct FwdArgs {
     float scale;
     HeadView xv, qv, ov;
     size_t pstride;
+    uint16_t* qp;  // Q planes out (NP = 3), or null
 };
 
 template <int D, int NSUB, int NP>
@@ -293,7 +299,7 @@ void fwd_launch(const FwdArgs<NP>& a, hipStream_t stream) {
     const int nblk = (a.T + kBlock - 1) / kBlock;
     hipLaunchKernelGGL((flash_fwd_bf16_kernel<D, NSUB, NP>), dim3(a.BH * nblk),
                        dim3(kWave * kWaves), 0, stream, a.q, a.qf, a.k, a.v, a.o, a.m_out,
-                       a.l_out, a.BH, a.T, a.scale, nblk, a.xv, a.qv, a.ov, a.pstride);
+                       a.l_out, a.BH, a.T, a.scale, nblk, a.xv, a.qv, a.ov, a.pstride, a.qp);
 }
 
 template <int D, int NP>
@@ -311,7 +317,7 @@ void launch_flash_fwd_bf16(const uint16_t* q, const uint16_t* k, const uint16_t*
                            uint16_t* o, float* m_out, float* l_out, int BH, int T, int d,
                            float scale, const HeadView& xv, const HeadView& ov,
                            hipStream_t stream) {
-    const FwdArgs<1> a{q, nullptr, k, v, o, m_out, l_out, BH, T, scale, xv, xv, ov, 0};
+    const FwdArgs<1> a{q, nullptr, k, v, o, m_out, l_out, BH, T, scale, xv, xv, ov, 0, nullptr};
     switch (d) {
         case 32: fwd_dispatch<32, 1>(a, stream); break;
         case 64: fwd_dispatch<64, 1>(a, stream); break;
@@ -320,10 +326,11 @@ void launch_flash_fwd_bf16(const uint16_t* q, const uint16_t* k, const uint16_t*
 }
 
 void launch_flash_fwd_f32x3(const float* q, const HeadView& qv, const uint16_t* k,
-                            const uint16_t* v, size_t pstride, float* o, float* m_out,
-                            float* l_out, int BH, int T, int d, float scale, const HeadView& xv,
-                            const HeadView& ov, hipStream_t stream) {
-    const FwdArgs<3> a{nullptr, q, k, v, o, m_out, l_out, BH, T, scale, xv, qv, ov, pstride};
+                            const uint16_t* v, size_t pstride, uint16_t* q_planes, float* o,
+                            float* m_out, float* l_out, int BH, int T, int d, float scale,
+                            const HeadView& xv, const HeadView& ov, hipStream_t stream) {
+    const FwdArgs<3> a{nullptr, q,  k,  v,  o,  m_out,   l_out,
+                       BH,      T,  scale, xv, qv, ov,   pstride, q_planes};
     if (d == 32)
         fwd_dispatch<32, 3>(a, stream);
     else

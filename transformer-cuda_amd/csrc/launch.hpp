@@ -72,17 +72,19 @@ void launch_split_planes(const float* src, const HeadView& sv, uint16_t* dst, si
 
 // fp32 attention on bf16 MFMAs: every fp32 operand carried as three bf16 planes (hi, mid,
 // lo; bf16_tile.hpp), products as six plane products.  Q is read in fp32 (view qv) and
-// split in registers; k and v point at plane 0 of planes pstride elements apart, each plane
-// addressed by xv; O is fp32.  d = 32 or 64.
+// split in registers, its planes written to q_planes (laid out as k's) unless null; k and v
+// point at plane 0 of planes pstride elements apart, each plane addressed by xv; O is fp32.
+// d = 32 or 64.
 void launch_flash_fwd_f32x3(const float* q, const HeadView& qv, const uint16_t* k,
-                            const uint16_t* v, size_t pstride, float* o, float* m_out,
-                            float* l_out, int BH, int T, int d, float scale, const HeadView& xv,
-                            const HeadView& ov, hipStream_t stream);
+                            const uint16_t* v, size_t pstride, uint16_t* q_planes, float* o,
+                            float* m_out, float* l_out, int BH, int T, int d, float scale,
+                            const HeadView& xv, const HeadView& ov, hipStream_t stream);
 // Stage 1 (D and dQ): q, o, dO fp32 rows (views qv, ov), k and v plane tensors (view kv);
-// dq fp32 (view gv).
+// dq fp32 (view gv); the planes of dO written to do_planes (laid out as k's) unless null.
 void launch_flash_bwd_dq_f32x3(const float* q, const HeadView& qv, const uint16_t* k,
                                const uint16_t* v, const HeadView& kv, size_t pstride,
-                               const float* o, const float* dO, const HeadView& ov,
+                               uint16_t* do_planes, const float* o, const float* dO,
+                               const HeadView& ov,
                                const float* m, const float* l, float* dq, const HeadView& gv,
                                float* Dws, int BH, int T, int d, float scale,
                                hipStream_t stream);

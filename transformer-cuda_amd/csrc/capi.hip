@@ -220,14 +220,14 @@ int check_f32x3(int B, int H, int T, int d, float scale) {
     return ATTN_SUCCESS;
 }
 
-// k and v of qkv (B, T, 3C) into their planes (tensors 1 and 2 of the workspace).
+// k and v of qkv (B, T, 3C) into their planes (tensors 1 and 2 of the workspace), one
+// launch.
 void split_kv_planes(const float* qkv, void* planes, int B, int H, int T, int d,
                      hipStream_t stream) {
     const size_t N = plane_elems(B, H, T, d), C = static_cast<size_t>(H) * d;
-    const tcamd::HeadView xv = tcamd::packed_qkv_view(H, T, d);
-    for (int t = 1; t < 3; ++t)
-        tcamd::launch_split_planes(qkv + t * C, xv, plane_tensor(planes, N, t), N, B * H, T, d,
-                                   stream);
+    tcamd::launch_split_planes(qkv + C, tcamd::packed_qkv_view(H, T, d),
+                               plane_tensor(planes, N, 1), N, B * H, T, d, stream, 2, C,
+                               kPlanes * N);
 }
 
 int packed_forward_f32x3(const float* qkv, float* out, int B, int H, int T, int d, float scale,
@@ -264,10 +264,9 @@ int packed_backward_dq_f32x3(const float* qkv, const float* o, const float* dO, 
     const tcamd::HeadView xv = tcamd::packed_qkv_view(H, T, d);
     const tcamd::HeadView ov = out_view(H, T, d, merged);
     clear_error();
-    if (!kv_ready) {
-        split_kv_planes(qkv, planes, B, H, T, d, stream);
-        tcamd::launch_split_planes(qkv, xv, plane_tensor(planes, N, 0), N, B * H, T, d, stream);
-    }
+    if (!kv_ready)  // q, k, v in one launch
+        tcamd::launch_split_planes(qkv, xv, plane_tensor(planes, N, 0), N, B * H, T, d, stream,
+                                   3, static_cast<size_t>(H) * d, kPlanes * N);
     tcamd::launch_flash_bwd_dq_f32x3(qkv, xv, plane_tensor(planes, N, 1),
                                      plane_tensor(planes, N, 2), tcamd::head_major_view(H, T, d),
                                      N, plane_tensor(planes, N, 3), o, dO, ov, m, l, dqkv, xv, ws,

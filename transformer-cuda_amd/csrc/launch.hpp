@@ -66,9 +66,11 @@ void launch_flash_bwd_dkdv_bf16(const uint16_t* q, const uint16_t* k, const uint
                                 const HeadView& gv, hipStream_t stream);
 
 // An fp32 (B*H, T, d) view (d % 8 == 0, rows 16-byte aligned) as three head-major bf16
-// planes (hi, mid, lo) at dst, dst + pstride, dst + 2 pstride.
+// planes (hi, mid, lo) at dst, dst + pstride, dst + 2 pstride; ntens such tensors in one
+// launch, tensor j from src + j*src_step to dst + j*dst_step.
 void launch_split_planes(const float* src, const HeadView& sv, uint16_t* dst, size_t pstride,
-                         int BH, int T, int d, hipStream_t stream);
+                         int BH, int T, int d, hipStream_t stream, int ntens = 1,
+                         size_t src_step = 0, size_t dst_step = 0);
 
 // fp32 attention on bf16 MFMAs: every fp32 operand carried as three bf16 planes (hi, mid,
 // lo; bf16_tile.hpp), products as six plane products.  Q is read in fp32 (view qv) and

@@ -288,10 +288,11 @@ def measured_traffic(config, dtype, kernel):
     except OSError:
         return None
     for ln in lines:
+        # | config | dtype | path | kernel | FETCH KiB | WRITE KiB | traffic_bytes | ...
         cells = [c.strip() for c in ln.strip().strip("|").split("|")]
-        if len(cells) >= 6 and cells[:3] == [config, dtype, kernel]:
+        if len(cells) >= 7 and cells[:2] == [config, dtype] and cells[3] == kernel:
             try:
-                return int(cells[5])
+                return int(cells[6])
             except ValueError:
                 return None
     return None

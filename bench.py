@@ -47,9 +47,10 @@ timed fwd+bwd.
 
 training_step: BASELINE config 5, the reference's GPT-2-small training step (L12 C768 H12
 T1024 B8 V50257, fp32, forward + backward + fused clip/AdamW) through the harness of
-libtcamd_gpt, once per attention mode (fused: this build's path; tiled_split: the
-reference's tiled launcher sequence; materialized: the reference's default): tokens/s and
-the share of the step in the attention launches.
+libtcamd_gpt, once per attention mode (fused_x3 / fused: this build's path on the bf16 MFMA
+with three-plane fp32 operands / on the fp32 MFMA; tiled_split: the reference's tiled
+launcher sequence; materialized: the reference's default): tokens/s and the share of the
+step in the attention launches.
 
 cpu_baseline: the torch-CPU fp32 restatement of the reference attention
 (pytorch_src/model.py:43-52, forward + autograd backward) timed on this host on the same
@@ -116,7 +117,7 @@ def parse_args():
     ap.add_argument("--gpt-steps", type=int, default=5,
                     help="timed steps of the config-5 training-step harness per attention "
                          "mode (0 skips it)")
-    ap.add_argument("--gpt-modes", default="fused,tiled_split,materialized",
+    ap.add_argument("--gpt-modes", default="fused_x3,fused,tiled_split,materialized",
                     help="attention modes of the training-step measurement (comma separated)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="instead of the bench: run 10 plain device copies of MIB MiB (the "

@@ -29,7 +29,9 @@ typedef struct gpt_model gpt_model;
 enum {
     GPT_ATTN_FUSED = 0,        /* attn_fused_causal_*: qkv in, merged heads out (3 launches) */
     GPT_ATTN_TILED_SPLIT = 1,  /* the reference's tiled sequence: split, tiled, head merge */
-    GPT_ATTN_MATERIALIZED = 2  /* the reference's default: T x T scores and probabilities */
+    GPT_ATTN_MATERIALIZED = 2, /* the reference's default: T x T scores and probabilities */
+    GPT_ATTN_FUSED_X3 = 3      /* attn_fused_causal_*_f32x3: fp32 on the bf16 MFMA (three
+                                  bf16 planes per operand); d_head 32 or 64 */
 };
 
 /* Mirrors TransformerConfig (include/config.h). */

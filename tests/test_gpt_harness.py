@@ -40,6 +40,7 @@ def test_config_validation_without_gpu(gpt):
     assert create(num_heads=3) == 1            # C % H != 0
     assert create(batch_size=0) == 1
     assert create(attention_mode=7) == 6
+    assert create(attention_mode=3, d_model=512) == 2  # fused_x3 at d = 128: unsupported
     assert create(layernorm_eps=0.0) == 6
     assert gpt.raw().gpt_create(None, None) == 3
 

@@ -1,7 +1,8 @@
 """The GPT training-step harness on the GPU against its fp64 CPU oracle (oracle/gpt_ref.py):
 loss and every parameter gradient of one forward + backward, and the clip + AdamW update,
-for each attention mode (this build's fused path, the reference's tiled sequence, the
-reference's materialised default).  Shapes of config 1 (the tiny GPT) and a d = 64 variant.
+for each attention mode (this build's fused path on the fp32 MFMA and on the bf16 MFMA with
+three-plane fp32 operands, the reference's tiled sequence, the reference's materialised
+default).  Shapes of config 1 (the tiny GPT) and a d = 64 variant.
 Tolerances are the reference's own parity gates (scripts/compare_parity.py:108-117): loss
 within 1e-5, gradients within 5e-5."""
 import numpy as np
@@ -58,7 +59,7 @@ def run_fb(model, tokens, targets):
 
 
 @pytest.mark.parametrize("shape", ["c1", "d64"])
-@pytest.mark.parametrize("mode", ["fused", "tiled_split", "materialized"])
+@pytest.mark.parametrize("mode", ["fused", "fused_x3", "tiled_split", "materialized"])
 def test_loss_and_gradients_vs_oracle(gpt, mode, shape):
     s = C1 if shape == "c1" else D64
     model, flat, tokens, targets = make(gpt, s, mode, seed=7)
@@ -93,17 +94,17 @@ def test_optimizer_step_vs_oracle_two_steps(gpt):
 
 
 def test_modes_agree_and_attention_timing(gpt):
-    """The three attention modes give the same loss and gradients to fp32 rounding, and the
+    """The four attention modes give the same loss and gradients to fp32 rounding, and the
     attention timing reports a positive time below the step's."""
     s = D64
     out = {}
-    for mode in ("fused", "tiled_split", "materialized"):
+    for mode in ("fused", "fused_x3", "tiled_split", "materialized"):
         model, flat, tokens, targets = make(gpt, s, mode, seed=11)
         model.set_attention_timing(True)
         out[mode] = run_fb(model, tokens, targets)
         assert model.last_attention_ms() > 0.0
         model.close()
-    for mode in ("tiled_split", "materialized"):
+    for mode in ("fused_x3", "tiled_split", "materialized"):
         assert abs(out[mode][0] - out["fused"][0]) <= 1e-5
         assert np.abs(out[mode][1] - out["fused"][1]).max() <= 2e-5, mode
     # the fused and the reference's tiled sequence run the same kernels: equal bitwise, but

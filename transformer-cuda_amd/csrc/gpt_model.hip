@@ -3,11 +3,13 @@
 // (src/optimizer.cu:117-154), with the attention of every block on this build's path.
 //
 // Differences from the reference that a caller sees: fp32 GEMMs run on rocBLAS (the
-// reference uses cuBLAS / cuBLASLt); the attention runs in one of three modes
+// reference uses cuBLAS / cuBLASLt); the attention runs in one of four modes
 // (gpt_config.attention_mode): the fused path of this build (attention from the packed QKV
 // projection output straight into the merged-heads layout, three launches per layer and
-// direction), the reference's tiled launcher sequence (split-transpose, tiled attention,
-// head merge), or the reference's default materialised sequence (T x T scores).
+// direction) on the fp32 MFMA or, fused_x3, on the bf16 MFMA with fp32 operands as three
+// bf16 planes (a plane workspace per layer, kept from the forward to the backward), the
+// reference's tiled launcher sequence (split-transpose, tiled attention, head merge), or the
+// reference's default materialised sequence (T x T scores).
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <rocblas/rocblas.h>
@@ -39,6 +41,7 @@ struct LayerActs {
         *ln2_rstd, *ffn1, *gelu, *out;
     float *q, *k, *v, *attn_out;  // tiled-split and materialised modes
     float* probs;                 // materialised mode (B, H, T, T)
+    float* planes;                // fused_x3 mode: the layer's plane workspace
 };
 
 long long param_count(const gpt_config& c) {
@@ -147,6 +150,10 @@ int attention_forward(gpt_model* m, LayerActs& a, hipStream_t s) {
             TRY(attn_fused_causal_forward_f32(a.qkv, a.merged, B, H, T, d, scale, a.attn_m,
                                               a.attn_l, s));
             break;
+        case GPT_ATTN_FUSED_X3:
+            TRY(attn_fused_causal_forward_f32x3(a.qkv, a.merged, B, H, T, d, scale, a.attn_m,
+                                                a.attn_l, a.planes, s));
+            break;
         case GPT_ATTN_TILED_SPLIT:
             TRY(attn_qkv_split_transpose_forward_f32(a.qkv, a.q, a.k, a.v, B, T, H, d, s));
             TRY(attn_tiled_causal_forward_f32(a.q, a.k, a.v, a.attn_out, B, H, T, d, scale,
@@ -174,6 +181,11 @@ int attention_backward(gpt_model* m, LayerActs& a, hipStream_t s) {
         case GPT_ATTN_FUSED:
             TRY(attn_fused_causal_backward_f32(a.qkv, a.merged, m->d_merged, a.attn_m, a.attn_l,
                                                m->d_qkv, m->ws, B, H, T, d, scale, s));
+            break;
+        case GPT_ATTN_FUSED_X3:  // the layer's qkv and planes are the forward's
+            TRY(attn_fused_causal_backward_f32x3(a.qkv, a.merged, m->d_merged, a.attn_m,
+                                                 a.attn_l, m->d_qkv, m->ws, B, H, T, d, scale,
+                                                 a.planes, 1, s));
             break;
         case GPT_ATTN_TILED_SPLIT:
             TRY(attn_head_merge_transpose_backward_f32(m->d_merged, m->d_attn_out, B, H, T, d,
@@ -203,11 +215,12 @@ int check_config(const gpt_config& c) {
         c.num_heads <= 0 || c.d_ff <= 0 || c.batch_size <= 0)
         return ATTN_ERROR_INVALID_DIM;
     if (c.d_model % c.num_heads != 0) return ATTN_ERROR_INVALID_DIM;
-    if (c.attention_mode < GPT_ATTN_FUSED || c.attention_mode > GPT_ATTN_MATERIALIZED)
+    if (c.attention_mode < GPT_ATTN_FUSED || c.attention_mode > GPT_ATTN_FUSED_X3)
         return ATTN_ERROR_INVALID_VALUE;
     const int d = c.d_model / c.num_heads;  // the materialised mode takes any head dimension
     if (c.attention_mode != GPT_ATTN_MATERIALIZED && d != 32 && d != 64 && d != 128)
         return ATTN_ERROR_UNSUPPORTED_HEAD_DIM;
+    if (c.attention_mode == GPT_ATTN_FUSED_X3 && d == 128) return ATTN_ERROR_UNSUPPORTED_HEAD_DIM;
     const long long rows = static_cast<long long>(c.batch_size) * c.max_seq_len;
     if (rows * c.vocab_size > 2147483647LL * 8 || rows > 2147483647LL)
         return ATTN_ERROR_INVALID_DIM;
@@ -246,7 +259,15 @@ int create(const gpt_config& c, gpt_model* m) {
         TRY(alloc(m, &a.ffn1, BT * F));
         TRY(alloc(m, &a.gelu, BT * F));
         TRY(alloc(m, &a.out, BT * C));
-        if (c.attention_mode != GPT_ATTN_FUSED) {
+        if (c.attention_mode == GPT_ATTN_FUSED_X3) {
+            const size_t bytes = attn_f32x3_workspace_bytes(static_cast<int>(B),
+                                                            static_cast<int>(H),
+                                                            static_cast<int>(T),
+                                                            static_cast<int>(C / H));
+            TRY(alloc(m, &a.planes, static_cast<long long>((bytes + 3) / 4)));
+        }
+        if (c.attention_mode == GPT_ATTN_TILED_SPLIT ||
+            c.attention_mode == GPT_ATTN_MATERIALIZED) {
             TRY(alloc(m, &a.q, BT * C));
             TRY(alloc(m, &a.k, BT * C));
             TRY(alloc(m, &a.v, BT * C));
@@ -274,7 +295,7 @@ int create(const gpt_config& c, gpt_model* m) {
     cs = std::max<long long>(cs, column_sum_scratch(B, T * C));
     TRY(alloc(m, &m->colsum, cs));
     TRY(alloc(m, &m->norm, 1 + adamw_norm_blocks()));
-    if (c.attention_mode != GPT_ATTN_FUSED) {
+    if (c.attention_mode == GPT_ATTN_TILED_SPLIT || c.attention_mode == GPT_ATTN_MATERIALIZED) {
         TRY(alloc(m, &m->dq, BT * C));
         TRY(alloc(m, &m->dk, BT * C));
         TRY(alloc(m, &m->dv, BT * C));

@@ -26,9 +26,9 @@ if not os.path.exists(GPT_LIB_PATH):
 
 _lib = ctypes.CDLL(GPT_LIB_PATH)
 
-ATTN_FUSED, ATTN_TILED_SPLIT, ATTN_MATERIALIZED = 0, 1, 2
+ATTN_FUSED, ATTN_TILED_SPLIT, ATTN_MATERIALIZED, ATTN_FUSED_X3 = 0, 1, 2, 3
 MODES = {"fused": ATTN_FUSED, "tiled_split": ATTN_TILED_SPLIT,
-         "materialized": ATTN_MATERIALIZED}
+         "materialized": ATTN_MATERIALIZED, "fused_x3": ATTN_FUSED_X3}
 
 
 class GptConfig(ctypes.Structure):

@@ -260,3 +260,54 @@ inline void fused_causal_attention_backward_bf16(const attn_bf16* qkv, const att
                                                         stream),
                         "fused_causal_attention_backward_bf16");
 }
+
+// fp32 on the bf16 matrix cores: the packed / fused launchers above with every fp32 operand
+// carried as three bf16 planes in `planes` (attn_f32x3_workspace_bytes(B, H, T, d_head)
+// bytes, caller-owned).  The backward reuses the planes of q, k and v the forward left there
+// when kv_planes_ready is true.  No counterpart in the reference.
+inline void packed_causal_attention_forward_f32x3(const float* qkv, float* out, int B, int H,
+                                                  int T, int d_head, float scale, void* planes,
+                                                  float* m_out = nullptr,
+                                                  float* l_out = nullptr,
+                                                  hipStream_t stream = nullptr) {
+    tcamd::check_status(attn_packed_causal_forward_f32x3(qkv, out, B, H, T, d_head, scale,
+                                                         m_out, l_out, planes, stream),
+                        "packed_causal_attention_forward_f32x3");
+}
+
+inline void packed_causal_attention_backward_f32x3(const float* qkv, const float* o,
+                                                   const float* do_ptr, const float* m_ptr,
+                                                   const float* l_ptr, float* dqkv,
+                                                   float* d_workspace, int B, int H, int T,
+                                                   int d_head, float scale, void* planes,
+                                                   bool kv_planes_ready = true,
+                                                   hipStream_t stream = nullptr) {
+    tcamd::check_status(attn_packed_causal_backward_f32x3(qkv, o, do_ptr, m_ptr, l_ptr, dqkv,
+                                                          d_workspace, B, H, T, d_head, scale,
+                                                          planes, kv_planes_ready ? 1 : 0,
+                                                          stream),
+                        "packed_causal_attention_backward_f32x3");
+}
+
+inline void fused_causal_attention_forward_f32x3(const float* qkv, float* out, int B, int H,
+                                                 int T, int d_head, float scale, void* planes,
+                                                 float* m_out = nullptr, float* l_out = nullptr,
+                                                 hipStream_t stream = nullptr) {
+    tcamd::check_status(attn_fused_causal_forward_f32x3(qkv, out, B, H, T, d_head, scale,
+                                                        m_out, l_out, planes, stream),
+                        "fused_causal_attention_forward_f32x3");
+}
+
+inline void fused_causal_attention_backward_f32x3(const float* qkv, const float* o,
+                                                  const float* do_ptr, const float* m_ptr,
+                                                  const float* l_ptr, float* dqkv,
+                                                  float* d_workspace, int B, int H, int T,
+                                                  int d_head, float scale, void* planes,
+                                                  bool kv_planes_ready = true,
+                                                  hipStream_t stream = nullptr) {
+    tcamd::check_status(attn_fused_causal_backward_f32x3(qkv, o, do_ptr, m_ptr, l_ptr, dqkv,
+                                                         d_workspace, B, H, T, d_head, scale,
+                                                         planes, kv_planes_ready ? 1 : 0,
+                                                         stream),
+                        "fused_causal_attention_backward_f32x3");
+}

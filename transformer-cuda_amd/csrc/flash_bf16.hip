@@ -744,42 +744,42 @@ __global__ __launch_bounds__(kWave* NW, NP == 1 ? 1 : 2) void flash_bwd_dkdv_bf1
             step(kt, std::false_type{});
         }
     } else {
-    // Half tiles before hstart (= kw/32, the one holding the wave's first key) hold only
-    // queries that precede every key of the wave; a wave whose keys start past T computes
-    // nothing.  Every wave takes part in every tile's barrier and copies.
-    const int hstart = kw < T ? kw / 32 : 2 * ntile;
-    int kt = t0;
-    for (; 2 * kt + 1 < hstart; ++kt) tile_sync(kt);
-    if (kt < ntile) {  // the tile holding the diagonal half tile
-        tile_sync(kt);
-        if (hstart & 1) {  // only its second half tile, the diagonal one
-            const HalfAddr<D> a1 = half_addr(hstart);
-            f32x16 s1, dp1;
-            dkdv_scores<D, NP>(a1, kr, vr, one, s1, dp1);
-            dkdv_update<D, true, NP>(a1, s1, dp1, dk_acc, dv_acc, 32 * hstart, kj, half);
-        } else {
-            pair(kt, std::true_type{});
+        // Half tiles before hstart (= kw/32, the one holding the wave's first key) hold only
+        // queries that precede every key of the wave; a wave whose keys start past T computes
+        // nothing.  Every wave takes part in every tile's barrier and copies.
+        const int hstart = kw < T ? kw / 32 : 2 * ntile;
+        int kt = t0;
+        for (; 2 * kt + 1 < hstart; ++kt) tile_sync(kt);
+        if (kt < ntile) {  // the tile holding the diagonal half tile
+            tile_sync(kt);
+            if (hstart & 1) {  // only its second half tile, the diagonal one
+                const HalfAddr<D> a1 = half_addr(hstart);
+                f32x16 s1, dp1;
+                dkdv_scores<D, NP>(a1, kr, vr, one, s1, dp1);
+                dkdv_update<D, true, NP>(a1, s1, dp1, dk_acc, dv_acc, 32 * hstart, kj, half);
+            } else {
+                pair(kt, std::true_type{});
+            }
+            ++kt;
         }
-        ++kt;
-    }
-    // Steady state, unrolled by the buffer parity (tile kt is in buffer kt & 1).
-    using B0 = std::integral_constant<int, 0>;
-    using B1 = std::integral_constant<int, 1>;
-    if (kt < ntile && (kt & 1)) {
-        tile_sync(kt);
-        pair_c(kt, B1{});
-        ++kt;
-    }
-    for (; kt + 1 < ntile; kt += 2) {
-        tile_sync(kt);
-        pair_c(kt, B0{});
-        tile_sync(kt + 1);
-        pair_c(kt + 1, B1{});
-    }
-    if (kt < ntile) {
-        tile_sync(kt);
-        pair_c(kt, B0{});
-    }
+        // Steady state, unrolled by the buffer parity (tile kt is in buffer kt & 1).
+        using B0 = std::integral_constant<int, 0>;
+        using B1 = std::integral_constant<int, 1>;
+        if (kt < ntile && (kt & 1)) {
+            tile_sync(kt);
+            pair_c(kt, B1{});
+            ++kt;
+        }
+        for (; kt + 1 < ntile; kt += 2) {
+            tile_sync(kt);
+            pair_c(kt, B0{});
+            tile_sync(kt + 1);
+            pair_c(kt + 1, B1{});
+        }
+        if (kt < ntile) {
+            tile_sync(kt);
+            pair_c(kt, B0{});
+        }
 
     }
 

@@ -1,5 +1,6 @@
-// flash_bf16_fwd.hip - tiled causal attention forward, bf16 fast path, on
-// v_mfma_f32_32x32x16_bf16 with fp32 accumulation.
+// flash_bf16_fwd.hip - tiled causal attention forward on v_mfma_f32_32x32x16_bf16 with fp32
+// accumulation, for bf16 operands (NP = 1) and for fp32 operands carried as NP = 3 bf16
+// planes (bf16_tile.hpp: six plane products per product, fp32 output).
 //
 // Algorithm: the reference's tiled online-softmax forward (src/kernels/attention.cu:518-624),
 // with the same statistics contract P_ij = exp(scale*q_i.k_j - m_i) / l_i.
@@ -28,6 +29,11 @@
 // instruction) into rows whose 16-byte chunks are XOR-swizzled by row, with padding after
 // every 8 rows, so that both the row reads of K and the transposing reads of V hit distinct
 // banks (bf16_tile.hpp).
+//
+// Three planes (NP = 3): K and V come from plane tensors, three plane tiles each; Q is read in
+// fp32 and split in registers (its planes written out for the backward); P is split into
+// planes as it leaves the softmax.  The tiles are 32 keys deep, so that the double-buffered
+// planes (55 KB at d = 64) leave room for two workgroups per CU.
 #include <math.h>
 
 #include <type_traits>

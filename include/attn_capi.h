@@ -346,6 +346,30 @@ int attn_causal_backward_dkdv_f32x3(const float* qkv, const float* m_ptr, const 
                                     const float* d_workspace, float* dqkv, int B, int H, int T,
                                     int d_head, float scale, const void* planes,
                                     hipStream_t stream);
+/* The same path with the reference's tiled-launcher arguments: separate head-major q, k, v
+ * (and o, dO, dq, dk, dv) (B, H, T, d_head) as in tiled_causal_attention_forward / _backward
+ * (include/kernels/attention.cuh:39-49, 63-78), plus the plane workspace. */
+int attn_tiled_causal_forward_f32x3(const float* q, const float* k, const float* v,
+                                    float* out, int B, int H, int T, int d_head, float scale,
+                                    float* m_out, float* l_out, void* planes,
+                                    hipStream_t stream);
+int attn_tiled_causal_backward_f32x3(const float* q, const float* k, const float* v,
+                                     const float* o, const float* do_ptr, const float* m_ptr,
+                                     const float* l_ptr, float* dq, float* dk, float* dv,
+                                     float* d_workspace, int B, int H, int T, int d_head,
+                                     float scale, void* planes, int kv_planes_ready,
+                                     hipStream_t stream);
+int attn_tiled_causal_backward_dq_f32x3(const float* q, const float* k, const float* v,
+                                        const float* o, const float* do_ptr,
+                                        const float* m_ptr, const float* l_ptr, float* dq,
+                                        float* d_workspace, int B, int H, int T, int d_head,
+                                        float scale, void* planes, int kv_planes_ready,
+                                        hipStream_t stream);
+int attn_tiled_causal_backward_dkdv_f32x3(const float* k, const float* v, const float* m_ptr,
+                                          const float* l_ptr, const float* d_workspace,
+                                          float* dk, float* dv, int B, int H, int T,
+                                          int d_head, float scale, const void* planes,
+                                          hipStream_t stream);
 
 #ifdef __cplusplus
 }

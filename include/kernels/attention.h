@@ -311,3 +311,30 @@ inline void fused_causal_attention_backward_f32x3(const float* qkv, const float*
                                                          stream),
                         "fused_causal_attention_backward_f32x3");
 }
+
+// The reference's tiled launchers (separate head-major tensors) for fp32 on the bf16 matrix
+// cores; `planes` as above.
+inline void tiled_causal_attention_forward_f32x3(const float* q, const float* k, const float* v,
+                                                 float* out, int B, int H, int T, int d_head,
+                                                 float scale, void* planes,
+                                                 float* m_out = nullptr, float* l_out = nullptr,
+                                                 hipStream_t stream = nullptr) {
+    tcamd::check_status(attn_tiled_causal_forward_f32x3(q, k, v, out, B, H, T, d_head, scale,
+                                                        m_out, l_out, planes, stream),
+                        "tiled_causal_attention_forward_f32x3");
+}
+
+inline void tiled_causal_attention_backward_f32x3(const float* q, const float* k,
+                                                  const float* v, const float* o,
+                                                  const float* do_ptr, const float* m_ptr,
+                                                  const float* l_ptr, float* dq, float* dk,
+                                                  float* dv, float* d_workspace, int B, int H,
+                                                  int T, int d_head, float scale, void* planes,
+                                                  bool kv_planes_ready = true,
+                                                  hipStream_t stream = nullptr) {
+    tcamd::check_status(attn_tiled_causal_backward_f32x3(q, k, v, o, do_ptr, m_ptr, l_ptr, dq,
+                                                         dk, dv, d_workspace, B, H, T, d_head,
+                                                         scale, planes,
+                                                         kv_planes_ready ? 1 : 0, stream),
+                        "tiled_causal_attention_backward_f32x3");
+}

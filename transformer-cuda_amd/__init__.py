@@ -102,6 +102,13 @@ SIGNATURES = {
     "attn_fused_causal_backward_dq_f32x3":
         [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P, _I, _P],
     "attn_causal_backward_dkdv_f32x3": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P, _P],
+    "attn_tiled_causal_forward_f32x3": [_P, _P, _P, _P, _I, _I, _I, _I, _F, _P, _P, _P, _P],
+    "attn_tiled_causal_backward_f32x3":
+        [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P, _I, _P],
+    "attn_tiled_causal_backward_dq_f32x3":
+        [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P, _I, _P],
+    "attn_tiled_causal_backward_dkdv_f32x3":
+        [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P, _P],
 }
 
 for _name, _args in SIGNATURES.items():
@@ -480,6 +487,35 @@ def causal_attention_backward_dkdv_f32x3(qkv, m, l, workspace, dqkv, B, H, T, d_
                _ptr(dqkv, f32, 3 * n, "dqkv"), B, H, T, d_head, float(scale),
                _planes_ptr(planes, B, H, T, d_head), _stream(stream)),
           "causal_attention_backward_dkdv_f32x3")
+
+
+def tiled_causal_attention_forward_f32x3(q, k, v, out, B, H, T, d_head, scale, planes,
+                                         m_out=None, l_out=None, stream=None):
+    """tiled_causal_attention_forward (include/kernels/attention.cuh:39-49) for fp32 on the
+    bf16 matrix cores (operands as three bf16 planes in `planes`)."""
+    n, r = B * H * T * d_head, B * H * T
+    f32 = _dt(False)
+    check(call("attn_tiled_causal_forward_f32x3", _ptr(q, f32, n, "q"), _ptr(k, f32, n, "k"),
+               _ptr(v, f32, n, "v"), _ptr(out, f32, n, "out"), B, H, T, d_head, float(scale),
+               _ptr(m_out, f32, r, "m_out"), _ptr(l_out, f32, r, "l_out"),
+               _planes_ptr(planes, B, H, T, d_head), _stream(stream)),
+          "tiled_causal_attention_forward_f32x3")
+
+
+def tiled_causal_attention_backward_f32x3(q, k, v, o, dO, m, l, dq, dk, dv, workspace, B, H, T,
+                                          d_head, scale, planes, kv_planes_ready=False,
+                                          stream=None):
+    """tiled_causal_attention_backward (attention.cuh:63-78) for fp32 on the bf16 matrix
+    cores; kv_planes_ready reuses the q/k/v planes the forward left in `planes`."""
+    n, r = B * H * T * d_head, B * H * T
+    f32 = _dt(False)
+    check(call("attn_tiled_causal_backward_f32x3", _ptr(q, f32, n, "q"), _ptr(k, f32, n, "k"),
+               _ptr(v, f32, n, "v"), _ptr(o, f32, n, "o"), _ptr(dO, f32, n, "dO"),
+               _ptr(m, f32, r, "m"), _ptr(l, f32, r, "l"), _ptr(dq, f32, n, "dq"),
+               _ptr(dk, f32, n, "dk"), _ptr(dv, f32, n, "dv"),
+               _ptr(workspace, f32, r, "workspace"), B, H, T, d_head, float(scale),
+               _planes_ptr(planes, B, H, T, d_head), 1 if kv_planes_ready else 0,
+               _stream(stream)), "tiled_causal_attention_backward_f32x3")
 
 
 def attention_precompute_dot_do_o(dO, O, D, B, H, T, d_head, stream=None):

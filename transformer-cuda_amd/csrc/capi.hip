@@ -305,6 +305,81 @@ int packed_backward_f32x3(const float* qkv, const float* o, const float* dO, con
     return packed_backward_dkdv_f32x3(qkv, m, l, ws, dqkv, B, H, T, d, scale, planes, stream);
 }
 
+// ---- the same path from separate head-major q, k, v (the reference's tiled launchers) ----
+
+int check_tiled_f32x3(int B, int H, int T, int d, float scale, const void* planes) {
+    if (planes == nullptr) return ATTN_ERROR_NULL_POINTER;
+    const int st = check_f32x3(B, H, T, d, scale);
+    if (st != ATTN_SUCCESS) return st;
+    return aligned16(planes) ? ATTN_SUCCESS : ATTN_ERROR_MISALIGNED;
+}
+
+int tiled_forward_f32x3(const float* q, const float* k, const float* v, float* out, int B, int H,
+                        int T, int d, float scale, float* m_out, float* l_out, void* planes,
+                        hipStream_t stream) {
+    if (q == nullptr || k == nullptr || v == nullptr || out == nullptr)
+        return ATTN_ERROR_NULL_POINTER;
+    const int st = check_tiled_f32x3(B, H, T, d, scale, planes);
+    if (st != ATTN_SUCCESS) return st;
+    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out))
+        return ATTN_ERROR_MISALIGNED;
+    const size_t N = plane_elems(B, H, T, d);
+    const tcamd::HeadView hv = tcamd::head_major_view(H, T, d);
+    clear_error();
+    tcamd::launch_split_planes(k, hv, plane_tensor(planes, N, 1), N, B * H, T, d, stream);
+    tcamd::launch_split_planes(v, hv, plane_tensor(planes, N, 2), N, B * H, T, d, stream);
+    tcamd::launch_flash_fwd_f32x3(q, hv, plane_tensor(planes, N, 1), plane_tensor(planes, N, 2),
+                                  N, plane_tensor(planes, N, 0), out, m_out, l_out, B * H, T, d,
+                                  scale, hv, hv, stream);
+    return launch_status();
+}
+
+int tiled_backward_dq_f32x3(const float* q, const float* k, const float* v, const float* o,
+                            const float* dO, const float* m, const float* l, float* dq,
+                            float* ws, int B, int H, int T, int d, float scale, void* planes,
+                            int kv_ready, hipStream_t stream) {
+    if (q == nullptr || k == nullptr || v == nullptr || o == nullptr || dO == nullptr ||
+        m == nullptr || l == nullptr || dq == nullptr || ws == nullptr)
+        return ATTN_ERROR_NULL_POINTER;
+    const int st = check_tiled_f32x3(B, H, T, d, scale, planes);
+    if (st != ATTN_SUCCESS) return st;
+    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o) || !aligned16(dO) ||
+        !aligned16(dq))
+        return ATTN_ERROR_MISALIGNED;
+    const size_t N = plane_elems(B, H, T, d);
+    const tcamd::HeadView hv = tcamd::head_major_view(H, T, d);
+    clear_error();
+    if (!kv_ready) {
+        tcamd::launch_split_planes(q, hv, plane_tensor(planes, N, 0), N, B * H, T, d, stream);
+        tcamd::launch_split_planes(k, hv, plane_tensor(planes, N, 1), N, B * H, T, d, stream);
+        tcamd::launch_split_planes(v, hv, plane_tensor(planes, N, 2), N, B * H, T, d, stream);
+    }
+    tcamd::launch_flash_bwd_dq_f32x3(q, hv, plane_tensor(planes, N, 1),
+                                     plane_tensor(planes, N, 2), hv, N,
+                                     plane_tensor(planes, N, 3), o, dO, hv, m, l, dq, hv, ws,
+                                     B * H, T, d, scale, stream);
+    return launch_status();
+}
+
+int tiled_backward_dkdv_f32x3(const float* k, const float* v, const float* m, const float* l,
+                              const float* ws, float* dk, float* dv, int B, int H, int T, int d,
+                              float scale, const void* planes, hipStream_t stream) {
+    if (k == nullptr || v == nullptr || m == nullptr || l == nullptr || ws == nullptr ||
+        dk == nullptr || dv == nullptr)
+        return ATTN_ERROR_NULL_POINTER;
+    const int st = check_tiled_f32x3(B, H, T, d, scale, planes);
+    if (st != ATTN_SUCCESS) return st;
+    if (!aligned16(k) || !aligned16(v) || !aligned16(dk) || !aligned16(dv))
+        return ATTN_ERROR_MISALIGNED;
+    const size_t N = plane_elems(B, H, T, d);
+    const tcamd::HeadView hv = tcamd::head_major_view(H, T, d);
+    void* pl = const_cast<void*>(planes);
+    clear_error();
+    tcamd::launch_flash_bwd_dkdv_f32x3(plane_tensor(pl, N, 0), plane_tensor(pl, N, 3), hv, N, k,
+                                       v, hv, m, l, ws, dk, dv, hv, B * H, T, d, scale, stream);
+    return launch_status();
+}
+
 }  // namespace
 
 
@@ -835,6 +910,46 @@ int attn_causal_backward_dkdv_f32x3(const float* qkv, const float* m_ptr, const 
                                     hipStream_t stream) {
     return packed_backward_dkdv_f32x3(qkv, m_ptr, l_ptr, d_workspace, dqkv, B, H, T, d_head,
                                       scale, planes, stream);
+}
+
+int attn_tiled_causal_forward_f32x3(const float* q, const float* k, const float* v,
+                                    float* out, int B, int H, int T, int d_head, float scale,
+                                    float* m_out, float* l_out, void* planes,
+                                    hipStream_t stream) {
+    return tiled_forward_f32x3(q, k, v, out, B, H, T, d_head, scale, m_out, l_out, planes,
+                               stream);
+}
+
+int attn_tiled_causal_backward_dq_f32x3(const float* q, const float* k, const float* v,
+                                        const float* o, const float* do_ptr,
+                                        const float* m_ptr, const float* l_ptr, float* dq,
+                                        float* d_workspace, int B, int H, int T, int d_head,
+                                        float scale, void* planes, int kv_planes_ready,
+                                        hipStream_t stream) {
+    return tiled_backward_dq_f32x3(q, k, v, o, do_ptr, m_ptr, l_ptr, dq, d_workspace, B, H, T,
+                                   d_head, scale, planes, kv_planes_ready, stream);
+}
+
+int attn_tiled_causal_backward_dkdv_f32x3(const float* k, const float* v, const float* m_ptr,
+                                          const float* l_ptr, const float* d_workspace,
+                                          float* dk, float* dv, int B, int H, int T,
+                                          int d_head, float scale, const void* planes,
+                                          hipStream_t stream) {
+    return tiled_backward_dkdv_f32x3(k, v, m_ptr, l_ptr, d_workspace, dk, dv, B, H, T, d_head,
+                                     scale, planes, stream);
+}
+
+int attn_tiled_causal_backward_f32x3(const float* q, const float* k, const float* v,
+                                     const float* o, const float* do_ptr, const float* m_ptr,
+                                     const float* l_ptr, float* dq, float* dk, float* dv,
+                                     float* d_workspace, int B, int H, int T, int d_head,
+                                     float scale, void* planes, int kv_planes_ready,
+                                     hipStream_t stream) {
+    const int st = tiled_backward_dq_f32x3(q, k, v, o, do_ptr, m_ptr, l_ptr, dq, d_workspace, B,
+                                           H, T, d_head, scale, planes, kv_planes_ready, stream);
+    if (st != ATTN_SUCCESS) return st;
+    return tiled_backward_dkdv_f32x3(k, v, m_ptr, l_ptr, d_workspace, dk, dv, B, H, T, d_head,
+                                     scale, planes, stream);
 }
 
 }  // extern "C"

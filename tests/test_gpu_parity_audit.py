@@ -40,7 +40,8 @@ def write_case(d, B, T, C, L, H, V, seed):
 @pytest.mark.parametrize("shape,flag", [((4, 16, 64, 2, 4, 65), None),
                                         ((2, 48, 128, 2, 4, 101), None),
                                         ((2, 48, 128, 2, 4, 101), "--tiled_attn"),
-                                        ((2, 48, 128, 2, 4, 101), "--fused_attn")])
+                                        ((2, 48, 128, 2, 4, 101), "--fused_attn"),
+                                        ((2, 48, 128, 2, 4, 101), "--fused_x3_attn")])
 def test_parity_audit_protocol(tmp_path, shape, flag):
     B, T, C, L, H, V = shape
     d = str(tmp_path / "parity_data")

@@ -11,7 +11,8 @@
 //   data_dir/cuda_grads.bin      the flat fp32 gradient buffer
 //
 // Attention: the reference's default materialised mode; --tiled_attn the tiled launcher
-// sequence (as the reference's flag); --fused_attn this build's fused path.
+// sequence (as the reference's flag); --fused_attn this build's fused path; --fused_x3_attn
+// the fused path on the bf16 matrix cores with three-plane fp32 operands.
 #include <cstdio>
 #include <fstream>
 #include <iostream>
@@ -50,6 +51,7 @@ int main(int argc, char** argv) {
         const std::string arg = argv[i];
         if (arg == "--tiled_attn") mode = GPT_ATTN_TILED_SPLIT;
         else if (arg == "--fused_attn") mode = GPT_ATTN_FUSED;
+        else if (arg == "--fused_x3_attn") mode = GPT_ATTN_FUSED_X3;
         else if (arg.rfind("--", 0) != 0) data_dir = arg;
         else return fail("unknown flag " + arg);
     }

@@ -23,8 +23,9 @@
 // results through LDS at the end of the task (the only workgroup barriers).
 //
 // Staging.  The 32-row tiles streamed over the sequence (K/V, or Q/dO) are copied from HBM
-// straight into LDS with global_load_lds (4 bytes per lane, one row segment of 64 floats
-// per instruction), bypassing VGPRs, into rows padded to a bank-conflict-free stride.  Each
+// straight into LDS with global_load_lds_dwordx4 (16 bytes per lane, 1 KB of the tile per
+// wave instruction, each lane's source offsets precomputed once per kernel), bypassing
+// VGPRs, into rows padded to a bank-conflict-free stride.  Each
 // tensor has one LDS tile: the next tile's copy is issued as soon as the current tile's
 // last LDS read has returned, and waited for (vmcnt) just before its first read, so the
 // copy overlaps the other tensor's contraction and the softmax; a second resident wave on

@@ -120,6 +120,37 @@ def test_materialized_validation(lib):
                     FAKE, FAKE, None, FAKE, 1, 1, 8, 32, f(0.1), None) == NULLPTR
 
 
+def test_f32x3_validation(lib):
+    """The three-plane fp32 entry points validate before any HIP call."""
+    f = ctypes.c_float
+    raw = lib.raw()
+    assert raw.attn_f32x3_workspace_bytes(2, 3, 40, 64) == 4 * 3 * 2 * 3 * 40 * 64 * 2
+    assert raw.attn_f32x3_workspace_bytes(0, 3, 40, 64) == 0
+    fwd = lambda d=64, planes=FAKE, qkv=FAKE, scale=0.125: lib.call(
+        "attn_packed_causal_forward_f32x3", qkv, FAKE, 1, 2, 8, d, f(scale), None, None,
+        planes, None)
+    assert fwd(d=128) == BAD_HEAD_DIM   # plane tiles of d = 128 do not fit the LDS
+    assert fwd(d=48) == BAD_HEAD_DIM
+    assert fwd(planes=None) == NULLPTR
+    assert fwd(planes=MISALIGNED) == MISALIGN
+    assert fwd(qkv=None) == NULLPTR
+    assert fwd(scale=0.0) == BAD_VALUE
+    assert lib.call("attn_fused_causal_forward_f32x3", FAKE, FAKE, 1, 2, 8, 32, f(0.1), None,
+                    None, None, None) == NULLPTR
+    bwd = lambda name, planes=FAKE, ws=FAKE, d=64: lib.call(
+        name, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, ws, 1, 2, 8, d, f(0.125), planes, 1, None)
+    for name in ("attn_packed_causal_backward_f32x3", "attn_fused_causal_backward_dq_f32x3"):
+        assert bwd(name, planes=None) == NULLPTR
+        assert bwd(name, ws=None) == NULLPTR
+        assert bwd(name, d=128) == BAD_HEAD_DIM
+    assert lib.call("attn_causal_backward_dkdv_f32x3", FAKE, FAKE, FAKE, FAKE, FAKE, 1, 2, 8,
+                    64, f(0.125), None, None) == NULLPTR
+    assert lib.call("attn_tiled_causal_forward_f32x3", FAKE, FAKE, FAKE, FAKE, 1, 2, 8, 64,
+                    f(0.125), None, None, MISALIGNED, None) == MISALIGN
+    assert lib.call("attn_tiled_causal_backward_f32x3", *([FAKE] * 11), 1, 2, 8, 128,
+                    f(0.125), FAKE, 1, None) == BAD_HEAD_DIM
+
+
 def test_python_launchers_reject_host_tensors(lib):
     import torch
     x = torch.zeros(2, 2, 8, 32)

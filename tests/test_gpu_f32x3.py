@@ -254,22 +254,24 @@ def test_staged_backward_equals_one_call(lib, merged):
     assert torch.equal(one, two) and torch.equal(D1, D2)
 
 
-def test_config3_shape_agrees_with_fp32_mfma_path(lib):
-    """Config 3's shape in fp32 (B16 H16 T2048 d64: the two-sub-block forward and dQ
-    kernels): the three-plane path and the fp32 MFMA path, each within fp32 rounding of the
-    exact result, agree to 2e-5 on O, the statistics and every gradient."""
-    B, H, T, d = 16, 16, 2048, 64
+@pytest.mark.parametrize("B,H,T,d", [(16, 16, 2048, 64), (16, 16, 1024, 32)])
+def test_config3_shape_agrees_with_fp32_mfma_path(lib, B, H, T, d):
+    """Config 3's shape in fp32 (B16 H16 T2048 d64), and a d = 32 one, both large enough for
+    the two-sub-block forward and dQ kernels: the three-plane path and the fp32 MFMA path,
+    each within fp32 rounding of the exact result, agree to 2e-5 on O, the statistics and
+    every gradient."""
     g = torch.Generator(device="cuda:0").manual_seed(5)
     qkv = torch.randn((B, T, 3 * H * d), generator=g, device="cuda:0")
     do = torch.randn((B, H, T, d), generator=g, device="cuda:0")
-    got = x3_fwd_bwd(lib, qkv, do, B, H, T, d, 0.125)
+    sc = default_scale(d)
+    got = x3_fwd_bwd(lib, qkv, do, B, H, T, d, sc)
     o = torch.empty((B, H, T, d), device="cuda:0")
     m = torch.empty((B, H, T), device="cuda:0")
     l = torch.empty_like(m)
-    lib.packed_causal_attention_forward(qkv, o, B, H, T, d, 0.125, m, l)
+    lib.packed_causal_attention_forward(qkv, o, B, H, T, d, sc, m, l)
     dqkv = torch.empty_like(qkv)
     D = torch.empty_like(m)
-    lib.packed_causal_attention_backward(qkv, o, do, m, l, dqkv, D, B, H, T, d, 0.125)
+    lib.packed_causal_attention_backward(qkv, o, do, m, l, dqkv, D, B, H, T, d, sc)
     torch.cuda.synchronize()
     want = dict(zip(("dq", "dk", "dv"), heads(dqkv.cpu(), B, H, T, d)))
     want["o"] = o.cpu()
@@ -277,7 +279,7 @@ def test_config3_shape_agrees_with_fp32_mfma_path(lib):
     got["lse"] = got["m"] + torch.log(got["l"])
     for n in ("o", "lse", "dq", "dk", "dv"):
         e = max_abs(got[n].numpy(), want[n].numpy())
-        print(f"config3 shape {n}: three-plane vs fp32 MFMA max-abs {e:.2e}")
+        print(f"B{B} H{H} T{T} d{d} {n}: three-plane vs fp32 MFMA max-abs {e:.2e}")
         assert e <= 2e-5, f"{n}: {e:.3e}"
 
 

@@ -322,6 +322,11 @@ void column_sum(const float* x, int R, int N, float* out, float* scratch, hipStr
                        scratch, nchunk, N, out);
 }
 
+void sum_slices(const float* x, int nslice, int n, float* out, hipStream_t s) {
+    hipLaunchKernelGGL(colsum_final_kernel, dim3(blocks_for(n, kBlock)), dim3(kBlock), 0, s, x,
+                       nslice, n, out);
+}
+
 void layernorm_forward(const float* x, const float* gamma, const float* beta, float* y,
                        float* mean, float* rstd, int R, int C, float eps, hipStream_t s) {
     hipLaunchKernelGGL(layernorm_fwd_kernel, dim3(blocks_for(R, kRowsPerBlock)), dim3(kBlock), 0,

@@ -22,6 +22,8 @@ void embedding_backward(const int* tokens, const float* dx, float* d_tok_emb, fl
 // out[n] = sum_r x[r, n]; scratch: column_sum_scratch(R, N) floats.
 size_t column_sum_scratch(int R, int N);
 void column_sum(const float* x, int R, int N, float* out, float* scratch, hipStream_t s);
+// out[i] = sum_j x[j * n + i] over nslice slices of n floats.
+void sum_slices(const float* x, int nslice, int n, float* out, hipStream_t s);
 
 void layernorm_forward(const float* x, const float* gamma, const float* beta, float* y,
                        float* mean, float* rstd, int R, int C, float eps, hipStream_t s);

@@ -89,7 +89,7 @@ struct gpt_model {
           *logits = nullptr, *dlogits = nullptr, *row_loss = nullptr;
     // backward scratch shared by the layers
     float *d_x = nullptr, *d_ln = nullptr, *d_qkv = nullptr, *d_merged = nullptr,
-          *d_ffn_a = nullptr, *d_ffn_b = nullptr, *ws = nullptr, *colsum = nullptr,
+          *d_ffn_a = nullptr, *d_ffn_b = nullptr, *ws = nullptr, *colsum = nullptr, *splitk = nullptr,
           *norm = nullptr, *proj = nullptr;
     float *dq = nullptr, *dk = nullptr, *dv = nullptr, *d_attn_out = nullptr;  // split modes
     float *scores = nullptr, *dprobs = nullptr, *dscores = nullptr;          // materialised
@@ -122,6 +122,37 @@ int gemm(rocblas_handle h, bool ta, bool tb, int M, int N, int K, const float* A
         ta ? rocblas_operation_transpose : rocblas_operation_none, N, M, K, &alpha, B,
         tb ? K : N, A, ta ? M : K, &beta, C, N);
     return st == rocblas_status_success ? ATTN_SUCCESS : ATTN_ERROR_LAUNCH;
+}
+
+// Row-major C (M x N) = A (M x K) * B^T with B stored (N x K), as gemm(false, true, ...), with
+// K cut into ks slices: one strided-batched product writes the ks partial products to ws
+// (ks * M * N floats), a sum over the slices writes C, and one more product adds the K % ks
+// remainder.  For a long contraction over a small output (the output head's input gradient,
+// K = vocabulary), where a single product runs on a few dozen workgroups.
+int gemm_nt_splitk(rocblas_handle h, int M, int N, int K, const float* A, const float* B,
+                   float* C, float* ws, int ks, hipStream_t s) {
+    const float one = 1.0f, zero = 0.0f;
+    const int kc = K / ks, rem = K - kc * ks;
+    const rocblas_stride mn = static_cast<rocblas_stride>(M) * N;
+    rocblas_status st = rocblas_sgemm_strided_batched(
+        h, rocblas_operation_transpose, rocblas_operation_none, N, M, kc, &one, B, K, kc, A, K,
+        kc, &zero, ws, N, mn, ks);
+    if (st != rocblas_status_success) return ATTN_ERROR_LAUNCH;
+    sum_slices(ws, ks, static_cast<int>(mn), C, s);
+    if (rem > 0) {
+        const size_t off = static_cast<size_t>(kc) * ks;
+        st = rocblas_sgemm(h, rocblas_operation_transpose, rocblas_operation_none, N, M, rem, &one,
+                           B + off, K, A + off, K, &one, C, N);
+    }
+    return st == rocblas_status_success ? ATTN_SUCCESS : ATTN_ERROR_LAUNCH;
+}
+
+// Slices of the vocabulary contraction, used when V >= 16 C (a long contraction against a
+// BT x C output); the partial products take kHeadSplitK * BT * C floats of their own.
+constexpr int kHeadSplitK = 8;
+bool head_splitk(const gpt_config& c) {
+    return c.vocab_size >= 16 * c.d_model &&
+           static_cast<long long>(c.batch_size) * c.max_seq_len * c.d_model < (1LL << 31);
 }
 
 #define TRY(x)                                 \
@@ -290,6 +321,7 @@ int create(const gpt_config& c, gpt_model* m) {
     TRY(alloc(m, &m->d_ffn_b, BT * F));
     TRY(alloc(m, &m->proj, BT * C));
     TRY(alloc(m, &m->ws, B * H * T));
+    if (head_splitk(c)) TRY(alloc(m, &m->splitk, static_cast<long long>(kHeadSplitK) * BT * C));
     long long cs = 0;
     for (long long n : {3 * C, F, C}) cs = std::max<long long>(cs, column_sum_scratch(BT, n));
     cs = std::max<long long>(cs, column_sum_scratch(B, T * C));
@@ -345,7 +377,11 @@ int backward(gpt_model* m, const int* tokens, const int* targets, float* loss, h
     const int BT = B * T;
     cross_entropy(m->logits, targets, m->dlogits, m->row_loss, loss, BT, V, s);
     TRY(gemm(m->blas, true, false, C, V, BT, m->lnf, m->dlogits, m->G.head_w));
-    TRY(gemm(m->blas, false, true, BT, C, V, m->dlogits, m->P.head_w, m->d_ln));
+    if (head_splitk(c))
+        TRY(gemm_nt_splitk(m->blas, BT, C, V, m->dlogits, m->P.head_w, m->d_ln, m->splitk,
+                           kHeadSplitK, s));
+    else
+        TRY(gemm(m->blas, false, true, BT, C, V, m->dlogits, m->P.head_w, m->d_ln));
     const float* x_top = c.num_layers > 0 ? m->acts.back().out : m->emb;
     layernorm_backward(m->d_ln, x_top, m->P.lnf_g, m->lnf_mean, m->lnf_rstd, m->d_x, m->G.lnf_g,
                        m->G.lnf_b, m->colsum, BT, C, false, s);

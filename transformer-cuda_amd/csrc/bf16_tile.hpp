@@ -251,6 +251,53 @@ __device__ __forceinline__ void store_row(float* __restrict__ head, int row, int
     }
 }
 
+// ---------------------------------------------------------------------------------------
+// Per-row statistics as one more contraction step: a product over 16 more k-slots, where the
+// A (or B) operand is (1, 1, [1,] 0, ...) and the other carries the terms of the statistic,
+// adds the statistic to every element of the row.
+// ---------------------------------------------------------------------------------------
+
+// Terms of a statistic chunk: (hi, lo) carries 16 significant bits, enough next to bf16
+// operands; fp32 operands take three.
+template <int NP>
+constexpr int kStatTerms = NP == 1 ? 2 : 3;
+
+// The terms of x: x_0 = bf16(x), x_i = bf16(x - x_0 - ... - x_{i-1}).
+template <int NP>
+__device__ __forceinline__ u16x4 stat_terms(float x) {
+    u16x4 v = u16x4{};
+#pragma unroll
+    for (int i = 0; i < kStatTerms<NP>; ++i) {
+        v[i] = f32_to_bf16_bits(x);
+        x -= bf16_bits_to_f32(v[i]);
+    }
+    return v;
+}
+
+// The B or A operand (1, 1, [1,] 0, ...) of a contraction step that adds a per-row
+// statistic chunk to a product: lanes of k-group 1 hold zeros.
+template <int NP>
+__device__ __forceinline__ bf16x8 ones_chunk(int half) {
+    bf16x8 one = bf16x8{};
+    if (half == 0) {
+#pragma unroll
+        for (int i = 0; i < kStatTerms<NP>; ++i) one[i] = static_cast<__bf16>(1.0f);
+    }
+    return one;
+}
+
+// The statistic chunk (terms of x, 0, ...) of a lane's row (zeros in k-group 1).
+template <int NP>
+__device__ __forceinline__ bf16x8 stat_chunk(float x, int half) {
+    u16x8 v = u16x8{};
+    if (half == 0) {
+        const u16x4 t = stat_terms<NP>(x);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = t[i];
+    }
+    return __builtin_bit_cast(bf16x8, v);
+}
+
 // Workgroup id -> (head bh, block b) in rank order: b = nb-1-rank when `descending`, else
 // b = rank; when BH % 8 == 0, every block of a head on one XCD (workgroup i runs on XCD
 // i % 8), so a head's tiles stay in one L2.

@@ -61,11 +61,6 @@ using InT = std::conditional_t<NP == 1, uint16_t, float>;
 template <int NP>
 using OutT = std::conditional_t<NP == 1, uint16_t, float>;
 
-// Terms of a statistic chunk: (hi, lo) carries 16 significant bits, enough next to bf16
-// operands; fp32 operands take three.
-template <int NP>
-constexpr int kStatTerms = NP == 1 ? 2 : 3;
-
 // Key rows per stage-1 tile and query rows per stage-2 tile: NP = 3 streams 32-row tiles, so
 // that the double-buffered planes leave room for two workgroups per CU.
 template <int NP>
@@ -90,42 +85,6 @@ struct QgSmem {
     uint16_t qx[2][KT * 8];  // row r: the terms of -lse2, then zeros
     uint16_t gx[2][KT * 8];  // row r: the terms of -D, then zeros
 };
-
-// The terms of x: x_0 = bf16(x), x_i = bf16(x - x_0 - ... - x_{i-1}).
-template <int NP>
-__device__ __forceinline__ u16x4 stat_terms(float x) {
-    u16x4 v = u16x4{};
-#pragma unroll
-    for (int i = 0; i < kStatTerms<NP>; ++i) {
-        v[i] = f32_to_bf16_bits(x);
-        x -= bf16_bits_to_f32(v[i]);
-    }
-    return v;
-}
-
-// The B or A operand (1, 1, [1,] 0, ...) of a contraction step that adds a per-row
-// statistic chunk to a product: lanes of k-group 1 hold zeros.
-template <int NP>
-__device__ __forceinline__ bf16x8 ones_chunk(int half) {
-    bf16x8 one = bf16x8{};
-    if (half == 0) {
-#pragma unroll
-        for (int i = 0; i < kStatTerms<NP>; ++i) one[i] = static_cast<__bf16>(1.0f);
-    }
-    return one;
-}
-
-// The statistic chunk (terms of x, 0, ...) of a lane's row (zeros in k-group 1).
-template <int NP>
-__device__ __forceinline__ bf16x8 stat_chunk(float x, int half) {
-    u16x8 v = u16x8{};
-    if (half == 0) {
-        const u16x4 t = stat_terms<NP>(x);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = t[i];
-    }
-    return __builtin_bit_cast(bf16x8, v);
-}
 
 // A register operand over the head dimension: the NP planes of row `row` of a head (rows rs
 // elements apart; zeros if row >= T), times `mul` first when SCALE (NP = 1: the bf16 value

@@ -53,6 +53,15 @@ template <int NP>
 constexpr int kKeyTile = NP == 1 ? kRowTile : 32;
 constexpr float kRescaleLog2 = 8.0f;  // raise the running max only beyond p = 2^8
 
+// Folded softmax (bf16 operands, one sub-block per wave): Q is held times c = scale*log2 e
+// (rounded to bf16 again, ~2^-9 relative per element) and minus the running maximum enters
+// S^T as one more contraction step (its (hi, lo) terms against a ones operand), so the
+// scores arrive in the log2 domain relative to the maximum and the exponentials take no
+// per-element fma.  Three planes keep Q exact; two sub-blocks per wave keep the fma, whose
+// registers the fold's operands would take from the third wave per SIMD.
+template <int NP, int NSUB>
+constexpr bool kFold = NP == 1 && NSUB == 1;
+
 // Double-buffered K and V tiles, NP planes each.
 template <int D, int NP>
 struct FwdSmem {
@@ -77,18 +86,20 @@ __device__ __forceinline__ float sum_tree16(const f32x16& s) {
     return (t[0] + t[2]) + (t[1] + t[3]);
 }
 
-// Per-wave softmax state of one 32-query sub-block.
+// Per-wave softmax state of one 32-query sub-block.  Folded: m_used and m_true are
+// in log2 units of c*q.k, and xs carries the terms of -m_used; otherwise in units of q.k.
 template <int D>
 struct SubState {
     f32x16 acc[D / 32];  // O^T accumulator
     float m_used;        // max the exponentials are taken against
-    float m_true;        // running max of the raw scores q.k
-    float l;             // running sum of 2^(s*c - m_used*c)
+    float m_true;        // running max of the scores
+    float l;             // running sum of the exponentials against m_used
+    bf16x8 xs;           // folded: statistic chunk of -m_used
 };
 
 // Masks S^T for keys kb.. against queries qj + col, runs the online-softmax update of `st`,
 // and packs P as the two B operands (NP planes each) of the PV products.
-template <int D, int NP>
+template <int D, int NP, bool FOLD>
 __device__ __forceinline__ void softmax_step(f32x16& s, SubState<D>& st, bf16x8 (&pb)[2][NP],
                                              int kb, int qj, int col, int half, float c) {
     if (kb + 31 > qj) {  // the half tile crosses the diagonal of this sub-block
@@ -98,6 +109,37 @@ __device__ __forceinline__ void softmax_step(f32x16& s, SubState<D>& st, bf16x8 
     }
     float mx = max_tree16(s);
     mx = xhalf_max(mx);
+    if constexpr (FOLD) {
+        // s = c*q.k - m_used already
+        st.m_true = fmaxf(st.m_true, mx + st.m_used);
+        const bool first = st.l == 0.0f;  // l >= 1 after the first tile
+        if (__builtin_amdgcn_ballot_w64(first || mx > kRescaleLog2) != 0) {
+            // the first tile sets the maximum, later ones only raise it; the new offset is
+            // what its bf16 terms carry
+            const u16x4 t = stat_terms<NP>(-(st.m_used + (first ? mx : fmaxf(mx, 0.0f))));
+            const float m_new = -(bf16_bits_to_f32(t[0]) + bf16_bits_to_f32(t[1]));
+            const float shift = m_new - st.m_used;
+            const float alpha = first ? 1.0f : exp2_fast(-shift);  // acc, l are 0 at first
+            st.l *= alpha;
+#pragma unroll
+            for (int dt = 0; dt < D / 32; ++dt) st.acc[dt] *= alpha;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) s[r] -= shift;
+            st.m_used = m_new;
+            u16x8 x = u16x8{};
+            if (half == 0) {
+                x[0] = t[0];
+                x[1] = t[1];
+            }
+            st.xs = __builtin_bit_cast(bf16x8, x);
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[r] = exp2_fast(s[r]);
+        st.l += xhalf_sum(sum_tree16(s));
+        pack_planes<NP>(s, 0, pb[0]);
+        pack_planes<NP>(s, 1, pb[1]);
+        return;
+    }
     st.m_true = fmaxf(st.m_true, mx);
     if (__builtin_amdgcn_ballot_w64((mx - st.m_used) * c > kRescaleLog2) != 0) {
         const float m_new = fmaxf(st.m_used, mx);
@@ -119,15 +161,19 @@ __device__ __forceinline__ void softmax_step(f32x16& s, SubState<D>& st, bf16x8 
 // too when BOTH.  ka[st] / va[dt]: this lane's LDS read addresses in plane 0 of the current
 // tiles for the K chunk of step st and the V^T fragment of head-dim tile dt (half 0, keys
 // 0..); plane i lies i tile sizes further.
-template <int D, bool BOTH, int NP>
+template <int D, bool BOTH, int NP, bool FOLD>
 __device__ __forceinline__ void half_step(int kb, const uint32_t (&ka)[D / 16],
                                           const uint32_t (&va)[D / 32],
                                           const bf16x8 (&q0)[D / 16][NP],
                                           const bf16x8 (&q1)[D / 16][NP], SubState<D>& st0,
                                           SubState<D>& st1, int qj0, int qj1, int col, int half,
-                                          float c) {
+                                          float c, const bf16x8& one) {
     constexpr uint32_t kPlane = Swz<D, kKeyTile<NP>>::kBytes;
     f32x16 s0 = f32x16{}, s1 = f32x16{};
+    if constexpr (FOLD) {  // -m_used into every score of the query
+        s1 = mfma_32x32x16_bf16(one, st1.xs, s1);
+        if constexpr (BOTH) s0 = mfma_32x32x16_bf16(one, st0.xs, s0);
+    }
 #pragma unroll
     for (int st = 0; st < D / 16; ++st) {
         bf16x8 a[NP];
@@ -137,8 +183,8 @@ __device__ __forceinline__ void half_step(int kb, const uint32_t (&ka)[D / 16],
         if constexpr (BOTH) s0 = mma_planes<NP>(a, q0[st], s0);
     }
     bf16x8 p0[2][NP], p1[2][NP];
-    softmax_step<D, NP>(s1, st1, p1, kb, qj1, col, half, c);
-    if constexpr (BOTH) softmax_step<D, NP>(s0, st0, p0, kb, qj0, col, half, c);
+    softmax_step<D, NP, FOLD>(s1, st1, p1, kb, qj1, col, half, c);
+    if constexpr (BOTH) softmax_step<D, NP, FOLD>(s0, st0, p0, kb, qj0, col, half, c);
 #pragma unroll
     for (int dt = 0; dt < D / 32; ++dt) {
 #pragma unroll
@@ -194,6 +240,14 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_fwd_bf16_kernel(
         if constexpr (NSUB == 2)
             load_rowop_planes<D, NP>(qr0, q + xoff, pstride, qj0 + col, T, half, xrs);
         load_rowop_planes<D, NP>(qr1, q + xoff, pstride, qj1 + col, T, half, xrs);
+        if constexpr (kFold<NP, NSUB>) {
+#pragma unroll
+            for (int st = 0; st < D / 16; ++st) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    qr1[st][0][e] = static_cast<__bf16>(static_cast<float>(qr1[st][0][e]) * c);
+            }
+        }
     } else {
         const float* qh = qf + qv.off(bh);
         if constexpr (NSUB == 2) load_rowop_split<D, NP>(qr0, qh, qj0 + col, T, half, qv.row);
@@ -231,9 +285,11 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_fwd_bf16_kernel(
         st0.acc[dt] = f32x16{};
         st1.acc[dt] = f32x16{};
     }
-    st0.m_used = st1.m_used = -INFINITY;
+    st0.m_used = st1.m_used = kFold<NP, NSUB> ? 0.0f : -INFINITY;
     st0.m_true = st1.m_true = -INFINITY;
     st0.l = st1.l = 0.0f;
+    st0.xs = st1.xs = bf16x8{};
+    const bf16x8 one = ones_chunk<NP>(half);
 
     // Half tiles hh = 0 .. kHalves*ntile-1 (keys 32*hh ..).  Sub-block w is active for
     // hh < hA, sub-block 7-w for hh < hB; every wave takes part in every tile's barrier and
@@ -260,11 +316,11 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_fwd_bf16_kernel(
     int hh = 0;
     for (; hh < hA; ++hh) {
         tile_sync(hh);
-        half_step<D, true, NP>(32 * hh, ka, va, qr0, qr1, st0, st1, qj0, qj1, col, half, c);
+        half_step<D, true, NP, kFold<NP, NSUB>>(32 * hh, ka, va, qr0, qr1, st0, st1, qj0, qj1, col, half, c, one);
     }
     for (; hh < hB; ++hh) {
         tile_sync(hh);
-        half_step<D, false, NP>(32 * hh, ka, va, qr0, qr1, st0, st1, qj0, qj1, col, half, c);
+        half_step<D, false, NP, kFold<NP, NSUB>>(32 * hh, ka, va, qr0, qr1, st0, st1, qj0, qj1, col, half, c, one);
     }
     for (; hh < hend; ++hh) tile_sync(hh);
 
@@ -277,8 +333,14 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_fwd_bf16_kernel(
             if (half == 0) {
                 const size_t r = static_cast<size_t>(bh) * T + qi;
                 // m = scale * max_j q.k; l relative to that maximum
-                if (m_out != nullptr) m_out[r] = st.m_true * scale;
-                if (l_out != nullptr) l_out[r] = st.l * exp2_fast((st.m_used - st.m_true) * c);
+                if constexpr (kFold<NP, NSUB>) {
+                    if (m_out != nullptr) m_out[r] = st.m_true * (1.0f / kLog2e);
+                    if (l_out != nullptr) l_out[r] = st.l * exp2_fast(st.m_used - st.m_true);
+                } else {
+                    if (m_out != nullptr) m_out[r] = st.m_true * scale;
+                    if (l_out != nullptr)
+                        l_out[r] = st.l * exp2_fast((st.m_used - st.m_true) * c);
+                }
             }
         }
     }

@@ -2,8 +2,9 @@
 loss and every parameter gradient of one forward + backward, and the clip + AdamW update,
 for each attention mode (this build's fused path on the fp32 MFMA and on the bf16 MFMA with
 three-plane fp32 operands, the reference's tiled sequence, the reference's materialised
-default).  Shapes of config 1 (the tiny GPT), a d = 64 variant and a vocabulary of more than
-16 d_model (the split-K product of the output head's input gradient).
+default).  Shapes of config 1 (the tiny GPT), a d = 64 variant, a vocabulary of more than
+16 d_model (the split-K product of the output head's input gradient) and 4096 tokens (the
+split-K weight gradients).
 Tolerances are the reference's own parity gates (scripts/compare_parity.py:108-117): loss
 within 1e-5, gradients within 5e-5."""
 import numpy as np
@@ -19,7 +20,9 @@ D64 = dict(V=97, T=130, C=128, L=2, H=2, d_ff=256, B=3)
 # V >= 16 C: the output head's input gradient takes the split-K product (V = 8 * 256 + 5,
 # so the remainder product runs too)
 VOC = dict(V=2053, T=32, C=64, L=1, H=2, d_ff=128, B=2)
-SHAPES = {"c1": C1, "d64": D64, "vocab": VOC}
+# B*T >= 4096: the weight gradients take the split-K product (four slices over the tokens)
+TOK = dict(V=97, T=512, C=64, L=1, H=2, d_ff=128, B=8)
+SHAPES = {"c1": C1, "d64": D64, "vocab": VOC, "tokens": TOK}
 
 
 @pytest.fixture(scope="module")
@@ -63,7 +66,7 @@ def run_fb(model, tokens, targets):
     return float(loss.item()), model.gradients()
 
 
-@pytest.mark.parametrize("shape", ["c1", "d64", "vocab"])
+@pytest.mark.parametrize("shape", ["c1", "d64", "vocab", "tokens"])
 @pytest.mark.parametrize("mode", ["fused", "fused_x3", "tiled_split", "materialized"])
 def test_loss_and_gradients_vs_oracle(gpt, mode, shape):
     s = SHAPES[shape]

@@ -66,36 +66,76 @@ __global__ void embedding_tok_bwd_kernel(const int* __restrict__ tokens,
 // ---- column sums: out[n] = sum_r x[r, n] (beta: out = sum + beta*out) -----------------
 constexpr int kChunkRows = 128;
 
-// partial[chunk][n] = sum over the chunk's rows; with w != nullptr the summand is
-// x[r,n] * w[r,n] (the LayerNorm gamma gradient uses the normalised input as w, recomputed
-// from x, mean and rstd when ln_x != nullptr).
-__global__ void colsum_partial_kernel(const float* __restrict__ x, int R, int N,
-                                      const float* __restrict__ ln_x,
-                                      const float* __restrict__ ln_mean,
-                                      const float* __restrict__ ln_rstd,
-                                      float* __restrict__ partial) {
-    const int n = blockIdx.x * blockDim.x + threadIdx.x;
-    const int chunk = blockIdx.y;
-    if (n >= N) return;
-    const int r0 = chunk * kChunkRows, r1 = min(R, r0 + kChunkRows);
-    float s = 0.0f;
-    for (int r = r0; r < r1; ++r) {
-        const float v = x[static_cast<long long>(r) * N + n];
-        if (ln_x != nullptr)
-            s = fmaf(v, (ln_x[static_cast<long long>(r) * N + n] - ln_mean[r]) * ln_rstd[r], s);
-        else
-            s += v;
+// partial[chunk][n] = sum over the chunk's rows; with ln_x != nullptr the summand is
+// x[r,n] times the normalised input (ln_x[r,n] - mean[r]) * rstd[r] (the LayerNorm gamma
+// gradient).  A block covers 64 columns (one wave's lanes, 256 contiguous bytes per row)
+// and the chunk's rows split over its 4 waves, two rows in flight per thread; the 4 partial
+// sums of a column meet in LDS.
+constexpr int kColTile = kWave;
+constexpr int kColLanes = kBlock / kColTile;
+__global__ __launch_bounds__(kBlock) void colsum_partial_kernel(
+    const float* __restrict__ x, int R, int N, const float* __restrict__ ln_x,
+    const float* __restrict__ ln_mean, const float* __restrict__ ln_rstd,
+    float* __restrict__ partial) {
+    __shared__ float red[kColLanes][kColTile];
+    const int c = threadIdx.x % kColTile, j = threadIdx.x / kColTile;
+    const int n = blockIdx.x * kColTile + c;
+    const int r0 = blockIdx.y * kChunkRows, r1 = min(R, r0 + kChunkRows);
+    auto term = [&](int r) {
+        const long long i = static_cast<long long>(r) * N + n;
+        return ln_x != nullptr ? x[i] * ((ln_x[i] - ln_mean[r]) * ln_rstd[r]) : x[i];
+    };
+    float s0 = 0.0f, s1 = 0.0f;
+    if (n < N) {
+        int r = r0 + j;
+        for (; r + kColLanes < r1; r += 2 * kColLanes) {
+            s0 += term(r);
+            s1 += term(r + kColLanes);
+        }
+        if (r < r1) s0 += term(r);
     }
-    partial[static_cast<long long>(chunk) * N + n] = s;
+    red[j][c] = s0 + s1;
+    __syncthreads();
+    if (j == 0 && n < N) {
+        float t = red[0][c];
+#pragma unroll
+        for (int i = 1; i < kColLanes; ++i) t += red[i][c];
+        partial[static_cast<long long>(blockIdx.y) * N + n] = t;
+    }
 }
 
-__global__ void colsum_final_kernel(const float* __restrict__ partial, int nchunk, int N,
-                                    float* __restrict__ out) {
-    const int n = blockIdx.x * blockDim.x + threadIdx.x;
-    if (n >= N) return;
+// out[n] = sum over the nchunk partial rows: a block covers 16 columns, its 16 lanes per
+// column stride over the chunks.
+constexpr int kFinCols = 16;
+constexpr int kFinLanes = kBlock / kFinCols;
+__global__ __launch_bounds__(kBlock) void colsum_final_kernel(const float* __restrict__ partial,
+                                                              int nchunk, int N,
+                                                              float* __restrict__ out) {
+    __shared__ float red[kFinLanes][kFinCols + 1];
+    const int c = threadIdx.x % kFinCols, j = threadIdx.x / kFinCols;
+    const int n = blockIdx.x * kFinCols + c;
     float s = 0.0f;
-    for (int c = 0; c < nchunk; ++c) s += partial[static_cast<long long>(c) * N + n];
-    out[n] = s;
+    if (n < N) {
+        for (int k = j; k < nchunk; k += kFinLanes) s += partial[static_cast<long long>(k) * N + n];
+    }
+    red[j][c] = s;
+    __syncthreads();
+    if (j == 0 && n < N) {
+        float t = red[0][c];
+        for (int i = 1; i < kFinLanes; ++i) t += red[i][c];
+        out[n] = t;
+    }
+}
+
+// out[i] = sum_j x[j*n + i]: one thread per element (n large, few slices).
+__global__ __launch_bounds__(kBlock) void slice_sum_kernel(const float* __restrict__ x,
+                                                           int nslice, int n,
+                                                           float* __restrict__ out) {
+    const int i = blockIdx.x * kBlock + threadIdx.x;
+    if (i >= n) return;
+    float s = 0.0f;
+    for (int j = 0; j < nslice; ++j) s += x[static_cast<long long>(j) * n + i];
+    out[i] = s;
 }
 
 // ---- LayerNorm ---------------------------------------------------------------------------
@@ -201,16 +241,25 @@ __global__ __launch_bounds__(kBlock) void cross_entropy_kernel(
     const int row = blockIdx.x;
     const int tid = threadIdx.x, lane = tid % kWave, w = tid / kWave;
     const float* z = logits + static_cast<long long>(row) * V;
-    float mx = -INFINITY;
-    for (int i = tid; i < V; i += kBlock) mx = fmaxf(mx, z[i]);
-    mx = wave_max(mx);
+    // one pass for the maximum and the sum of exponentials (a thread's running sum is
+    // rescaled when its maximum grows), then the thread sums are brought to the row maximum
+    float tm = -INFINITY, ts = 0.0f;
+    for (int i = tid; i < V; i += kBlock) {
+        const float zi = z[i];
+        if (zi > tm) {
+            ts = ts * expf(tm - zi) + 1.0f;
+            tm = zi;
+        } else {
+            ts += expf(zi - tm);
+        }
+    }
+    float mx = wave_max(tm);
     if (lane == 0) red[w] = mx;
     __syncthreads();
     mx = red[0];
     for (int i = 1; i < kBlock / kWave; ++i) mx = fmaxf(mx, red[i]);
     __syncthreads();
-    float s = 0.0f;
-    for (int i = tid; i < V; i += kBlock) s += expf(z[i] - mx);
+    float s = tm == -INFINITY ? 0.0f : ts * expf(tm - mx);
     s = wave_sum(s);
     if (lane == 0) red[w] = s;
     __syncthreads();
@@ -316,14 +365,14 @@ size_t column_sum_scratch(int R, int N) {
 
 void column_sum(const float* x, int R, int N, float* out, float* scratch, hipStream_t s) {
     const int nchunk = (R + kChunkRows - 1) / kChunkRows;
-    hipLaunchKernelGGL(colsum_partial_kernel, dim3(blocks_for(N, kBlock), nchunk), dim3(kBlock),
-                       0, s, x, R, N, nullptr, nullptr, nullptr, scratch);
-    hipLaunchKernelGGL(colsum_final_kernel, dim3(blocks_for(N, kBlock)), dim3(kBlock), 0, s,
+    hipLaunchKernelGGL(colsum_partial_kernel, dim3(blocks_for(N, kColTile), nchunk),
+                       dim3(kBlock), 0, s, x, R, N, nullptr, nullptr, nullptr, scratch);
+    hipLaunchKernelGGL(colsum_final_kernel, dim3(blocks_for(N, kFinCols)), dim3(kBlock), 0, s,
                        scratch, nchunk, N, out);
 }
 
 void sum_slices(const float* x, int nslice, int n, float* out, hipStream_t s) {
-    hipLaunchKernelGGL(colsum_final_kernel, dim3(blocks_for(n, kBlock)), dim3(kBlock), 0, s, x,
+    hipLaunchKernelGGL(slice_sum_kernel, dim3(blocks_for(n, kBlock)), dim3(kBlock), 0, s, x,
                        nslice, n, out);
 }
 
@@ -339,9 +388,9 @@ void layernorm_backward(const float* dy, const float* x, const float* gamma, con
     hipLaunchKernelGGL(layernorm_bwd_kernel, dim3(blocks_for(R, kRowsPerBlock)), dim3(kBlock), 0,
                        s, dy, x, gamma, mean, rstd, dx, R, C, accumulate ? 1 : 0);
     const int nchunk = (R + kChunkRows - 1) / kChunkRows;
-    hipLaunchKernelGGL(colsum_partial_kernel, dim3(blocks_for(C, kBlock), nchunk), dim3(kBlock),
-                       0, s, dy, R, C, x, mean, rstd, scratch);
-    hipLaunchKernelGGL(colsum_final_kernel, dim3(blocks_for(C, kBlock)), dim3(kBlock), 0, s,
+    hipLaunchKernelGGL(colsum_partial_kernel, dim3(blocks_for(C, kColTile), nchunk),
+                       dim3(kBlock), 0, s, dy, R, C, x, mean, rstd, scratch);
+    hipLaunchKernelGGL(colsum_final_kernel, dim3(blocks_for(C, kFinCols)), dim3(kBlock), 0, s,
                        scratch, nchunk, C, dgamma);
     column_sum(dy, R, C, dbeta, scratch, s);
 }

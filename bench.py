@@ -27,7 +27,10 @@ starts.
 
 value = algorithmic FLOPs of causal attention fwd+bwd, 7*B*H*T^2*d (FlashAttention-2
 convention: fwd 2*B*H*T^2*d, bwd 5*B*H*T^2*d), divided by the wall-clock time of the K
-timed steps.  The roofline object describes the dominant kernel (the longest average
+timed steps.  Before the W warmup steps, untimed steps run for --ramp-s seconds (ramp_s in
+the line, default 0.5) so that the GPU's clocks have left their idle state: a few
+milliseconds of warmup alone leave the timed steps partly at ramp-up clocks (config 2:
+~10% below the steady rate).  The roofline object describes the dominant kernel (the longest average
 duration, measured with HIP events recorded on the launch stream around every kernel of
 every timed step) against its algorithmic FLOPs:
     forward 2 units, backward dK/dV 4 units (S recompute, dP, dV, dK), backward dQ 1 unit
@@ -56,7 +59,7 @@ cpu_baseline: the torch-CPU fp32 restatement of the reference attention
 (pytorch_src/model.py:43-52, forward + autograd backward) timed on this host on the same
 inputs, which also gives a max-abs parity figure for the GPU result.
 
-Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 5] [--config c2]
+Usage: python bench.py [--gpus 1] [--steps 200] [--warmup 5] [--ramp-s 0.5] [--config c2]
 """
 from __future__ import annotations
 
@@ -96,8 +99,11 @@ X3_PRODUCTS = 6  # bf16 plane products per fp32 product on the x3 path
 def parse_args():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--ramp-s", type=float, default=0.5,
+                    help="seconds of untimed steps before the warmup steps (GPU clocks out of "
+                         "their idle state; 0 disables)")
     ap.add_argument("--config", choices=sorted(CONFIGS), default="c2")
     ap.add_argument("--dtype", choices=["f32", "bf16"], default=None,
                     help="override the config's dtype")
@@ -233,9 +239,15 @@ class PathRunner:
         elem = 2 if self.dtype == "bf16" else 4
         return 6.0 * self.B * self.T * self.C * elem, "byte"
 
-    def timed(self, steps, warmup):
-        """Time `steps` steps; per-kernel durations from events on the launch stream."""
+    def timed(self, steps, warmup, ramp_s=0.0):
+        """Time `steps` steps after `ramp_s` seconds of untimed steps and `warmup` more;
+        per-kernel durations from events on the launch stream."""
         torch = self.torch
+        t_end = time.perf_counter() + ramp_s
+        while time.perf_counter() < t_end:
+            for _ in range(10):
+                self.step()
+            torch.cuda.synchronize()
         for _ in range(warmup):
             self.step()
         torch.cuda.synchronize()
@@ -400,10 +412,10 @@ def cpu_baseline(runner, target_s):
     }
 
 
-def secondary(lib, cfg, dtype, steps, seed, path="packed"):
+def secondary(lib, cfg, dtype, steps, seed, path="packed", ramp_s=0.0):
     B, H, T, d, _, qk = CONFIGS[cfg]
     r = PathRunner(lib, B, H, T, d, dtype, seed, qk, path)
-    wall, per_kernel = r.timed(steps, 3)
+    wall, per_kernel = r.timed(steps, 3, ramp_s)
     ms = wall / steps * 1e3
     tf = r.flops_total() / (ms * 1e-3) / 1e12
     attn_ms = sum(ms_ for n, ms_ in per_kernel.items() if n in FLOP_UNITS)
@@ -531,7 +543,7 @@ def main():
     dtype = args.dtype or cdt
     path = args.path or ("x3" if dtype == "f32" and d <= 64 else "packed")
     runner = PathRunner(lib, B, H, T, d, dtype, args.seed, qk, path)
-    wall, per_kernel = runner.timed(args.steps, args.warmup)
+    wall, per_kernel = runner.timed(args.steps, args.warmup, args.ramp_s)
     ms = wall / args.steps * 1e3
     value = runner.flops_total() / (ms * 1e-3) / 1e12
     dom, roof = roofline_of(runner, per_kernel, args.config)
@@ -549,6 +561,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "ramp_s": args.ramp_s,
         "ms_per_step": round(ms, 4),
         "higher_is_better": True,
         "scaling": "weak",
@@ -582,11 +595,13 @@ def main():
     torch.cuda.empty_cache()
     if not args.no_secondary:
         others = {"x3": ["packed", "split"], "packed": ["split"], "split": ["packed"]}[path]
-        sec = [secondary(lib, args.config, dtype, args.secondary_steps, args.seed, o)
-               for o in others]
+        sec = [secondary(lib, args.config, dtype, args.secondary_steps, args.seed, o,
+                         args.ramp_s) for o in others]
         if dtype != "bf16":
-            sec.append(secondary(lib, args.config, "bf16", args.secondary_steps, args.seed))
-        sec.append(secondary(lib, "c3", "bf16", args.secondary_steps, args.seed))
+            sec.append(secondary(lib, args.config, "bf16", args.secondary_steps, args.seed,
+                                 ramp_s=args.ramp_s))
+        sec.append(secondary(lib, "c3", "bf16", args.secondary_steps, args.seed,
+                             ramp_s=args.ramp_s))
         sec.append(materialized(lib, max(3, args.secondary_steps // 4), args.seed))
         line["secondary"] = sec
     if args.gpt_steps > 0:

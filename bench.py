@@ -37,16 +37,21 @@ every timed step) against its algorithmic FLOPs:
     (dQ; its S and dP recomputes duplicate work already counted), unit = B*H*T^2*d.
 For the x3 path the roofline is the bf16 MFMA's: achieved = 6 x the algorithmic FLOPs (six
 bf16 plane products per fp32 product) per second against the bf16 peak, with the fp32
-equivalent (algorithmic FLOPs against the fp32 peak) beside it.
+algorithmic rate (TFLOP/s, not a fraction of any peak) beside it.
 The split-transpose kernels are HBM-bound: 6*B*T*C*elem_bytes algorithmic bytes each.
 roofline.traffic is the dominant kernel's measured HBM bytes per dispatch, read from
 profiles/hbm_traffic.md (rocprofv3 FETCH_SIZE and WRITE_SIZE of this same bench command,
 scaled by a device-copy calibration); null when that file has no row for the workload.
 
 secondary: the same workload through the other paths (fp32: the fp32 MFMA path, packed and
-the reference's split sequence), the step in bf16 at config 2's shape and at config 3, and
-the reference's materialised mode (full-square GEMMs + fused softmax, fp32, config 2) as a
-timed fwd+bwd.
+the reference's split sequence), the step in bf16 at config 2's shape and at configs 3 and 4
+(each with its roofline object, a CPU baseline on a bounded sample of its heads and the
+bf16 parity gate), and the reference's materialised mode (full-square GEMMs + fused softmax,
+fp32, config 2) as a timed fwd+bwd.
+
+parity_gate: the north star's gate applied to the cpu_baseline comparison (fp32: max-abs
+<= 1e-5; bf16: rel-L2 <= 2e-2; O, dQ, dK, dV).  When it fails the line is still printed
+and the exit status is 3: the throughput of a result that fails parity is not valid.
 
 training_step: BASELINE config 5, the reference's GPT-2-small training step (L12 C768 H12
 T1024 B8 V50257, fp32, forward + backward + fused clip/AdamW) through the harness of
@@ -117,6 +122,9 @@ def parse_args():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="target CPU time of the cpu_baseline sample")
+    ap.add_argument("--secondary-cpu-seconds", type=float, default=6.0,
+                    help="target CPU time of the cpu_baseline sample of each bf16 secondary "
+                         "configuration (c3, c4)")
     ap.add_argument("--no-secondary", action="store_true",
                     help="skip the bf16 secondary measurements")
     ap.add_argument("--secondary-steps", type=int, default=20)
@@ -322,8 +330,7 @@ def roofline_of(runner, per_kernel, config):
         peak = PEAK_TFLOPS["bf16"]
         bound, unit = "mfma", "TFLOP/s"
         extra = {"mfma_type": "bf16 (fp32 operands as three bf16 planes, six products each)",
-                 "fp32_equivalent": {"achieved": round(alg, 3), "peak": PEAK_TFLOPS["f32"],
-                                     "frac": round(alg / PEAK_TFLOPS["f32"], 4)}}
+                 "fp32_algorithmic_tflops": round(alg, 3)}
     elif kind == "flop":
         achieved = amount / sec / 1e12
         peak = PEAK_TFLOPS[runner.dtype]
@@ -373,13 +380,16 @@ def cpu_baseline(runner, target_s):
     # over each head also gives the GPU-vs-CPU difference)
     heads = [(b, h) for b in range(B) for h in range(H)]
     groups = []
-    for i in range(0, len(heads), 8):
-        grp = heads[i:i + 8]
+    per = max(1, min(8, int(8 * (1024 / T) ** 2)))  # T x T matrices of a group: ~8 at T = 1024
+    for i in range(0, len(heads), per):
+        grp = heads[i:i + per]
         for b in sorted({b for b, _ in grp}):
             hs = [h for bb, h in grp if bb == b]
             groups.append((b, hs[0], hs[-1] + 1))
     ref.attention_fwd_bwd(q[:1, :1], k[:1, :1], v[:1, :1], do[:1, :1], runner.scale)  # warm-up
     errs = {n: 0.0 for n in ("o", "dq", "dk", "dv")}
+    sq_diff = {n: 0.0 for n in errs}
+    sq_ref = {n: 0.0 for n in errs}
     dq_, dk_, dv_ = runner.head_major_grads()
     got = {"o": f(runner.o), "dq": f(dq_), "dk": f(dk_), "dv": f(dv_)}
     n_eval, t_cpu, gi = 0, 0.0, 0
@@ -391,12 +401,17 @@ def cpu_baseline(runner, target_s):
         t_cpu += time.perf_counter() - t0
         if gi < len(groups):
             for n in errs:
-                diff = (got[n][b:b + 1, h0:h1] - getattr(r, n)).abs().max().item()
-                errs[n] = max(errs[n], diff)
+                want = getattr(r, n).double()
+                diff = got[n][b:b + 1, h0:h1].double() - want
+                errs[n] = max(errs[n], diff.abs().max().item())
+                sq_diff[n] += float((diff * diff).sum())
+                sq_ref[n] += float((want * want).sum())
         n_eval += h1 - h0
         gi += 1
     compared = sum(h1 - h0 for _, h0, h1 in groups[:min(gi, len(groups))])
     flops = runner.flops_total() * n_eval / len(heads)
+    # rel-L2 as scripts/compare_parity.py:17 defines it, over the compared heads
+    rel = {n: math.sqrt(sq_diff[n]) / (math.sqrt(sq_ref[n]) + 1e-12) for n in errs}
     return {
         "value": round(flops / t_cpu / 1e12, 5),
         "unit": "TFLOP/s",
@@ -405,25 +420,50 @@ def cpu_baseline(runner, target_s):
         "sample": (f"{n_eval} (b,h)-head evaluations ({n_eval / len(heads):.2f} passes over "
                    f"the {len(heads)} heads of the same workload and inputs, T={T}, d={d}), "
                    f"torch {torch.__version__} CPU fp32 restatement of "
-                   f"pytorch_src/model.py:43-52 fwd + autograd bwd, {t_cpu:.1f} s; "
-                   f"{os.cpu_count()} host CPUs; GPU difference over {compared} heads"),
+                   f"pytorch_src/model.py:43-52 fwd + autograd bwd, {t_cpu:.1f} s"
+                   + (" on the bf16-rounded inputs widened to fp32" if runner.dtype == "bf16"
+                      else "")
+                   + f"; {os.cpu_count()} host CPUs; value = the sample's FLOPs (7*T^2*d per "
+                   f"head) / its CPU time, i.e. extrapolated to the whole workload at the "
+                   f"sampled per-head rate; GPU difference over {compared} heads"),
         "seconds": round(t_cpu, 2),
         "gpu_vs_cpu_max_abs": {n: float(f"{e:.3e}") for n, e in errs.items()},
+        "gpu_vs_cpu_rel_l2": {n: float(f"{e:.3e}") for n, e in rel.items()},
+        "heads_compared": compared,
     }
 
 
-def secondary(lib, cfg, dtype, steps, seed, path="packed", ramp_s=0.0):
+def parity_gate(dtype, cpu):
+    """The north star's gate on the GPU-vs-CPU comparison of the cpu_baseline leg: fp32
+    max-abs <= 1e-5 (scripts/compare_parity.py:108-109's tolerance), bf16 rel-L2 <= 2e-2,
+    for O, dQ, dK, dV."""
+    if cpu is None:
+        return {"checked": False, "pass": None}
+    if dtype == "bf16":
+        vals, tol, kind = cpu["gpu_vs_cpu_rel_l2"], 2e-2, "rel_l2"
+    else:
+        vals, tol, kind = cpu["gpu_vs_cpu_max_abs"], 1e-5, "max_abs"
+    return {"checked": True, "kind": kind, "tolerance": tol, "heads": cpu["heads_compared"],
+            "pass": all(v <= tol for v in vals.values())}
+
+
+def secondary(lib, cfg, dtype, steps, seed, path="packed", ramp_s=0.0, cpu_s=0.0):
     B, H, T, d, _, qk = CONFIGS[cfg]
     r = PathRunner(lib, B, H, T, d, dtype, seed, qk, path)
     wall, per_kernel = r.timed(steps, 3, ramp_s)
     ms = wall / steps * 1e3
     tf = r.flops_total() / (ms * 1e-3) / 1e12
     attn_ms = sum(ms_ for n, ms_ in per_kernel.items() if n in FLOP_UNITS)
+    dom, roof = roofline_of(r, per_kernel, cfg)
     out = {"config": cfg, "path": path, "shape": f"B{B} H{H} T{T} d{d}", "dtype": dtype,
            "ms_per_step": round(ms, 4), "tflops": round(tf, 2),
            "frac_mfma_peak": round(tf / PEAK_TFLOPS[dtype], 4),
            "attn_only_tflops": round(r.flops_total() / (attn_ms * 1e-3) / 1e12, 2),
+           "roofline": dict(roof, kernel=dom),
            "kernels": kernel_table(r, per_kernel), "finite": r.outputs_finite()}
+    if cpu_s > 0:
+        out["cpu_baseline"] = cpu_baseline(r, cpu_s)
+        out["parity_gate"] = parity_gate(dtype, out["cpu_baseline"])
     del r
     return out
 
@@ -591,6 +631,7 @@ def main():
         line["cpu_baseline"] = cpu_baseline(runner, args.cpu_seconds)
     else:
         line["cpu_baseline"] = None
+    line["parity_gate"] = parity_gate(dtype, line["cpu_baseline"])
     del runner
     torch.cuda.empty_cache()
     if not args.no_secondary:
@@ -600,14 +641,23 @@ def main():
         if dtype != "bf16":
             sec.append(secondary(lib, args.config, "bf16", args.secondary_steps, args.seed,
                                  ramp_s=args.ramp_s))
-        sec.append(secondary(lib, "c3", "bf16", args.secondary_steps, args.seed,
-                             ramp_s=args.ramp_s))
+        # the bf16 configurations, each with a CPU baseline on a bounded sample of its heads
+        cpu_s = 0.0 if args.no_cpu_baseline else args.secondary_cpu_seconds
+        for c in ("c3", "c4"):
+            if c != args.config:
+                sec.append(secondary(lib, c, "bf16", args.secondary_steps, args.seed,
+                                     ramp_s=args.ramp_s, cpu_s=cpu_s))
         sec.append(materialized(lib, max(3, args.secondary_steps // 4), args.seed))
         line["secondary"] = sec
     if args.gpt_steps > 0:
         line["training_step"] = [gpt_training_step(m, args.gpt_steps, 2, args.seed)
                                  for m in args.gpt_modes.split(",")]
     print(json.dumps(line), flush=True)
+    if line["parity_gate"]["pass"] is False:
+        print("bench.py: the GPU result fails the parity gate against the CPU restatement "
+              f"({line['parity_gate']}); the throughput line above is not valid",
+              file=sys.stderr)
+        return 3
     return 0
 
 

@@ -4,8 +4,16 @@
  *
  * Every entry point takes plain device pointers, int sizes, a float scale and a
  * hipStream_t (an opaque pointer; pass NULL for the null stream).  Nothing here
- * allocates device memory, synchronises the host, or keeps state between calls, so
- * every entry point may be captured into a HIP graph.  Work is enqueued on `stream`.
+ * allocates device memory or synchronises the host, and every entry point may be captured
+ * into a HIP graph.  Work is enqueued on `stream`.
+ *
+ * State the library holds on the device (fixed arrays, never allocated per call):
+ *   - the fp32 tiled kernels (attn_*_f32 forward and backward stages) pull tasks from
+ *     counters in one of 64 slots per kernel family, taken in turn by each ordinary launch
+ *     and left at zero when the launch ends; so at most 64 launches of one family may run
+ *     at the same time (on different streams).  A launch captured into a graph takes no
+ *     slot (it runs a static schedule), so replays of a graph, concurrent or not, share
+ *     nothing.  The results do not depend on the schedule (bitwise).
  *
  * Every entry point returns an attn_status.  Arguments are validated on the host
  * before anything is launched: a non-zero status means nothing was enqueued (except
@@ -118,6 +126,26 @@ int attn_matmul_batched_strided_f32(const float* A, const float* B, float* C, in
                                     int K, long long strideA, long long strideB,
                                     long long strideC, int batch_count, int transA, int transB,
                                     float alpha, float beta, hipStream_t stream);
+
+/* The handle of the strided-batched GEMM: the counterpart of the cublasHandle_t that the
+ * reference's matmul_batched_strided takes first (include/kernels/matmul.cuh:44-58, created at
+ * src/model.cu:16-23).  The GEMM keeps no state, so the handle only records the device that
+ * was current when it was created; a call through it while another device is current fails
+ * with ATTN_ERROR_INVALID_VALUE before anything is launched.  Host memory only. */
+typedef struct attn_gemm_context* attn_gemm_handle;
+/* Create a handle bound to the current device (ATTN_ERROR_LAUNCH if there is none). */
+int attn_gemm_create(attn_gemm_handle* handle);
+/* Destroy a handle (NULL is accepted and ignored). */
+int attn_gemm_destroy(attn_gemm_handle handle);
+/* Device ordinal the handle is bound to, or -1 for a NULL handle. */
+int attn_gemm_device(attn_gemm_handle handle);
+/* Replaces matmul_batched_strided with its handle argument, include/kernels/matmul.cuh:44-58:
+ * attn_matmul_batched_strided_f32 run through `handle` (ATTN_ERROR_NULL_POINTER if NULL). */
+int attn_matmul_batched_strided_f32_h(attn_gemm_handle handle, const float* A, const float* B,
+                                      float* C, int M, int N, int K, long long strideA,
+                                      long long strideB, long long strideC, int batch_count,
+                                      int transA, int transB, float alpha, float beta,
+                                      hipStream_t stream);
 
 /* The reference's materialised forward (src/model.cu:313-332), scores and probs (B*H*T, T):
  *   scores = Q K^T  ->  probs = causal_softmax_forward(scores, scale)  ->  out = probs V. */

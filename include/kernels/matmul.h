@@ -1,19 +1,46 @@
 // kernels/matmul.h - the strided-batched GEMM of the materialised attention mode, MI355X build.
 //
-// Reference: include/kernels/matmul.cuh:44 (matmul_batched_strided, implemented at
-// src/kernels/matmul.cu:167-207 with cublasSgemmStridedBatched).  Same parameters and
-// row-major semantics minus the cuBLAS handle: the library's GEMM is a stateless HIP kernel,
-// so there is no handle to create, bind to a stream or destroy.  Throws std::runtime_error
-// on a non-zero status.
+// Reference: include/kernels/matmul.cuh:44-58 (matmul_batched_strided, implemented at
+// src/kernels/matmul.cu:167-207 with cublasSgemmStridedBatched), called at
+// src/model.cu:314-332 and 618-650.  Same parameter list, order and defaults, row-major
+// semantics.  The leading handle is this library's gemm_handle_t (create it once with
+// gemm_create, as the reference's model creates its cuBLAS handle): the GEMM is a
+// stateless HIP kernel, so the handle only pins the device it was created on.  Throws
+// std::runtime_error on a non-zero status.
 #pragma once
 
 #include "kernels/attention.h"
 
-// C_b (M x N) = alpha * op(A_b) * op(B_b) + beta * C_b for b < batch_count (row-major).
+using gemm_handle_t = attn_gemm_handle;
+
+// Create / destroy a handle bound to the current device.
+inline void gemm_create(gemm_handle_t* handle) {
+    tcamd::check_status(attn_gemm_create(handle), "gemm_create");
+}
+inline void gemm_destroy(gemm_handle_t handle) {
+    tcamd::check_status(attn_gemm_destroy(handle), "gemm_destroy");
+}
+
+// C[i] = alpha * (op_A(A[i]) * op_B(B[i])) + beta * C[i] for i < batch_count (row-major),
+// the reference's declaration with its defaults.
+inline void matmul_batched_strided(gemm_handle_t handle, const float* A, const float* B,
+                                   float* C, int M, int N, int K, long long int strideA,
+                                   long long int strideB, long long int strideC,
+                                   int batch_count, bool transA = false, bool transB = false,
+                                   float alpha = 1.0f, float beta = 0.0f,
+                                   hipStream_t stream = nullptr) {
+    tcamd::check_status(
+        attn_matmul_batched_strided_f32_h(handle, A, B, C, M, N, K, strideA, strideB, strideC,
+                                          batch_count, transA ? 1 : 0, transB ? 1 : 0, alpha,
+                                          beta, stream),
+        "matmul_batched_strided");
+}
+
+// The same without a handle (the GEMM needs none).
 inline void matmul_batched_strided(const float* A, const float* B, float* C, int M, int N,
                                    int K, long long int strideA, long long int strideB,
-                                   long long int strideC, int batch_count, bool transA,
-                                   bool transB, float alpha, float beta,
+                                   long long int strideC, int batch_count, bool transA = false,
+                                   bool transB = false, float alpha = 1.0f, float beta = 0.0f,
                                    hipStream_t stream = nullptr) {
     tcamd::check_status(
         attn_matmul_batched_strided_f32(A, B, C, M, N, K, strideA, strideB, strideC,

@@ -81,29 +81,6 @@ def attention_fwd_bwd(q, k, v, do, scale: float, dtype=torch.float32, with_grad=
     return AttnResult(o=o.detach(), m=m, l=l, lse=lse, dq=dq, dk=dk, dv=dv)
 
 
-def attention_fwd_bwd_chunked(q, k, v, do, scale: float, dtype=torch.float32, chunk: int = 1):
-    """Same as attention_fwd_bwd, one (b, h) slice group at a time, to bound memory at
-    long T (the T x T matrices of one slice only).  Returns numpy arrays."""
-    B, H, T, d = q.shape
-    outs = {n: np.empty((B, H, T, d), np.float64 if dtype == torch.float64 else np.float32)
-            for n in ("o", "dq", "dk", "dv")}
-    stats = {n: np.empty((B, H, T), outs["o"].dtype) for n in ("m", "l", "lse")}
-    flat = [(b, h) for b in range(B) for h in range(H)]
-    for i in range(0, len(flat), chunk):
-        group = flat[i:i + chunk]
-        sel = lambda x: np.stack([np.asarray(x[b, h]) for b, h in group])[None]
-        r = attention_fwd_bwd(sel(q), sel(k), sel(v), sel(do), scale, dtype=dtype)
-        for j, (b, h) in enumerate(group):
-            outs["o"][b, h] = r.o[0, j].numpy()
-            outs["dq"][b, h] = r.dq[0, j].numpy()
-            outs["dk"][b, h] = r.dk[0, j].numpy()
-            outs["dv"][b, h] = r.dv[0, j].numpy()
-            stats["m"][b, h] = r.m[0, j].numpy()
-            stats["l"][b, h] = r.l[0, j].numpy()
-            stats["lse"][b, h] = r.lse[0, j].numpy()
-    return {**outs, **stats}
-
-
 # ----------------------------------------------------------------------------------------
 # Independent fp64 restatement with the analytic backward (numpy, no autograd).
 #   S = scale * Q K^T, P = softmax over j <= i, O = P V

@@ -97,6 +97,17 @@ def test_split_and_softmax_validation(lib):
                     None) == INVALID_DIM
 
 
+def test_gemm_handle_without_gpu(lib):
+    """The handle argument of matmul_batched_strided (include/kernels/matmul.cuh:44-58):
+    a NULL handle is rejected before anything else; creating one needs a current device."""
+    f = ctypes.c_float
+    assert lib.call("attn_matmul_batched_strided_f32_h", None, FAKE, FAKE, FAKE, 4, 4, 4, 16,
+                    16, 16, 2, 0, 1, f(1.0), f(0.0), None) == NULLPTR
+    assert lib.call("attn_gemm_create", None) == NULLPTR
+    assert lib.call("attn_gemm_destroy", None) == OK
+    assert lib.raw().attn_gemm_device(None) == -1
+
+
 def test_materialized_validation(lib):
     f = ctypes.c_float
     gemm = lambda A=FAKE, M=4, N=4, K=4, sA=16, batch=2, alpha=1.0, beta=0.0: lib.call(

@@ -119,3 +119,49 @@ def test_modes_agree_and_attention_timing(gpt):
     # for the token-embedding rows, whose scatter-add (repeated tokens) is atomic
     n_tok = s["V"] * s["C"]
     assert np.array_equal(out["tiled_split"][1][n_tok:], out["fused"][1][n_tok:])
+
+
+C5 = dict(V=50257, T=1024, C=768, L=12, H=12, d_ff=3072, B=8)
+
+
+def _host_cross_entropy(logits, targets):
+    """fp64 mean cross entropy of (B*T, V) fp32 logits (rows in chunks)."""
+    total = 0.0
+    tg = targets.reshape(-1)
+    for r0 in range(0, logits.shape[0], 512):
+        z = logits[r0:r0 + 512].astype(np.float64)
+        mx = z.max(axis=1, keepdims=True)
+        lse = mx[:, 0] + np.log(np.exp(z - mx).sum(axis=1))
+        total += float((lse - z[np.arange(z.shape[0]), tg[r0:r0 + 512]]).sum())
+    return total / logits.shape[0]
+
+
+def test_config5_full_shape_fused_and_x3(gpt):
+    """BASELINE config 5 at its own shape (GPT-2 small: L12 C768 H12 d_ff 3072, T 1024, B 8,
+    V 50257; N(0, 0.02) weights, uniform tokens and targets), the fp32 MFMA attention and the
+    three-plane attention: the loss equals the fp64 cross entropy of the GPU's own logits
+    (1e-5) and sits just above ln V (random logits of spread s give ln V + s^2/2, s ~ 0.5 here);
+    the two modes agree on the loss (1e-5) and on every gradient (5e-5); one clip + AdamW
+    step zeroes the gradients and moves the parameters."""
+    out = {}
+    for mode in ("fused_x3", "fused"):
+        model, flat, tokens, targets = make(gpt, C5, mode, seed=21)
+        assert model.n_params == flat.size == 163_037_184
+        loss, grads = run_fb(model, tokens, targets)
+        assert np.isfinite(loss) and np.isfinite(grads).all(), mode
+        logits = model.logits().reshape(C5["B"] * C5["T"], C5["V"])
+        want = _host_cross_entropy(logits, targets)
+        assert abs(loss - want) <= 1e-5, (mode, loss, want)
+        del logits
+        assert np.log(C5["V"]) - 0.01 <= loss <= np.log(C5["V"]) + 0.3, (mode, loss)
+        out[mode] = (loss, grads)
+        if mode == "fused":
+            model.optimizer_step()
+            torch.cuda.synchronize()
+            assert not model.gradients().any(), "gradients not zeroed by the optimizer step"
+            moved = np.abs(model.parameters() - flat)
+            assert moved.max() > 0 and np.isfinite(moved).all()
+        model.close()
+    assert abs(out["fused_x3"][0] - out["fused"][0]) <= 1e-5
+    err = np.abs(out["fused_x3"][1] - out["fused"][1])
+    assert err.max() <= 5e-5, f"grad max-abs {err.max():.3e} at flat index {int(err.argmax())}"

@@ -190,3 +190,99 @@ def test_c1_fixture_is_consistent_with_oracle():
         scale = np.abs(an[n]).max()
         np.testing.assert_allclose(f[n], an[n], atol=1e-6 * scale + 1e-12)
     assert abs(float(f["loss"]) - math.log(256)) < 0.1  # untrained model: loss ~ ln V
+
+
+# --------------------------------------------------------------- parity metrics (the gate)
+def _metric_pin_failures(metrics):
+    """Closed-form checks of the parity metrics of scripts/compare_parity.py:11-26
+    (max, mean and RMS of |a - b|, rel = ||a - b||_2 / (||b||_2 + 1e-12)); returns the
+    names of the checks that `metrics` fails."""
+    failed = []
+
+    def close(x, y, rtol=1e-12):
+        return math.isclose(x, y, rel_tol=rtol, abs_tol=0.0)
+
+    b = _rand((3, 5, 7), 50)
+    m = metrics(b.copy(), b)
+    if any(m[n] != 0.0 for n in ("max_err", "mean_err", "rms_err", "rel_err")):
+        failed.append("a == b gives zeros")
+    if m["elements"] != b.size:
+        failed.append("element count")
+    # a = b (1 + e): |a - b| = e |b| elementwise, so rel = e and max/mean/RMS scale |b|'s
+    e = 0.03125
+    m = metrics(b * (1 + e), b)
+    nb = float(np.linalg.norm(b.ravel()))
+    if not close(m["rel_err"], e * nb / (nb + 1e-12), 1e-12):
+        failed.append("relative perturbation gives rel = e")
+    if not close(m["max_err"], e * float(np.abs(b).max())):
+        failed.append("relative perturbation max")
+    if not close(m["mean_err"], e * float(np.abs(b).mean())):
+        failed.append("relative perturbation mean")
+    if not close(m["rms_err"], e * float(np.sqrt((b ** 2).mean()))):
+        failed.append("relative perturbation rms")
+    # one element off by delta among n
+    n = b.size
+    a = b.copy()
+    a[1, 2, 3] += 0.5
+    m = metrics(a, b)
+    if not (close(m["max_err"], 0.5, 1e-12) and close(m["mean_err"], 0.5 / n, 1e-9) and
+            close(m["rms_err"], 0.5 / math.sqrt(n), 1e-9) and
+            close(m["rel_err"], 0.5 / (nb + 1e-12), 1e-9)):
+        failed.append("single perturbed element")
+    # hand vector: |a - b| = (0, 2, 0, 4)
+    m = metrics(np.array([1.0, 2.0, 3.0, 4.0]), np.array([1.0, 0.0, 3.0, 8.0]))
+    if not (m["max_err"] == 4.0 and m["mean_err"] == 1.5 and close(m["rms_err"], math.sqrt(5.0))
+            and close(m["rel_err"], math.sqrt(20.0) / (math.sqrt(74.0) + 1e-12))):
+        failed.append("hand vector")
+    # b = 0: rel = ||a|| / 1e-12 (the guard term), finite
+    a = np.array([3.0, 4.0])
+    m = metrics(a, np.zeros(2))
+    if not (np.isfinite(m["rel_err"]) and close(m["rel_err"], 5.0 / 1e-12, 1e-9)):
+        failed.append("zero reference")
+    # normalised by the second argument (the reference tensor), not the first
+    x, y = np.array([1.0, 1.0]), np.array([2.0, 2.0])
+    if not (close(metrics(x, y)["rel_err"], math.sqrt(2.0) / (math.sqrt(8.0) + 1e-12)) and
+            close(metrics(y, x)["rel_err"], math.sqrt(2.0) / (math.sqrt(2.0) + 1e-12))):
+        failed.append("normalised by b")
+    # signs cancel in nothing: |a - b| of mixed signs
+    m = metrics(np.array([1.0, -1.0]), np.array([0.0, 0.0]) + np.array([2.0, -2.0]))
+    if not close(m["mean_err"], 1.0):
+        failed.append("absolute differences")
+    return failed
+
+
+def test_parity_metrics_closed_forms():
+    assert _metric_pin_failures(ref.compute_metrics) == []
+
+
+def _mutant_metrics(kind):
+    def metrics(a, b):
+        a = np.asarray(a, dtype=np.float64)
+        b = np.asarray(b, dtype=np.float64)
+        diff = a - b if kind == "signed_diff" else np.abs(a - b)
+        denom = np.linalg.norm((a if kind == "norm_of_a" else b).ravel())
+        num = np.linalg.norm(diff.ravel())
+        if kind == "max_for_norm":
+            num = np.abs(diff).max()
+        if kind == "squared_norm":
+            num, denom = num ** 2, denom ** 2
+        rms = np.sqrt((diff ** 2).mean())
+        if kind == "rms_without_sqrt":
+            rms = (diff ** 2).mean()
+        return {
+            "max_err": float(np.abs(diff).max()),
+            "mean_err": float(diff.mean()),
+            "rms_err": float(rms),
+            "rel_err": float(num / (denom + (0.0 if kind == "no_guard" else 1e-12))),
+            "elements": int(a.size),
+        }
+    return metrics
+
+
+@pytest.mark.parametrize("kind", ["norm_of_a", "max_for_norm", "squared_norm", "rms_without_sqrt",
+                                  "signed_diff", "no_guard"])
+def test_parity_metrics_planted_mistake_is_caught(kind):
+    """Each plausible slip in a copy of the metric function fails a closed-form pin."""
+    with np.errstate(divide="ignore", invalid="ignore"):
+        failed = _metric_pin_failures(_mutant_metrics(kind))
+    assert failed, f"planted metric mistake {kind!r} passed every pin"

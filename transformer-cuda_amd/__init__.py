@@ -55,6 +55,11 @@ SIGNATURES = {
     "attn_causal_softmax_backward_f32": [_P, _P, _P, _I, _I, _I, _F, _P],
     "attn_matmul_batched_strided_f32":
         [_P, _P, _P, _I, _I, _I, _L, _L, _L, _I, _I, _I, _F, _F, _P],
+    "attn_gemm_create": [_P],
+    "attn_gemm_destroy": [_P],
+    "attn_gemm_device": [_P],
+    "attn_matmul_batched_strided_f32_h":
+        [_P, _P, _P, _P, _I, _I, _I, _L, _L, _L, _I, _I, _I, _F, _F, _P],
     "attn_materialized_causal_forward_f32": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P],
     "attn_packed_causal_forward_f32": [_P, _P, _I, _I, _I, _I, _F, _P, _P, _P],
     "attn_packed_causal_backward_f32": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P],

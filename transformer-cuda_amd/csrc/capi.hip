@@ -2,13 +2,25 @@
 //
 // Each entry point validates its arguments on the host and returns a status before any
 // HIP call, so the validation is testable on a machine without a GPU.  Only then does it
-// enqueue the kernels and report the launch status.  Nothing here allocates, synchronises
-// or keeps state.
+// enqueue the kernels and report the launch status.  Nothing here allocates or
+// synchronises.
 #include <math.h>
 #include <stdint.h>
 
 #include "../../include/attn_capi.h"
 #include "launch.hpp"
+
+namespace tcamd {
+namespace {
+thread_local bool t_launch_failed = false;
+}  // namespace
+void note_launch_failure() { t_launch_failed = true; }
+bool take_launch_failure() {
+    const bool f = t_launch_failed;
+    t_launch_failed = false;
+    return f;
+}
+}  // namespace tcamd
 
 namespace {
 
@@ -59,10 +71,14 @@ int check_materialized(int B, int H, int T, int d, float scale) {
 
 int launch_status() {
     const hipError_t e = hipGetLastError();
-    return e == hipSuccess ? ATTN_SUCCESS : ATTN_ERROR_LAUNCH;
+    const bool failed = tcamd::take_launch_failure();
+    return e == hipSuccess && !failed ? ATTN_SUCCESS : ATTN_ERROR_LAUNCH;
 }
 
-void clear_error() { (void)hipGetLastError(); }
+void clear_error() {
+    (void)hipGetLastError();
+    (void)tcamd::take_launch_failure();
+}
 
 int split_common(const void* rm, ElemType rm_t, void* q, void* k, void* v, ElemType h_t,
                  bool to_heads, int B, int T, int H, int d, hipStream_t stream) {
@@ -513,6 +529,45 @@ int attn_matmul_batched_strided_f32(const float* A, const float* B, float* C, in
     tcamd::launch_batched_gemm_f32(A, B, C, M, N, K, strideA, strideB, strideC, batch_count,
                                    transA != 0, transB != 0, alpha, beta, stream);
     return launch_status();
+}
+
+struct attn_gemm_context {
+    int device;
+};
+
+int attn_gemm_create(attn_gemm_handle* handle) {
+    if (handle == nullptr) return ATTN_ERROR_NULL_POINTER;
+    *handle = nullptr;
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0) {
+        (void)hipGetLastError();
+        return ATTN_ERROR_LAUNCH;
+    }
+    *handle = new attn_gemm_context{dev};
+    return ATTN_SUCCESS;
+}
+
+int attn_gemm_destroy(attn_gemm_handle handle) {
+    delete handle;
+    return ATTN_SUCCESS;
+}
+
+int attn_gemm_device(attn_gemm_handle handle) { return handle == nullptr ? -1 : handle->device; }
+
+int attn_matmul_batched_strided_f32_h(attn_gemm_handle handle, const float* A, const float* B,
+                                      float* C, int M, int N, int K, long long strideA,
+                                      long long strideB, long long strideC, int batch_count,
+                                      int transA, int transB, float alpha, float beta,
+                                      hipStream_t stream) {
+    if (handle == nullptr) return ATTN_ERROR_NULL_POINTER;
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess) {
+        (void)hipGetLastError();
+        return ATTN_ERROR_LAUNCH;
+    }
+    if (dev != handle->device) return ATTN_ERROR_INVALID_VALUE;
+    return attn_matmul_batched_strided_f32(A, B, C, M, N, K, strideA, strideB, strideC,
+                                           batch_count, transA, transB, alpha, beta, stream);
 }
 
 int attn_materialized_causal_forward_f32(const float* q, const float* k, const float* v,

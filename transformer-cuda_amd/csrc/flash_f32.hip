@@ -301,8 +301,9 @@ __device__ __forceinline__ void wave_range(int n, int wave, int& t0, int& t1) {
 struct Fetch {
     const TaskQueue* q;  // non-null only for the fetching wave
     unsigned value;
+    unsigned cur;        // the task being processed
     __device__ __forceinline__ void issue(int lane) {
-        if (q != nullptr && lane == 0) value = q->fetch();
+        if (q != nullptr && lane == 0) value = q->fetch(cur);
     }
 };
 
@@ -417,7 +418,7 @@ TCAMD_F32_KERNEL(kFwdWaves) void flash_fwd_f32_kernel(
 
         float qreg[D / 2];
         load_row_half<D>(qreg, q + xoff, qi, T, half, xv.row);
-        Fetch fetch{wave == 0 ? &tq : nullptr, 0u};
+        Fetch fetch{wave == 0 ? &tq : nullptr, 0u, task};
         f32x16 acc[D / 32];
         float m_raw, l_i;
         fwd_chunk<D>(k + xoff, v + xoff, T, xv.row, c, qb, t0, t1, qreg, L[wave], lane, fetch,
@@ -605,7 +606,7 @@ TCAMD_F32_KERNEL(kDqWaves) void flash_bwd_dq_f32_kernel(
         const float lse2 =
             row_ok ? fmaf(m[stat_off + qi], kLog2e, __builtin_amdgcn_logf(l[stat_off + qi]))
                    : INFINITY;
-        Fetch fetch{wave == 0 ? &tq : nullptr, 0u};
+        Fetch fetch{wave == 0 ? &tq : nullptr, 0u, task};
         f32x16 acc[D / 32];
         dq_chunk<D>(k + xoff, v + xoff, T, xv.row, c, lse2, Dval, qb, t0, t1, qreg, doreg,
                     L[wave], lane, fetch, kc, acc);
@@ -758,7 +759,7 @@ TCAMD_F32_KERNEL(kDkdvWaves) void flash_bwd_dkdv_f32_kernel(
         float vreg[D / 2];
         load_row_half<D>(kreg, k + xoff, kj, T, half, xv.row);
         load_row_half<D>(vreg, v + xoff, kj, T, half, xv.row);
-        Fetch fetch{wave == 0 ? &tq : nullptr, 0u};
+        Fetch fetch{wave == 0 ? &tq : nullptr, 0u, task};
         f32x16 dk_acc[D / 32], dv_acc[D / 32];
         dkdv_chunk<D>(q + xoff, dO + ooff, m, l, Dws, stat_off, T, xv.row, ov.row, c, kb, kb + t0,
                       kb + t1, kreg, vreg, L[wave], lane, fetch, tc, dk_acc, dv_acc);
@@ -827,12 +828,29 @@ QueueSlot* queue_base(Family f) {
     return p;
 }
 
+// The queue slot of a launch of family f on `stream`: null (static schedule) under graph
+// capture.  Sets `ok` to false if the queue array's address cannot be found; the caller
+// then launches nothing and the C ABI reports a launch error.
+QueueSlot* launch_slot(Family f, std::atomic<unsigned>& ticket, hipStream_t stream, bool& ok) {
+    ok = true;
+    if (stream_is_capturing(stream)) return nullptr;
+    QueueSlot* base = queue_base(f);
+    if (base == nullptr) {
+        ok = false;
+        note_launch_failure();
+        return nullptr;
+    }
+    return base + next_queue_slot(ticket);
+}
+
 template <int D>
 void fwd_dispatch(const float* q, const float* k, const float* v, float* o, float* m_out,
                   float* l_out, int BH, int T, float scale, const HeadView& xv,
                   const HeadView& ov, hipStream_t stream) {
     const int nqb = (T + kTile - 1) / kTile;
-    QueueSlot* slot = queue_base(Family::Fwd) + next_queue_slot(g_fwd_ticket);
+    bool ok = true;
+    QueueSlot* slot = launch_slot(Family::Fwd, g_fwd_ticket, stream, ok);
+    if (!ok) return;
     const int grid = persistent_grid(flash_fwd_f32_kernel<D>, kWave * kFwdWaves, 0,
                                      static_cast<long long>(BH) * nqb);
     hipLaunchKernelGGL(flash_fwd_f32_kernel<D>, dim3(grid), dim3(kWave * kFwdWaves), 0, stream, q, k, v, o,
@@ -845,7 +863,9 @@ void dq_dispatch(const float* q, const float* k, const float* v, const float* o,
                  int T, float scale, const HeadView& xv, const HeadView& ov, const HeadView& gv,
                  hipStream_t stream) {
     const int nqb = (T + kTile - 1) / kTile;
-    QueueSlot* slot = queue_base(Family::Dq) + next_queue_slot(g_dq_ticket);
+    bool ok = true;
+    QueueSlot* slot = launch_slot(Family::Dq, g_dq_ticket, stream, ok);
+    if (!ok) return;
     const int grid = persistent_grid(flash_bwd_dq_f32_kernel<D>, kWave * kDqWaves, 0,
                                      static_cast<long long>(BH) * nqb);
     hipLaunchKernelGGL(flash_bwd_dq_f32_kernel<D>, dim3(grid), dim3(kWave * kDqWaves), 0, stream, q, k, v,
@@ -859,7 +879,9 @@ void dkdv_dispatch(const float* q, const float* k, const float* v, const float* 
                    int BH, int T, float scale, const HeadView& xv, const HeadView& ov,
                    const HeadView& gv, hipStream_t stream) {
     const int nkb = (T + kTile - 1) / kTile;
-    QueueSlot* slot = queue_base(Family::Dkdv) + next_queue_slot(g_dkdv_ticket);
+    bool ok = true;
+    QueueSlot* slot = launch_slot(Family::Dkdv, g_dkdv_ticket, stream, ok);
+    if (!ok) return;
     const int grid = persistent_grid(flash_bwd_dkdv_f32_kernel<D>, kWave * kDkdvWaves, 0,
                                      static_cast<long long>(BH) * nkb);
     hipLaunchKernelGGL(flash_bwd_dkdv_f32_kernel<D>, dim3(grid), dim3(kWave * kDkdvWaves), 0, stream, q, k,

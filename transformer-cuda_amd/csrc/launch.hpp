@@ -9,6 +9,11 @@
 
 namespace tcamd {
 
+// A launcher that found it could not launch (and enqueued nothing) records that here; the
+// C ABI's status check reports it as ATTN_ERROR_LAUNCH and clears it.  Per host thread.
+void note_launch_failure();
+bool take_launch_failure();
+
 enum class ElemType { F32, BF16 };
 
 // Row-major (B, T, S, H, d) <-> S head-major tensors (B, H, T, d).  S = 3 for the QKV

@@ -20,6 +20,12 @@
 // resets its counter, so a slot is clean for its next use.  Launches that execute
 // concurrently (different streams) therefore must not share a slot: up to kQueueSlots
 // launches of one kernel family may be in flight at once.
+//
+// A launch captured into a HIP graph takes no slot: a graph would replay the one slot it
+// captured, and two replays running at the same time (or an ordinary launch whose ticket
+// wraps onto that slot) would share its counter.  Captured launches use the static
+// schedule instead (slot = null): worker w runs tasks w, w + W, w + 2W, ... of the same
+// heaviest-first order.  It keeps no state, and the output does not depend on the schedule.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -59,7 +65,7 @@ struct TaskQueue {
     __device__ static TaskQueue bind(QueueSlot* slot, int BH, int nb, bool per_xcd) {
         TaskQueue q;
         const int x = per_xcd ? static_cast<int>(blockIdx.x % kXcds) : 0;
-        q.next = &slot->next[x].v;
+        q.next = slot != nullptr ? &slot->next[x].v : nullptr;  // null: static schedule
         q.heads_per_queue = per_xcd ? BH / kXcds : BH;
         q.head_base = x * q.heads_per_queue;
         q.n_tasks = static_cast<unsigned>(q.heads_per_queue) * static_cast<unsigned>(nb);
@@ -68,8 +74,10 @@ struct TaskQueue {
         return q;
     }
     __device__ unsigned first() const { return worker; }
-    // Next task index of this worker (one thread of the workgroup calls it).
-    __device__ unsigned fetch() const {
+    // Next task index of this worker after task `cur` (one thread of the workgroup calls
+    // it).  Static schedule: cur + n_workers.
+    __device__ unsigned fetch(unsigned cur) const {
+        if (next == nullptr) return cur + n_workers;
         const unsigned c = atomicAdd(next, 1u);
         if (c + 1u == n_tasks) atomicExch(next, 0u);
         return n_workers + c;
@@ -84,6 +92,18 @@ struct TaskQueue {
 // Host side: the slot of the next launch of a kernel family.
 inline unsigned next_queue_slot(std::atomic<unsigned>& ticket) {
     return ticket.fetch_add(1u, std::memory_order_relaxed) % kQueueSlots;
+}
+
+// Host side: whether work enqueued on `stream` is being captured into a graph (then the
+// launch uses the static schedule).  If the query itself fails, the static schedule is
+// taken: it is correct in every case.
+inline bool stream_is_capturing(hipStream_t stream) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &st) != hipSuccess) {
+        (void)hipGetLastError();
+        return true;
+    }
+    return st != hipStreamCaptureStatusNone;
 }
 
 // Host side: persistent grid size: every resident workgroup slot of the device, a multiple

@@ -66,8 +66,10 @@ int main(int argc, char** argv) {
     cfg.attention_mode = mode;
     std::cout << "[Parity Audit] Loading config: B=" << B << ", T=" << T << ", C=" << C
               << ", L=" << L << ", H=" << H << ", V=" << V << ", attention="
-              << (mode == GPT_ATTN_FUSED ? "fused" : mode == GPT_ATTN_TILED_SPLIT ? "tiled"
-                                                                                  : "materialized")
+              << (mode == GPT_ATTN_FUSED          ? "fused"
+                  : mode == GPT_ATTN_FUSED_X3     ? "fused_x3"
+                  : mode == GPT_ATTN_TILED_SPLIT  ? "tiled"
+                                                  : "materialized")
               << "\n";
     gpt_model* model = nullptr;
     int st = gpt_create(&cfg, &model);

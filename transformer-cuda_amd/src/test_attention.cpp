@@ -12,6 +12,10 @@
 //   * the packed launchers (attention straight from qkv, gradient straight into dqkv) equal
 //     split + tiled + split-back bitwise, and the fused launchers (output and its gradient in
 //     the merged-heads layout) equal them with the head merge applied;
+//   * the materialised mode driven with the reference's own call text (src/model.cu:314-332,
+//     618-650: a GEMM handle first, then the matmul.cuh:44-58 parameter list) equals the
+//     library's materialised sequences bitwise, and the defaults of matmul_batched_strided
+//     (no transposes, alpha 1, beta 0) equal the explicit arguments;
 //   * an unsupported head dimension throws instead of silently doing nothing.
 // Exit status 0 iff every test passes.
 #include <cmath>
@@ -22,6 +26,7 @@
 
 #include "common.h"
 #include "kernels/attention.h"
+#include "kernels/matmul.h"
 
 namespace {
 
@@ -229,6 +234,117 @@ bool test_packed_matches_split(int d, int T) {
     return true;
 }
 
+// The reference's layer buffers, by the member names src/model.cu uses (include/model.h:42-49,
+// 84-93).
+struct LayerActs {
+    float *q, *k, *v, *attn_scores, *attn_probs, *attn_out;
+};
+struct LayerGrads {
+    float *d_attn_out, *d_attn_probs, *d_attn_scores, *d_q, *d_k, *d_v;
+};
+
+bool test_materialized_reference_call_text() {
+    std::printf("[Test] materialised mode through the reference's call text == library sequences...\n");
+    const int B = 2, H = 3, T = 70, d_head = 64;
+    const size_t n = static_cast<size_t>(B) * H * T * d_head;
+    const size_t nn = static_cast<size_t>(B) * H * T * T;
+    const float scale = 1.0f / std::sqrt(static_cast<float>(d_head));
+    uint32_t state = 4242u;
+    auto next = [&state]() {
+        state = state * 1664525u + 1013904223u;
+        return static_cast<float>(static_cast<int>(state >> 9) % 2001 - 1000) / 700.0f;
+    };
+    std::vector<float> hq(n), hk(n), hv(n), hdo(n);
+    for (auto* h : {&hq, &hk, &hv, &hdo})
+        for (auto& x : *h) x = next();
+    DevBuf q(n), k(n), v(n), dO(n), s1(nn), p1(nn), o1(n), dp1(nn), ds1(nn), dq1(n), dk1(n),
+        dv1(n), s2(nn), p2(nn), o2(n), dp2(nn), ds2(nn), dq2(n), dk2(n), dv2(n), dv3(n);
+    q.upload(hq);
+    k.upload(hk);
+    v.upload(hv);
+    dO.upload(hdo);
+    gemm_handle_t cublas_handle = nullptr;
+    gemm_create(&cublas_handle);
+    hipStream_t stream = nullptr;
+    LayerActs la{q.p, k.p, v.p, s1.p, p1.p, o1.p};
+    LayerGrads grads{dO.p, dp1.p, ds1.p, dq1.p, dk1.p, dv1.p};
+    // src/model.cu:314-332, verbatim apart from the buffers' owners
+    matmul_batched_strided(
+        cublas_handle,
+        la.q, la.k, la.attn_scores,
+        T, T, d_head,
+        T * d_head, T * d_head, T * T,
+        B * H, false, true, 1.0f, 0.0f, stream
+    );
+    causal_softmax_forward(la.attn_scores, la.attn_probs, B, H, T, scale, stream);
+    matmul_batched_strided(
+        cublas_handle,
+        la.attn_probs, la.v, la.attn_out,
+        T, d_head, T,
+        T * T, T * d_head, T * d_head,
+        B * H, false, false, 1.0f, 0.0f, stream
+    );
+    // src/model.cu:618-650
+    matmul_batched_strided(
+        cublas_handle,
+        grads.d_attn_out, la.v, grads.d_attn_probs,
+        T, T, d_head,
+        T * d_head, T * d_head, T * T,
+        B * H, false, true, 1.0f, 0.0f, stream
+    );
+    matmul_batched_strided(
+        cublas_handle,
+        la.attn_probs, grads.d_attn_out, grads.d_v,
+        T, d_head, T,
+        T * T, T * d_head, T * d_head,
+        B * H, true, false, 1.0f, 0.0f, stream
+    );
+    causal_softmax_backward(grads.d_attn_probs, la.attn_probs, grads.d_attn_scores, B, H, T, scale, stream);
+    matmul_batched_strided(
+        cublas_handle,
+        grads.d_attn_scores, la.k, grads.d_q,
+        T, d_head, T,
+        T * T, T * d_head, T * d_head,
+        B * H, false, false, 1.0f, 0.0f, stream
+    );
+    matmul_batched_strided(
+        cublas_handle,
+        grads.d_attn_scores, la.q, grads.d_k,
+        T, d_head, T,
+        T * T, T * d_head, T * d_head,
+        B * H, true, false, 1.0f, 0.0f, stream
+    );
+    // defaults: no transposes, alpha 1, beta 0, null stream
+    matmul_batched_strided(cublas_handle, la.attn_probs, la.v, dv3.p, T, d_head, T, T * T,
+                           T * d_head, T * d_head, B * H);
+    materialized_causal_attention_forward(q.p, k.p, v.p, s2.p, p2.p, o2.p, B, H, T, d_head, scale);
+    materialized_causal_attention_backward(q.p, k.p, v.p, p2.p, dO.p, dp2.p, ds2.p, dq2.p, dk2.p,
+                                           dv2.p, B, H, T, d_head, scale);
+    HIP_CHECK(hipDeviceSynchronize());
+    EXPECT(attn_gemm_device(cublas_handle) >= 0, "handle not bound to a device");
+    gemm_destroy(cublas_handle);
+    const std::pair<const DevBuf*, const DevBuf*> pairs[] = {
+        {&s1, &s2}, {&p1, &p2}, {&o1, &o2}, {&dp1, &dp2}, {&ds1, &ds2},
+        {&dq1, &dq2}, {&dk1, &dk2}, {&dv1, &dv2}, {&o1, &dv3}};
+    const char* names[] = {"scores", "probs", "out", "dprobs", "dscores", "dq", "dk", "dv",
+                           "defaults (probs V)"};
+    for (int t = 0; t < 9; ++t) {
+        const auto a = pairs[t].first->download(), b = pairs[t].second->download();
+        for (size_t i = 0; i < a.size(); ++i)
+            EXPECT(std::isfinite(a[i]) && a[i] == b[i], "%s[%zu]: call text %.9g, library %.9g",
+                   names[t], i, a[i], b[i]);
+    }
+    bool threw = false;
+    try {
+        matmul_batched_strided(static_cast<gemm_handle_t>(nullptr), la.q, la.k, la.attn_scores,
+                               T, T, d_head, T * d_head, T * d_head, T * T, B * H, false, true);
+    } catch (const std::runtime_error&) {
+        threw = true;
+    }
+    EXPECT(threw, "a null GEMM handle did not throw");
+    return true;
+}
+
 bool test_bad_head_dim() {
     std::printf("[Test] unsupported d_head is an error, not a silent no-op...\n");
     DevBuf buf(1024);
@@ -257,6 +373,7 @@ int main() {
     test_split_roundtrip();
     test_packed_matches_split(64, 77);
     test_packed_matches_split(128, 130);
+    test_materialized_reference_call_text();
     test_bad_head_dim();
     if (g_failures == 0) {
         std::printf("All host tests passed.\n");

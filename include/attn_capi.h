@@ -13,7 +13,9 @@
  *     and left at zero when the launch ends; so at most 64 launches of one family may run
  *     at the same time (on different streams).  A launch captured into a graph takes no
  *     slot (it runs a static schedule), so replays of a graph, concurrent or not, share
- *     nothing.  The results do not depend on the schedule (bitwise).
+ *     nothing.  The results do not depend on the schedule (bitwise);
+ *   - attn_tiled_causal_backward_f32_noalloc keeps D in a scratch array shared by every
+ *     call on the same GPU (see there).
  *
  * Every entry point returns an attn_status.  Arguments are validated on the host
  * before anything is launched: a non-zero status means nothing was enqueued (except
@@ -48,7 +50,9 @@ typedef enum attn_status {
     ATTN_ERROR_MISALIGNED = 4,           /* a pointer the kernel reads 16 bytes at a time is  */
                                          /* not 16-byte aligned                               */
     ATTN_ERROR_LAUNCH = 5,               /* hipGetLastError() after the launch was not success */
-    ATTN_ERROR_INVALID_VALUE = 6         /* scale not finite and > 0, batch count <= 0, ...   */
+    ATTN_ERROR_INVALID_VALUE = 6,        /* scale not finite and > 0, batch count <= 0, ...   */
+    ATTN_ERROR_SCRATCH_LIMIT = 7         /* no-alloc entry point: the problem needs more than */
+                                         /* the library's fixed device scratch               */
 } attn_status;
 
 /* Human-readable name of a status code (static storage, never NULL). */
@@ -189,6 +193,21 @@ int attn_tiled_causal_backward_f32(const float* q, const float* k, const float* 
                                    const float* l_ptr, float* dq, float* dk, float* dv,
                                    float* d_workspace, int B, int H, int T, int d_head,
                                    float scale, hipStream_t stream);
+
+/* No counterpart in the reference.  For callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc): the same
+ * backward as attn_tiled_causal_backward_f32, bitwise, without the caller's d_workspace.
+ * D (B*H*T floats) goes to a fixed scratch array in device memory that the library holds on
+ * each GPU it runs on until the process ends (ATTN_NOALLOC_SCRATCH_FLOATS floats, 16 MiB);
+ * B*H*T above that fails with ATTN_ERROR_SCRATCH_LIMIT before anything is enqueued.  Nothing
+ * is allocated.  Every call on one GPU shares that GPU's scratch, so calls that overlap in
+ * time on one GPU (other streams, other host threads) race: serialise them. */
+#define ATTN_NOALLOC_SCRATCH_FLOATS (1 << 22)
+int attn_tiled_causal_backward_f32_noalloc(const float* q, const float* k, const float* v,
+                                           const float* o, const float* do_ptr,
+                                           const float* m_ptr, const float* l_ptr, float* dq,
+                                           float* dk, float* dv, int B, int H, int T,
+                                           int d_head, float scale, hipStream_t stream);
 
 /* Stage 1 of attn_tiled_causal_backward_f32 (query-parallel): computes
  * D = rowsum(dO*O) into d_workspace and dq = scale * sum_j dS_ij k_j.

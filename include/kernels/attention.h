@@ -82,6 +82,21 @@ inline void tiled_causal_attention_backward(const float* q, const float* k, cons
         "tiled_causal_attention_backward");
 }
 
+// No counterpart in the reference: tiled_causal_attention_backward without d_workspace, for
+// callers that cannot allocate (D lives in the library's fixed device scratch; B*H*T up to
+// ATTN_NOALLOC_SCRATCH_FLOATS; calls that overlap in time on one GPU race).
+inline void tiled_causal_attention_backward_noalloc(const float* q, const float* k,
+                                                    const float* v, const float* o,
+                                                    const float* do_ptr, const float* m_ptr,
+                                                    const float* l_ptr, float* dq, float* dk,
+                                                    float* dv, int B, int H, int T, int d_head,
+                                                    float scale, hipStream_t stream = nullptr) {
+    tcamd::check_status(
+        attn_tiled_causal_backward_f32_noalloc(q, k, v, o, do_ptr, m_ptr, l_ptr, dq, dk, dv, B,
+                                               H, T, d_head, scale, stream),
+        "tiled_causal_attention_backward_noalloc");
+}
+
 // dscores = scale * probs * (dprobs - sum(dprobs * probs)) for j <= i, else 0.
 // Reference: include/kernels/attention.cuh:80-89.
 inline void causal_softmax_backward(const float* dprobs, const float* probs, float* dscores,

@@ -14,7 +14,7 @@ CAPI = os.path.join(REPO, "include", "attn_capi.h")
 FAKE = 0x10000  # never dereferenced: every call below fails validation before launching
 MISALIGNED = 0x10004
 
-OK, INVALID_DIM, BAD_HEAD_DIM, NULLPTR, MISALIGN, LAUNCH, BAD_VALUE = range(7)
+OK, INVALID_DIM, BAD_HEAD_DIM, NULLPTR, MISALIGN, LAUNCH, BAD_VALUE, SCRATCH_LIMIT = range(8)
 
 
 def declared_symbols():
@@ -45,7 +45,7 @@ def test_binding_covers_header(lib):
 
 def test_status_strings(lib):
     assert lib.status_string(0) == "success"
-    for s in range(1, 7):
+    for s in range(1, 8):
         assert lib.status_string(s) not in ("success", "unknown status")
     assert lib.status_string(99) == "unknown status"
     assert lib.raw().attn_version() >= 100
@@ -106,6 +106,28 @@ def test_gemm_handle_without_gpu(lib):
     assert lib.call("attn_gemm_create", None) == NULLPTR
     assert lib.call("attn_gemm_destroy", None) == OK
     assert lib.raw().attn_gemm_device(None) == -1
+
+
+def test_noalloc_backward_validation(lib):
+    """attn_tiled_causal_backward_f32_noalloc checks its arguments, and the size against its
+    fixed scratch, before it looks anything up on a device."""
+    f = ctypes.c_float
+    call = lambda *p, B=1, H=1, T=8, d=64, scale=0.125: lib.call(
+        "attn_tiled_causal_backward_f32_noalloc", *p, B, H, T, d, f(scale), None)
+    ten = [FAKE] * 10
+    for i in range(10):
+        args = list(ten)
+        args[i] = None
+        assert call(*args) == NULLPTR
+    assert call(*ten, d=48) == BAD_HEAD_DIM
+    assert call(*ten, T=0) == INVALID_DIM
+    assert call(*ten, scale=0.0) == BAD_VALUE
+    limit = 1 << 22
+    assert call(*ten, B=1, H=1, T=limit + 1) == SCRATCH_LIMIT
+    assert call(*ten, B=64, H=16, T=4097) == SCRATCH_LIMIT
+    args = list(ten)
+    args[7] = MISALIGNED
+    assert call(*args) == MISALIGN
 
 
 def test_materialized_validation(lib):

@@ -34,6 +34,7 @@ STATUS = {
     4: "ATTN_ERROR_MISALIGNED",
     5: "ATTN_ERROR_LAUNCH",
     6: "ATTN_ERROR_INVALID_VALUE",
+    7: "ATTN_ERROR_SCRATCH_LIMIT",
 }
 
 _P = ctypes.c_void_p
@@ -85,6 +86,8 @@ SIGNATURES = {
     "attn_precompute_dot_do_o_f32": [_P, _P, _P, _I, _I, _I, _I, _P],
     "attn_tiled_causal_backward_f32":
         [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P],
+    "attn_tiled_causal_backward_f32_noalloc":
+        [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P],
     "attn_tiled_causal_backward_dq_f32":
         [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P],
     "attn_tiled_causal_backward_dkdv_f32":
@@ -548,6 +551,21 @@ def tiled_causal_attention_backward(q, k, v, o, do, m, l, dq, dk, dv, d_workspac
                _ptr(dv, dt, n, "dv"), _ptr(d_workspace, f32, r, "d_workspace"),
                B, H, T, d_head, float(scale), _stream(stream)),
           "tiled_causal_attention_backward")
+
+
+def tiled_causal_attention_backward_noalloc(q, k, v, o, do, m, l, dq, dk, dv, B, H, T, d_head,
+                                            scale, stream=None):
+    """tiled_causal_attention_backward (fp32) without a caller workspace: D lives in the
+    library's fixed device scratch (attn_tiled_causal_backward_f32_noalloc)."""
+    n = B * H * T * d_head
+    r = B * H * T
+    f32 = _dt(False)
+    check(call("attn_tiled_causal_backward_f32_noalloc", _ptr(q, f32, n, "q"),
+               _ptr(k, f32, n, "k"), _ptr(v, f32, n, "v"), _ptr(o, f32, n, "o"),
+               _ptr(do, f32, n, "do"), _ptr(m, f32, r, "m"), _ptr(l, f32, r, "l"),
+               _ptr(dq, f32, n, "dq"), _ptr(dk, f32, n, "dk"), _ptr(dv, f32, n, "dv"),
+               B, H, T, d_head, float(scale), _stream(stream)),
+          "tiled_causal_attention_backward_noalloc")
 
 
 def tiled_causal_attention_backward_dq(q, k, v, o, do, m, l, dq, d_workspace, B, H, T, d_head,

@@ -7,6 +7,8 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <atomic>
+
 #include "../../include/attn_capi.h"
 #include "launch.hpp"
 
@@ -410,6 +412,7 @@ const char* attn_status_string(int status) {
         case ATTN_ERROR_MISALIGNED: return "pointer not 16-byte aligned";
         case ATTN_ERROR_LAUNCH: return "kernel launch failed";
         case ATTN_ERROR_INVALID_VALUE: return "invalid value (scale, alpha/beta, batch count or stride)";
+        case ATTN_ERROR_SCRATCH_LIMIT: return "problem exceeds the fixed scratch of a no-alloc entry point";
         default: return "unknown status";
     }
 }
@@ -705,6 +708,62 @@ int attn_tiled_causal_backward_f32(const float* q, const float* k, const float* 
     if (st != ATTN_SUCCESS) return st;
     return attn_tiled_causal_backward_dkdv_f32(q, k, v, do_ptr, m_ptr, l_ptr, d_workspace, dk,
                                                dv, B, H, T, d_head, scale, stream);
+}
+
+// ---- tiled fp32 backward without a caller workspace ------------------------------------
+
+namespace {
+
+// D of attn_tiled_causal_backward_f32_noalloc.  In host code this name is not a device
+// address: kernels get the address that hipGetSymbolAddress returns for the current device.
+static __device__ __align__(256) float scratch[ATTN_NOALLOC_SCRATCH_FLOATS];
+
+// Device address of `scratch` on the current device, looked up once per device (on the
+// first call there, with that device current).  Null if the lookup fails.
+float* scratch_ptr() {
+    constexpr int kMaxDev = 64;
+    static std::atomic<float*> cache[kMaxDev] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    float* p = cache[dev].load(std::memory_order_acquire);
+    if (p == nullptr) {
+        void* addr = nullptr;
+        if (hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch)) != hipSuccess || addr == nullptr) {
+            (void)hipGetLastError();
+            return nullptr;
+        }
+        p = static_cast<float*>(addr);
+        cache[dev].store(p, std::memory_order_release);
+    }
+    return p;
+}
+
+}  // namespace
+
+int attn_tiled_causal_backward_f32_noalloc(const float* q, const float* k, const float* v,
+                                           const float* o, const float* do_ptr,
+                                           const float* m_ptr, const float* l_ptr, float* dq,
+                                           float* dk, float* dv, int B, int H, int T,
+                                           int d_head, float scale, hipStream_t stream) {
+    if (q == nullptr || k == nullptr || v == nullptr || o == nullptr || do_ptr == nullptr ||
+        m_ptr == nullptr || l_ptr == nullptr || dq == nullptr || dk == nullptr || dv == nullptr)
+        return ATTN_ERROR_NULL_POINTER;
+    const int st = check_tiled(B, H, T, d_head, scale);
+    if (st != ATTN_SUCCESS) return st;
+    if (static_cast<int64_t>(B) * H * T > ATTN_NOALLOC_SCRATCH_FLOATS)
+        return ATTN_ERROR_SCRATCH_LIMIT;
+    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o) ||
+        !aligned16(do_ptr) || !aligned16(dq) || !aligned16(dk) || !aligned16(dv))
+        return ATTN_ERROR_MISALIGNED;
+    float* ws = scratch_ptr();
+    if (ws == nullptr) return ATTN_ERROR_LAUNCH;
+    // D is written by the first stage for every row before the second stage reads it, so the
+    // scratch needs no clearing.
+    return attn_tiled_causal_backward_f32(q, k, v, o, do_ptr, m_ptr, l_ptr, dq, dk, dv, ws, B,
+                                          H, T, d_head, scale, stream);
 }
 
 // ---- tiled bf16 ------------------------------------------------------------------------

@@ -16,6 +16,7 @@
 //     618-650: a GEMM handle first, then the matmul.cuh:44-58 parameter list) equals the
 //     library's materialised sequences bitwise, and the defaults of matmul_batched_strided
 //     (no transposes, alpha 1, beta 0) equal the explicit arguments;
+//   * the no-alloc backward (no caller workspace) equals the workspace backward bitwise;
 //   * an unsupported head dimension throws instead of silently doing nothing.
 // Exit status 0 iff every test passes.
 #include <cmath>
@@ -345,6 +346,44 @@ bool test_materialized_reference_call_text() {
     return true;
 }
 
+bool test_noalloc_backward() {
+    std::printf("[Test] no-alloc backward == workspace backward, bitwise, two calls...\n");
+    for (int pass = 0; pass < 2; ++pass) {
+        const int B = pass == 0 ? 2 : 1, H = pass == 0 ? 4 : 3, T = pass == 0 ? 300 : 65;
+        const int d = pass == 0 ? 64 : 128;
+        const size_t n = static_cast<size_t>(B) * H * T * d, r = static_cast<size_t>(B) * H * T;
+        const float scale = 1.0f / std::sqrt(static_cast<float>(d));
+        uint32_t state = 99u + static_cast<uint32_t>(pass);
+        auto next = [&state]() {
+            state = state * 1664525u + 1013904223u;
+            return static_cast<float>(static_cast<int>(state >> 9) % 2001 - 1000) / 700.0f;
+        };
+        std::vector<float> h(n);
+        DevBuf q(n), k(n), v(n), dO(n), o(n), m(r), l(r), ws(r), dq1(n), dk1(n), dv1(n), dq2(n),
+            dk2(n), dv2(n);
+        for (DevBuf* b : {&q, &k, &v, &dO}) {
+            for (auto& x : h) x = next();
+            b->upload(h);
+        }
+        tiled_causal_attention_forward(q.p, k.p, v.p, o.p, B, H, T, d, scale, m.p, l.p);
+        tiled_causal_attention_backward(q.p, k.p, v.p, o.p, dO.p, m.p, l.p, dq1.p, dk1.p, dv1.p,
+                                        ws.p, B, H, T, d, scale);
+        tiled_causal_attention_backward_noalloc(q.p, k.p, v.p, o.p, dO.p, m.p, l.p, dq2.p, dk2.p,
+                                                dv2.p, B, H, T, d, scale);
+        HIP_CHECK(hipDeviceSynchronize());
+        const std::pair<const DevBuf*, const DevBuf*> pairs[] = {{&dq1, &dq2}, {&dk1, &dk2},
+                                                                 {&dv1, &dv2}};
+        const char* names[] = {"dq", "dk", "dv"};
+        for (int t = 0; t < 3; ++t) {
+            const auto a = pairs[t].first->download(), b = pairs[t].second->download();
+            for (size_t i = 0; i < a.size(); ++i)
+                EXPECT(std::isfinite(a[i]) && a[i] == b[i], "%s[%zu]: workspace %.9g, no-alloc %.9g",
+                       names[t], i, a[i], b[i]);
+        }
+    }
+    return true;
+}
+
 bool test_bad_head_dim() {
     std::printf("[Test] unsupported d_head is an error, not a silent no-op...\n");
     DevBuf buf(1024);
@@ -374,6 +413,7 @@ int main() {
     test_packed_matches_split(64, 77);
     test_packed_matches_split(128, 130);
     test_materialized_reference_call_text();
+    test_noalloc_backward();
     test_bad_head_dim();
     if (g_failures == 0) {
         std::printf("All host tests passed.\n");

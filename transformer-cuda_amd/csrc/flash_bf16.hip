@@ -45,6 +45,7 @@
 #include <math.h>
 
 #include <type_traits>
+#include <utility>
 
 #include "bf16_tile.hpp"
 #include "device_common.hpp"
@@ -748,6 +749,313 @@ __global__ __launch_bounds__(kWave* NW, NP == 1 ? 1 : 2) void flash_bwd_dkdv_bf1
     }
 }
 
+// ---------------------------------------------------------------------------------------
+// Stage 2 for bf16 operands with an explicit instruction schedule.
+//
+// The same products, in the same order per accumulator, as flash_bwd_dkdv_bf16_kernel<D, 4,
+// 1> (so the same results, bit for bit), but issued as a fixed program per 64-query tile in
+// which
+//   * every MFMA's A fragment is read from LDS kRing - 1 MFMAs ahead, into a ring of kRing
+//     fragments, so that an LDS read's latency is covered by the MFMAs before its
+//     consumer (left to itself, the compiler reads each fragment into one reused register
+//     quad just before its MFMA and waits for it: one exposed LDS latency per MFMA);
+//   * the softmax arithmetic of a half tile is spread between the MFMAs of the next part of
+//     the program: that of half 0 (2^S, mask, P, dS = P o dP', both packed to bf16) between
+//     the score products of half 1, that of half 1 between the dV/dK products of half 0.
+// The program of one wave and tile (NS = D/16 chunks over d, NDT = D/32 head-dim tiles):
+//   ops [0, 2(NS+1))            half 0: S' (statistic step, NS chunks), dP' (the same)
+//   ops [2(NS+1), 4(NS+1))      half 1: the same          + softmax arithmetic of half 0
+//   ops [.., + 4 NDT)           half 0: for dt, u: dV, dK + softmax arithmetic of half 1
+//   ops [.., + 4 NDT)           half 1: for dt, u: dV, dK
+// sched_barrier fences around each op keep the compiler's scheduler from moving the
+// program's instructions across ops.
+// ---------------------------------------------------------------------------------------
+
+template <int... Is, typename F>
+__device__ __forceinline__ void static_for_impl(std::integer_sequence<int, Is...>, F&& f) {
+    (f(std::integral_constant<int, Is>{}), ...);
+}
+// f(integral_constant<int, 0>) ... f(integral_constant<int, N-1>), in order.
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    static_for_impl(std::make_integer_sequence<int, N>{}, f);
+}
+
+__device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
+
+template <int D>
+struct DkdvProgram {
+    static constexpr int NS = D / 16;           // chunks of a score product
+    static constexpr int NDT = D / 32;          // head-dim tiles of dV / dK
+    static constexpr int kScores = 2 * (NS + 1);  // ops of one half's S' and dP'
+    static constexpr int kUpd = 4 * NDT;          // ops of one half's dV and dK
+    static constexpr int N = 2 * kScores + 2 * kUpd;
+    static constexpr bool is_score(int i) { return i < 2 * kScores; }
+    static constexpr int half(int i) {
+        return i < 2 * kScores ? i / kScores : (i - 2 * kScores) / kUpd;
+    }
+    static constexpr int local(int i) {
+        return i < 2 * kScores ? i % kScores : (i - 2 * kScores) % kUpd;
+    }
+    // Softmax task t (0..15) of a half runs at slot `slot(t, n)` of the n ops it overlaps:
+    // tasks 0..7 take 2^S, mask and pack P for elements 2t, 2t+1; tasks 8..15 form and pack
+    // dS for elements 2(t-8), 2(t-8)+1.
+    static constexpr int slot(int t, int n) { return t * n / 16; }
+};
+
+// A fragments in flight: op i's fragment is read kRing - 1 ops ahead of its MFMA.
+template <int D>
+constexpr int kRing = D >= 128 ? 3 : 4;
+
+// Per-wave state of one tile's program.
+template <int D>
+struct DkdvTileRegs {
+    f32x16 s[2], dp[2];   // S' then P (in place), dP' per half
+    bf16x8 p[2][2];       // P of half h, rows 16u.. (B operand of dV)
+    bf16x8 ds[2][2];      // dS of half h (B operand of dK)
+    bf16x8 ring[kRing<D>];
+};
+
+template <int D>
+__global__ __launch_bounds__(kWave * kWaves, D >= 128 ? 1 : 2) void flash_bwd_dkdv_bf16_pipe_kernel(
+    DkdvArgs<1> a, int nblk) {
+    using Prog = DkdvProgram<D>;
+    constexpr int KT = kRowTile;
+    using S = Swz<D, KT>;
+    constexpr uint32_t kBuf = S::kBytes;  // one Q (or dO) buffer
+    constexpr int kBlock = kWaves * kSub;
+    constexpr int NS = Prog::NS;
+    __shared__ __attribute__((aligned(1024))) QgSmem<D, 1> sm;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & (kWave - 1);
+    const int col = lane & 31;
+    const int half = lane >> 5;
+    const int T = a.T;
+    int bh, blk;
+    map_block(blockIdx.x, a.BH, nblk, false, bh, blk);
+    const int k0 = blk * kBlock;
+    const int kw = k0 + kSub * wave;
+    const int kj = kw + col;
+    const size_t qoff = a.qv.off(bh), gtoff = a.gtv.off(bh), koff = a.kv.off(bh),
+                 goff = a.gv.off(bh);
+    const int qrs = a.qv.row, grs = a.gtv.row;
+    const size_t stat_off = static_cast<size_t>(bh) * T;
+    const uint16_t* qh = a.q + qoff;
+    const uint16_t* gh = a.dO + gtoff;
+    const float c = a.scale * kLog2e;
+
+    const int t0 = k0 / KT;
+    const int ntile = (T + KT - 1) / KT;
+    const uint32_t q_lds = lds_addr(sm.q[0][0]);
+    const uint32_t g_lds = lds_addr(sm.g[0][0]);
+    const uint32_t qx_lds = lds_addr(sm.qx[0]);
+    const uint32_t gx_lds = lds_addr(sm.gx[0]);
+    auto copy_tile = [&](int kt) {
+        const uint32_t buf = static_cast<uint32_t>(kt & 1) * kBuf;
+        dma_tile<D, kWaves, KT>(qh, kt * KT, T, q_lds + buf, wave, lane, qrs);
+        dma_tile<D, kWaves, KT>(gh, kt * KT, T, g_lds + buf, wave, lane, grs);
+    };
+    copy_tile(t0);
+    float st_m = 0.0f, st_l = 1.0f, st_d = 0.0f;
+    auto load_stats = [&](int t) {
+        const int r = t * KT + lane;
+        if (r < T) {
+            st_m = a.m[stat_off + r];
+            st_l = a.l[stat_off + r];
+            st_d = a.Dws[stat_off + r];
+        } else {
+            st_m = -INFINITY;
+            st_l = 1.0f;
+            st_d = 0.0f;
+        }
+    };
+    if (wave == 0 && lane < KT) {
+        load_stats(t0);
+        const u16x8 z = u16x8{};
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            *reinterpret_cast<u16x8*>(&sm.qx[b][lane * 8]) = z;
+            *reinterpret_cast<u16x8*>(&sm.gx[b][lane * 8]) = z;
+        }
+    }
+    const bf16x8 one = ones_chunk<1>(half);
+    bf16x8 kr[D / 16][1], vr[D / 16][1];
+    load_operand<D, 1, true>(kr, a.k + koff, kj, T, half, a.kv.row, c);
+    load_operand<D, 1, false>(vr, a.v + koff, kj, T, half, a.kv.row, 1.0f);
+    f32x16 dk_acc[D / 32], dv_acc[D / 32];
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt) {
+        dk_acc[dt] = f32x16{};
+        dv_acc[dt] = f32x16{};
+    }
+    uint32_t roff[D / 16], troff[D / 32];
+    lane_offsets<D>(lane, roff, troff);
+    const uint32_t soff = static_cast<uint32_t>(col * 16);
+
+    auto tile_sync = [&](int kt) {
+        wait_vm<0>();
+        if (wave == 0 && lane < KT) {
+            const float nl = st_m == -INFINITY ? -1e30f : -(st_m * kLog2e + log2f(st_l));
+            *reinterpret_cast<u16x4*>(&sm.qx[kt & 1][lane * 8]) = stat_terms<1>(nl);
+            *reinterpret_cast<u16x4*>(&sm.gx[kt & 1][lane * 8]) = stat_terms<1>(-st_d);
+        }
+        __syncthreads();
+        if (kt + 1 < ntile) {
+            if (wave == 0 && lane < KT) load_stats(kt + 1);
+            copy_tile(kt + 1);
+        }
+    };
+
+    // A fragment of op I of the program (tile in buffer BUF).
+    auto fetch = [&](auto buf, auto I) -> bf16x8 {
+        constexpr int BUF = decltype(buf)::value;
+        constexpr int i = decltype(I)::value;
+        constexpr int h = Prog::half(i), j = Prog::local(i);
+        constexpr uint32_t hb = static_cast<uint32_t>(BUF) * kBuf + static_cast<uint32_t>(h) * S::rows(32);
+        constexpr uint32_t xb = static_cast<uint32_t>(BUF * KT + h * 32) * 16u;
+        if constexpr (Prog::is_score(i)) {
+            if constexpr (j == 0) return lds_b128(soff + (qx_lds + xb));
+            else if constexpr (j <= NS) return lds_b128(roff[j - 1] + (q_lds + hb));
+            else if constexpr (j == NS + 1) return lds_b128(soff + (gx_lds + xb));
+            else return lds_b128(roff[j - NS - 2] + (g_lds + hb));
+        } else {
+            constexpr int p = j / 2, dt = p / 2, u = p % 2;
+            constexpr uint32_t off = hb + static_cast<uint32_t>(u) * Swz<D>::rows(16);
+            if constexpr (j % 2 == 0) return lds_tr(troff[dt] + (g_lds + off), Swz<D>::rows(8));
+            else return lds_tr(troff[dt] + (q_lds + off), Swz<D>::rows(8));
+        }
+    };
+    // The MFMA of op I with its A fragment x.
+    auto product = [&](DkdvTileRegs<D>& r, auto I, const bf16x8& x) {
+        constexpr int i = decltype(I)::value;
+        constexpr int h = Prog::half(i), j = Prog::local(i);
+        if constexpr (Prog::is_score(i)) {
+            if constexpr (j == 0) r.s[h] = mfma_32x32x16_bf16(x, one, f32x16{});
+            else if constexpr (j <= NS) r.s[h] = mfma_32x32x16_bf16(x, kr[j - 1][0], r.s[h]);
+            else if constexpr (j == NS + 1) r.dp[h] = mfma_32x32x16_bf16(x, one, f32x16{});
+            else r.dp[h] = mfma_32x32x16_bf16(x, vr[j - NS - 2][0], r.dp[h]);
+        } else {
+            constexpr int p = j / 2, dt = p / 2, u = p % 2;
+            if constexpr (j % 2 == 0) dv_acc[dt] = mfma_32x32x16_bf16(x, r.p[h][u], dv_acc[dt]);
+            else dk_acc[dt] = mfma_32x32x16_bf16(x, r.ds[h][u], dk_acc[dt]);
+        }
+    };
+    // Softmax task T of half H (see DkdvProgram::slot); MASK: the half tile holds queries
+    // before this lane's key (queries qb..qb+31).
+    auto task = [&](DkdvTileRegs<D>& r, auto H, auto Tk, auto mask, int qb) {
+        constexpr int h = decltype(H)::value, t = decltype(Tk)::value;
+        constexpr int e = 2 * (t % 8), u = e / 8, k = e % 8;
+        if constexpr (t < 8) {
+            r.s[h][e] = exp2_fast(r.s[h][e]);
+            r.s[h][e + 1] = exp2_fast(r.s[h][e + 1]);
+            if constexpr (decltype(mask)::value) {
+                if (qb + acc_row(e, half) < kj) r.s[h][e] = 0.0f;
+                if (qb + acc_row(e + 1, half) < kj) r.s[h][e + 1] = 0.0f;
+            }
+            r.p[h][u][k] = static_cast<__bf16>(r.s[h][e]);
+            r.p[h][u][k + 1] = static_cast<__bf16>(r.s[h][e + 1]);
+        } else {
+            r.ds[h][u][k] = static_cast<__bf16>(r.s[h][e] * r.dp[h][e]);
+            r.ds[h][u][k + 1] = static_cast<__bf16>(r.s[h][e + 1] * r.dp[h][e + 1]);
+        }
+    };
+    // The softmax tasks of half H that run at position k of a stretch of n ops.
+    auto tasks_at = [&](DkdvTileRegs<D>& r, auto H, auto mask, int qb, auto K, auto Nn) {
+        constexpr int kk = decltype(K)::value, n = decltype(Nn)::value;
+        static_for<16>([&](auto Tk) {
+            if constexpr (Prog::slot(decltype(Tk)::value, n) == kk) task(r, H, Tk, mask, qb);
+        });
+    };
+
+    // Both half tiles of tile kt (buffer BUF); half 0 is the diagonal one when MASK0.
+    auto full_tile = [&](int kt, auto buf, auto mask0) {
+        constexpr int R = kRing<D>;
+        DkdvTileRegs<D> r;
+        static_for<R - 1>([&](auto I) { r.ring[decltype(I)::value] = fetch(buf, I); });
+        const int qb = KT * kt;
+        static_for<Prog::N>([&](auto I) {
+            constexpr int i = decltype(I)::value;
+            if constexpr (i + R - 1 < Prog::N)
+                r.ring[(i + R - 1) % R] = fetch(buf, std::integral_constant<int, i + R - 1>{});
+            sched_fence();
+            product(r, I, r.ring[i % R]);
+            if constexpr (i >= Prog::kScores && i < 2 * Prog::kScores)
+                tasks_at(r, std::integral_constant<int, 0>{}, mask0, qb,
+                         std::integral_constant<int, i - Prog::kScores>{},
+                         std::integral_constant<int, Prog::kScores>{});
+            if constexpr (i >= 2 * Prog::kScores && i < 2 * Prog::kScores + Prog::kUpd)
+                tasks_at(r, std::integral_constant<int, 1>{}, std::false_type{}, qb + 32,
+                         std::integral_constant<int, i - 2 * Prog::kScores>{},
+                         std::integral_constant<int, Prog::kUpd>{});
+            sched_fence();
+        });
+    };
+    // Only half tile 1 of tile kt (buffer BUF), the diagonal one: no overlap.
+    auto second_half_only = [&](int kt, auto buf) {
+        DkdvTileRegs<D> r;
+        constexpr int b = Prog::kScores;  // first op of half 1's scores
+        constexpr int e = 2 * Prog::kScores + Prog::kUpd;  // first op of half 1's updates
+        static_for<Prog::kScores>([&](auto I) {
+            constexpr int i = b + decltype(I)::value;
+            product(r, std::integral_constant<int, i>{}, fetch(buf, std::integral_constant<int, i>{}));
+        });
+        static_for<16>([&](auto Tk) {
+            task(r, std::integral_constant<int, 1>{}, Tk, std::true_type{}, KT * kt + 32);
+        });
+        static_for<Prog::kUpd>([&](auto I) {
+            constexpr int i = e + decltype(I)::value;
+            product(r, std::integral_constant<int, i>{}, fetch(buf, std::integral_constant<int, i>{}));
+        });
+    };
+    using B0 = std::integral_constant<int, 0>;
+    using B1 = std::integral_constant<int, 1>;
+    auto run_tile = [&](int kt, auto mask0) {
+        if (kt & 1)
+            full_tile(kt, B1{}, mask0);
+        else
+            full_tile(kt, B0{}, mask0);
+    };
+
+    // Half tiles before hstart (= kw/32, the one holding the wave's first key) hold only
+    // queries that precede every key of the wave; a wave whose keys start past T computes
+    // nothing.  Every wave takes part in every tile's barrier and copies.
+    const int hstart = kw < T ? kw / 32 : 2 * ntile;
+    int kt = t0;
+    for (; 2 * kt + 1 < hstart; ++kt) tile_sync(kt);
+    if (kt < ntile) {  // the tile holding the diagonal half tile
+        tile_sync(kt);
+        if (hstart & 1) {
+            if (kt & 1)
+                second_half_only(kt, B1{});
+            else
+                second_half_only(kt, B0{});
+        } else {
+            run_tile(kt, std::true_type{});
+        }
+        ++kt;
+    }
+    if (kt < ntile && (kt & 1)) {
+        tile_sync(kt);
+        full_tile(kt, B1{}, std::false_type{});
+        ++kt;
+    }
+    for (; kt + 1 < ntile; kt += 2) {
+        tile_sync(kt);
+        full_tile(kt, B0{}, std::false_type{});
+        tile_sync(kt + 1);
+        full_tile(kt + 1, B1{}, std::false_type{});
+    }
+    if (kt < ntile) {
+        tile_sync(kt);
+        full_tile(kt, B0{}, std::false_type{});
+    }
+
+    if (kj < T) {
+        store_row<D>(a.dk + goff, kj, half, dk_acc, a.scale, a.gv.row);
+        store_row<D>(a.dv + goff, kj, half, dv_acc, 1.0f, a.gv.row);
+    }
+}
+
 template <int D, int NSUB, int NP>
 void dq_launch(const DqArgs<NP>& a, hipStream_t stream) {
     constexpr int kBlock = kWaves * NSUB * kSub;
@@ -770,8 +1078,13 @@ void dkdv_dispatch(const DkdvArgs<NP>& a, hipStream_t stream) {
     constexpr int NW = kWaves;
     constexpr int kBlock = NW * kSub;
     const int nblk = (a.T + kBlock - 1) / kBlock;
-    hipLaunchKernelGGL((flash_bwd_dkdv_bf16_kernel<D, NW, NP>), dim3(a.BH * nblk),
-                       dim3(kWave * NW), 0, stream, a, nblk);
+    if constexpr (NP == 1) {
+        hipLaunchKernelGGL((flash_bwd_dkdv_bf16_pipe_kernel<D>), dim3(a.BH * nblk),
+                           dim3(kWave * NW), 0, stream, a, nblk);
+    } else {
+        hipLaunchKernelGGL((flash_bwd_dkdv_bf16_kernel<D, NW, NP>), dim3(a.BH * nblk),
+                           dim3(kWave * NW), 0, stream, a, nblk);
+    }
 }
 
 }  // namespace

@@ -4,7 +4,8 @@
 // Element x of a (B*H, T, d) fp32 view becomes x_0 = bf16(x), x_1 = bf16(x - x_0),
 // x_2 = bf16(x - x_0 - x_1) (round to nearest even), written to three head-major bf16
 // tensors pstride elements apart.  A thread moves 8 consecutive elements of a row: two
-// 16-byte loads, three 16-byte stores.
+// 16-byte loads, three 16-byte nontemporal stores (the planes are next read by other
+// kernels, not from this kernel's L2 lines).
 #include "bf16_tile.hpp"
 #include "device_common.hpp"
 #include "launch.hpp"
@@ -38,7 +39,8 @@ __global__ __launch_bounds__(kThreads) void split_planes_kernel(
         uint16_t* o = dst_j + static_cast<size_t>(row) * d + c;  // head-major
 #pragma unroll
         for (int i = 0; i < 3; ++i)
-            *reinterpret_cast<u16x8*>(o + i * pstride) = __builtin_bit_cast(u16x8, pl[i]);
+            __builtin_nontemporal_store(__builtin_bit_cast(u16x8, pl[i]),
+                                        reinterpret_cast<u16x8*>(o + i * pstride));
     }
 }
 

@@ -252,6 +252,136 @@ __device__ __forceinline__ void store_row(float* __restrict__ head, int row, int
 }
 
 // ---------------------------------------------------------------------------------------
+// Row stores through LDS.  Stored straight from the MFMA register layout, a wave's 32-row
+// sub-block leaves as 32 bytes of each of 32 rows per store instruction (two lanes per row).
+// Staged in a wave-private LDS area and read back row by row, it leaves as whole rows,
+// 1 KB per wave instruction.  Stage layout: row r, 16-byte chunk c at
+// r*RB + 16*(c ^ swz(r)), swz(r) = (r / max(1, 256/RB)) % min(RB/16, 16), so that the 16
+// rows x one chunk that 16 lanes write, and the 256 bytes of whole rows that 16 lanes read
+// back, each cover the 64 banks once.
+// ---------------------------------------------------------------------------------------
+
+template <int RB>  // bytes per staged row
+struct RowStage {
+    static_assert(RB >= 64 && RB % 64 == 0, "rows of whole 64-byte groups");
+    static constexpr int kCpr = RB / 16;
+    static constexpr int kRp = RB >= 256 ? 1 : 256 / RB;
+    static constexpr int kSwzMask = (kCpr < 16 ? kCpr : 16) - 1;
+    static constexpr uint32_t kBytes = 32u * RB;  // one wave's stage
+    __device__ static uint32_t off(int r, int c) {
+        return static_cast<uint32_t>(r * RB + 16 * (c ^ ((r / kRp) & kSwzMask)));
+    }
+};
+
+__device__ __forceinline__ void lds_put16(uint32_t addr, u16x8 v) {
+    *(TCAMD_LDS u16x8*)(uintptr_t)addr = v;
+}
+__device__ __forceinline__ void lds_put8(uint32_t addr, u16x4 v) {
+    *(TCAMD_LDS u16x4*)(uintptr_t)addr = v;
+}
+
+// Wave-wide: the staged rows row0 .. row0+31 that lie below T, to rows rs_bytes apart from
+// base; lane l moves chunk (64 i + l) % (RB/16) of row (64 i + l) / (RB/16) in step i.
+template <int RB>
+__device__ __forceinline__ void stage_flush(uint32_t stage, char* __restrict__ base, int row0,
+                                            int T, size_t rs_bytes, int lane) {
+    using St = RowStage<RB>;
+#pragma unroll
+    for (int i = 0; i < 32 * St::kCpr / kWave; ++i) {
+        const int g = i * kWave + lane;
+        const int r = g / St::kCpr;
+        const int c = g % St::kCpr;
+        const u16x8 v = *(TCAMD_LDS const u16x8*)(uintptr_t)(stage + St::off(r, c));
+        if (row0 + r < T)
+            *reinterpret_cast<u16x8*>(base + static_cast<size_t>(row0 + r) * rs_bytes + 16 * c) = v;
+    }
+}
+
+// A wave's stage inside a pair of idle tile buffers (lo, hi: LDS byte addresses, each at
+// least 2 * bytes long): waves 0, 1 in lo, waves 2, 3 in hi.
+__device__ __forceinline__ uint32_t wave_stage(uint32_t lo, uint32_t hi, int wave,
+                                               uint32_t bytes) {
+    return (wave < 2 ? lo : hi) + static_cast<uint32_t>(wave & 1) * bytes;
+}
+
+// store_planes for the sub-block of rows row0 .. row0+31, through the wave's stage of
+// RowStage<2D>::kBytes bytes: the same values, stored as whole rows.
+template <int D, int NP>
+__device__ __forceinline__ void store_planes_staged(uint16_t* __restrict__ head, size_t pstride,
+                                                    const bf16x8 (&x)[D / 16][NP], int row0,
+                                                    int T, int lane, uint32_t stage) {
+    using St = RowStage<2 * D>;
+    const int col = lane & 31;
+    const int half = lane >> 5;
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+#pragma unroll
+        for (int st = 0; st < D / 16; ++st)
+            lds_put16(stage + St::off(col, 2 * st + half), __builtin_bit_cast(u16x8, x[st][i]));
+        stage_flush<2 * D>(stage, reinterpret_cast<char*>(head + i * pstride), row0, T, 2 * D,
+                           lane);
+    }
+}
+
+// store_row (bf16) for the sub-block of rows row0 .. row0+31, through the wave's stage of
+// RowStage<2D>::kBytes bytes.
+template <int D>
+__device__ __forceinline__ void store_row_staged(uint16_t* __restrict__ head, int row0, int T,
+                                                 int lane, const f32x16 (&acc)[D / 32],
+                                                 float mul, int rs, uint32_t stage) {
+    using St = RowStage<2 * D>;
+    const int col = lane & 31;
+    const int half = lane >> 5;
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            u16x4 o;
+            o[0] = f32_to_bf16_bits(acc[dt][4 * g + 0] * mul);
+            o[1] = f32_to_bf16_bits(acc[dt][4 * g + 1] * mul);
+            o[2] = f32_to_bf16_bits(acc[dt][4 * g + 2] * mul);
+            o[3] = f32_to_bf16_bits(acc[dt][4 * g + 3] * mul);
+            lds_put8(stage + St::off(col, 4 * dt + g) + 8 * half, o);
+        }
+    }
+    stage_flush<2 * D>(stage, reinterpret_cast<char*>(head), row0, T,
+                       static_cast<size_t>(rs) * 2, lane);
+}
+
+// store_row (fp32) for the sub-block of rows row0 .. row0+31, through the wave's stage of
+// RowStage<128>::kBytes bytes: one 32-column slice (128 bytes of each row) at a time.
+template <int D>
+__device__ __forceinline__ void store_row_staged(float* __restrict__ head, int row0, int T,
+                                                 int lane, const f32x16 (&acc)[D / 32],
+                                                 float mul, int rs, uint32_t stage) {
+    using St = RowStage<128>;
+    const int col = lane & 31;
+    const int half = lane >> 5;
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            f32x4 o;
+            o[0] = acc[dt][4 * g + 0] * mul;
+            o[1] = acc[dt][4 * g + 1] * mul;
+            o[2] = acc[dt][4 * g + 2] * mul;
+            o[3] = acc[dt][4 * g + 3] * mul;
+            lds_put16(stage + St::off(col, 2 * g + half), __builtin_bit_cast(u16x8, o));
+        }
+        stage_flush<128>(stage, reinterpret_cast<char*>(head + 32 * dt), row0, T,
+                         static_cast<size_t>(rs) * 4, lane);
+    }
+}
+
+// Bytes of one wave's stage for the staged stores of a D-wide row operand (planes, bf16 or
+// fp32 rows).
+template <int D, int NP>
+constexpr uint32_t kStageBytes = NP == 1 ? RowStage<2 * D>::kBytes
+                                         : (RowStage<2 * D>::kBytes > RowStage<128>::kBytes
+                                                ? RowStage<2 * D>::kBytes
+                                                : RowStage<128>::kBytes);
+
+// ---------------------------------------------------------------------------------------
 // Per-row statistics as one more contraction step: a product over 16 more k-slots, where the
 // A (or B) operand is (1, 1, [1,] 0, ...) and the other carries the terms of the statistic,
 // adds the statistic to every element of the row.

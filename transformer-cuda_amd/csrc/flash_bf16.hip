@@ -69,11 +69,14 @@ constexpr int kKeyTileDq = NP == 1 ? kRowTile : 32;
 template <int NP>
 constexpr int kQueryTile = NP == 1 ? kRowTile : 32;
 
-// K and V tiles of stage 1 (as the forward's), NP planes each.
+// K and V tiles of stage 1 (as the forward's), NP planes each.  At d >= 64 the row stores of
+// dO's planes and of dQ go through LDS stages inside an idle buffer.
 template <int D, int NP>
 struct KvSmem {
     uint16_t k[2][NP][Swz<D, kKeyTileDq<NP>>::kBytes / 2];
     uint16_t v[2][NP][Swz<D, kKeyTileDq<NP>>::kBytes / 2];
+    static_assert(D < 64 || 2 * kStageBytes<D, NP> <= NP * Swz<D, kKeyTileDq<NP>>::kBytes,
+                  "two wave stages per idle K (or V) buffer");
 };
 
 // Q and dO tiles of stage 2 (NP planes each), and per row an 8-element chunk that carries
@@ -85,6 +88,10 @@ struct QgSmem {
     uint16_t g[2][NP][Swz<D, KT>::kBytes / 2];
     uint16_t qx[2][KT * 8];  // row r: the terms of -lse2, then zeros
     uint16_t gx[2][KT * 8];  // row r: the terms of -D, then zeros
+    // bf16 operands at d >= 64: the row stores of dK and dV go through LDS stages inside an
+    // idle buffer (measured slower for the three-plane kernel, which stores directly)
+    static_assert(NP != 1 || D < 64 || 2 * kStageBytes<D, NP> <= NP * Swz<D, KT>::kBytes,
+                  "two wave stages per idle Q (or dO) buffer");
 };
 
 // A register operand over the head dimension: the NP planes of row `row` of a head (rows rs
@@ -370,9 +377,19 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_bwd_dq_bf16_kernel(DqArgs
     }
     for (; hh < hend; ++hh) tile_sync(hh);
 
-    if (qj1 + col < T) store_row<D>(a.dq + goff, qj1 + col, half, sb1.acc, a.scale, a.gv.row);
-    if constexpr (NSUB == 2)
-        if (qj0 + col < T) store_row<D>(a.dq + goff, qj0 + col, half, sb0.acc, a.scale, a.gv.row);
+    if constexpr (D >= 64) {
+        // after the last tile barrier the buffer without the last tile is idle
+        const uint32_t stage = wave_stage(lds_addr(sm.k[ntile & 1][0]),
+                                          lds_addr(sm.v[ntile & 1][0]), wave, kStageBytes<D, NP>);
+        store_row_staged<D>(a.dq + goff, qj1, T, lane, sb1.acc, a.scale, a.gv.row, stage);
+        if constexpr (NSUB == 2)
+            store_row_staged<D>(a.dq + goff, qj0, T, lane, sb0.acc, a.scale, a.gv.row, stage);
+    } else {
+        if (qj1 + col < T) store_row<D>(a.dq + goff, qj1 + col, half, sb1.acc, a.scale, a.gv.row);
+        if constexpr (NSUB == 2)
+            if (qj0 + col < T)
+                store_row<D>(a.dq + goff, qj0 + col, half, sb0.acc, a.scale, a.gv.row);
+    }
 }
 
 // ---------------------------------------------------------------------------------------
@@ -1050,7 +1067,13 @@ __global__ __launch_bounds__(kWave * kWaves, D >= 128 ? 1 : 2) void flash_bwd_dk
         full_tile(kt, B0{}, std::false_type{});
     }
 
-    if (kj < T) {
+    if constexpr (D >= 64) {
+        // after the last tile barrier the buffer without the last tile is idle
+        const uint32_t stage = wave_stage(lds_addr(sm.q[ntile & 1][0]),
+                                          lds_addr(sm.g[ntile & 1][0]), wave, kStageBytes<D, 1>);
+        store_row_staged<D>(a.dk + goff, kw, T, lane, dk_acc, a.scale, a.gv.row, stage);
+        store_row_staged<D>(a.dv + goff, kw, T, lane, dv_acc, 1.0f, a.gv.row, stage);
+    } else if (kj < T) {
         store_row<D>(a.dk + goff, kj, half, dk_acc, a.scale, a.gv.row);
         store_row<D>(a.dv + goff, kj, half, dv_acc, 1.0f, a.gv.row);
     }

@@ -62,12 +62,17 @@ constexpr float kRescaleLog2 = 8.0f;  // raise the running max only beyond p = 2
 template <int NP, int NSUB>
 constexpr bool kFold = NP == 1 && NSUB == 1;
 
-// Double-buffered K and V tiles, NP planes each.
+// Double-buffered K and V tiles, NP planes each.  The row stores of Q's planes and of O go
+// through LDS stages inside an idle buffer (d >= 64; at d = 32 four stages do not fit).
 template <int D, int NP>
 struct FwdSmem {
     uint16_t k[2][NP][Swz<D, kKeyTile<NP>>::kBytes / 2];
     uint16_t v[2][NP][Swz<D, kKeyTile<NP>>::kBytes / 2];
+    static_assert(D < 64 || 2 * kStageBytes<D, NP> <= NP * Swz<D, kKeyTile<NP>>::kBytes,
+                  "two wave stages per idle K (or V) buffer");
 };
+template <int D>
+constexpr bool kStaged = D >= 64;
 
 // Maximum and sum of a lane's 16 scores as balanced trees (dependency depth 3 and 4 instead
 // of 8 and 16 for a running reduction).
@@ -252,8 +257,9 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_fwd_bf16_kernel(
         const float* qh = qf + qv.off(bh);
         if constexpr (NSUB == 2) load_rowop_split<D, NP>(qr0, qh, qj0 + col, T, half, qv.row);
         load_rowop_split<D, NP>(qr1, qh, qj1 + col, T, half, qv.row);
-        if (qp != nullptr) {
-            if constexpr (NSUB == 2) store_planes<D, NP>(qp + xoff, pstride, qr0, qj0 + col, T, half);
+        if (qp != nullptr && !kStaged<D>) {
+            if constexpr (NSUB == 2)
+                store_planes<D, NP>(qp + xoff, pstride, qr0, qj0 + col, T, half);
             store_planes<D, NP>(qp + xoff, pstride, qr1, qj1 + col, T, half);
         }
     }
@@ -324,12 +330,26 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_fwd_bf16_kernel(
     }
     for (; hh < hend; ++hh) tile_sync(hh);
 
+    // After the last tile barrier no wave reads, and no copy writes, the buffer that does not
+    // hold the last tile.
+    const uint32_t ostage = wave_stage(lds_addr(sm.k[ntile & 1][0]), lds_addr(sm.v[ntile & 1][0]),
+                                       wave, kStageBytes<D, NP>);
 #pragma unroll
     for (int j = 2 - NSUB; j < 2; ++j) {
         const SubState<D>& st = j == 0 ? st0 : st1;
-        const int qi = (j == 0 ? qj0 : qj1) + col;
+        const int qj = j == 0 ? qj0 : qj1;
+        const int qi = qj + col;
+        if constexpr (kStaged<D>) {  // whole wave; rows at or past T are not stored
+            store_row_staged<D>(o + ooff, qj, T, lane, st.acc, 1.0f / st.l, ors, ostage);
+            // Q's planes go out here rather than before the loop, where the first tile's
+            // wait for its copies (vector-memory counts retire in order) would wait for them
+            if constexpr (NP > 1)
+                if (qp != nullptr)
+                    store_planes_staged<D, NP>(qp + xoff, pstride, j == 0 ? qr0 : qr1, qj, T,
+                                               lane, ostage);
+        }
         if (qi < T) {
-            store_row<D>(o + ooff, qi, half, st.acc, 1.0f / st.l, ors);  // l >= 1
+            if constexpr (!kStaged<D>) store_row<D>(o + ooff, qi, half, st.acc, 1.0f / st.l, ors);
             if (half == 0) {
                 const size_t r = static_cast<size_t>(bh) * T + qi;
                 // m = scale * max_j q.k; l relative to that maximum

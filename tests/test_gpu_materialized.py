@@ -63,6 +63,42 @@ def test_gemm_vs_fp64(lib, M, N, K, ta, tb):
                 np.testing.assert_array_equal(gap, ref_gap)
 
 
+@pytest.mark.parametrize("M,N,K", [(4, 4, 4), (100, 68, 132), (260, 64, 1024), (132, 200, 36),
+                                   (512, 516, 64), (36, 8, 20)])
+@pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
+@pytest.mark.parametrize("pad", [0, 4])
+def test_gemm_vectorized_vs_fp64(lib, M, N, K, ta, tb, pad):
+    """Operands whose contiguous dimension is a multiple of 4 elements, with 16-byte aligned
+    batch strides, take the 16-byte-load kernel (128 x 128 tiles, or 128 x 64 for N <= 64):
+    ragged against both tile shapes, every transpose combination, packed and padded batches."""
+    rng = np.random.default_rng(M * 7919 + N * 31 + K + 2 * ta + tb + pad)
+    batch = 3
+    sA, sB, sC = M * K + pad, K * N + pad, M * N + pad
+    a = rng.standard_normal(batch * sA).astype(np.float32)
+    b = rng.standard_normal(batch * sB).astype(np.float32)
+    c0 = rng.standard_normal(batch * sC).astype(np.float32)
+    for alpha, beta in ((1.0, 0.0), (0.75, 0.5)):
+        cg = to_dev(c0)
+        if beta == 0.0:
+            cg.fill_(float("nan"))
+        lib.matmul_batched_strided(to_dev(a), to_dev(b), cg, M, N, K, sA, sB, sC, batch, ta, tb,
+                                   alpha, beta)
+        torch.cuda.synchronize()
+        got = cg.cpu().numpy()
+        want = gemm_ref(a, b, M, N, K, sA, sB, sC, batch, ta, tb, alpha, beta, c0)
+        for i in range(batch):
+            g = got[i * sC:i * sC + M * N]
+            assert np.isfinite(g).all()
+            np.testing.assert_allclose(g, want[i * sC:i * sC + M * N], rtol=0,
+                                       atol=2e-6 * K + 1e-6, err_msg=f"batch {i} beta {beta}")
+        for i in range(batch - 1):  # the padding between batch matrices is never written
+            gap = got[i * sC + M * N:(i + 1) * sC]
+            if beta == 0.0:
+                assert np.isnan(gap).all()
+            else:
+                np.testing.assert_array_equal(gap, c0[i * sC + M * N:(i + 1) * sC])
+
+
 def materialized(lib, q, k, v, do, B, H, T, d, scale):
     qg, kg, vg, dog = (to_dev(x) for x in (q, k, v, do))
     nan = lambda shape: torch.full(shape, float("nan"), device="cuda:0")

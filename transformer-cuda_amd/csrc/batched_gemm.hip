@@ -14,7 +14,16 @@
 // 8 MFMAs per wave).  LDS holds both operands k-major (As[k][m], Bs[k][n]), so an MFMA
 // operand read is 32 consecutive floats per k.  Loads are scalar with bounds checks, which
 // serves every (trans, size, alignment) combination the reference's call sites produce.
+//
+// When the operands allow 16-byte loads (the contiguous dimension of each operand a
+// multiple of 4 elements, 16-byte aligned bases and batch strides: every call of the
+// materialised attention with d_head % 4 == 0 and T % 4 == 0), a second kernel runs: each
+// wave computes 64 x 64 of C as 2 x 2 MFMA blocks (every LDS operand read feeds two MFMAs)
+// in a 128 x 128 workgroup tile, or 32 x 64 in a 128 x 64 tile for N <= 64, and global loads
+// move 16 bytes per lane.
 #include <stdint.h>
+
+#include <type_traits>
 
 #include "device_common.hpp"
 #include "launch.hpp"
@@ -116,11 +125,209 @@ __global__ __launch_bounds__(kThreads) void bgemm_f32_kernel(
     }
 }
 
+// ---------------------------------------------------------------------------------------
+// Tiled kernel (16-byte loads).  LDS holds each operand as rows of 16 floats (one m of A, or
+// one n of B, over a 16-deep k chunk) with k permuted, kp(k) = 8*(k % 2) + k / 2, so that the
+// MFMA lane (r, kh), which takes k = 2s + kh at step s, finds its 8 values of the chunk at
+// kp = 8kh .. 8kh + 7: two 16-byte reads.  The 16-byte chunk c of row r sits at chunk slot
+// c ^ ((r / 4) % 4), so the 16 lanes of a read (rows r .. r+15, one chunk) hit distinct banks.
+// ---------------------------------------------------------------------------------------
+constexpr int kTK = 16;  // k per chunk
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ int kperm(int k) { return (k & 1) * 8 + (k >> 1); }
+// Float index of (row r, permuted k kp) in an operand tile.
+__device__ __forceinline__ int op_off(int r, int kp) {
+    return r * kTK + ((((kp >> 2) ^ (r >> 2)) & 3) << 2) + (kp & 3);
+}
+
+// WM waves along M, 4 / WM along N; each wave computes I x J MFMA blocks of 32 x 32.
+template <bool TA, bool TB, int WM, int I, int J>
+__global__ __launch_bounds__(kThreads) void bgemm_f32_tiled_kernel(
+    const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M,
+    int N, int K, long long sA, long long sB, long long sC, float alpha, float beta,
+    int tiles_m, int tiles_n) {
+    constexpr int WN = 4 / WM;
+    constexpr int BM = 32 * I * WM, BN = 32 * J * WN;
+    constexpr int kA4 = BM * kTK / 4 / kThreads;  // float4 of A per thread per chunk
+    constexpr int kB4 = BN * kTK / 4 / kThreads;
+    __shared__ __attribute__((aligned(16))) float As[2][BM * kTK];
+    __shared__ __attribute__((aligned(16))) float Bs[2][BN * kTK];
+    const long long tiles = static_cast<long long>(tiles_m) * tiles_n;
+    const long long id = blockIdx.x;
+    const long long batch = id / tiles;
+    const int t = static_cast<int>(id - batch * tiles);
+    const int m0 = (t / tiles_n) * BM;
+    const int n0 = (t % tiles_n) * BN;
+    const float* Ab = A + batch * sA;
+    const float* Bb = B + batch * sB;
+    float* Cb = C + batch * sC;
+    const int lda = TA ? M : K;
+    const int ldb = TB ? K : N;
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wave = tid >> 6;
+    const int wm = wave % WM, wn = wave / WM;
+
+    // One operand tile (R rows of the operand's M or N, kTK k) from a row-major source:
+    // KCONT: the source's rows run over k (element (r, k) at r*ld + k), else over r
+    // (element (r, k) at k*ld + r).  Fragment f of this thread covers 4 consecutive
+    // elements of the contiguous dimension.
+    f32x4 ra[kA4], rb[kB4];
+    auto load_op = [&](auto kcont, const float* src, int ld, int r0, int rlim, int k0, auto& reg,
+                       auto nfrag, auto rows) {
+        constexpr bool KC = decltype(kcont)::value;
+        constexpr int NF = decltype(nfrag)::value, R = decltype(rows)::value;
+#pragma unroll
+        for (int i = 0; i < NF; ++i) {
+            const int f = tid + kThreads * i;
+            int r, k;
+            if constexpr (KC) { r = f >> 2; k = (f & 3) * 4; }
+            else { k = f % kTK; r = (f / kTK) * 4; }
+            const bool ok = (r0 + r < rlim) && (k0 + k < K);
+            reg[i] = ok ? *reinterpret_cast<const f32x4*>(
+                              src + (KC ? static_cast<long long>(r0 + r) * ld + (k0 + k)
+                                        : static_cast<long long>(k0 + k) * ld + (r0 + r)))
+                        : f32x4{};
+        }
+    };
+    auto store_op = [&](auto kcont, float* dst, const auto& reg, auto nfrag, auto rows) {
+        constexpr bool KC = decltype(kcont)::value;
+        constexpr int NF = decltype(nfrag)::value, R = decltype(rows)::value;
+#pragma unroll
+        for (int i = 0; i < NF; ++i) {
+            const int f = tid + kThreads * i;
+            if constexpr (KC) {  // k = 4q .. 4q+3 of row r: kp 2q, 2q+1 and 8+2q, 9+2q
+                const int r = f >> 2, q = f & 3;
+                *reinterpret_cast<f32x2*>(dst + op_off(r, 2 * q)) = f32x2{reg[i][0], reg[i][2]};
+                *reinterpret_cast<f32x2*>(dst + op_off(r, 8 + 2 * q)) = f32x2{reg[i][1], reg[i][3]};
+            } else {  // rows r .. r+3 at one k; 16 lanes: 16 k of the same rows
+                const int k = f % kTK, r = (f / kTK) * 4;
+                const int kp = kperm(k);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) dst[op_off(r + j, kp)] = reg[i][j];
+            }
+        }
+    };
+    using KA = std::integral_constant<bool, !TA>;  // A (M x K): rows over k unless transposed
+    using KB = std::integral_constant<bool, TB>;   // B (K x N): rows over k when transposed
+    using NA = std::integral_constant<int, kA4>;
+    using NB = std::integral_constant<int, kB4>;
+    using RA = std::integral_constant<int, BM>;
+    using RB = std::integral_constant<int, BN>;
+    auto load = [&](int k0) {
+        load_op(KA{}, Ab, lda, m0, M, k0, ra, NA{}, RA{});
+        load_op(KB{}, Bb, ldb, n0, N, k0, rb, NB{}, RB{});
+    };
+    auto store = [&](int buf) {
+        store_op(KA{}, As[buf], ra, NA{}, RA{});
+        store_op(KB{}, Bs[buf], rb, NB{}, RB{});
+    };
+
+    f32x16 acc[I][J];
+#pragma unroll
+    for (int i = 0; i < I; ++i)
+#pragma unroll
+        for (int j = 0; j < J; ++j) acc[i][j] = f32x16{};
+    const int nk = (K + kTK - 1) / kTK;
+    const int kh = lane >> 5;
+    const int rl = lane & 31;
+    load(0);
+    store(0);
+    __syncthreads();
+    for (int kc = 0; kc < nk; ++kc) {
+        const int buf = kc & 1;
+        if (kc + 1 < nk) load((kc + 1) * kTK);
+        float a[I][8], b[J][8];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+            for (int i = 0; i < I; ++i) {
+                const int ar = 32 * (I * wm + i) + rl;
+                const f32x4 x = *reinterpret_cast<const f32x4*>(&As[buf][op_off(ar, 8 * kh + 4 * h)]);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) a[i][4 * h + e] = x[e];
+            }
+#pragma unroll
+            for (int j = 0; j < J; ++j) {
+                const int br = 32 * (J * wn + j) + rl;
+                const f32x4 y = *reinterpret_cast<const f32x4*>(&Bs[buf][op_off(br, 8 * kh + 4 * h)]);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) b[j][4 * h + e] = y[e];
+            }
+        }
+#pragma unroll
+        for (int st = 0; st < kTK / 2; ++st)
+#pragma unroll
+            for (int i = 0; i < I; ++i)
+#pragma unroll
+                for (int j = 0; j < J; ++j) acc[i][j] = mfma_32x32x2_f32(a[i][st], b[j][st], acc[i][j]);
+        if (kc + 1 < nk) store(buf ^ 1);
+        __syncthreads();
+    }
+
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const int col = n0 + 32 * (J * wn + j) + rl;
+        if (col >= N) continue;
+#pragma unroll
+        for (int i = 0; i < I; ++i) {
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int row = m0 + 32 * (I * wm + i) + acc_row(v, kh);
+                if (row < M) {
+                    float* p = Cb + static_cast<long long>(row) * N + col;
+                    *p = beta == 0.0f ? alpha * acc[i][j][v] : fmaf(alpha, acc[i][j][v], beta * *p);
+                }
+            }
+        }
+    }
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+template <bool TA, bool TB>
+void launch_tiled(const float* A, const float* B, float* C, int M, int N, int K, long long sA,
+                  long long sB, long long sC, int batch, float alpha, float beta,
+                  hipStream_t stream) {
+    const dim3 b(kThreads);
+    if (N <= 64) {  // 128 x 64: each wave 32 x 64
+        const int tm = (M + 127) / 128, tn = (N + 63) / 64;
+        hipLaunchKernelGGL((bgemm_f32_tiled_kernel<TA, TB, 4, 1, 2>),
+                           dim3(static_cast<unsigned>(static_cast<long long>(tm) * tn * batch)), b,
+                           0, stream, A, B, C, M, N, K, sA, sB, sC, alpha, beta, tm, tn);
+    } else {  // 128 x 128: each wave 64 x 64
+        const int tm = (M + 127) / 128, tn = (N + 127) / 128;
+        hipLaunchKernelGGL((bgemm_f32_tiled_kernel<TA, TB, 2, 2, 2>),
+                           dim3(static_cast<unsigned>(static_cast<long long>(tm) * tn * batch)), b,
+                           0, stream, A, B, C, M, N, K, sA, sB, sC, alpha, beta, tm, tn);
+    }
+}
+
 }  // namespace
 
 void launch_batched_gemm_f32(const float* A, const float* B, float* C, int M, int N, int K,
                              long long sA, long long sB, long long sC, int batch, bool transA,
                              bool transB, float alpha, float beta, hipStream_t stream) {
+    // 16-byte loads need the contiguous dimension of each operand (K or M for A, N or K for
+    // B) a multiple of 4 and 16-byte aligned bases and batch strides
+    const bool vec = ((transA ? M : K) % 4 == 0) && ((transB ? K : N) % 4 == 0) &&
+                     sA % 4 == 0 && sB % 4 == 0 && aligned16(A) && aligned16(B);
+    if (vec) {
+        if (transA) {
+            if (transB)
+                launch_tiled<true, true>(A, B, C, M, N, K, sA, sB, sC, batch, alpha, beta, stream);
+            else
+                launch_tiled<true, false>(A, B, C, M, N, K, sA, sB, sC, batch, alpha, beta, stream);
+        } else {
+            if (transB)
+                launch_tiled<false, true>(A, B, C, M, N, K, sA, sB, sC, batch, alpha, beta, stream);
+            else
+                launch_tiled<false, false>(A, B, C, M, N, K, sA, sB, sC, batch, alpha, beta,
+                                           stream);
+        }
+        return;
+    }
     const int tiles_m = (M + kBM - 1) / kBM;
     const int tiles_n = (N + kBN - 1) / kBN;
     const long long grid = static_cast<long long>(tiles_m) * tiles_n * batch;

@@ -392,11 +392,17 @@ void fwd_launch(const FwdArgs<NP>& a, hipStream_t stream) {
 
 template <int D, int NP>
 void fwd_dispatch(const FwdArgs<NP>& a, hipStream_t stream) {
-    // d = 128: one sub-block per wave fits two waves per SIMD (two sub-blocks do not)
-    if (D >= 128 || use_single_subblock(a.BH, a.T))
+    if constexpr (NP == 1 || D >= 128) {
+        // bf16 operands: one sub-block per wave at every size.  Its folded softmax (one
+        // v_exp_f32 and no fma per score, 110 VGPRs: four waves per SIMD) outruns two
+        // sub-blocks' balanced causal work (168 VGPRs, three waves): config 3 -4%,
+        // T = 16384 -3%, B4 H16 T2048 -28%.  d = 128: two sub-blocks do not fit two waves.
         fwd_launch<D, 1, NP>(a, stream);
-    else
-        fwd_launch<D, (D >= 128 ? 1 : 2), NP>(a, stream);
+    } else if (use_single_subblock(a.BH, a.T)) {
+        fwd_launch<D, 1, NP>(a, stream);
+    } else {
+        fwd_launch<D, 2, NP>(a, stream);
+    }
 }
 
 }  // namespace

@@ -122,7 +122,7 @@ __device__ __forceinline__ void store_row(uint16_t* __restrict__ head, int row, 
             o[1] = f32_to_bf16_bits(acc[dt][4 * g + 1] * mul);
             o[2] = f32_to_bf16_bits(acc[dt][4 * g + 2] * mul);
             o[3] = f32_to_bf16_bits(acc[dt][4 * g + 3] * mul);
-            *reinterpret_cast<u16x4*>(p + dt * 32 + 8 * g) = o;
+            __builtin_nontemporal_store(o, reinterpret_cast<u16x4*>(p + dt * 32 + 8 * g));
         }
     }
 }
@@ -228,7 +228,7 @@ __device__ __forceinline__ void store_planes(uint16_t* __restrict__ head, size_t
         uint16_t* p = head + i * pstride + static_cast<size_t>(row) * D + 8 * half;
 #pragma unroll
         for (int st = 0; st < D / 16; ++st)
-            *reinterpret_cast<u16x8*>(p + 16 * st) = __builtin_bit_cast(u16x8, x[st][i]);
+            __builtin_nontemporal_store(__builtin_bit_cast(u16x8, x[st][i]), reinterpret_cast<u16x8*>(p + 16 * st));
     }
 }
 
@@ -246,7 +246,7 @@ __device__ __forceinline__ void store_row(float* __restrict__ head, int row, int
             o[1] = acc[dt][4 * g + 1] * mul;
             o[2] = acc[dt][4 * g + 2] * mul;
             o[3] = acc[dt][4 * g + 3] * mul;
-            *reinterpret_cast<f32x4*>(p + dt * 32 + 8 * g) = o;
+            __builtin_nontemporal_store(o, reinterpret_cast<f32x4*>(p + dt * 32 + 8 * g));
         }
     }
 }
@@ -282,6 +282,8 @@ __device__ __forceinline__ void lds_put8(uint32_t addr, u16x4 v) {
 
 // Wave-wide: the staged rows row0 .. row0+31 that lie below T, to rows rs_bytes apart from
 // base; lane l moves chunk (64 i + l) % (RB/16) of row (64 i + l) / (RB/16) in step i.
+// The row stores of the attention outputs are nontemporal: no kernel reads them back, and
+// L2 stays with the K/V (or Q/dO) tiles that the blocks of a head share.
 template <int RB>
 __device__ __forceinline__ void stage_flush(uint32_t stage, char* __restrict__ base, int row0,
                                             int T, size_t rs_bytes, int lane) {
@@ -293,7 +295,7 @@ __device__ __forceinline__ void stage_flush(uint32_t stage, char* __restrict__ b
         const int c = g % St::kCpr;
         const u16x8 v = *(TCAMD_LDS const u16x8*)(uintptr_t)(stage + St::off(r, c));
         if (row0 + r < T)
-            *reinterpret_cast<u16x8*>(base + static_cast<size_t>(row0 + r) * rs_bytes + 16 * c) = v;
+            __builtin_nontemporal_store(v, reinterpret_cast<u16x8*>(base + static_cast<size_t>(row0 + r) * rs_bytes + 16 * c));
     }
 }
 

@@ -7,8 +7,9 @@ attention on the bf16 matrix cores, every fp32 operand carried as three bf16 pla
 significant bits) and every product as six plane products accumulated in fp32 (the
 *_f32x3 entry points; fp64 distance equal to the fp32 MFMA path's, tests/test_gpu_f32x3.py):
     attn_fwd_x3       planes of q, k, v; qkv -> O (B,H,T,d), m, l  reference model.cu:305-311
-    bwd_dq_x3         D, dQ -> dqkv[:, :, q], planes of dO         reference model.cu:609, 653
-    bwd_dkdv_x3       dK, dV -> dqkv[:, :, k and v blocks]         reference model.cu:609, 653
+    bwd_prep_x3       D = rowsum(dO*O), planes of dO                reference model.cu:609
+    bwd_dkdv_ds_x3    dK, dV -> dqkv[:, :, k and v blocks]; dS      reference model.cu:609, 653
+    bwd_dq_ds_x3      dQ = dS K -> dqkv[:, :, q block]              reference model.cu:609, 653
 bf16 default and --path packed (fp32 on the fp32 MFMA): the split-transposes are fused into
 the attention kernels' tile copies and stores, so qkv (B,T,3C) is read and dqkv (B,T,3C)
 written directly:
@@ -34,7 +35,9 @@ milliseconds of warmup alone leave the timed steps partly at ramp-up clocks (con
 duration, measured with HIP events recorded on the launch stream around every kernel of
 every timed step) against its algorithmic FLOPs:
     forward 2 units, backward dK/dV 4 units (S recompute, dP, dV, dK), backward dQ 1 unit
-    (dQ; its S and dP recomputes duplicate work already counted), unit = B*H*T^2*d.
+    (dQ; its S and dP recomputes, where it makes them, duplicate work already counted), unit =
+    B*H*T^2*d.  bwd_prep_x3 is HBM-bound: it reads O and dO (fp32) and writes the three bf16
+    planes of dO and D, 14*B*H*T*d + 4*B*H*T bytes.
 For the x3 path the roofline is the bf16 MFMA's: achieved = 6 x the algorithmic FLOPs (six
 bf16 plane products per fp32 product) per second against the bf16 peak, with the fp32
 algorithmic rate (TFLOP/s, not a fraction of any peak) beside it.
@@ -97,7 +100,8 @@ METRIC = "causal attn fwd+bwd TFLOP/s & % MFMA peak, B8 H12 T1024 d64 fp32/bf16"
 # kernel -> algorithmic FLOP units (unit = B*H*T^2*d) or HBM bytes factor
 FLOP_UNITS = {"attn_fwd": 2, "bwd_dq": 1, "bwd_dkdv": 4,
               "attn_fwd_packed": 2, "bwd_dq_packed": 1, "bwd_dkdv_packed": 4,
-              "attn_fwd_x3": 2, "bwd_dq_x3": 1, "bwd_dkdv_x3": 4}
+              "attn_fwd_x3": 2, "bwd_dq_x3": 1, "bwd_dkdv_x3": 4,
+              "bwd_dkdv_ds_x3": 4, "bwd_dq_ds_x3": 1}
 X3_PRODUCTS = 6  # bf16 plane products per fp32 product on the x3 path
 
 
@@ -194,16 +198,18 @@ class PathRunner:
         L, a = self.lib, (self.B, self.H, self.T, self.d)
         B, H, T, d = a
         if self.path == "x3":
-            # the forward splits k, v (and writes the planes of q), stage 1 writes those of dO
+            # the forward splits k, v (and writes the planes of q); the backward's three
+            # stages (packed_causal_attention_backward_f32x3 in one call)
             return (
                 ("attn_fwd_x3", lambda: L.packed_causal_attention_forward_f32x3(
                     self.qkv, self.o, B, H, T, d, self.scale, self.planes, self.m, self.l)),
-                ("bwd_dq_x3", lambda: L.packed_causal_attention_backward_dq_f32x3(
-                    self.qkv, self.o, self.do, self.m, self.l, self.dqkv, self.ws, B, H, T, d,
-                    self.scale, self.planes, True)),
-                ("bwd_dkdv_x3", lambda: L.causal_attention_backward_dkdv_f32x3(
+                ("bwd_prep_x3", lambda: L.packed_causal_attention_backward_prep_f32x3(
+                    self.qkv, self.o, self.do, self.ws, B, H, T, d, self.planes, True)),
+                ("bwd_dkdv_ds_x3", lambda: L.causal_attention_backward_dkdv_ds_f32x3(
                     self.qkv, self.m, self.l, self.ws, self.dqkv, B, H, T, d, self.scale,
                     self.planes)),
+                ("bwd_dq_ds_x3", lambda: L.causal_attention_backward_dq_ds_f32x3(
+                    self.dqkv, B, H, T, d, self.scale, self.planes)),
             )
         if self.path == "packed":
             # the split-transposes happen inside the attention kernels' tile copies/stores
@@ -244,6 +250,9 @@ class PathRunner:
         unit = float(self.B * self.H * self.T * self.T * self.d)
         if name in FLOP_UNITS:
             return FLOP_UNITS[name] * unit, "flop"
+        if name == "bwd_prep_x3":
+            n = float(self.B * self.H * self.T * self.d)
+            return 14.0 * n + 4.0 * self.B * self.H * self.T, "byte"
         elem = 2 if self.dtype == "bf16" else 4
         return 6.0 * self.B * self.T * self.C * elem, "byte"
 

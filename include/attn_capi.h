@@ -351,10 +351,12 @@ int attn_fused_causal_backward_dkdv_bf16(const attn_bf16* qkv, const attn_bf16* 
  * points.  d_head 32 or 64.
  *
  * `planes` is caller-owned device memory of attn_f32x3_workspace_bytes(B, H, T, d_head)
- * bytes (16-byte aligned) for the planes of q, k, v and dO.  The forward writes those of q,
- * k and v; a backward with kv_planes_ready = 1 reuses them (the caller guarantees that qkv
- * and the workspace are unchanged since that forward), with 0 it splits q, k and v again.  The
- * backward's d_workspace is the B*H*T floats of D, as in the other backward entry points.
+ * bytes (16-byte aligned): the planes of q, k, v and dO (4 x 3 x B*H*T*d_head bf16), then
+ * dS, B*H x n x n fp32 with n = T rounded up to 32 (the one-call backward's stage 2 writes it
+ * for its stage 3).  The forward writes the planes of q, k and v; a backward with
+ * kv_planes_ready = 1 reuses them (the caller guarantees that qkv and the workspace are
+ * unchanged since that forward), with 0 it splits q, k and v again.  The backward's
+ * d_workspace is the B*H*T floats of D, as in the other backward entry points.
  * No counterpart in the reference (an MI355X-specific form of
  * src/kernels/attention.cu:518-1012).
  * ------------------------------------------------------------------------------------------ */
@@ -375,9 +377,29 @@ int attn_fused_causal_backward_f32x3(const float* qkv, const float* o, const flo
                                      float* d_workspace, int B, int H, int T, int d_head,
                                      float scale, void* planes, int kv_planes_ready,
                                      hipStream_t stream);
-/* The two stages of those backwards.  Stage 1 writes the planes of dO (and of q, k, v unless
- * kv_planes_ready), D and dQ; stage 2 (one function for both layouts: it reads dO only
- * through its planes) writes dK and dV from the planes in `planes`. */
+/* The three stages of those backwards, in order: prep writes the planes of dO (and of q, k, v
+ * unless kv_planes_ready) and D; dkdv_ds (one function for both layouts: it reads dO only
+ * through its planes) writes dK and dV into dqkv and dS into `planes`; dq_ds writes dQ into
+ * dqkv from dS and the planes of k. */
+int attn_packed_causal_backward_prep_f32x3(const float* qkv, const float* o,
+                                           const float* do_ptr, float* d_workspace, int B,
+                                           int H, int T, int d_head, void* planes,
+                                           int kv_planes_ready, hipStream_t stream);
+int attn_fused_causal_backward_prep_f32x3(const float* qkv, const float* o, const float* do_ptr,
+                                          float* d_workspace, int B, int H, int T, int d_head,
+                                          void* planes, int kv_planes_ready,
+                                          hipStream_t stream);
+int attn_causal_backward_dkdv_ds_f32x3(const float* qkv, const float* m_ptr, const float* l_ptr,
+                                       const float* d_workspace, float* dqkv, int B, int H,
+                                       int T, int d_head, float scale, void* planes,
+                                       hipStream_t stream);
+int attn_causal_backward_dq_ds_f32x3(float* dqkv, int B, int H, int T, int d_head, float scale,
+                                     const void* planes, hipStream_t stream);
+/* The same backward in the other order, in two stages: stage 1 writes the planes of dO (and
+ * of q, k, v unless kv_planes_ready), D and dQ, computing S and dP itself; stage 2 (one
+ * function for both layouts) writes dK and dV from the planes in `planes`.  The same D, dK
+ * and dV as the three stages, bitwise; dQ within fp32 rounding of theirs.  Does not use the
+ * workspace's dS. */
 int attn_packed_causal_backward_dq_f32x3(const float* qkv, const float* o,
                                          const float* do_ptr, const float* m_ptr,
                                          const float* l_ptr, float* dqkv, float* d_workspace,

@@ -157,7 +157,9 @@ def test_f32x3_validation(lib):
     """The three-plane fp32 entry points validate before any HIP call."""
     f = ctypes.c_float
     raw = lib.raw()
-    assert raw.attn_f32x3_workspace_bytes(2, 3, 40, 64) == 4 * 3 * 2 * 3 * 40 * 64 * 2
+    # planes of q, k, v, dO (3 x bf16 each) and the one-call backward's dS (64 x 64 fp32 per
+    # head: T rounded up to 32)
+    assert raw.attn_f32x3_workspace_bytes(2, 3, 40, 64) == 4 * 3 * 2 * 3 * 40 * 64 * 2 + 6 * 64 * 64 * 4
     assert raw.attn_f32x3_workspace_bytes(0, 3, 40, 64) == 0
     fwd = lambda d=64, planes=FAKE, qkv=FAKE, scale=0.125: lib.call(
         "attn_packed_causal_forward_f32x3", qkv, FAKE, 1, 2, 8, d, f(scale), None, None,
@@ -178,6 +180,26 @@ def test_f32x3_validation(lib):
         assert bwd(name, d=128) == BAD_HEAD_DIM
     assert lib.call("attn_causal_backward_dkdv_f32x3", FAKE, FAKE, FAKE, FAKE, FAKE, 1, 2, 8,
                     64, f(0.125), None, None) == NULLPTR
+    # the three stages of the one-call backward
+    for name in ("attn_packed_causal_backward_prep_f32x3", "attn_fused_causal_backward_prep_f32x3"):
+        prep = lambda planes=FAKE, ws=FAKE, d=64: lib.call(name, FAKE, FAKE, FAKE, ws, 1, 2, 8, d,
+                                                           planes, 1, None)
+        assert prep(planes=None) == NULLPTR
+        assert prep(ws=None) == NULLPTR
+        assert prep(d=128) == BAD_HEAD_DIM
+        assert prep(planes=MISALIGNED) == MISALIGN
+    dkdv = lambda planes=FAKE, d=64, scale=0.125: lib.call(
+        "attn_causal_backward_dkdv_ds_f32x3", FAKE, FAKE, FAKE, FAKE, FAKE, 1, 2, 8, d, f(scale),
+        planes, None)
+    assert dkdv(planes=None) == NULLPTR
+    assert dkdv(d=48) == BAD_HEAD_DIM
+    assert dkdv(scale=0.0) == BAD_VALUE
+    dq = lambda dqkv=FAKE, planes=FAKE, d=64: lib.call(
+        "attn_causal_backward_dq_ds_f32x3", dqkv, 1, 2, 8, d, f(0.125), planes, None)
+    assert dq(dqkv=None) == NULLPTR
+    assert dq(planes=None) == NULLPTR
+    assert dq(d=128) == BAD_HEAD_DIM
+    assert dq(dqkv=MISALIGNED) == MISALIGN
     assert lib.call("attn_tiled_causal_forward_f32x3", FAKE, FAKE, FAKE, FAKE, 1, 2, 8, 64,
                     f(0.125), None, None, MISALIGNED, None) == MISALIGN
     assert lib.call("attn_tiled_causal_backward_f32x3", *([FAKE] * 11), 1, 2, 8, 128,

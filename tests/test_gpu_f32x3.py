@@ -114,7 +114,8 @@ def test_forward_closed_forms(lib):
 
 def test_workspace_and_validation(lib):
     B, H, T, d = 2, 3, 40, 64
-    assert lib.f32x3_workspace_bytes(B, H, T, d) == 4 * 3 * B * H * T * d * 2
+    n = (T + 31) // 32 * 32  # the one-call backward's dS: n x n fp32 per head
+    assert lib.f32x3_workspace_bytes(B, H, T, d) == 4 * 3 * B * H * T * d * 2 + B * H * n * n * 4
     assert lib.f32x3_workspace_bytes(0, H, T, d) == 0
     qkv = torch.zeros((B, T, 3 * H * d), device="cuda:0")
     o = torch.empty((B, H, T, d), device="cuda:0")
@@ -179,8 +180,16 @@ def test_backward_vs_oracle(lib, B, H, T, d, merged, kv_ready):
 
 
 def test_backward_config2_against_fp64(lib):
-    """every gradient within the gate of torch fp32 and as close to fp64
-    as the fp32 MFMA path's."""
+    """every gradient within the gate of torch fp32, and as close to fp64
+    as the fp32 MFMA path's: max-abs within 3x of the larger of that path's and torch fp32's,
+    rms within 4x of that path's (measured: O 1.0x; dQ, dK, dV 2.4x - 3.0x, the rounding of
+    P and dS to planes; a missing plane product would be orders of magnitude more).  The
+    max-abs factor is 3, not 2, for dQ: it is computed from the dS
+    of the dK/dV stage (whose dK carries the same dS), and on these inputs one dS element of
+    the 50M (row 346, key 246 of head (7, 0)) is 5 ulp off in its score, the tail of 24 fp32
+    accumulations, which puts dQ's max-abs at 2.2x the fp32 MFMA path's; its rms is that of
+    the two-stage order (9.8e-8), and other seeds put the two orders' max-abs side by
+    side."""
     B, H, T, d = 8, 12, 1024, 64
     g = torch.Generator(device="cpu").manual_seed(42)
     qkv = torch.randn((B, T, 3 * H * d), generator=g)
@@ -200,14 +209,17 @@ def test_backward_config2_against_fp64(lib):
     q, k, v = heads(qkv, B, H, T, d)
     want = ref.attention_fwd_bwd(q, k, v, do, 0.125, dtype=torch.float32)
     w64 = ref.attention_fwd_bwd(q, k, v, do, 0.125, dtype=torch.float64)
+    rms = lambda a, b: float(np.sqrt(np.mean((a.astype(np.float64) - b) ** 2)))
     for n in ("o", "dq", "dk", "dv"):
         w = getattr(w64, n).numpy()
         e = (max_abs(got[n].numpy(), w), max_abs(mf[n].numpy(), w),
              max_abs(getattr(want, n).numpy(), w))
+        r = (rms(got[n].numpy(), w), rms(mf[n].numpy(), w))
         print(f"config2 {n} max-abs to fp64 (x3, mfma f32, torch f32): "
-              f"{e[0]:.2e} {e[1]:.2e} {e[2]:.2e}")
+              f"{e[0]:.2e} {e[1]:.2e} {e[2]:.2e}; rms (x3, mfma f32): {r[0]:.2e} {r[1]:.2e}")
         assert max_abs(got[n].numpy(), getattr(want, n).numpy()) <= TOL
-        assert e[0] <= 2 * max(e[1], e[2])
+        assert e[0] <= 3 * max(e[1], e[2])
+        assert r[0] <= 4 * r[1]
 
 
 def test_backward_reference_kat(lib):
@@ -227,9 +239,45 @@ def test_backward_reference_kat(lib):
 
 
 @pytest.mark.parametrize("merged", [False, True])
+def test_three_stages_equal_one_call(lib, merged):
+    """prep, dkdv_ds and dq_ds launched one by one give bitwise the one-call backward's
+    results, over a workspace whose dS area holds NaNs from the start (every element dq_ds
+    reads is written by dkdv_ds first)."""
+    B, H, T, d = 2, 3, 300, 64
+    g = torch.Generator(device="cpu").manual_seed(19)
+    qkv = torch.randn((B, T, 3 * H * d), generator=g).to("cuda:0")
+    do = torch.randn((B, H, T, d), generator=g).to("cuda:0")
+    if merged:
+        do = do.permute(0, 2, 1, 3).reshape(B, T, H * d).contiguous()
+    shape = (B, T, H * d) if merged else (B, H, T, d)
+    o = torch.empty(shape, device="cuda:0")
+    m = torch.empty((B, H, T), device="cuda:0")
+    l = torch.empty_like(m)
+    ws = planes(lib, B, H, T, d)
+    fam = "fused" if merged else "packed"
+    getattr(lib, f"{fam}_causal_attention_forward_f32x3")(qkv, o, B, H, T, d, 0.125, ws, m, l)
+    ws[4 * 3 * B * H * T * d * 2:].view(torch.float32).fill_(float("nan"))
+    ws2 = ws.clone()
+    one, D1 = torch.full_like(qkv, float("nan")), torch.full_like(m, float("nan"))
+    getattr(lib, f"{fam}_causal_attention_backward_f32x3")(qkv, o, do, m, l, one, D1, B, H, T,
+                                                          d, 0.125, ws, True)
+    three, D3 = torch.full_like(qkv, float("nan")), torch.full_like(m, float("nan"))
+    getattr(lib, f"{fam}_causal_attention_backward_prep_f32x3")(qkv, o, do, D3, B, H, T, d, ws2,
+                                                               True)
+    lib.causal_attention_backward_dkdv_ds_f32x3(qkv, m, l, D3, three, B, H, T, d, 0.125, ws2)
+    lib.causal_attention_backward_dq_ds_f32x3(three, B, H, T, d, 0.125, ws2)
+    torch.cuda.synchronize()
+    assert torch.isfinite(one).all()
+    assert torch.equal(one, three) and torch.equal(D1, D3)
+
+
+@pytest.mark.parametrize("merged", [False, True])
 def test_staged_backward_equals_one_call(lib, merged):
-    """Stage 1 (planes of q and dO, D, dQ) then stage 2 (dK, dV) give bitwise the one-call
-    backward's results."""
+    """Stage 1 (planes of q and dO, D, dQ) then stage 2 (dK, dV) against the one-call backward
+    (D and the planes of dO, then dK and dV writing dS, then dQ = dS K): the same D, dK and dV
+    bitwise (the same operations in the same order), dQ within fp32 rounding (the staged dQ
+    recomputes S and dP with K as the A operand, the one-call path keeps the dK/dV stage's
+    dS, so their dS differ in the last bits)."""
     B, H, T, d = 2, 3, 300, 64
     g = torch.Generator(device="cpu").manual_seed(9)
     qkv = torch.randn((B, T, 3 * H * d), generator=g).to("cuda:0")
@@ -251,7 +299,11 @@ def test_staged_backward_equals_one_call(lib, merged):
                                                              T, d, 0.125, ws, True)
     lib.causal_attention_backward_dkdv_f32x3(qkv, m, l, D2, two, B, H, T, d, 0.125, ws)
     torch.cuda.synchronize()
-    assert torch.equal(one, two) and torch.equal(D1, D2)
+    C = H * d
+    assert torch.equal(one[..., C:], two[..., C:]) and torch.equal(D1, D2)
+    dq1, dq2 = one[..., :C], two[..., :C]
+    assert torch.isfinite(dq1).all()
+    assert (dq1 - dq2).abs().max().item() <= 2e-6 * dq2.abs().max().item()
 
 
 @pytest.mark.parametrize("B,H,T,d", [(16, 16, 2048, 64), (16, 16, 1024, 32)])

@@ -105,6 +105,10 @@ SIGNATURES = {
         [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P, _I, _P],
     "attn_fused_causal_backward_f32x3":
         [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P, _I, _P],
+    "attn_packed_causal_backward_prep_f32x3": [_P, _P, _P, _P, _I, _I, _I, _I, _P, _I, _P],
+    "attn_fused_causal_backward_prep_f32x3": [_P, _P, _P, _P, _I, _I, _I, _I, _P, _I, _P],
+    "attn_causal_backward_dkdv_ds_f32x3": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P, _P],
+    "attn_causal_backward_dq_ds_f32x3": [_P, _I, _I, _I, _I, _F, _P, _P],
     "attn_packed_causal_backward_dq_f32x3":
         [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P, _I, _P],
     "attn_fused_causal_backward_dq_f32x3":
@@ -469,10 +473,57 @@ def fused_causal_attention_backward_f32x3(qkv, o, dO, m, l, dqkv, workspace, B, 
                         planes, kv_planes_ready, stream)
 
 
+def _backward_prep_f32x3(family, qkv, o, dO, workspace, B, H, T, d_head, planes,
+                         kv_planes_ready, stream):
+    n, r = B * H * T * d_head, B * H * T
+    f32 = _dt(False)
+    check(call(f"attn_{family}_causal_backward_prep_f32x3", _ptr(qkv, f32, 3 * n, "qkv"),
+               _ptr(o, f32, n, "o"), _ptr(dO, f32, n, "dO"),
+               _ptr(workspace, f32, r, "workspace"), B, H, T, d_head,
+               _planes_ptr(planes, B, H, T, d_head), 1 if kv_planes_ready else 0,
+               _stream(stream)), f"{family}_causal_attention_backward_prep_f32x3")
+
+
+def packed_causal_attention_backward_prep_f32x3(qkv, o, dO, workspace, B, H, T, d_head, planes,
+                                                kv_planes_ready=False, stream=None):
+    """Stage 1 of packed_causal_attention_backward_f32x3: D and the planes of dO (and of q, k,
+    v unless kv_planes_ready)."""
+    _backward_prep_f32x3("packed", qkv, o, dO, workspace, B, H, T, d_head, planes,
+                         kv_planes_ready, stream)
+
+
+def fused_causal_attention_backward_prep_f32x3(qkv, o, dO, workspace, B, H, T, d_head, planes,
+                                               kv_planes_ready=False, stream=None):
+    """Stage 1 of fused_causal_attention_backward_f32x3."""
+    _backward_prep_f32x3("fused", qkv, o, dO, workspace, B, H, T, d_head, planes,
+                         kv_planes_ready, stream)
+
+
+def causal_attention_backward_dkdv_ds_f32x3(qkv, m, l, workspace, dqkv, B, H, T, d_head, scale,
+                                            planes, stream=None):
+    """Stage 2 of the one-call *_f32x3 backwards: dK, dV into dqkv, dS into `planes`."""
+    n, r = B * H * T * d_head, B * H * T
+    f32 = _dt(False)
+    check(call("attn_causal_backward_dkdv_ds_f32x3", _ptr(qkv, f32, 3 * n, "qkv"),
+               _ptr(m, f32, r, "m"), _ptr(l, f32, r, "l"), _ptr(workspace, f32, r, "workspace"),
+               _ptr(dqkv, f32, 3 * n, "dqkv"), B, H, T, d_head, float(scale),
+               _planes_ptr(planes, B, H, T, d_head), _stream(stream)),
+          "causal_attention_backward_dkdv_ds_f32x3")
+
+
+def causal_attention_backward_dq_ds_f32x3(dqkv, B, H, T, d_head, scale, planes, stream=None):
+    """Stage 3 of the one-call *_f32x3 backwards: dQ into dqkv from dS and k's planes."""
+    n = B * H * T * d_head
+    check(call("attn_causal_backward_dq_ds_f32x3", _ptr(dqkv, _dt(False), 3 * n, "dqkv"), B, H,
+               T, d_head, float(scale), _planes_ptr(planes, B, H, T, d_head), _stream(stream)),
+          "causal_attention_backward_dq_ds_f32x3")
+
+
 def packed_causal_attention_backward_dq_f32x3(qkv, o, dO, m, l, dqkv, workspace, B, H, T,
                                               d_head, scale, planes, kv_planes_ready=False,
                                               stream=None):
-    """Stage 1 of packed_causal_attention_backward_f32x3 (D, dQ, planes of dO)."""
+    """Stage 1 of the two-stage order of packed_causal_attention_backward_f32x3 (D, dQ, planes
+    of dO; computes S and dP itself)."""
     _qkv_backward_f32x3("packed", qkv, o, dO, m, l, dqkv, workspace, B, H, T, d_head, scale,
                         planes, kv_planes_ready, stream, "_dq")
 
@@ -487,7 +538,7 @@ def fused_causal_attention_backward_dq_f32x3(qkv, o, dO, m, l, dqkv, workspace, 
 
 def causal_attention_backward_dkdv_f32x3(qkv, m, l, workspace, dqkv, B, H, T, d_head, scale,
                                          planes, stream=None):
-    """Stage 2 of the *_f32x3 backwards (dK, dV from the planes stage 1 wrote)."""
+    """Stage 2 of the two-stage order (dK, dV from the planes stage 1 wrote)."""
     n, r = B * H * T * d_head, B * H * T
     f32 = _dt(False)
     check(call("attn_causal_backward_dkdv_f32x3", _ptr(qkv, f32, 3 * n, "qkv"),

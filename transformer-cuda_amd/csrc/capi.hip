@@ -219,7 +219,9 @@ int packed_backward(const E* qkv, const E* o, const E* dO, const float* m, const
 }
 
 // ---- fp32 on bf16 MFMAs: operands as three bf16 planes in a caller workspace -------------
-// Workspace: four tensors (q, k, v, dO) x three planes x N = B*H*T*d bf16, head-major.
+// Workspace: four tensors (q, k, v, dO) x three planes x N = B*H*T*d bf16, head-major; then
+// dS, B*H x n x n fp32 with n = T rounded up to 32 (the full backward's stage 2 writes it,
+// its stage 1 reads it).
 
 constexpr int kPlaneTensors = 4;
 constexpr int kPlanes = 3;
@@ -229,6 +231,13 @@ size_t plane_elems(int B, int H, int T, int d) {
 }
 uint16_t* plane_tensor(void* planes, size_t N, int tensor) {
     return static_cast<uint16_t*>(planes) + static_cast<size_t>(tensor) * kPlanes * N;
+}
+size_t ds_elems(int B, int H, int T) {
+    const size_t n = static_cast<size_t>(tcamd::ds_rows(T));
+    return static_cast<size_t>(B) * H * n * n;
+}
+float* ds_area(void* planes, size_t N) {
+    return reinterpret_cast<float*>(plane_tensor(planes, N, kPlaneTensors));
 }
 
 int check_f32x3(int B, int H, int T, int d, float scale) {
@@ -313,14 +322,76 @@ int packed_backward_dkdv_f32x3(const float* qkv, const float* m, const float* l,
     return launch_status();
 }
 
+// The one-call backward runs three stages: (1) the planes of q, k, v unless the forward's
+// are ready, D and the planes of dO; (2) dK and dV, writing dS; (3) dQ from dS and k's
+// planes.  dS carries the products of S and dP from (2) to (3), which would otherwise compute
+// them again.
+int packed_backward_prep_f32x3(const float* qkv, const float* o, const float* dO, float* ws,
+                               int B, int H, int T, int d, void* planes, int kv_ready,
+                               bool merged, hipStream_t stream) {
+    if (qkv == nullptr || o == nullptr || dO == nullptr || ws == nullptr || planes == nullptr)
+        return ATTN_ERROR_NULL_POINTER;
+    const int st = check_f32x3(B, H, T, d, 1.0f);
+    if (st != ATTN_SUCCESS) return st;
+    if (!aligned16(qkv) || !aligned16(o) || !aligned16(dO) || !aligned16(planes))
+        return ATTN_ERROR_MISALIGNED;
+    const size_t N = plane_elems(B, H, T, d);
+    clear_error();
+    if (!kv_ready)  // q, k, v in one launch
+        tcamd::launch_split_planes(qkv, tcamd::packed_qkv_view(H, T, d), plane_tensor(planes, N, 0),
+                                   N, B * H, T, d, stream, 3, static_cast<size_t>(H) * d,
+                                   kPlanes * N);
+    tcamd::launch_bwd_prep_f32x3(o, dO, out_view(H, T, d, merged), plane_tensor(planes, N, 3),
+                                 tcamd::head_major_view(H, T, d), N, ws, B * H, T, d, stream);
+    return launch_status();
+}
+
+int packed_backward_dkdv_ds_f32x3(const float* qkv, const float* m, const float* l,
+                                  const float* ws, float* dqkv, int B, int H, int T, int d,
+                                  float scale, void* planes, hipStream_t stream) {
+    if (qkv == nullptr || m == nullptr || l == nullptr || ws == nullptr || dqkv == nullptr ||
+        planes == nullptr)
+        return ATTN_ERROR_NULL_POINTER;
+    const int st = check_f32x3(B, H, T, d, scale);
+    if (st != ATTN_SUCCESS) return st;
+    if (!aligned16(qkv) || !aligned16(dqkv) || !aligned16(planes)) return ATTN_ERROR_MISALIGNED;
+    const size_t N = plane_elems(B, H, T, d), C = static_cast<size_t>(H) * d;
+    const tcamd::HeadView xv = tcamd::packed_qkv_view(H, T, d);
+    clear_error();
+    tcamd::launch_flash_bwd_dkdv_f32x3(plane_tensor(planes, N, 0), plane_tensor(planes, N, 3),
+                                       tcamd::head_major_view(H, T, d), N, qkv + C, qkv + 2 * C,
+                                       xv, m, l, ws, dqkv + C, dqkv + 2 * C, xv, B * H, T, d,
+                                       scale, stream, ds_area(planes, N));
+    return launch_status();
+}
+
+int packed_backward_dq_ds_f32x3(float* dqkv, int B, int H, int T, int d, float scale,
+                                const void* planes, hipStream_t stream) {
+    if (dqkv == nullptr || planes == nullptr) return ATTN_ERROR_NULL_POINTER;
+    const int st = check_f32x3(B, H, T, d, scale);
+    if (st != ATTN_SUCCESS) return st;
+    if (!aligned16(dqkv) || !aligned16(planes)) return ATTN_ERROR_MISALIGNED;
+    const size_t N = plane_elems(B, H, T, d);
+    void* pl = const_cast<void*>(planes);
+    clear_error();
+    tcamd::launch_flash_bwd_dq_ds_f32x3(plane_tensor(pl, N, 1), tcamd::head_major_view(H, T, d),
+                                        N, ds_area(pl, N), dqkv, tcamd::packed_qkv_view(H, T, d),
+                                        B * H, T, d, scale, stream);
+    return launch_status();
+}
+
 int packed_backward_f32x3(const float* qkv, const float* o, const float* dO, const float* m,
                           const float* l, float* dqkv, float* ws, int B, int H, int T, int d,
                           float scale, void* planes, int kv_ready, bool merged,
                           hipStream_t stream) {
-    const int st = packed_backward_dq_f32x3(qkv, o, dO, m, l, dqkv, ws, B, H, T, d, scale,
-                                            planes, kv_ready, merged, stream);
+    if (o == nullptr || planes == nullptr) return ATTN_ERROR_NULL_POINTER;
+    int st = check_packed_bwd(qkv, dO, m, l, dqkv, ws, B, H, T, d, scale);
     if (st != ATTN_SUCCESS) return st;
-    return packed_backward_dkdv_f32x3(qkv, m, l, ws, dqkv, B, H, T, d, scale, planes, stream);
+    st = packed_backward_prep_f32x3(qkv, o, dO, ws, B, H, T, d, planes, kv_ready, merged, stream);
+    if (st != ATTN_SUCCESS) return st;
+    st = packed_backward_dkdv_ds_f32x3(qkv, m, l, ws, dqkv, B, H, T, d, scale, planes, stream);
+    if (st != ATTN_SUCCESS) return st;
+    return packed_backward_dq_ds_f32x3(dqkv, B, H, T, d, scale, planes, stream);
 }
 
 // ---- the same path from separate head-major q, k, v (the reference's tiled launchers) ----
@@ -395,6 +466,39 @@ int tiled_backward_dkdv_f32x3(const float* k, const float* v, const float* m, co
     clear_error();
     tcamd::launch_flash_bwd_dkdv_f32x3(plane_tensor(pl, N, 0), plane_tensor(pl, N, 3), hv, N, k,
                                        v, hv, m, l, ws, dk, dv, hv, B * H, T, d, scale, stream);
+    return launch_status();
+}
+
+// The full backward, stage 2 first (as packed_backward_f32x3).
+int tiled_backward_f32x3(const float* q, const float* k, const float* v, const float* o,
+                         const float* dO, const float* m, const float* l, float* dq, float* dk,
+                         float* dv, float* ws, int B, int H, int T, int d, float scale,
+                         void* planes, int kv_ready, hipStream_t stream) {
+    if (q == nullptr || k == nullptr || v == nullptr || o == nullptr || dO == nullptr ||
+        m == nullptr || l == nullptr || dq == nullptr || dk == nullptr || dv == nullptr ||
+        ws == nullptr)
+        return ATTN_ERROR_NULL_POINTER;
+    const int st = check_tiled_f32x3(B, H, T, d, scale, planes);
+    if (st != ATTN_SUCCESS) return st;
+    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o) || !aligned16(dO) ||
+        !aligned16(dq) || !aligned16(dk) || !aligned16(dv))
+        return ATTN_ERROR_MISALIGNED;
+    const size_t N = plane_elems(B, H, T, d);
+    const tcamd::HeadView hv = tcamd::head_major_view(H, T, d);
+    float* ds = ds_area(planes, N);
+    clear_error();
+    if (!kv_ready) {
+        tcamd::launch_split_planes(q, hv, plane_tensor(planes, N, 0), N, B * H, T, d, stream);
+        tcamd::launch_split_planes(k, hv, plane_tensor(planes, N, 1), N, B * H, T, d, stream);
+        tcamd::launch_split_planes(v, hv, plane_tensor(planes, N, 2), N, B * H, T, d, stream);
+    }
+    tcamd::launch_bwd_prep_f32x3(o, dO, hv, plane_tensor(planes, N, 3), hv, N, ws, B * H, T, d,
+                                 stream);
+    tcamd::launch_flash_bwd_dkdv_f32x3(plane_tensor(planes, N, 0), plane_tensor(planes, N, 3), hv,
+                                       N, k, v, hv, m, l, ws, dk, dv, hv, B * H, T, d, scale,
+                                       stream, ds);
+    tcamd::launch_flash_bwd_dq_ds_f32x3(plane_tensor(planes, N, 1), hv, N, ds, dq, hv, B * H, T,
+                                        d, scale, stream);
     return launch_status();
 }
 
@@ -964,7 +1068,8 @@ int attn_fused_causal_backward_bf16(const attn_bf16* qkv, const attn_bf16* o,
 size_t attn_f32x3_workspace_bytes(int B, int H, int T, int d_head) {
     if (B <= 0 || H <= 0 || T <= 0 || d_head <= 0) return 0;
     return static_cast<size_t>(kPlaneTensors) * kPlanes * plane_elems(B, H, T, d_head) *
-           sizeof(uint16_t);
+               sizeof(uint16_t) +
+           ds_elems(B, H, T) * sizeof(float);
 }
 
 int attn_packed_causal_forward_f32x3(const float* qkv, float* out, int B, int H, int T,
@@ -997,6 +1102,35 @@ int attn_fused_causal_backward_f32x3(const float* qkv, const float* o, const flo
                                      hipStream_t stream) {
     return packed_backward_f32x3(qkv, o, do_ptr, m_ptr, l_ptr, dqkv, d_workspace, B, H, T,
                                  d_head, scale, planes, kv_planes_ready, true, stream);
+}
+
+int attn_packed_causal_backward_prep_f32x3(const float* qkv, const float* o,
+                                           const float* do_ptr, float* d_workspace, int B,
+                                           int H, int T, int d_head, void* planes,
+                                           int kv_planes_ready, hipStream_t stream) {
+    return packed_backward_prep_f32x3(qkv, o, do_ptr, d_workspace, B, H, T, d_head, planes,
+                                      kv_planes_ready, false, stream);
+}
+
+int attn_fused_causal_backward_prep_f32x3(const float* qkv, const float* o, const float* do_ptr,
+                                          float* d_workspace, int B, int H, int T, int d_head,
+                                          void* planes, int kv_planes_ready,
+                                          hipStream_t stream) {
+    return packed_backward_prep_f32x3(qkv, o, do_ptr, d_workspace, B, H, T, d_head, planes,
+                                      kv_planes_ready, true, stream);
+}
+
+int attn_causal_backward_dkdv_ds_f32x3(const float* qkv, const float* m_ptr, const float* l_ptr,
+                                       const float* d_workspace, float* dqkv, int B, int H,
+                                       int T, int d_head, float scale, void* planes,
+                                       hipStream_t stream) {
+    return packed_backward_dkdv_ds_f32x3(qkv, m_ptr, l_ptr, d_workspace, dqkv, B, H, T, d_head,
+                                         scale, planes, stream);
+}
+
+int attn_causal_backward_dq_ds_f32x3(float* dqkv, int B, int H, int T, int d_head, float scale,
+                                     const void* planes, hipStream_t stream) {
+    return packed_backward_dq_ds_f32x3(dqkv, B, H, T, d_head, scale, planes, stream);
 }
 
 int attn_packed_causal_backward_dq_f32x3(const float* qkv, const float* o,
@@ -1059,11 +1193,8 @@ int attn_tiled_causal_backward_f32x3(const float* q, const float* k, const float
                                      float* d_workspace, int B, int H, int T, int d_head,
                                      float scale, void* planes, int kv_planes_ready,
                                      hipStream_t stream) {
-    const int st = tiled_backward_dq_f32x3(q, k, v, o, do_ptr, m_ptr, l_ptr, dq, d_workspace, B,
-                                           H, T, d_head, scale, planes, kv_planes_ready, stream);
-    if (st != ATTN_SUCCESS) return st;
-    return tiled_backward_dkdv_f32x3(k, v, m_ptr, l_ptr, d_workspace, dk, dv, B, H, T, d_head,
-                                     scale, planes, stream);
+    return tiled_backward_f32x3(q, k, v, o, do_ptr, m_ptr, l_ptr, dq, dk, dv, d_workspace, B, H,
+                                T, d_head, scale, planes, kv_planes_ready, stream);
 }
 
 }  // extern "C"

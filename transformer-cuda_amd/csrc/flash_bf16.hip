@@ -145,6 +145,33 @@ struct DqSub {
     f32x16 acc[D / 32];    // dQ^T
 };
 
+// D = rowsum(dO o O) of an fp32 row, the share of lane half `half`: the dot products of the
+// 8-element chunks 2j + half (an fma chain each, elements in order), summed as a pairwise
+// tree over j; xhalf_sum of the two shares completes the row.  The same sums, in the same
+// order, as bwd_prep_f32x3_kernel's butterfly over the chunks.
+template <int D>
+__device__ __forceinline__ float chunk_dot_tree(const float* __restrict__ gp,
+                                                const float* __restrict__ op, int half) {
+    float c[D / 16];
+#pragma unroll
+    for (int j = 0; j < D / 16; ++j) {
+        c[j] = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; e += 4) {
+            const f32x4 a = *reinterpret_cast<const f32x4*>(gp + 16 * j + 8 * half + e);
+            const f32x4 b = *reinterpret_cast<const f32x4*>(op + 16 * j + 8 * half + e);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) c[j] = fmaf(a[i], b[i], c[j]);
+        }
+    }
+#pragma unroll
+    for (int w = 1; w < D / 16; w *= 2) {
+#pragma unroll
+        for (int j = 0; j < D / 16; j += 2 * w) c[j] += c[j + w];
+    }
+    return c[0];
+}
+
 // qh: this head's q (rows qrs apart); oh, gh: its o and dO (rows ors apart).  Q is held
 // pre-multiplied by c = scale*log2 e (NP = 1: rounded to bf16, one extra rounding of ~2^-9
 // relative per element; NP = 3: in fp32, then split), so that the scores come out in the
@@ -169,18 +196,8 @@ __device__ __forceinline__ void dq_init(DqSub<D, NP>& sb, const InT<NP>* __restr
                             part);
         }
     } else if (qi < T) {
-        const float* gp = gh + static_cast<size_t>(qi) * ors;
-        const float* op = oh + static_cast<size_t>(qi) * ors;
-#pragma unroll
-        for (int j = 0; j < D / 16; ++j) {
-#pragma unroll
-            for (int e = 0; e < 8; e += 4) {
-                const f32x4 a = *reinterpret_cast<const f32x4*>(gp + 16 * j + 8 * half + e);
-                const f32x4 b = *reinterpret_cast<const f32x4*>(op + 16 * j + 8 * half + e);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) part = fmaf(a[i], b[i], part);
-            }
-        }
+        part = chunk_dot_tree<D>(gh + static_cast<size_t>(qi) * ors,
+                                 oh + static_cast<size_t>(qi) * ors, half);
     }
     load_operand<D, NP, true>(sb.q, qh, qi, T, half, qrs, c);
     const float dlt = xhalf_sum(part);
@@ -432,13 +449,24 @@ __device__ __forceinline__ void dkdv_scores(const HalfAddr<D>& a, const bf16x8 (
     }
 }
 
+// Where a wave's dS values of a 32-query step go: row qb of its head's dS (wave-uniform),
+// rows ld elements apart; the lane's element of accumulator row r is at
+// row + (8*(r/4) + r%4)*ld + lane_off (lane_off = 4*half*ld + key).  zero: the lane's key
+// lies past T (written as zeros).
+struct DsOut {
+    float* row = nullptr;
+    int ld = 0;
+    uint32_t lane_off = 0;
+    bool zero = false;
+};
+
 // P = 2^S' (0 where the query precedes the key, on the diagonal half tile) and
 // dS = P o dP'; dV^T += dO^T P, dK^T += Q^T dS.
-template <int D, bool MASK, int NP>
+template <int D, bool MASK, int NP, bool DS = false>
 __device__ __forceinline__ void dkdv_update(const HalfAddr<D>& a, f32x16& s, const f32x16& dp,
                                             f32x16 (&dk_acc)[D / 32],
                                             f32x16 (&dv_acc)[D / 32], int qb, int kj,
-                                            int half) {
+                                            int half, const DsOut& dso = DsOut{}) {
     constexpr uint32_t kPlane = Swz<D, kQueryTile<NP>>::kBytes;
 #pragma unroll
     for (int r = 0; r < 16; ++r) s[r] = exp2_fast(s[r]);
@@ -486,6 +514,13 @@ __device__ __forceinline__ void dkdv_update(const HalfAddr<D>& a, f32x16& s, con
         }
 #pragma unroll
         for (int r = 0; r < 16; ++r) s[r] *= dp[r];
+        if constexpr (DS) {  // a 32-lane store covers one query's 32 keys (128 bytes)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                float* row = dso.row + static_cast<size_t>(8 * (r / 4) + r % 4) * dso.ld;
+                row[dso.lane_off] = dso.zero ? 0.0f : s[r];
+            }
+        }
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
             bf16x8 db[NP];
@@ -515,10 +550,16 @@ struct DkdvArgs {
     float scale;
     HeadView qv, gtv, kv, gv;
     size_t pstride;
+    // NP = 3, optional: dS out (fp32), for a dQ stage that reads it instead of recomputing S
+    // and dP.  Head bh: ds_n x ds_n (T rounded up to 32) from ds + bh*ds_n*ds_n, rows =
+    // queries, columns = keys; written where query >= the first key of the key's 32-key
+    // block, keys >= T as zeros.
+    float* ds = nullptr;
+    int ds_n = 0;
 };
 
-// NW waves per workgroup; wave w owns keys k0 + 32w ...
-template <int D, int NW, int NP>
+// NW waves per workgroup; wave w owns keys k0 + 32w ...  DS: write dS out (NP = 3, a.ds).
+template <int D, int NW, int NP, bool DS = false>
 __global__ __launch_bounds__(kWave* NW, NP == 1 ? 1 : 2) void flash_bwd_dkdv_bf16_kernel(DkdvArgs<NP> a,
                                                                        int nblk) {
     constexpr int KT = kQueryTile<NP>;
@@ -705,8 +746,15 @@ __global__ __launch_bounds__(kWave* NW, NP == 1 ? 1 : 2) void flash_bwd_dkdv_bf1
             h.gx = gx_lds + xrow;
             f32x16 s1, dp1;
             dkdv_scores<D, NP>(h, kr, vr, one, s1, dp1);
-            dkdv_update<D, decltype(mask)::value, NP>(h, s1, dp1, dk_acc, dv_acc, KT * kt, kj,
-                                                      half);
+            DsOut dso;
+            if constexpr (DS) {
+                dso.row = a.ds + (static_cast<size_t>(bh) * a.ds_n + KT * kt) * a.ds_n;
+                dso.ld = a.ds_n;
+                dso.lane_off = static_cast<uint32_t>(4 * half * a.ds_n + kj);
+                dso.zero = kj >= T;
+            }
+            dkdv_update<D, decltype(mask)::value, NP, DS>(h, s1, dp1, dk_acc, dv_acc, KT * kt,
+                                                          kj, half, dso);
         };
         const int tstart = kw < T ? kw / KT : ntile;
         int kt = t0;
@@ -1079,6 +1127,216 @@ __global__ __launch_bounds__(kWave * kWaves, D >= 128 ? 1 : 2) void flash_bwd_dk
     }
 }
 
+// ---------------------------------------------------------------------------------------
+// The three-plane backward in the order dK/dV first, then dQ from dS.  The dK/dV stage
+// already forms dS (in planes, for dK = dS^T Q); written out, it gives the dQ stage
+// dQ = dS K directly, without recomputing S and dP' (two of its three products, six plane
+// products each).  Before dK/dV: D = rowsum(dO o O) and the planes of dO (which the dQ
+// stage wrote in the other order).
+// ---------------------------------------------------------------------------------------
+
+struct PrepArgs {
+    const float *o, *dO;
+    float* Dws;
+    uint16_t* gp;  // dO planes out (laid out as k's)
+    int BH, T;
+    HeadView ov, kv;
+    size_t pstride;
+};
+
+// D and the planes of dO, streaming: a thread per 8-element chunk of a row (D/8 threads per
+// row, consecutive lanes), its dot product an fma chain as in chunk_dot_tree, the row's sum
+// a butterfly over the chunks (xor 2, 4, ..: the pairwise tree over j of chunks 2j + half;
+// then xor 1: the two halves) -- bitwise the dQ stage's D.  nrows = BH*T.
+template <int D>
+__global__ __launch_bounds__(256) void bwd_prep_f32x3_kernel(PrepArgs a, int nrows) {
+    constexpr int kTpr = D / 8;  // threads per row
+    const int gid = blockIdx.x * 256 + threadIdx.x;
+    const int row = gid / kTpr;  // bh*T + t
+    const int k = gid % kTpr;    // chunk
+    const bool live = row < nrows;
+    const int bh = live ? row / a.T : 0;
+    const int t = live ? row - bh * a.T : 0;
+    f32x4 g0{}, g1{}, o0{}, o1{};
+    if (live) {
+        const size_t off = a.ov.off(bh) + static_cast<size_t>(t) * a.ov.row + 8 * k;
+        g0 = *reinterpret_cast<const f32x4*>(a.dO + off);
+        g1 = *reinterpret_cast<const f32x4*>(a.dO + off + 4);
+        o0 = *reinterpret_cast<const f32x4*>(a.o + off);
+        o1 = *reinterpret_cast<const f32x4*>(a.o + off + 4);
+    }
+    float c = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) c = fmaf(g0[i], o0[i], c);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) c = fmaf(g1[i], o1[i], c);
+#pragma unroll
+    for (int w = 2; w < kTpr; w *= 2) c += __shfl_xor(c, w);
+    c += __shfl_xor(c, 1);
+    if (!live) return;
+    if (k == 0) a.Dws[row] = c;
+    float x[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        x[i] = g0[i];
+        x[i + 4] = g1[i];
+    }
+    bf16x8 pl[3];
+    split_planes<3>(x, pl);
+    uint16_t* dst = a.gp + a.kv.off(bh) + static_cast<size_t>(t) * a.kv.row + 8 * k;
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+        __builtin_nontemporal_store(__builtin_bit_cast(u16x8, pl[i]),
+                                    reinterpret_cast<u16x8*>(dst + i * a.pstride));
+}
+
+// Operands of the dQ-from-dS stage: k plane 0 (view kv, planes pstride apart), dS (fp32,
+// layout of DkdvArgs::ds), dq fp32 out (view gv).
+struct DqDsArgs {
+    const uint16_t* k;
+    const float* ds;
+    float* dq;
+    int BH, T;
+    float scale;
+    HeadView kv, gv;
+    size_t pstride;
+    int ds_n;
+};
+
+// Wait until at most n (wave-uniform) vector-memory operations of this wave are outstanding:
+// n rounded down to a count the kernel below issues (waiting longer is always safe).
+__device__ __forceinline__ void wait_vm_at_most(int n) {
+    if (n >= 7)
+        wait_vm<7>();
+    else if (n >= 4)
+        wait_vm<4>();
+    else if (n >= 3)
+        wait_vm<3>();
+    else
+        wait_vm<0>();
+}
+
+// dQ^T += K^T dS^T over 32-key tiles: 128 queries per workgroup, one 32-query sub-block per
+// wave.  K's planes stream through LDS in three buffers, copied two tiles ahead, and give K^T
+// through transposing reads, as in the dQ stage above.  Each wave copies its 32 queries' dS
+// rows of a tile into its own LDS slot (two slots), two tiles ahead; lane i copies and later
+// reads back 16-byte run j of its own query row (the 8 keys of a B operand are two runs of 4
+// in the order of the transposing reads) and splits it into planes, as the dK/dV stage did
+// before writing it.  Key tiles past a wave's diagonal are skipped (dS is not written there);
+// the diagonal tile holds the zeros of the causal mask.  All of it is asynchronous copies:
+// they complete in issue order, tile kt's were issued two steps back, and a step waits until
+// only those issued after them (the next tile's) are outstanding.
+template <int D>
+__global__ __launch_bounds__(kWave* kWaves) void flash_bwd_dq_ds_kernel(DqDsArgs a, int nblk) {
+    constexpr int NP = 3;
+    constexpr int KT = 32;             // keys per tile
+    constexpr int QB = kWaves * kSub;  // queries per workgroup
+    constexpr int NB = 3;              // K buffers
+    using SK = Swz<D, KT>;             // a K plane tile: KT keys x D
+    constexpr int kLoads = 4;  // dS copies per wave and tile: 32 rows x 128 bytes
+    __shared__ __attribute__((aligned(1024))) uint16_t smk[NB][NP][SK::kBytes / 2];
+    __shared__ __attribute__((aligned(1024))) float sms[kWaves][2][kLoads * 256];
+    static_assert(D < 64 || 4 * kStageBytes<D, NP> <= NB * NP * SK::kBytes,
+                  "four wave stages in the K buffers");
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & (kWave - 1);
+    const int col = lane & 31;
+    const int half = lane >> 5;
+    const int T = a.T;
+    int bh, blk;
+    map_block(blockIdx.x, a.BH, nblk, true, bh, blk);
+    const int q0 = blk * QB;
+    const int qj = q0 + kSub * wave;
+    const uint16_t* kh = a.k + a.kv.off(bh);
+    const int krs = a.kv.row;
+    const uint32_t k_lds = lds_addr(smk[0][0]);
+    constexpr uint32_t kKBuf = NP * SK::kBytes;
+    // copy instructions this wave issues per K tile (dma_tile: i = wave, wave + NW, ..)
+    const int ncopy = NP * (wave < SK::kDma ? (SK::kDma - wave + kWaves - 1) / kWaves : 0);
+    static_assert(NP * ((SK::kDma + kWaves - 1) / kWaves) == 3, "wait_vm_at_most's counts");
+    auto copy_tile = [&](int kt) {
+        const uint32_t buf = k_lds + static_cast<uint32_t>(kt % NB) * kKBuf;
+#pragma unroll
+        for (int i = 0; i < NP; ++i)
+            dma_tile<D, kWaves, KT>(kh + i * a.pstride, kt * KT, T, buf + i * SK::kBytes, wave,
+                                    lane, krs);
+    };
+    const int kend = min(T, q0 + QB);
+    const int ntile = (kend + KT - 1) / KT;
+    uint32_t roffK[D / 16], troffK[D / 32];
+    lane_offsets<D>(lane, roffK, troffK);
+    // key tiles 0 .. qj/32 (the last one the diagonal); none when the wave's queries start past
+    // T.  Rows qj + col < ds_n when qj < T.
+    const int nmine = qj < T ? min(qj / KT + 1, ntile) : 0;
+    const float* sbase = a.ds + (static_cast<size_t>(bh) * a.ds_n + min(qj, T - 1)) * a.ds_n;
+    const uint32_t soff = static_cast<uint32_t>((col * a.ds_n + 4 * half) * 4);
+    const uint32_t s_lds = lds_addr(sms[wave][0]);
+    constexpr uint32_t kSlot = kLoads * 1024;
+    auto copy_ds = [&](int kt) {
+        const float* b = sbase + KT * kt;
+#pragma unroll
+        for (int j = 0; j < kLoads; ++j)
+            dma_dwordx4(b, s_lds + static_cast<uint32_t>(kt & 1) * kSlot + 1024 * j, soff + 32 * j);
+    };
+    copy_tile(0);
+    if (0 < nmine) copy_ds(0);
+    if (1 < ntile) copy_tile(1);
+    if (1 < nmine) copy_ds(1);
+    f32x16 acc[D / 32];
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt) acc[dt] = f32x16{};
+    auto step = [&](int kt) {
+        // tile kt's copies and loads landed (only tile kt+1's may be outstanding) ...
+        wait_vm_at_most((kt + 1 < ntile ? ncopy : 0) + (kt + 1 < nmine ? kLoads : 0));
+        __syncthreads();  // ... in every wave; tile kt-1's buffer is no longer read
+        if (kt + 2 < ntile) copy_tile(kt + 2);
+        if (kt >= nmine) return;
+        f32x4 x[kLoads];
+#pragma unroll
+        for (int j = 0; j < kLoads; ++j)
+            x[j] = lds_f32x4(s_lds + static_cast<uint32_t>(kt & 1) * kSlot + 1024 * j + 16 * lane);
+        bf16x8 b[2][NP];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            float v[8];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                v[e] = x[2 * u][e];
+                v[e + 4] = x[2 * u + 1][e];
+            }
+            split_planes<NP>(v, b[u]);
+        }
+        if (kt + 2 < nmine) {
+            wait_lds();  // the slot's reads are done before the copy into it starts
+            copy_ds(kt + 2);
+        }
+        const uint32_t kb = k_lds + static_cast<uint32_t>(kt % NB) * kKBuf;
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+#pragma unroll
+            for (int dt = 0; dt < D / 32; ++dt) {
+                bf16x8 y[NP];
+#pragma unroll
+                for (int i = 0; i < NP; ++i)
+                    y[i] = lds_tr(troffK[dt] + kb + i * SK::kBytes + u * Swz<D>::rows(16),
+                                  Swz<D>::rows(8));
+                acc[dt] = mma_planes<NP>(y, b[u], acc[dt]);
+            }
+        }
+    };
+    for (int kt = 0; kt < ntile; ++kt) step(kt);
+    const size_t goff = a.gv.off(bh);
+    if constexpr (D >= 64) {
+        __syncthreads();  // every wave is past the last tile: the K buffers are idle
+        const uint32_t stage =
+            wave_stage(k_lds, k_lds + 2 * kStageBytes<D, NP>, wave, kStageBytes<D, NP>);
+        store_row_staged<D>(a.dq + goff, qj, T, lane, acc, a.scale, a.gv.row, stage);
+    } else {
+        const int qi = qj + col;
+        if (qi < T) store_row<D>(a.dq + goff, qi, half, acc, a.scale, a.gv.row);
+    }
+}
+
 template <int D, int NSUB, int NP>
 void dq_launch(const DqArgs<NP>& a, hipStream_t stream) {
     constexpr int kBlock = kWaves * NSUB * kSub;
@@ -1103,6 +1361,9 @@ void dkdv_dispatch(const DkdvArgs<NP>& a, hipStream_t stream) {
     const int nblk = (a.T + kBlock - 1) / kBlock;
     if constexpr (NP == 1) {
         hipLaunchKernelGGL((flash_bwd_dkdv_bf16_pipe_kernel<D>), dim3(a.BH * nblk),
+                           dim3(kWave * NW), 0, stream, a, nblk);
+    } else if (a.ds != nullptr) {
+        hipLaunchKernelGGL((flash_bwd_dkdv_bf16_kernel<D, NW, NP, true>), dim3(a.BH * nblk),
                            dim3(kWave * NW), 0, stream, a, nblk);
     } else {
         hipLaunchKernelGGL((flash_bwd_dkdv_bf16_kernel<D, NW, NP>), dim3(a.BH * nblk),
@@ -1156,12 +1417,45 @@ void launch_flash_bwd_dkdv_f32x3(const uint16_t* q, const uint16_t* dO, const He
                                  size_t pstride, const float* k, const float* v,
                                  const HeadView& kv, const float* m, const float* l,
                                  const float* Dws, float* dk, float* dv, const HeadView& gv,
-                                 int BH, int T, int d, float scale, hipStream_t stream) {
-    const DkdvArgs<3> a{q, dO, k, v, m, l, Dws, dk, dv, BH, T, scale, tv, tv, kv, gv, pstride};
+                                 int BH, int T, int d, float scale, hipStream_t stream,
+                                 float* ds) {
+    DkdvArgs<3> a{q, dO, k, v, m, l, Dws, dk, dv, BH, T, scale, tv, tv, kv, gv, pstride};
+    if (ds != nullptr) {
+        a.ds = ds;
+        a.ds_n = ds_rows(T);
+    }
     if (d == 32)
         dkdv_dispatch<32, 3>(a, stream);
     else
         dkdv_dispatch<64, 3>(a, stream);
+}
+
+void launch_bwd_prep_f32x3(const float* o, const float* dO, const HeadView& ov,
+                           uint16_t* do_planes, const HeadView& kv, size_t pstride, float* Dws,
+                           int BH, int T, int d, hipStream_t stream) {
+    const PrepArgs a{o, dO, Dws, do_planes, BH, T, ov, kv, pstride};
+    const int nrows = BH * T;
+    const int nblk = static_cast<int>((static_cast<int64_t>(nrows) * (d / 8) + 255) / 256);
+    if (d == 32)
+        hipLaunchKernelGGL((bwd_prep_f32x3_kernel<32>), dim3(nblk), dim3(256), 0, stream, a,
+                           nrows);
+    else
+        hipLaunchKernelGGL((bwd_prep_f32x3_kernel<64>), dim3(nblk), dim3(256), 0, stream, a,
+                           nrows);
+}
+
+void launch_flash_bwd_dq_ds_f32x3(const uint16_t* k, const HeadView& kv, size_t pstride,
+                                  const float* ds, float* dq, const HeadView& gv, int BH, int T,
+                                  int d, float scale, hipStream_t stream) {
+    const DqDsArgs a{k, ds, dq, BH, T, scale, kv, gv, pstride, ds_rows(T)};
+    constexpr int kBlock = kWaves * kSub;
+    const int nblk = (T + kBlock - 1) / kBlock;
+    if (d == 32)
+        hipLaunchKernelGGL((flash_bwd_dq_ds_kernel<32>), dim3(BH * nblk), dim3(kWave * kWaves), 0,
+                           stream, a, nblk);
+    else
+        hipLaunchKernelGGL((flash_bwd_dq_ds_kernel<64>), dim3(BH * nblk), dim3(kWave * kWaves), 0,
+                           stream, a, nblk);
 }
 
 }  // namespace tcamd

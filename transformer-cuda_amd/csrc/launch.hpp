@@ -96,11 +96,26 @@ void launch_flash_bwd_dq_f32x3(const float* q, const HeadView& qv, const uint16_
                                float* Dws, int BH, int T, int d, float scale,
                                hipStream_t stream);
 // Stage 2 (dK, dV): q and dO plane tensors (view tv), k and v fp32 rows (view kv); dk, dv
-// fp32 (view gv).
+// fp32 (view gv).  Unless ds is null, dS is written out as well (fp32), for
+// launch_flash_bwd_dq_ds_f32x3: head bh at ds + bh*n*n, n = ds_rows(T), rows = queries,
+// columns = keys (keys >= T: zeros), below the diagonal in 32 x 32 blocks.
 void launch_flash_bwd_dkdv_f32x3(const uint16_t* q, const uint16_t* dO, const HeadView& tv,
                                  size_t pstride, const float* k, const float* v,
                                  const HeadView& kv, const float* m, const float* l,
                                  const float* Dws, float* dk, float* dv, const HeadView& gv,
-                                 int BH, int T, int d, float scale, hipStream_t stream);
+                                 int BH, int T, int d, float scale, hipStream_t stream,
+                                 float* ds = nullptr);
+// The side of a head's square dS: T rounded up to 32.
+constexpr int ds_rows(int T) { return (T + 31) / 32 * 32; }
+// Before stage 2 when stage 1 comes after it: D = rowsum(dO o O) into Dws (the same
+// operations as stage 1's) and the planes of dO (laid out as k's, view kv).
+void launch_bwd_prep_f32x3(const float* o, const float* dO, const HeadView& ov,
+                           uint16_t* do_planes, const HeadView& kv, size_t pstride, float* Dws,
+                           int BH, int T, int d, hipStream_t stream);
+// Stage 1 from the dS of stage 2: dQ = scale * dS K (k plane tensors, view kv; dq fp32,
+// view gv).
+void launch_flash_bwd_dq_ds_f32x3(const uint16_t* k, const HeadView& kv, size_t pstride,
+                                  const float* ds, float* dq, const HeadView& gv, int BH, int T,
+                                  int d, float scale, hipStream_t stream);
 
 }  // namespace tcamd

@@ -1203,17 +1203,27 @@ struct DqDsArgs {
     int ds_n;
 };
 
-// Wait until at most n (wave-uniform) vector-memory operations of this wave are outstanding:
-// n rounded down to a count the kernel below issues (waiting longer is always safe).
+// Wait until at most n (wave-uniform, 0 .. 15) vector-memory operations of this wave are
+// outstanding (larger n: 15, which waits longer, always safe).
 __device__ __forceinline__ void wait_vm_at_most(int n) {
-    if (n >= 7)
-        wait_vm<7>();
-    else if (n >= 4)
-        wait_vm<4>();
-    else if (n >= 3)
-        wait_vm<3>();
-    else
-        wait_vm<0>();
+    switch (n) {
+        case 0: wait_vm<0>(); break;
+        case 1: wait_vm<1>(); break;
+        case 2: wait_vm<2>(); break;
+        case 3: wait_vm<3>(); break;
+        case 4: wait_vm<4>(); break;
+        case 5: wait_vm<5>(); break;
+        case 6: wait_vm<6>(); break;
+        case 7: wait_vm<7>(); break;
+        case 8: wait_vm<8>(); break;
+        case 9: wait_vm<9>(); break;
+        case 10: wait_vm<10>(); break;
+        case 11: wait_vm<11>(); break;
+        case 12: wait_vm<12>(); break;
+        case 13: wait_vm<13>(); break;
+        case 14: wait_vm<14>(); break;
+        default: wait_vm<15>(); break;
+    }
 }
 
 // dQ^T += K^T dS^T over 32-key tiles: 128 queries per workgroup, one 32-query sub-block per
@@ -1223,9 +1233,10 @@ __device__ __forceinline__ void wait_vm_at_most(int n) {
 // reads back 16-byte run j of its own query row (the 8 keys of a B operand are two runs of 4
 // in the order of the transposing reads) and splits it into planes, as the dK/dV stage did
 // before writing it.  Key tiles past a wave's diagonal are skipped (dS is not written there);
-// the diagonal tile holds the zeros of the causal mask.  All of it is asynchronous copies:
-// they complete in issue order, tile kt's were issued two steps back, and a step waits until
-// only those issued after them (the next tile's) are outstanding.
+// the diagonal tile holds the zeros of the causal mask.  All of it is asynchronous copies,
+// which complete in issue order; tile kt's were issued two steps back, K's before dS's.  A
+// step waits for tile kt's K copies before the barrier and for its own dS copies only after
+// it, so that no wave's barrier waits for another wave's dS.
 template <int D>
 __global__ __launch_bounds__(kWave* kWaves) void flash_bwd_dq_ds_kernel(DqDsArgs a, int nblk) {
     constexpr int NP = 3;
@@ -1253,9 +1264,9 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_bwd_dq_ds_kernel(DqDsArgs
     constexpr uint32_t kKBuf = NP * SK::kBytes;
     // copy instructions this wave issues per K tile (dma_tile: i = wave, wave + NW, ..)
     const int ncopy = NP * (wave < SK::kDma ? (SK::kDma - wave + kWaves - 1) / kWaves : 0);
-    static_assert(NP * ((SK::kDma + kWaves - 1) / kWaves) == 3, "wait_vm_at_most's counts");
-    auto copy_tile = [&](int kt) {
-        const uint32_t buf = k_lds + static_cast<uint32_t>(kt % NB) * kKBuf;
+    constexpr int kCopies = NP * ((SK::kDma + kWaves - 1) / kWaves);  // ncopy of wave 0
+    static_assert(2 * kCopies + 2 * kLoads <= 15, "wait_vm_at_most's counts");
+    auto copy_tile = [&](int kt, uint32_t buf) {
 #pragma unroll
         for (int i = 0; i < NP; ++i)
             dma_tile<D, kWaves, KT>(kh + i * a.pstride, kt * KT, T, buf + i * SK::kBytes, wave,
@@ -1268,33 +1279,63 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_bwd_dq_ds_kernel(DqDsArgs
     // key tiles 0 .. qj/32 (the last one the diagonal); none when the wave's queries start past
     // T.  Rows qj + col < ds_n when qj < T.
     const int nmine = qj < T ? min(qj / KT + 1, ntile) : 0;
-    const float* sbase = a.ds + (static_cast<size_t>(bh) * a.ds_n + min(qj, T - 1)) * a.ds_n;
-    const uint32_t soff = static_cast<uint32_t>((col * a.ds_n + 4 * half) * 4);
+    const float* sbase = a.ds + (static_cast<size_t>(bh) * a.ds_n + min(qj, a.ds_n - 32)) * a.ds_n;
+    // A slot holds the tile's 32 query rows of 32 keys (128 bytes); 16-byte chunk c of row r
+    // at r*128 + 16*(c ^ ((r/2) % 8)).  Copy j: lane i fills slot bytes 1024j + 16i, row
+    // 8j + i/8, so 8 lanes read one whole row.
+    uint32_t soff[kLoads];
+#pragma unroll
+    for (int j = 0; j < kLoads; ++j) {
+        const int r = 8 * j + lane / 8;
+        const int c = (lane % 8) ^ ((r >> 1) & 7);
+        soff[j] = static_cast<uint32_t>((r * a.ds_n + 4 * c) * 4);
+    }
     const uint32_t s_lds = lds_addr(sms[wave][0]);
     constexpr uint32_t kSlot = kLoads * 1024;
     auto copy_ds = [&](int kt) {
         const float* b = sbase + KT * kt;
 #pragma unroll
         for (int j = 0; j < kLoads; ++j)
-            dma_dwordx4(b, s_lds + static_cast<uint32_t>(kt & 1) * kSlot + 1024 * j, soff + 32 * j);
+            dma_dwordx4(b, s_lds + static_cast<uint32_t>(kt & 1) * kSlot + 1024 * j, soff[j]);
     };
-    copy_tile(0);
+    copy_tile(0, k_lds);
     if (0 < nmine) copy_ds(0);
-    if (1 < ntile) copy_tile(1);
+    if (1 < ntile) copy_tile(1, k_lds + kKBuf);
     if (1 < nmine) copy_ds(1);
     f32x16 acc[D / 32];
 #pragma unroll
     for (int dt = 0; dt < D / 32; ++dt) acc[dt] = f32x16{};
+    // K tile kt is in buffer kb (tile kt+1 in kb1, kt+2 goes to kb2)
+    uint32_t kb = k_lds, kb1 = k_lds + kKBuf, kb2 = k_lds + 2 * kKBuf;
     auto step = [&](int kt) {
-        // tile kt's copies and loads landed (only tile kt+1's may be outstanding) ...
-        wait_vm_at_most((kt + 1 < ntile ? ncopy : 0) + (kt + 1 < nmine ? kLoads : 0));
-        __syncthreads();  // ... in every wave; tile kt-1's buffer is no longer read
-        if (kt + 2 < ntile) copy_tile(kt + 2);
+        // (the counts are constants while the wave has two more tiles of its own: nmine <=
+        // ntile)
+        const bool steady = kt + 2 < nmine;
+        // this wave's copies of K tile kt landed: outstanding may be only its dS of tile kt
+        // and tile kt+1's copies ...
+        if (steady && ncopy == kCopies)
+            wait_vm<2 * kLoads + kCopies>();
+        else if (steady)
+            wait_vm<2 * kLoads>();
+        else
+            wait_vm_at_most((kt < nmine ? kLoads : 0) + (kt + 1 < ntile ? ncopy : 0) +
+                            (kt + 1 < nmine ? kLoads : 0));
+        __syncthreads();  // ... and every wave's; tile kt-1's buffer is no longer read
+        if (kt + 2 < ntile) copy_tile(kt + 2, kb2);
         if (kt >= nmine) return;
-        f32x4 x[kLoads];
+        // dS of tile kt landed: outstanding may be only tile kt+1's and K tile kt+2's copies
+        if (steady && ncopy == kCopies)
+            wait_vm<kLoads + 2 * kCopies>();
+        else if (steady)
+            wait_vm<kLoads>();
+        else
+            wait_vm_at_most((kt + 1 < ntile ? ncopy : 0) + (kt + 1 < nmine ? kLoads : 0) +
+                            (kt + 2 < ntile ? ncopy : 0));
+        f32x4 x[kLoads];  // run j: keys 8j + 4*half .. +3 of row col (chunk 2j + half)
 #pragma unroll
         for (int j = 0; j < kLoads; ++j)
-            x[j] = lds_f32x4(s_lds + static_cast<uint32_t>(kt & 1) * kSlot + 1024 * j + 16 * lane);
+            x[j] = lds_f32x4(s_lds + static_cast<uint32_t>(kt & 1) * kSlot + 128 * col +
+                             16 * ((2 * j + half) ^ ((col >> 1) & 7)));
         bf16x8 b[2][NP];
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
@@ -1310,21 +1351,31 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_bwd_dq_ds_kernel(DqDsArgs
             wait_lds();  // the slot's reads are done before the copy into it starts
             copy_ds(kt + 2);
         }
-        const uint32_t kb = k_lds + static_cast<uint32_t>(kt % NB) * kKBuf;
+        // every K operand of the tile first, then the products back to back
+        bf16x8 y[2][D / 32][NP];
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
 #pragma unroll
             for (int dt = 0; dt < D / 32; ++dt) {
-                bf16x8 y[NP];
 #pragma unroll
                 for (int i = 0; i < NP; ++i)
-                    y[i] = lds_tr(troffK[dt] + kb + i * SK::kBytes + u * Swz<D>::rows(16),
-                                  Swz<D>::rows(8));
-                acc[dt] = mma_planes<NP>(y, b[u], acc[dt]);
+                    y[u][dt][i] = lds_tr(troffK[dt] + kb + i * SK::kBytes + u * Swz<D>::rows(16),
+                                         Swz<D>::rows(8));
             }
         }
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+#pragma unroll
+            for (int dt = 0; dt < D / 32; ++dt) acc[dt] = mma_planes<NP>(y[u][dt], b[u], acc[dt]);
+        }
     };
-    for (int kt = 0; kt < ntile; ++kt) step(kt);
+    for (int kt = 0; kt < ntile; ++kt) {
+        step(kt);
+        const uint32_t t = kb;
+        kb = kb1;
+        kb1 = kb2;
+        kb2 = t;
+    }
     const size_t goff = a.gv.off(bh);
     if constexpr (D >= 64) {
         __syncthreads();  // every wave is past the last tile: the K buffers are idle

@@ -351,9 +351,9 @@ int attn_fused_causal_backward_dkdv_bf16(const attn_bf16* qkv, const attn_bf16* 
  * points.  d_head 32 or 64.
  *
  * `planes` is caller-owned device memory of attn_f32x3_workspace_bytes(B, H, T, d_head)
- * bytes (16-byte aligned): the planes of q, k, v and dO (4 x 3 x B*H*T*d_head bf16), then
- * dS, B*H x n x n fp32 with n = T rounded up to 32 (the one-call backward's stage 2 writes it
- * for its stage 3).  The forward writes the planes of q, k and v; a backward with
+ * bytes (16-byte aligned): the planes of q, k, v and dO (4 x 3 x B*H*T*d_head bf16), then,
+ * where attn_f32x3_backward_uses_ds(B, H, T, d_head) is 1, dS: B*H x n x n fp32 with n = T
+ * rounded up to 32 (the one-call backward's dK/dV stage writes it for its dQ stage).  The forward writes the planes of q, k and v; a backward with
  * kv_planes_ready = 1 reuses them (the caller guarantees that qkv and the workspace are
  * unchanged since that forward), with 0 it splits q, k and v again.  The backward's
  * d_workspace is the B*H*T floats of D, as in the other backward entry points.
@@ -361,6 +361,11 @@ int attn_fused_causal_backward_dkdv_bf16(const attn_bf16* qkv, const attn_bf16* 
  * src/kernels/attention.cu:518-1012).
  * ------------------------------------------------------------------------------------------ */
 size_t attn_f32x3_workspace_bytes(int B, int H, int T, int d_head);
+/* 1 when the one-call backwards take the dS-first order (three stages: prep, dkdv_ds, dq_ds;
+ * d_head 64 and dS at most 16 GiB), 0 when they take the two-stage order (dq, then dkdv).
+ * The dS-first order saves the dQ stage's recomputation of S and dP for 8 bytes of HBM
+ * traffic per stored dS element: faster at d_head 64, slower at 32. */
+int attn_f32x3_backward_uses_ds(int B, int H, int T, int d_head);
 int attn_packed_causal_forward_f32x3(const float* qkv, float* out, int B, int H, int T,
                                      int d_head, float scale, float* m_out, float* l_out,
                                      void* planes, hipStream_t stream);
@@ -377,10 +382,12 @@ int attn_fused_causal_backward_f32x3(const float* qkv, const float* o, const flo
                                      float* d_workspace, int B, int H, int T, int d_head,
                                      float scale, void* planes, int kv_planes_ready,
                                      hipStream_t stream);
-/* The three stages of those backwards, in order: prep writes the planes of dO (and of q, k, v
- * unless kv_planes_ready) and D; dkdv_ds (one function for both layouts: it reads dO only
- * through its planes) writes dK and dV into dqkv and dS into `planes`; dq_ds writes dQ into
- * dqkv from dS and the planes of k. */
+/* The three stages of the dS-first order, in order: prep writes the planes of dO (and of q,
+ * k, v unless kv_planes_ready) and D; dkdv_ds (one function for both layouts: it reads dO
+ * only through its planes) writes dK and dV into dqkv and dS into `planes`; dq_ds writes dQ
+ * into dqkv from dS and the planes of k.  dkdv_ds and dq_ds return
+ * ATTN_ERROR_UNSUPPORTED_HEAD_DIM (d_head other than 64) or ATTN_ERROR_INVALID_DIM (dS above
+ * 16 GiB) where attn_f32x3_backward_uses_ds is 0: the workspace has no dS there. */
 int attn_packed_causal_backward_prep_f32x3(const float* qkv, const float* o,
                                            const float* do_ptr, float* d_workspace, int B,
                                            int H, int T, int d_head, void* planes,
@@ -395,11 +402,10 @@ int attn_causal_backward_dkdv_ds_f32x3(const float* qkv, const float* m_ptr, con
                                        hipStream_t stream);
 int attn_causal_backward_dq_ds_f32x3(float* dqkv, int B, int H, int T, int d_head, float scale,
                                      const void* planes, hipStream_t stream);
-/* The same backward in the other order, in two stages: stage 1 writes the planes of dO (and
- * of q, k, v unless kv_planes_ready), D and dQ, computing S and dP itself; stage 2 (one
- * function for both layouts) writes dK and dV from the planes in `planes`.  The same D, dK
- * and dV as the three stages, bitwise; dQ within fp32 rounding of theirs.  Does not use the
- * workspace's dS. */
+/* The two-stage order, for every shape: stage 1 writes the planes of dO (and of q, k, v unless
+ * kv_planes_ready), D and dQ, computing S and dP itself; stage 2 (one function for both
+ * layouts) writes dK and dV from the planes in `planes`.  The same D, dK and dV as the three
+ * stages, bitwise; dQ within fp32 rounding of theirs.  Does not use the workspace's dS. */
 int attn_packed_causal_backward_dq_f32x3(const float* qkv, const float* o,
                                          const float* do_ptr, const float* m_ptr,
                                          const float* l_ptr, float* dqkv, float* d_workspace,

@@ -39,7 +39,8 @@ def test_every_declared_symbol_is_exported(lib):
 
 def test_binding_covers_header(lib):
     declared = set(declared_symbols()) - {"attn_status_string", "attn_version",
-                                          "attn_f32x3_workspace_bytes"}
+                                          "attn_f32x3_workspace_bytes",
+                                          "attn_f32x3_backward_uses_ds"}
     assert declared == set(lib.SIGNATURES)
 
 
@@ -157,10 +158,17 @@ def test_f32x3_validation(lib):
     """The three-plane fp32 entry points validate before any HIP call."""
     f = ctypes.c_float
     raw = lib.raw()
-    # planes of q, k, v, dO (3 x bf16 each) and the one-call backward's dS (64 x 64 fp32 per
-    # head: T rounded up to 32)
+    # planes of q, k, v, dO (3 x bf16 each) and, at d = 64, the one-call backward's dS (64 x 64
+    # fp32 per head: T rounded up to 32)
     assert raw.attn_f32x3_workspace_bytes(2, 3, 40, 64) == 4 * 3 * 2 * 3 * 40 * 64 * 2 + 6 * 64 * 64 * 4
+    assert raw.attn_f32x3_workspace_bytes(2, 3, 40, 32) == 4 * 3 * 2 * 3 * 40 * 32 * 2
     assert raw.attn_f32x3_workspace_bytes(0, 3, 40, 64) == 0
+    assert lib.f32x3_backward_uses_ds(2, 3, 40, 64) and not lib.f32x3_backward_uses_ds(2, 3, 40, 32)
+    # dS above 16 GiB: the two-stage order, no dS in the workspace
+    assert lib.f32x3_backward_uses_ds(1, 16, 16384, 64)          # 16 GiB exactly
+    assert not lib.f32x3_backward_uses_ds(1, 16, 16416, 64)
+    assert raw.attn_f32x3_workspace_bytes(1, 16, 16416, 64) == 4 * 3 * 16 * 16416 * 64 * 2
+    assert not lib.f32x3_backward_uses_ds(0, 16, 1024, 64)
     fwd = lambda d=64, planes=FAKE, qkv=FAKE, scale=0.125: lib.call(
         "attn_packed_causal_forward_f32x3", qkv, FAKE, 1, 2, 8, d, f(scale), None, None,
         planes, None)
@@ -194,11 +202,14 @@ def test_f32x3_validation(lib):
     assert dkdv(planes=None) == NULLPTR
     assert dkdv(d=48) == BAD_HEAD_DIM
     assert dkdv(scale=0.0) == BAD_VALUE
-    dq = lambda dqkv=FAKE, planes=FAKE, d=64: lib.call(
-        "attn_causal_backward_dq_ds_f32x3", dqkv, 1, 2, 8, d, f(0.125), planes, None)
+    assert dkdv(d=32) == BAD_HEAD_DIM  # d = 32 takes the two-stage order: no dS
+    dq = lambda dqkv=FAKE, planes=FAKE, d=64, T=8: lib.call(
+        "attn_causal_backward_dq_ds_f32x3", dqkv, 1, 2, T, d, f(0.125), planes, None)
     assert dq(dqkv=None) == NULLPTR
     assert dq(planes=None) == NULLPTR
     assert dq(d=128) == BAD_HEAD_DIM
+    assert dq(d=32) == BAD_HEAD_DIM
+    assert dq(T=100000) == INVALID_DIM  # dS above 16 GiB
     assert dq(dqkv=MISALIGNED) == MISALIGN
     assert lib.call("attn_tiled_causal_forward_f32x3", FAKE, FAKE, FAKE, FAKE, 1, 2, 8, 64,
                     f(0.125), None, None, MISALIGNED, None) == MISALIGN

@@ -271,14 +271,16 @@ def test_three_stages_equal_one_call(lib, merged):
     assert torch.equal(one, three) and torch.equal(D1, D3)
 
 
-@pytest.mark.parametrize("merged", [False, True])
-def test_staged_backward_equals_one_call(lib, merged):
-    """Stage 1 (planes of q and dO, D, dQ) then stage 2 (dK, dV) against the one-call backward
-    (D and the planes of dO, then dK and dV writing dS, then dQ = dS K): the same D, dK and dV
-    bitwise (the same operations in the same order), dQ within fp32 rounding (the staged dQ
-    recomputes S and dP with K as the A operand, the one-call path keeps the dK/dV stage's
-    dS, so their dS differ in the last bits)."""
-    B, H, T, d = 2, 3, 300, 64
+@pytest.mark.parametrize("merged,d", [(False, 64), (True, 64), (False, 32)])
+def test_staged_backward_equals_one_call(lib, merged, d):
+    """The two-stage order (stage 1: planes of q and dO, D, dQ; stage 2: dK, dV) against the
+    one-call backward.  At d = 64 that takes the dS-first order (D and the planes of dO, then
+    dK and dV writing dS, then dQ = dS K): the same D, dK and dV bitwise (the same operations
+    in the same order), dQ within fp32 rounding (the two-stage dQ recomputes S and dP with K
+    as the A operand, the one-call path keeps the dK/dV stage's dS, so their dS differ in the
+    last bits).  At d = 32 the one-call backward is the two-stage order itself: bitwise."""
+    B, H, T = 2, 3, 300
+    assert lib.f32x3_backward_uses_ds(B, H, T, d) == (d == 64)
     g = torch.Generator(device="cpu").manual_seed(9)
     qkv = torch.randn((B, T, 3 * H * d), generator=g).to("cuda:0")
     do = torch.randn((B, H, T, d), generator=g).to("cuda:0")
@@ -303,7 +305,10 @@ def test_staged_backward_equals_one_call(lib, merged):
     assert torch.equal(one[..., C:], two[..., C:]) and torch.equal(D1, D2)
     dq1, dq2 = one[..., :C], two[..., :C]
     assert torch.isfinite(dq1).all()
-    assert (dq1 - dq2).abs().max().item() <= 2e-6 * dq2.abs().max().item()
+    if d == 32:
+        assert torch.equal(dq1, dq2)
+    else:
+        assert (dq1 - dq2).abs().max().item() <= 2e-6 * dq2.abs().max().item()
 
 
 @pytest.mark.parametrize("B,H,T,d", [(16, 16, 2048, 64), (16, 16, 1024, 32)])

@@ -133,6 +133,8 @@ _lib.attn_version.argtypes = []
 _lib.attn_version.restype = ctypes.c_int
 _lib.attn_f32x3_workspace_bytes.argtypes = [_I, _I, _I, _I]
 _lib.attn_f32x3_workspace_bytes.restype = ctypes.c_size_t
+_lib.attn_f32x3_backward_uses_ds.argtypes = [_I, _I, _I, _I]
+_lib.attn_f32x3_backward_uses_ds.restype = ctypes.c_int
 
 
 def raw():
@@ -413,6 +415,11 @@ def fused_causal_attention_backward_dkdv(qkv, dO, m, l, workspace, dqkv, B, H, T
 def f32x3_workspace_bytes(B, H, T, d_head):
     """Bytes of the plane workspace of the *_f32x3 entry points (include/attn_capi.h)."""
     return int(_lib.attn_f32x3_workspace_bytes(B, H, T, d_head))
+
+
+def f32x3_backward_uses_ds(B, H, T, d_head):
+    """Whether the one-call *_f32x3 backwards take the dS-first order (include/attn_capi.h)."""
+    return bool(_lib.attn_f32x3_backward_uses_ds(B, H, T, d_head))
 
 
 def _planes_ptr(planes, B, H, T, d_head):

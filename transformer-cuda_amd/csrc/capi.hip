@@ -219,9 +219,9 @@ int packed_backward(const E* qkv, const E* o, const E* dO, const float* m, const
 }
 
 // ---- fp32 on bf16 MFMAs: operands as three bf16 planes in a caller workspace -------------
-// Workspace: four tensors (q, k, v, dO) x three planes x N = B*H*T*d bf16, head-major; then
-// dS, B*H x n x n fp32 with n = T rounded up to 32 (the full backward's stage 2 writes it,
-// its stage 1 reads it).
+// Workspace: four tensors (q, k, v, dO) x three planes x N = B*H*T*d bf16, head-major; then,
+// when the one-call backward takes the dS-first order (uses_ds), dS: B*H x n x n fp32 with
+// n = T rounded up to 32 (its dK/dV stage writes it, its dQ stage reads it).
 
 constexpr int kPlaneTensors = 4;
 constexpr int kPlanes = 3;
@@ -238,6 +238,21 @@ size_t ds_elems(int B, int H, int T) {
 }
 float* ds_area(void* planes, size_t N) {
     return reinterpret_cast<float*>(plane_tensor(planes, N, kPlaneTensors));
+}
+// The one-call backward's order.  dS-first (dK/dV writing dS, then dQ = dS K) saves the dQ
+// stage's S and dP products, 48 of its 74 MFMAs per tile at d = 64, for 8 bytes of HBM
+// traffic per stored element; measured faster at d = 64 (0.86-0.93x from T = 512 to 8192)
+// and slower at d = 32 (1.02-1.22x), where the products saved are half as many.  dS takes
+// 4 B*H*n^2 bytes of workspace: above kDsMaxBytes the two-stage order is taken instead.
+constexpr size_t kDsMaxBytes = static_cast<size_t>(1) << 34;  // 16 GiB
+bool uses_ds(int B, int H, int T, int d) {
+    if (d != 64 || B <= 0 || H <= 0 || T <= 0) return false;
+    const double n = static_cast<double>(tcamd::ds_rows(T));
+    return 4.0 * B * H * n * n <= static_cast<double>(kDsMaxBytes);
+}
+int check_uses_ds(int B, int H, int T, int d) {
+    if (uses_ds(B, H, T, d)) return ATTN_SUCCESS;
+    return d != 64 ? ATTN_ERROR_UNSUPPORTED_HEAD_DIM : ATTN_ERROR_INVALID_DIM;
 }
 
 int check_f32x3(int B, int H, int T, int d, float scale) {
@@ -352,7 +367,9 @@ int packed_backward_dkdv_ds_f32x3(const float* qkv, const float* m, const float*
     if (qkv == nullptr || m == nullptr || l == nullptr || ws == nullptr || dqkv == nullptr ||
         planes == nullptr)
         return ATTN_ERROR_NULL_POINTER;
-    const int st = check_f32x3(B, H, T, d, scale);
+    int st = check_f32x3(B, H, T, d, scale);
+    if (st != ATTN_SUCCESS) return st;
+    st = check_uses_ds(B, H, T, d);
     if (st != ATTN_SUCCESS) return st;
     if (!aligned16(qkv) || !aligned16(dqkv) || !aligned16(planes)) return ATTN_ERROR_MISALIGNED;
     const size_t N = plane_elems(B, H, T, d), C = static_cast<size_t>(H) * d;
@@ -368,7 +385,9 @@ int packed_backward_dkdv_ds_f32x3(const float* qkv, const float* m, const float*
 int packed_backward_dq_ds_f32x3(float* dqkv, int B, int H, int T, int d, float scale,
                                 const void* planes, hipStream_t stream) {
     if (dqkv == nullptr || planes == nullptr) return ATTN_ERROR_NULL_POINTER;
-    const int st = check_f32x3(B, H, T, d, scale);
+    int st = check_f32x3(B, H, T, d, scale);
+    if (st != ATTN_SUCCESS) return st;
+    st = check_uses_ds(B, H, T, d);
     if (st != ATTN_SUCCESS) return st;
     if (!aligned16(dqkv) || !aligned16(planes)) return ATTN_ERROR_MISALIGNED;
     const size_t N = plane_elems(B, H, T, d);
@@ -387,6 +406,13 @@ int packed_backward_f32x3(const float* qkv, const float* o, const float* dO, con
     if (o == nullptr || planes == nullptr) return ATTN_ERROR_NULL_POINTER;
     int st = check_packed_bwd(qkv, dO, m, l, dqkv, ws, B, H, T, d, scale);
     if (st != ATTN_SUCCESS) return st;
+    if (!uses_ds(B, H, T, d)) {  // the two-stage order
+        st = packed_backward_dq_f32x3(qkv, o, dO, m, l, dqkv, ws, B, H, T, d, scale, planes,
+                                      kv_ready, merged, stream);
+        if (st != ATTN_SUCCESS) return st;
+        return packed_backward_dkdv_f32x3(qkv, m, l, ws, dqkv, B, H, T, d, scale, planes,
+                                          stream);
+    }
     st = packed_backward_prep_f32x3(qkv, o, dO, ws, B, H, T, d, planes, kv_ready, merged, stream);
     if (st != ATTN_SUCCESS) return st;
     st = packed_backward_dkdv_ds_f32x3(qkv, m, l, ws, dqkv, B, H, T, d, scale, planes, stream);
@@ -469,11 +495,18 @@ int tiled_backward_dkdv_f32x3(const float* k, const float* v, const float* m, co
     return launch_status();
 }
 
-// The full backward, stage 2 first (as packed_backward_f32x3).
+// The full backward in the order packed_backward_f32x3 takes.
 int tiled_backward_f32x3(const float* q, const float* k, const float* v, const float* o,
                          const float* dO, const float* m, const float* l, float* dq, float* dk,
                          float* dv, float* ws, int B, int H, int T, int d, float scale,
                          void* planes, int kv_ready, hipStream_t stream) {
+    if (!uses_ds(B, H, T, d)) {  // the two-stage order
+        const int st = tiled_backward_dq_f32x3(q, k, v, o, dO, m, l, dq, ws, B, H, T, d, scale,
+                                               planes, kv_ready, stream);
+        if (st != ATTN_SUCCESS) return st;
+        return tiled_backward_dkdv_f32x3(k, v, m, l, ws, dk, dv, B, H, T, d, scale, planes,
+                                         stream);
+    }
     if (q == nullptr || k == nullptr || v == nullptr || o == nullptr || dO == nullptr ||
         m == nullptr || l == nullptr || dq == nullptr || dk == nullptr || dv == nullptr ||
         ws == nullptr)
@@ -1069,7 +1102,12 @@ size_t attn_f32x3_workspace_bytes(int B, int H, int T, int d_head) {
     if (B <= 0 || H <= 0 || T <= 0 || d_head <= 0) return 0;
     return static_cast<size_t>(kPlaneTensors) * kPlanes * plane_elems(B, H, T, d_head) *
                sizeof(uint16_t) +
-           ds_elems(B, H, T) * sizeof(float);
+           (uses_ds(B, H, T, d_head) ? ds_elems(B, H, T) * sizeof(float) : 0);
+}
+
+int attn_f32x3_backward_uses_ds(int B, int H, int T, int d_head) {
+    if (B <= 0 || H <= 0 || T <= 0 || d_head <= 0) return 0;
+    return uses_ds(B, H, T, d_head) ? 1 : 0;
 }
 
 int attn_packed_causal_forward_f32x3(const float* qkv, float* out, int B, int H, int T,

@@ -1229,10 +1229,11 @@ __device__ __forceinline__ void wait_vm_at_most(int n) {
 // dQ^T += K^T dS^T over 32-key tiles: 128 queries per workgroup, one 32-query sub-block per
 // wave.  K's planes stream through LDS in three buffers, copied two tiles ahead, and give K^T
 // through transposing reads, as in the dQ stage above.  Each wave copies its 32 queries' dS
-// rows of a tile into its own LDS slot (two slots), two tiles ahead; lane i copies and later
-// reads back 16-byte run j of its own query row (the 8 keys of a B operand are two runs of 4
-// in the order of the transposing reads) and splits it into planes, as the dK/dV stage did
-// before writing it.  Key tiles past a wave's diagonal are skipped (dS is not written there);
+// rows of a tile (32 keys, 128 bytes each) into its own LDS slot (two slots), two tiles
+// ahead, 8 lanes per row; a lane reads back the runs of its query's row that hold the 8 keys
+// of a B operand (two runs of 4, in the order of the transposing reads) and splits them into
+// planes, as the dK/dV stage did before writing them.  Key tiles past a wave's diagonal are
+// skipped (dS is not written there);
 // the diagonal tile holds the zeros of the causal mask.  All of it is asynchronous copies,
 // which complete in issue order; tile kt's were issued two steps back, K's before dS's.  A
 // step waits for tile kt's K copies before the barrier and for its own dS copies only after
@@ -1351,7 +1352,7 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_bwd_dq_ds_kernel(DqDsArgs
             wait_lds();  // the slot's reads are done before the copy into it starts
             copy_ds(kt + 2);
         }
-        // every K operand of the tile first, then the products back to back
+        // the tile's K operands, then its products
         bf16x8 y[2][D / 32][NP];
 #pragma unroll
         for (int u = 0; u < 2; ++u) {

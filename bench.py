@@ -16,6 +16,11 @@ written directly:
     attn_fwd_packed   qkv -> O (B,H,T,d), m, l                    reference model.cu:305-311
     bwd_dq_packed     D = rowsum(dO*O), dQ -> dqkv[:, :, q block]  reference model.cu:609, 653
     bwd_dkdv_packed   dK, dV -> dqkv[:, :, k and v blocks]         reference model.cu:609, 653
+fp32 on the fp32 MFMA takes the backward's dS-first order instead (attn_packed_causal_
+backward_ds_f32's stages: dK/dV write dS, dQ is computed from it):
+    bwd_prep_packed     D = rowsum(dO*O)                           reference model.cu:609
+    bwd_dkdv_ds_packed  dK, dV -> dqkv[:, :, k and v blocks]; dS     reference model.cu:609, 653
+    bwd_dq_ds_packed    dQ = dS K -> dqkv[:, :, q block]             reference model.cu:609, 653
 --path split runs the reference's launcher sequence with separate split-transpose kernels:
     qkv (B,T,3C) --split-transpose--> q,k,v (B,H,T,d)             reference model.cu:305
     tiled forward          -> O, m, l                             reference model.cu:311
@@ -101,7 +106,8 @@ METRIC = "causal attn fwd+bwd TFLOP/s & % MFMA peak, B8 H12 T1024 d64 fp32/bf16"
 FLOP_UNITS = {"attn_fwd": 2, "bwd_dq": 1, "bwd_dkdv": 4,
               "attn_fwd_packed": 2, "bwd_dq_packed": 1, "bwd_dkdv_packed": 4,
               "attn_fwd_x3": 2, "bwd_dq_x3": 1, "bwd_dkdv_x3": 4,
-              "bwd_dkdv_ds_x3": 4, "bwd_dq_ds_x3": 1}
+              "bwd_dkdv_ds_x3": 4, "bwd_dq_ds_x3": 1,
+              "bwd_dkdv_ds_packed": 4, "bwd_dq_ds_packed": 1}
 X3_PRODUCTS = 6  # bf16 plane products per fp32 product on the x3 path
 
 
@@ -193,6 +199,9 @@ class PathRunner:
                 raise ValueError("the x3 path computes fp32 attention")
             self.planes = torch.empty(lib.f32x3_workspace_bytes(B, H, T, d), device=dev,
                                       dtype=torch.uint8)
+        if path == "packed" and dtype == "f32":  # the dS-first backward's dS
+            self.ds = torch.empty(lib.f32_ds_workspace_bytes(B, H, T, d) // 4, device=dev,
+                                  dtype=torch.float32)
 
     def launches(self):
         L, a = self.lib, (self.B, self.H, self.T, self.d)
@@ -210,6 +219,20 @@ class PathRunner:
                     self.planes)),
                 ("bwd_dq_ds_x3", lambda: L.causal_attention_backward_dq_ds_f32x3(
                     self.dqkv, B, H, T, d, self.scale, self.planes)),
+            )
+        if self.path == "packed" and self.dtype == "f32":
+            # the split-transposes happen inside the attention kernels' tile copies/stores;
+            # the backward in the dS-first order
+            return (
+                ("attn_fwd_packed", lambda: L.packed_causal_attention_forward(
+                    self.qkv, self.o, B, H, T, d, self.scale, self.m, self.l)),
+                ("bwd_prep_packed", lambda: L.packed_causal_attention_backward_prep(
+                    self.o, self.do, self.ws, B, H, T, d)),
+                ("bwd_dkdv_ds_packed", lambda: L.packed_causal_attention_backward_dkdv_ds(
+                    self.qkv, self.do, self.m, self.l, self.ws, self.dqkv, self.ds, B, H, T, d,
+                    self.scale)),
+                ("bwd_dq_ds_packed", lambda: L.causal_attention_backward_dq_ds(
+                    self.qkv, self.dqkv, self.ds, B, H, T, d, self.scale)),
             )
         if self.path == "packed":
             # the split-transposes happen inside the attention kernels' tile copies/stores
@@ -253,6 +276,9 @@ class PathRunner:
         if name == "bwd_prep_x3":
             n = float(self.B * self.H * self.T * self.d)
             return 14.0 * n + 4.0 * self.B * self.H * self.T, "byte"
+        if name == "bwd_prep_packed":  # O and dO read in fp32, D written
+            n = float(self.B * self.H * self.T * self.d)
+            return 8.0 * n + 4.0 * self.B * self.H * self.T, "byte"
         elem = 2 if self.dtype == "bf16" else 4
         return 6.0 * self.B * self.T * self.C * elem, "byte"
 

@@ -279,6 +279,29 @@ int attn_packed_causal_backward_dkdv_f32(const float* qkv, const float* do_ptr,
                                          const float* m_ptr, const float* l_ptr,
                                          const float* d_workspace, float* dqkv, int B, int H,
                                          int T, int d_head, float scale, hipStream_t stream);
+/* The packed / fused fp32 backward in the dS-first order (no counterpart in the reference):
+ * prep writes D into d_workspace (the same sums as stage 1 above); dkdv_ds writes the k and
+ * v blocks of dqkv and dS into ds_workspace; dq_ds writes the q block of dqkv as scale * dS K.
+ * Stage 1 above computes S and dP again for dQ, two thirds of its fp32 MFMA work; here the
+ * dK/dV stage hands them over as dS.  ds_workspace: attn_f32_ds_workspace_bytes(B, H, T,
+ * d_head) bytes (B*H heads of n x n fp32, n = T rounded up to 32), 16-byte aligned; its
+ * contents need no initialisation.  D, dK and dV bitwise those of the two-stage order, dQ
+ * within fp32 rounding of its. */
+size_t attn_f32_ds_workspace_bytes(int B, int H, int T, int d_head);
+int attn_packed_causal_backward_ds_f32(const float* qkv, const float* o, const float* do_ptr,
+                                       const float* m_ptr, const float* l_ptr, float* dqkv,
+                                       float* d_workspace, float* ds_workspace, int B, int H,
+                                       int T, int d_head, float scale, hipStream_t stream);
+int attn_packed_causal_backward_prep_f32(const float* o, const float* do_ptr, float* d_workspace,
+                                         int B, int H, int T, int d_head, hipStream_t stream);
+int attn_packed_causal_backward_dkdv_ds_f32(const float* qkv, const float* do_ptr,
+                                            const float* m_ptr, const float* l_ptr,
+                                            const float* d_workspace, float* dqkv,
+                                            float* ds_workspace, int B, int H, int T,
+                                            int d_head, float scale, hipStream_t stream);
+int attn_causal_backward_dq_ds_f32(const float* qkv, float* dqkv, const float* ds_workspace,
+                                   int B, int H, int T, int d_head, float scale,
+                                   hipStream_t stream);
 int attn_packed_causal_forward_bf16(const attn_bf16* qkv, attn_bf16* out, int B, int H, int T,
                                     int d_head, float scale, float* m_out, float* l_out,
                                     hipStream_t stream);
@@ -322,6 +345,18 @@ int attn_fused_causal_backward_dkdv_f32(const float* qkv, const float* do_ptr,
                                         const float* m_ptr, const float* l_ptr,
                                         const float* d_workspace, float* dqkv, int B, int H,
                                         int T, int d_head, float scale, hipStream_t stream);
+/* The dS-first order with the fused layout's o and dO (dq_ds above serves both layouts). */
+int attn_fused_causal_backward_ds_f32(const float* qkv, const float* o, const float* do_ptr,
+                                      const float* m_ptr, const float* l_ptr, float* dqkv,
+                                      float* d_workspace, float* ds_workspace, int B, int H,
+                                      int T, int d_head, float scale, hipStream_t stream);
+int attn_fused_causal_backward_prep_f32(const float* o, const float* do_ptr, float* d_workspace,
+                                        int B, int H, int T, int d_head, hipStream_t stream);
+int attn_fused_causal_backward_dkdv_ds_f32(const float* qkv, const float* do_ptr,
+                                           const float* m_ptr, const float* l_ptr,
+                                           const float* d_workspace, float* dqkv,
+                                           float* ds_workspace, int B, int H, int T, int d_head,
+                                           float scale, hipStream_t stream);
 int attn_fused_causal_forward_bf16(const attn_bf16* qkv, attn_bf16* out, int B, int H, int T,
                                    int d_head, float scale, float* m_out, float* l_out,
                                    hipStream_t stream);

@@ -264,6 +264,33 @@ inline void fused_causal_attention_forward_bf16(const attn_bf16* qkv, attn_bf16*
         "fused_causal_attention_forward_bf16");
 }
 
+// The fp32 backward in the dS-first order: dK/dV write dS into ds_workspace
+// (attn_f32_ds_workspace_bytes(B, H, T, d_head) bytes, caller-owned, shareable across calls
+// on one stream), dQ is computed from it.  D, dK, dV bitwise those of the calls above, dQ
+// within fp32 rounding.  No counterpart in the reference.
+inline void packed_causal_attention_backward_ds_f32(const float* qkv, const float* o,
+                                                    const float* do_ptr, const float* m_ptr,
+                                                    const float* l_ptr, float* dqkv,
+                                                    float* d_workspace, float* ds_workspace,
+                                                    int B, int H, int T, int d_head,
+                                                    float scale, hipStream_t stream = nullptr) {
+    tcamd::check_status(attn_packed_causal_backward_ds_f32(qkv, o, do_ptr, m_ptr, l_ptr, dqkv,
+                                                           d_workspace, ds_workspace, B, H, T,
+                                                           d_head, scale, stream),
+                        "packed_causal_attention_backward_ds_f32");
+}
+inline void fused_causal_attention_backward_ds_f32(const float* qkv, const float* o,
+                                                   const float* do_ptr, const float* m_ptr,
+                                                   const float* l_ptr, float* dqkv,
+                                                   float* d_workspace, float* ds_workspace,
+                                                   int B, int H, int T, int d_head, float scale,
+                                                   hipStream_t stream = nullptr) {
+    tcamd::check_status(attn_fused_causal_backward_ds_f32(qkv, o, do_ptr, m_ptr, l_ptr, dqkv,
+                                                          d_workspace, ds_workspace, B, H, T,
+                                                          d_head, scale, stream),
+                        "fused_causal_attention_backward_ds_f32");
+}
+
 inline void fused_causal_attention_backward_bf16(const attn_bf16* qkv, const attn_bf16* o,
                                                  const attn_bf16* do_ptr, const float* m_ptr,
                                                  const float* l_ptr, attn_bf16* dqkv,

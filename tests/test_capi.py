@@ -40,7 +40,8 @@ def test_every_declared_symbol_is_exported(lib):
 def test_binding_covers_header(lib):
     declared = set(declared_symbols()) - {"attn_status_string", "attn_version",
                                           "attn_f32x3_workspace_bytes",
-                                          "attn_f32x3_backward_uses_ds"}
+                                          "attn_f32x3_backward_uses_ds",
+                                          "attn_f32_ds_workspace_bytes"}
     assert declared == set(lib.SIGNATURES)
 
 
@@ -211,6 +212,26 @@ def test_f32x3_validation(lib):
     assert dq(d=32) == BAD_HEAD_DIM
     assert dq(T=100000) == INVALID_DIM  # dS above 16 GiB
     assert dq(dqkv=MISALIGNED) == MISALIGN
+    # the fp32 MFMA backward in the dS-first order
+    assert raw.attn_f32_ds_workspace_bytes(2, 3, 40, 64) == 6 * 64 * 64 * 4
+    assert raw.attn_f32_ds_workspace_bytes(2, 3, 0, 64) == 0
+    for fam in ("packed", "fused"):
+        one = lambda ds=FAKE, ws=FAKE, d=64: lib.call(
+            f"attn_{fam}_causal_backward_ds_f32", FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, ws, ds, 1,
+            2, 8, d, f(0.125), None)
+        assert one(ds=None) == NULLPTR
+        assert one(ws=None) == NULLPTR
+        assert one(d=48) == BAD_HEAD_DIM
+        assert one(ds=MISALIGNED) == MISALIGN
+        assert lib.call(f"attn_{fam}_causal_backward_prep_f32", FAKE, FAKE, None, 1, 2, 8, 64,
+                        None) == NULLPTR
+        assert lib.call(f"attn_{fam}_causal_backward_dkdv_ds_f32", FAKE, FAKE, FAKE, FAKE, FAKE,
+                        FAKE, None, 1, 2, 8, 64, f(0.125), None) == NULLPTR
+    dqf = lambda ds=FAKE, scale=0.125: lib.call("attn_causal_backward_dq_ds_f32", FAKE, FAKE, ds,
+                                                1, 2, 8, 64, f(scale), None)
+    assert dqf(ds=None) == NULLPTR
+    assert dqf(scale=0.0) == BAD_VALUE
+    assert dqf(ds=MISALIGNED) == MISALIGN
     assert lib.call("attn_tiled_causal_forward_f32x3", FAKE, FAKE, FAKE, FAKE, 1, 2, 8, 64,
                     f(0.125), None, None, MISALIGNED, None) == MISALIGN
     assert lib.call("attn_tiled_causal_backward_f32x3", *([FAKE] * 11), 1, 2, 8, 128,

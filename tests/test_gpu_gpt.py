@@ -115,10 +115,10 @@ def test_modes_agree_and_attention_timing(gpt):
     for mode in ("fused_x3", "tiled_split", "materialized"):
         assert abs(out[mode][0] - out["fused"][0]) <= 1e-5
         assert np.abs(out[mode][1] - out["fused"][1]).max() <= 2e-5, mode
-    # the fused and the reference's tiled sequence run the same kernels: equal bitwise, but
-    # for the token-embedding rows, whose scatter-add (repeated tokens) is atomic
-    n_tok = s["V"] * s["C"]
-    assert np.array_equal(out["tiled_split"][1][n_tok:], out["fused"][1][n_tok:])
+    # The fused mode's backward takes the dS-first order (dQ from the dK/dV kernel's dS) and
+    # the reference's tiled sequence the two-stage one: the same forward kernels, so the same
+    # loss bitwise, and gradients within fp32 rounding (above).
+    assert out["tiled_split"][0] == out["fused"][0]
 
 
 C5 = dict(V=50257, T=1024, C=768, L=12, H=12, d_ff=3072, B=8)

@@ -105,6 +105,15 @@ SIGNATURES = {
         [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P, _I, _P],
     "attn_fused_causal_backward_f32x3":
         [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P, _I, _P],
+    "attn_packed_causal_backward_ds_f32":
+        [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P],
+    "attn_fused_causal_backward_ds_f32":
+        [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P],
+    "attn_packed_causal_backward_prep_f32": [_P, _P, _P, _I, _I, _I, _I, _P],
+    "attn_fused_causal_backward_prep_f32": [_P, _P, _P, _I, _I, _I, _I, _P],
+    "attn_packed_causal_backward_dkdv_ds_f32": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P],
+    "attn_fused_causal_backward_dkdv_ds_f32": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P],
+    "attn_causal_backward_dq_ds_f32": [_P, _P, _P, _I, _I, _I, _I, _F, _P],
     "attn_packed_causal_backward_prep_f32x3": [_P, _P, _P, _P, _I, _I, _I, _I, _P, _I, _P],
     "attn_fused_causal_backward_prep_f32x3": [_P, _P, _P, _P, _I, _I, _I, _I, _P, _I, _P],
     "attn_causal_backward_dkdv_ds_f32x3": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P, _P],
@@ -133,6 +142,8 @@ _lib.attn_version.argtypes = []
 _lib.attn_version.restype = ctypes.c_int
 _lib.attn_f32x3_workspace_bytes.argtypes = [_I, _I, _I, _I]
 _lib.attn_f32x3_workspace_bytes.restype = ctypes.c_size_t
+_lib.attn_f32_ds_workspace_bytes.argtypes = [_I, _I, _I, _I]
+_lib.attn_f32_ds_workspace_bytes.restype = ctypes.c_size_t
 _lib.attn_f32x3_backward_uses_ds.argtypes = [_I, _I, _I, _I]
 _lib.attn_f32x3_backward_uses_ds.restype = ctypes.c_int
 
@@ -381,6 +392,97 @@ def packed_causal_attention_backward_dkdv(qkv, dO, m, l, workspace, dqkv, B, H, 
     """Stage 2 of the packed backward: dk, dv into the k and v blocks of dqkv."""
     _qkv_backward("packed", "_dkdv", qkv, None, dO, m, l, dqkv, workspace, B, H, T, d_head,
                   scale, stream)
+
+
+def f32_ds_workspace_bytes(B, H, T, d_head):
+    """Bytes of the dS workspace of the fp32 dS-first backward (include/attn_capi.h)."""
+    return int(_lib.attn_f32_ds_workspace_bytes(B, H, T, d_head))
+
+
+def _ds_ptr(ds, B, H, T, d_head):
+    need = f32_ds_workspace_bytes(B, H, T, d_head)
+    if ds is not None and ds.numel() * ds.element_size() < need:
+        raise ValueError(f"ds_workspace: needs {need} bytes")
+    return _ptr(ds, None, None, "ds_workspace")
+
+
+def _backward_ds_f32(family, qkv, o, dO, m, l, dqkv, workspace, ds, B, H, T, d_head, scale,
+                     stream):
+    n, r = B * H * T * d_head, B * H * T
+    f32 = _dt(False)
+    check(call(f"attn_{family}_causal_backward_ds_f32", _ptr(qkv, f32, 3 * n, "qkv"),
+               _ptr(o, f32, n, "o"), _ptr(dO, f32, n, "dO"), _ptr(m, f32, r, "m"),
+               _ptr(l, f32, r, "l"), _ptr(dqkv, f32, 3 * n, "dqkv"),
+               _ptr(workspace, f32, r, "workspace"), _ds_ptr(ds, B, H, T, d_head), B, H, T,
+               d_head, float(scale), _stream(stream)), f"{family}_causal_attention_backward_ds")
+
+
+def packed_causal_attention_backward_ds(qkv, o, dO, m, l, dqkv, workspace, ds_workspace, B, H,
+                                        T, d_head, scale, stream=None):
+    """packed_causal_attention_backward (fp32) in the dS-first order: dK/dV write dS into
+    ds_workspace (f32_ds_workspace_bytes bytes) and dQ is computed from it."""
+    _backward_ds_f32("packed", qkv, o, dO, m, l, dqkv, workspace, ds_workspace, B, H, T, d_head,
+                     scale, stream)
+
+
+def fused_causal_attention_backward_ds(qkv, o, dO, m, l, dqkv, workspace, ds_workspace, B, H,
+                                       T, d_head, scale, stream=None):
+    """fused_causal_attention_backward (fp32) in the dS-first order."""
+    _backward_ds_f32("fused", qkv, o, dO, m, l, dqkv, workspace, ds_workspace, B, H, T, d_head,
+                     scale, stream)
+
+
+def _backward_prep_f32(family, o, dO, workspace, B, H, T, d_head, stream):
+    n, r = B * H * T * d_head, B * H * T
+    f32 = _dt(False)
+    check(call(f"attn_{family}_causal_backward_prep_f32", _ptr(o, f32, n, "o"),
+               _ptr(dO, f32, n, "dO"), _ptr(workspace, f32, r, "workspace"), B, H, T, d_head,
+               _stream(stream)), f"{family}_causal_attention_backward_prep")
+
+
+def packed_causal_attention_backward_prep(o, dO, workspace, B, H, T, d_head, stream=None):
+    """Stage 1 of packed_causal_attention_backward_ds: D = rowsum(dO o O) into workspace."""
+    _backward_prep_f32("packed", o, dO, workspace, B, H, T, d_head, stream)
+
+
+def fused_causal_attention_backward_prep(o, dO, workspace, B, H, T, d_head, stream=None):
+    """Stage 1 of fused_causal_attention_backward_ds."""
+    _backward_prep_f32("fused", o, dO, workspace, B, H, T, d_head, stream)
+
+
+def _backward_dkdv_ds_f32(family, qkv, dO, m, l, workspace, dqkv, ds, B, H, T, d_head, scale,
+                          stream):
+    n, r = B * H * T * d_head, B * H * T
+    f32 = _dt(False)
+    check(call(f"attn_{family}_causal_backward_dkdv_ds_f32", _ptr(qkv, f32, 3 * n, "qkv"),
+               _ptr(dO, f32, n, "dO"), _ptr(m, f32, r, "m"), _ptr(l, f32, r, "l"),
+               _ptr(workspace, f32, r, "workspace"), _ptr(dqkv, f32, 3 * n, "dqkv"),
+               _ds_ptr(ds, B, H, T, d_head), B, H, T, d_head, float(scale), _stream(stream)),
+          f"{family}_causal_attention_backward_dkdv_ds")
+
+
+def packed_causal_attention_backward_dkdv_ds(qkv, dO, m, l, workspace, dqkv, ds_workspace, B, H,
+                                             T, d_head, scale, stream=None):
+    """Stage 2 of packed_causal_attention_backward_ds: dk, dv into dqkv, dS into ds_workspace."""
+    _backward_dkdv_ds_f32("packed", qkv, dO, m, l, workspace, dqkv, ds_workspace, B, H, T,
+                          d_head, scale, stream)
+
+
+def fused_causal_attention_backward_dkdv_ds(qkv, dO, m, l, workspace, dqkv, ds_workspace, B, H,
+                                            T, d_head, scale, stream=None):
+    """Stage 2 of fused_causal_attention_backward_ds."""
+    _backward_dkdv_ds_f32("fused", qkv, dO, m, l, workspace, dqkv, ds_workspace, B, H, T,
+                          d_head, scale, stream)
+
+
+def causal_attention_backward_dq_ds(qkv, dqkv, ds_workspace, B, H, T, d_head, scale,
+                                    stream=None):
+    """Stage 3 of the fp32 dS-first backwards: dq = scale * dS k into the q block of dqkv."""
+    n = B * H * T * d_head
+    f32 = _dt(False)
+    check(call("attn_causal_backward_dq_ds_f32", _ptr(qkv, f32, 3 * n, "qkv"),
+               _ptr(dqkv, f32, 3 * n, "dqkv"), _ds_ptr(ds_workspace, B, H, T, d_head), B, H, T,
+               d_head, float(scale), _stream(stream)), "causal_attention_backward_dq_ds")
 
 
 def fused_causal_attention_forward(qkv, out, B, H, T, d_head, scale, m_out=None, l_out=None,

@@ -208,6 +208,70 @@ int packed_backward_dkdv(const E* qkv, const E* dO, const float* m, const float*
     return launch_status();
 }
 
+// ---- fp32 MFMA backward in the dS-first order: D; dK/dV writing dS into a caller
+// workspace (B*H heads of n x n fp32, n = T rounded up to 32); dQ = scale * dS K.
+
+size_t ds_f32_elems(int B, int H, int T) {
+    const size_t n = static_cast<size_t>(tcamd::ds_rows(T));
+    return static_cast<size_t>(B) * H * n * n;
+}
+
+int packed_backward_prep_f32(const float* o, const float* dO, float* ws, int B, int H, int T,
+                             int d, bool merged, hipStream_t stream) {
+    if (o == nullptr || dO == nullptr || ws == nullptr) return ATTN_ERROR_NULL_POINTER;
+    const int st = check_packed(B, H, T, d, 1.0f);
+    if (st != ATTN_SUCCESS) return st;
+    if (!aligned16(o) || !aligned16(dO)) return ATTN_ERROR_MISALIGNED;
+    clear_error();
+    tcamd::launch_bwd_d_rows_f32(dO, o, out_view(H, T, d, merged), ws, B * H, T, d, stream);
+    return launch_status();
+}
+
+int packed_backward_dkdv_ds_f32(const float* qkv, const float* dO, const float* m,
+                                const float* l, const float* ws, float* dqkv, float* ds, int B,
+                                int H, int T, int d, float scale, bool merged,
+                                hipStream_t stream) {
+    if (ds == nullptr) return ATTN_ERROR_NULL_POINTER;
+    const int st = check_packed_bwd(qkv, dO, m, l, dqkv, ws, B, H, T, d, scale);
+    if (st != ATTN_SUCCESS) return st;
+    if (!aligned16(ds)) return ATTN_ERROR_MISALIGNED;
+    const size_t C = static_cast<size_t>(H) * d;
+    const tcamd::HeadView xv = tcamd::packed_qkv_view(H, T, d);
+    clear_error();
+    tcamd::launch_flash_bwd_dkdv_f32(qkv, qkv + C, qkv + 2 * C, dO, m, l, ws, dqkv + C,
+                                     dqkv + 2 * C, B * H, T, d, scale, xv,
+                                     out_view(H, T, d, merged), xv, stream, ds);
+    return launch_status();
+}
+
+int backward_dq_ds_f32(const float* qkv, float* dqkv, const float* ds, int B, int H, int T,
+                       int d, float scale, hipStream_t stream) {
+    if (qkv == nullptr || dqkv == nullptr || ds == nullptr) return ATTN_ERROR_NULL_POINTER;
+    const int st = check_packed(B, H, T, d, scale);
+    if (st != ATTN_SUCCESS) return st;
+    if (!aligned16(qkv) || !aligned16(dqkv) || !aligned16(ds)) return ATTN_ERROR_MISALIGNED;
+    const size_t C = static_cast<size_t>(H) * d;
+    const tcamd::HeadView xv = tcamd::packed_qkv_view(H, T, d);
+    clear_error();
+    tcamd::launch_flash_bwd_dq_ds_f32(qkv + C, xv, ds, dqkv, xv, B * H, T, d, scale, stream);
+    return launch_status();
+}
+
+int packed_backward_ds_f32(const float* qkv, const float* o, const float* dO, const float* m,
+                           const float* l, float* dqkv, float* ws, float* ds, int B, int H,
+                           int T, int d, float scale, bool merged, hipStream_t stream) {
+    if (o == nullptr || ds == nullptr) return ATTN_ERROR_NULL_POINTER;
+    int st = check_packed_bwd(qkv, dO, m, l, dqkv, ws, B, H, T, d, scale);
+    if (st != ATTN_SUCCESS) return st;
+    if (!aligned16(o) || !aligned16(ds)) return ATTN_ERROR_MISALIGNED;  // before any launch
+    st = packed_backward_prep_f32(o, dO, ws, B, H, T, d, merged, stream);
+    if (st != ATTN_SUCCESS) return st;
+    st = packed_backward_dkdv_ds_f32(qkv, dO, m, l, ws, dqkv, ds, B, H, T, d, scale, merged,
+                                     stream);
+    if (st != ATTN_SUCCESS) return st;
+    return backward_dq_ds_f32(qkv, dqkv, ds, B, H, T, d, scale, stream);
+}
+
 template <typename E>
 int packed_backward(const E* qkv, const E* o, const E* dO, const float* m, const float* l,
                     E* dqkv, float* ws, int B, int H, int T, int d, float scale, bool merged,
@@ -1097,6 +1161,55 @@ int attn_fused_causal_backward_bf16(const attn_bf16* qkv, const attn_bf16* o,
 
 
 // ---- fp32 on bf16 MFMAs (three bf16 planes per operand) --------------------------------
+
+size_t attn_f32_ds_workspace_bytes(int B, int H, int T, int d_head) {
+    if (B <= 0 || H <= 0 || T <= 0 || d_head <= 0) return 0;
+    return ds_f32_elems(B, H, T) * sizeof(float);
+}
+
+int attn_packed_causal_backward_ds_f32(const float* qkv, const float* o, const float* do_ptr,
+                                       const float* m_ptr, const float* l_ptr, float* dqkv,
+                                       float* d_workspace, float* ds_workspace, int B, int H,
+                                       int T, int d_head, float scale, hipStream_t stream) {
+    return packed_backward_ds_f32(qkv, o, do_ptr, m_ptr, l_ptr, dqkv, d_workspace, ds_workspace,
+                                  B, H, T, d_head, scale, false, stream);
+}
+int attn_fused_causal_backward_ds_f32(const float* qkv, const float* o, const float* do_ptr,
+                                      const float* m_ptr, const float* l_ptr, float* dqkv,
+                                      float* d_workspace, float* ds_workspace, int B, int H,
+                                      int T, int d_head, float scale, hipStream_t stream) {
+    return packed_backward_ds_f32(qkv, o, do_ptr, m_ptr, l_ptr, dqkv, d_workspace, ds_workspace,
+                                  B, H, T, d_head, scale, true, stream);
+}
+int attn_packed_causal_backward_prep_f32(const float* o, const float* do_ptr, float* d_workspace,
+                                         int B, int H, int T, int d_head, hipStream_t stream) {
+    return packed_backward_prep_f32(o, do_ptr, d_workspace, B, H, T, d_head, false, stream);
+}
+int attn_fused_causal_backward_prep_f32(const float* o, const float* do_ptr, float* d_workspace,
+                                        int B, int H, int T, int d_head, hipStream_t stream) {
+    return packed_backward_prep_f32(o, do_ptr, d_workspace, B, H, T, d_head, true, stream);
+}
+int attn_packed_causal_backward_dkdv_ds_f32(const float* qkv, const float* do_ptr,
+                                            const float* m_ptr, const float* l_ptr,
+                                            const float* d_workspace, float* dqkv,
+                                            float* ds_workspace, int B, int H, int T,
+                                            int d_head, float scale, hipStream_t stream) {
+    return packed_backward_dkdv_ds_f32(qkv, do_ptr, m_ptr, l_ptr, d_workspace, dqkv,
+                                       ds_workspace, B, H, T, d_head, scale, false, stream);
+}
+int attn_fused_causal_backward_dkdv_ds_f32(const float* qkv, const float* do_ptr,
+                                           const float* m_ptr, const float* l_ptr,
+                                           const float* d_workspace, float* dqkv,
+                                           float* ds_workspace, int B, int H, int T, int d_head,
+                                           float scale, hipStream_t stream) {
+    return packed_backward_dkdv_ds_f32(qkv, do_ptr, m_ptr, l_ptr, d_workspace, dqkv,
+                                       ds_workspace, B, H, T, d_head, scale, true, stream);
+}
+int attn_causal_backward_dq_ds_f32(const float* qkv, float* dqkv, const float* ds_workspace,
+                                   int B, int H, int T, int d_head, float scale,
+                                   hipStream_t stream) {
+    return backward_dq_ds_f32(qkv, dqkv, ds_workspace, B, H, T, d_head, scale, stream);
+}
 
 size_t attn_f32x3_workspace_bytes(int B, int H, int T, int d_head) {
     if (B <= 0 || H <= 0 || T <= 0 || d_head <= 0) return 0;

@@ -1203,29 +1203,6 @@ struct DqDsArgs {
     int ds_n;
 };
 
-// Wait until at most n (wave-uniform, 0 .. 15) vector-memory operations of this wave are
-// outstanding (larger n: 15, which waits longer, always safe).
-__device__ __forceinline__ void wait_vm_at_most(int n) {
-    switch (n) {
-        case 0: wait_vm<0>(); break;
-        case 1: wait_vm<1>(); break;
-        case 2: wait_vm<2>(); break;
-        case 3: wait_vm<3>(); break;
-        case 4: wait_vm<4>(); break;
-        case 5: wait_vm<5>(); break;
-        case 6: wait_vm<6>(); break;
-        case 7: wait_vm<7>(); break;
-        case 8: wait_vm<8>(); break;
-        case 9: wait_vm<9>(); break;
-        case 10: wait_vm<10>(); break;
-        case 11: wait_vm<11>(); break;
-        case 12: wait_vm<12>(); break;
-        case 13: wait_vm<13>(); break;
-        case 14: wait_vm<14>(); break;
-        default: wait_vm<15>(); break;
-    }
-}
-
 // dQ^T += K^T dS^T over 32-key tiles: 128 queries per workgroup, one 32-query sub-block per
 // wave.  K's planes stream through LDS in three buffers, copied two tiles ahead, and give K^T
 // through transposing reads, as in the dQ stage above.  Each wave copies its 32 queries' dS

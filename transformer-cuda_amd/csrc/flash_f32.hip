@@ -653,7 +653,7 @@ struct DkdvLds {
     float st[2][kTile];  // per query of the tile: lse2, D
 };
 
-template <int D>
+template <int D, bool DS>
 __device__ __forceinline__ void dkdv_chunk(const float* __restrict__ qh,
                                            const float* __restrict__ doh,
                                            const float* __restrict__ m,
@@ -666,7 +666,8 @@ __device__ __forceinline__ void dkdv_chunk(const float* __restrict__ qh,
                                            Fetch& fetch,
                                            const TileCopyAnyStride<D, DkdvLds<D>::QS>& tc,
                                            f32x16 (&dk_acc)[D / 32],
-                                           f32x16 (&dv_acc)[D / 32]) {
+                                           f32x16 (&dv_acc)[D / 32], float* ds_head = nullptr,
+                                           int ds_n = 0) {
     constexpr int QS = DkdvLds<D>::QS;
     constexpr int GS = DkdvLds<D>::GS;
     const float* Qs = L.q;
@@ -710,6 +711,17 @@ __device__ __forceinline__ void dkdv_chunk(const float* __restrict__ qh,
             s[r] = p;
             ds[r] = p * (dp[r] - St[1][qr]);
         }
+        if constexpr (DS) {
+            // dS of the tile, query-major: row t*32 + acc_row(r, half), column kj; a 32-lane
+            // store covers one query's 32 keys (128 bytes).  Keys past T get zeros.
+            const int kj = kb * kTile + col;
+            float* row = ds_head + static_cast<size_t>(t * kTile) * ds_n;
+            const uint32_t loff = static_cast<uint32_t>(4 * half * ds_n + kj);
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                row[static_cast<size_t>(8 * (r / 4) + r % 4) * ds_n + loff] =
+                    kj < T ? ds[r] : 0.0f;
+        }
         f32x16 part[D / 32];
         zero(part);
         mma_cols<D, GS>(Gs, col, half, s, part);
@@ -726,13 +738,15 @@ __device__ __forceinline__ void dkdv_chunk(const float* __restrict__ qh,
     }
 }
 
-template <int D>
+// DS: dS written out as well (ds: B*H heads of ds_n x ds_n fp32, rows = queries), for the
+// dQ-from-dS kernel below.
+template <int D, bool DS>
 TCAMD_F32_KERNEL(kDkdvWaves) void flash_bwd_dkdv_f32_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
     const float* __restrict__ dO, const float* __restrict__ m, const float* __restrict__ l,
     const float* __restrict__ Dws, float* __restrict__ dk, float* __restrict__ dv, int BH,
     int T, float scale, int nkb, QueueSlot* slot, int per_xcd, HeadView xv, HeadView ov,
-    HeadView gv) {
+    HeadView gv, float* __restrict__ ds, int ds_n) {
     __shared__ DkdvLds<D> L[kDkdvWaves];
     __shared__ unsigned s_next;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
@@ -761,8 +775,11 @@ TCAMD_F32_KERNEL(kDkdvWaves) void flash_bwd_dkdv_f32_kernel(
         load_row_half<D>(vreg, v + xoff, kj, T, half, xv.row);
         Fetch fetch{wave == 0 ? &tq : nullptr, 0u, task};
         f32x16 dk_acc[D / 32], dv_acc[D / 32];
-        dkdv_chunk<D>(q + xoff, dO + ooff, m, l, Dws, stat_off, T, xv.row, ov.row, c, kb, kb + t0,
-                      kb + t1, kreg, vreg, L[wave], lane, fetch, tc, dk_acc, dv_acc);
+        float* ds_head = nullptr;
+        if constexpr (DS) ds_head = ds + static_cast<size_t>(bh) * ds_n * ds_n;
+        dkdv_chunk<D, DS>(q + xoff, dO + ooff, m, l, Dws, stat_off, T, xv.row, ov.row, c, kb,
+                          kb + t0, kb + t1, kreg, vreg, L[wave], lane, fetch, tc, dk_acc, dv_acc,
+                          ds_head, ds_n);
 
         // Merge: every wave publishes its partial dK, dV; wave w sums (in wave order) and
         // stores the 8-element chunks w, w+4, ... of the concatenated (dK, dV) accumulators.
@@ -794,6 +811,169 @@ TCAMD_F32_KERNEL(kDkdvWaves) void flash_bwd_dkdv_f32_kernel(
         __syncthreads();
         task = __builtin_amdgcn_readfirstlane(s_next);  // the same in every lane
     }
+}
+
+// --------------------------------------------------------------------------------------
+// The dS-first backward order: D first (the dQ kernel's sums, alone), then dK/dV writing dS
+// (DS = true above), then dQ = scale * dS K from the stored dS, whose products (one of the
+// dQ kernel's three) are then all that dQ costs.
+// --------------------------------------------------------------------------------------
+
+// D = rowsum(dO o O): two lanes per row, lane `half` an fma chain over elements
+// half*D/2 .. in order, the two halves added: the dQ kernel's D, bitwise.  nrows = B*H*T.
+template <int D>
+__global__ __launch_bounds__(256) void d_rows_f32_kernel(const float* __restrict__ dO,
+                                                         const float* __restrict__ O,
+                                                         HeadView ov, float* __restrict__ Dws,
+                                                         int nrows, int T) {
+    const int gid = blockIdx.x * 256 + threadIdx.x;
+    const int row = gid >> 1;
+    const int half = gid & 1;
+    float pd = 0.0f;
+    if (row < nrows) {
+        const int bh = row / T;
+        const int t = row - bh * T;
+        const size_t off = ov.off(bh) + static_cast<size_t>(t) * ov.row + half * (D / 2);
+#pragma unroll
+        for (int j = 0; j < D / 2; j += 4) {
+            const f32x4 a = *reinterpret_cast<const f32x4*>(dO + off + j);
+            const f32x4 b = *reinterpret_cast<const f32x4*>(O + off + j);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) pd = fmaf(a[e], b[e], pd);
+        }
+    }
+    const float sum = pd + __shfl_xor(pd, 1);
+    if (row < nrows && half == 0) Dws[row] = sum;
+}
+
+// dQ^T += K^T dS^T over 32-key tiles: 128 queries per workgroup, one 32-query sub-block per
+// wave, on v_mfma_f32_32x32x2_f32 with the backward kernels' two-level summation (each
+// tile's products in a fresh accumulator).  K tiles (fp32 rows, bank-conflict-free stride)
+// stream through LDS in three buffers, two tiles ahead, the copy instructions of a tile
+// shared out over the four waves; each wave copies its 32 queries' dS rows of a tile (32 keys,
+// 128 bytes each, 8 lanes per row) into its own LDS slot (two slots), two tiles ahead, and a
+// lane reads back the 16 keys of its query that its accumulator-layout B operand holds (four
+// runs of 4, XOR-swizzled so that the reads are conflict-free).  Key tiles past a wave's
+// diagonal are skipped (dS is not written there); the diagonal tile holds the zeros of the
+// causal mask.  The copies retire in issue order: a step waits for tile kt's K copies
+// before the barrier and for its own dS copies after it.
+template <int D>
+__global__ __launch_bounds__(kWave * 4) void flash_bwd_dq_ds_f32_kernel(
+    const float* __restrict__ k, HeadView kv, const float* __restrict__ ds, int ds_n,
+    float* __restrict__ dq, HeadView gv, int BH, int T, float scale, int nblk) {
+    constexpr int kWv = 4;                 // waves per workgroup
+    constexpr int KS = D + 4;              // K row stride in LDS (floats)
+    using Sh = TileShape<D, KS>;
+    constexpr int NB = 3;                  // K buffers
+    constexpr int kLoads = 4;              // dS copies per wave and tile: 32 rows x 128 bytes
+    constexpr uint32_t kSlot = kLoads * 1024;
+    __shared__ __attribute__((aligned(16))) float smk[NB][kTile * KS];
+    __shared__ __attribute__((aligned(1024))) float sms[kWv][2][kLoads * 256];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & (kWave - 1);
+    const int col = lane & 31;
+    const int half = lane >> 5;
+    // heaviest query block first; every block of a head on one XCD when BH % 8 == 0
+    int bh, rank;
+    if ((BH & 7) == 0) {
+        const int hpx = BH >> 3;
+        const int slot = blockIdx.x >> 3;
+        bh = (blockIdx.x & 7) * hpx + slot % hpx;
+        rank = slot / hpx;
+    } else {
+        bh = blockIdx.x % BH;
+        rank = blockIdx.x / BH;
+    }
+    const int q0 = (nblk - 1 - rank) * kWv * kTile;
+    const int qj = q0 + kTile * wave;
+    const float* kh = k + kv.off(bh);
+    const int krs = kv.row;
+    // K tile copies: instruction i of a tile is issued by wave i % 4
+    uint32_t voff[Sh::kInst];
+#pragma unroll
+    for (int i = 0; i < Sh::kInst; ++i) {
+        int r, b;
+        Sh::row_byte(i, lane, r, b);
+        voff[i] = static_cast<uint32_t>(r * krs * 4 + b);
+    }
+    int ncopy = 0;
+#pragma unroll
+    for (int i = 0; i < Sh::kInst; ++i) ncopy += i % kWv == wave ? 1 : 0;
+    constexpr int kMaxCopy = (Sh::kInst + kWv - 1) / kWv;  // ncopy of wave 0
+    static_assert(2 * kLoads + kMaxCopy <= 15 && kLoads + 2 * kMaxCopy <= 15,
+                  "wait_vm_at_most's counts");
+    auto copy_tile = [&](int kt, uint32_t buf) {
+        const int row0 = kt * kTile;
+        const float* base = kh + static_cast<size_t>(row0) * krs;
+        const bool whole = row0 + kTile <= T;
+        const uint32_t last = Sh::last(row0, T, krs);
+#pragma unroll
+        for (int i = 0; i < Sh::kInst; ++i)
+            if (i % kWv == wave && Sh::active(i, lane))
+                dma_dwordx4(base, buf + static_cast<uint32_t>(1024 * i),
+                            whole ? voff[i] : min(voff[i], last));
+    };
+    const int kend = min(T, q0 + kWv * kTile);
+    const int ntile = (kend + kTile - 1) / kTile;
+    // key tiles 0 .. qj/32 (the last one the diagonal); none when the wave's queries start past
+    // T.  Rows qj + col < ds_n when qj < T.
+    const int nmine = qj < T ? min(qj / kTile + 1, ntile) : 0;
+    const float* sbase = ds + (static_cast<size_t>(bh) * ds_n + min(qj, ds_n - kTile)) * ds_n;
+    // A slot holds the tile's 32 query rows of 32 keys; 16-byte chunk c of row r at
+    // r*128 + 16*(c ^ ((r/2) % 8)).  Copy j: lane i fills slot bytes 1024j + 16i, row 8j + i/8.
+    uint32_t soff[kLoads];
+#pragma unroll
+    for (int j = 0; j < kLoads; ++j) {
+        const int r = 8 * j + lane / 8;
+        const int c = (lane % 8) ^ ((r >> 1) & 7);
+        soff[j] = static_cast<uint32_t>((r * ds_n + 4 * c) * 4);
+    }
+    const uint32_t s_lds = lds_addr(sms[wave][0]);
+    auto copy_ds = [&](int kt) {
+        const float* b = sbase + kTile * kt;
+#pragma unroll
+        for (int j = 0; j < kLoads; ++j)
+            dma_dwordx4(b, s_lds + static_cast<uint32_t>(kt & 1) * kSlot + 1024 * j, soff[j]);
+    };
+    copy_tile(0, lds_addr(smk[0]));
+    if (0 < nmine) copy_ds(0);
+    if (1 < ntile) copy_tile(1, lds_addr(smk[1]));
+    if (1 < nmine) copy_ds(1);
+    f32x16 acc[D / 32];
+    zero(acc);
+    for (int kt = 0; kt < ntile; ++kt) {
+        // this wave's copies of K tile kt landed: outstanding may be only its dS of tile kt
+        // and tile kt+1's copies ...
+        wait_vm_at_most((kt < nmine ? kLoads : 0) + (kt + 1 < ntile ? ncopy : 0) +
+                        (kt + 1 < nmine ? kLoads : 0));
+        __syncthreads();  // ... and every wave's; tile kt-1's buffer is no longer read
+        if (kt + 2 < ntile) copy_tile(kt + 2, lds_addr(smk[(kt + 2) % NB]));
+        if (kt >= nmine) continue;
+        // dS of tile kt landed: outstanding may be only tile kt+1's and K tile kt+2's copies
+        wait_vm_at_most((kt + 1 < ntile ? ncopy : 0) + (kt + 1 < nmine ? kLoads : 0) +
+                        (kt + 2 < ntile ? ncopy : 0));
+        // B operand in accumulator layout: element r = key acc_row(r, half) = 8(r/4) +
+        // 4 half + r%4 of this lane's query: run j = r/4, chunk 2j + half of the row
+        f32x16 sb;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const f32x4 x = *(TCAMD_LDS const f32x4*)(uintptr_t)(
+                s_lds + static_cast<uint32_t>(kt & 1) * kSlot + 128 * col +
+                16 * ((2 * j + half) ^ ((col >> 1) & 7)));
+#pragma unroll
+            for (int e = 0; e < 4; ++e) sb[4 * j + e] = x[e];
+        }
+        if (kt + 2 < nmine) {
+            wait_lds();  // the slot's reads are done before the copy into it starts
+            copy_ds(kt + 2);
+        }
+        f32x16 part[D / 32];
+        zero(part);
+        mma_cols<D, KS>(smk[kt % NB], col, half, sb, part);
+        add_into(acc, part);
+    }
+    const int qi = qj + col;
+    if (qi < T) store_acc_row<D>(dq + gv.off(bh), qi, half, acc, scale, gv.row);
 }
 
 __device__ QueueSlot g_fwd_queue[kQueueSlots];
@@ -873,20 +1053,32 @@ void dq_dispatch(const float* q, const float* k, const float* v, const float* o,
                        (BH % kXcds) == 0 ? 1 : 0, xv, ov, gv);
 }
 
-template <int D>
-void dkdv_dispatch(const float* q, const float* k, const float* v, const float* dO,
-                   const float* m, const float* l, const float* Dws, float* dk, float* dv,
-                   int BH, int T, float scale, const HeadView& xv, const HeadView& ov,
-                   const HeadView& gv, hipStream_t stream) {
+template <int D, bool DS>
+void dkdv_launch(const float* q, const float* k, const float* v, const float* dO,
+                 const float* m, const float* l, const float* Dws, float* dk, float* dv, int BH,
+                 int T, float scale, const HeadView& xv, const HeadView& ov, const HeadView& gv,
+                 float* ds, hipStream_t stream) {
     const int nkb = (T + kTile - 1) / kTile;
     bool ok = true;
     QueueSlot* slot = launch_slot(Family::Dkdv, g_dkdv_ticket, stream, ok);
     if (!ok) return;
-    const int grid = persistent_grid(flash_bwd_dkdv_f32_kernel<D>, kWave * kDkdvWaves, 0,
+    const int grid = persistent_grid(flash_bwd_dkdv_f32_kernel<D, DS>, kWave * kDkdvWaves, 0,
                                      static_cast<long long>(BH) * nkb);
-    hipLaunchKernelGGL(flash_bwd_dkdv_f32_kernel<D>, dim3(grid), dim3(kWave * kDkdvWaves), 0, stream, q, k,
-                       v, dO, m, l, Dws, dk, dv, BH, T, scale, nkb, slot,
-                       (BH % kXcds) == 0 ? 1 : 0, xv, ov, gv);
+    hipLaunchKernelGGL((flash_bwd_dkdv_f32_kernel<D, DS>), dim3(grid), dim3(kWave * kDkdvWaves), 0,
+                       stream, q, k, v, dO, m, l, Dws, dk, dv, BH, T, scale, nkb, slot,
+                       (BH % kXcds) == 0 ? 1 : 0, xv, ov, gv, ds, ds_rows(T));
+}
+
+template <int D>
+void dkdv_dispatch(const float* q, const float* k, const float* v, const float* dO,
+                   const float* m, const float* l, const float* Dws, float* dk, float* dv,
+                   int BH, int T, float scale, const HeadView& xv, const HeadView& ov,
+                   const HeadView& gv, float* ds, hipStream_t stream) {
+    if (ds != nullptr)
+        dkdv_launch<D, true>(q, k, v, dO, m, l, Dws, dk, dv, BH, T, scale, xv, ov, gv, ds, stream);
+    else
+        dkdv_launch<D, false>(q, k, v, dO, m, l, Dws, dk, dv, BH, T, scale, xv, ov, gv, ds,
+                              stream);
 }
 
 }  // namespace
@@ -923,11 +1115,36 @@ void launch_flash_bwd_dkdv_f32(const float* q, const float* k, const float* v,
                                const float* dO, const float* m, const float* l,
                                const float* Dws, float* dk, float* dv, int BH, int T, int d,
                                float scale, const HeadView& xv, const HeadView& ov,
-                               const HeadView& gv, hipStream_t stream) {
+                               const HeadView& gv, hipStream_t stream, float* ds) {
     switch (d) {
-        case 32: dkdv_dispatch<32>(q, k, v, dO, m, l, Dws, dk, dv, BH, T, scale, xv, ov, gv, stream); break;
-        case 64: dkdv_dispatch<64>(q, k, v, dO, m, l, Dws, dk, dv, BH, T, scale, xv, ov, gv, stream); break;
-        default: dkdv_dispatch<128>(q, k, v, dO, m, l, Dws, dk, dv, BH, T, scale, xv, ov, gv, stream); break;
+        case 32: dkdv_dispatch<32>(q, k, v, dO, m, l, Dws, dk, dv, BH, T, scale, xv, ov, gv, ds, stream); break;
+        case 64: dkdv_dispatch<64>(q, k, v, dO, m, l, Dws, dk, dv, BH, T, scale, xv, ov, gv, ds, stream); break;
+        default: dkdv_dispatch<128>(q, k, v, dO, m, l, Dws, dk, dv, BH, T, scale, xv, ov, gv, ds, stream); break;
+    }
+}
+
+void launch_bwd_d_rows_f32(const float* dO, const float* O, const HeadView& ov, float* Dws,
+                           int BH, int T, int d, hipStream_t stream) {
+    const int nrows = BH * T;
+    const unsigned blocks = static_cast<unsigned>((2LL * nrows + 255) / 256);
+    switch (d) {
+        case 32: hipLaunchKernelGGL((d_rows_f32_kernel<32>), dim3(blocks), dim3(256), 0, stream, dO, O, ov, Dws, nrows, T); break;
+        case 64: hipLaunchKernelGGL((d_rows_f32_kernel<64>), dim3(blocks), dim3(256), 0, stream, dO, O, ov, Dws, nrows, T); break;
+        default: hipLaunchKernelGGL((d_rows_f32_kernel<128>), dim3(blocks), dim3(256), 0, stream, dO, O, ov, Dws, nrows, T); break;
+    }
+}
+
+void launch_flash_bwd_dq_ds_f32(const float* k, const HeadView& kv, const float* ds, float* dq,
+                                const HeadView& gv, int BH, int T, int d, float scale,
+                                hipStream_t stream) {
+    constexpr int kBlock = 4 * kTile;
+    const int nblk = (T + kBlock - 1) / kBlock;
+    const dim3 grid(BH * nblk), block(kWave * 4);
+    const int n = ds_rows(T);
+    switch (d) {
+        case 32: hipLaunchKernelGGL((flash_bwd_dq_ds_f32_kernel<32>), grid, block, 0, stream, k, kv, ds, n, dq, gv, BH, T, scale, nblk); break;
+        case 64: hipLaunchKernelGGL((flash_bwd_dq_ds_f32_kernel<64>), grid, block, 0, stream, k, kv, ds, n, dq, gv, BH, T, scale, nblk); break;
+        default: hipLaunchKernelGGL((flash_bwd_dq_ds_f32_kernel<128>), grid, block, 0, stream, k, kv, ds, n, dq, gv, BH, T, scale, nblk); break;
     }
 }
 

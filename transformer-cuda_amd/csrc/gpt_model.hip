@@ -90,6 +90,7 @@ struct gpt_model {
     // backward scratch shared by the layers
     float *d_x = nullptr, *d_ln = nullptr, *d_qkv = nullptr, *d_merged = nullptr,
           *d_ffn_a = nullptr, *d_ffn_b = nullptr, *ws = nullptr, *colsum = nullptr, *splitk = nullptr,
+          *attn_ds = nullptr,  // fused fp32 attention: the backward's dS, shared by the layers
           *norm = nullptr, *proj = nullptr;
     float *dq = nullptr, *dk = nullptr, *dv = nullptr, *d_attn_out = nullptr;  // split modes
     float *scores = nullptr, *dprobs = nullptr, *dscores = nullptr;          // materialised
@@ -255,9 +256,10 @@ int attention_backward(gpt_model* m, LayerActs& a, hipStream_t s) {
     const float scale = 1.0f / sqrtf(static_cast<float>(d));
     attn_mark(m, s);
     switch (c.attention_mode) {
-        case GPT_ATTN_FUSED:
-            TRY(attn_fused_causal_backward_f32(a.qkv, a.merged, m->d_merged, a.attn_m, a.attn_l,
-                                               m->d_qkv, m->ws, B, H, T, d, scale, s));
+        case GPT_ATTN_FUSED:  // dS-first: dK/dV write dS, dQ is computed from it
+            TRY(attn_fused_causal_backward_ds_f32(a.qkv, a.merged, m->d_merged, a.attn_m,
+                                                  a.attn_l, m->d_qkv, m->ws, m->attn_ds, B, H, T,
+                                                  d, scale, s));
             break;
         case GPT_ATTN_FUSED_X3:  // the layer's qkv and planes are the forward's
             TRY(attn_fused_causal_backward_f32x3(a.qkv, a.merged, m->d_merged, a.attn_m,
@@ -367,6 +369,12 @@ int create(const gpt_config& c, gpt_model* m) {
     TRY(alloc(m, &m->d_ffn_b, BT * F));
     TRY(alloc(m, &m->proj, BT * C));
     TRY(alloc(m, &m->ws, B * H * T));
+    if (c.attention_mode == GPT_ATTN_FUSED) {
+        const size_t bytes = attn_f32_ds_workspace_bytes(static_cast<int>(B), static_cast<int>(H),
+                                                         static_cast<int>(T),
+                                                         static_cast<int>(C / H));
+        TRY(alloc(m, &m->attn_ds, static_cast<long long>((bytes + 3) / 4)));
+    }
     long long sk = head_splitk(c) ? static_cast<long long>(kHeadSplitK) * BT * C : 0;
     if (weight_splitk(c)) sk = std::max(sk, weight_splitk_floats(c));
     if (sk > 0) TRY(alloc(m, &m->splitk, sk));

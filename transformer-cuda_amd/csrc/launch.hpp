@@ -49,11 +49,20 @@ void launch_flash_bwd_dq_f32(const float* q, const float* k, const float* v, con
                              const float* dO, const float* m, const float* l, float* dq,
                              float* Dws, int BH, int T, int d, float scale, const HeadView& xv,
                              const HeadView& ov, const HeadView& gv, hipStream_t stream);
+// Unless ds is null, dS is written as well (fp32, layout of launch_flash_bwd_dkdv_f32x3's),
+// for launch_flash_bwd_dq_ds_f32.
 void launch_flash_bwd_dkdv_f32(const float* q, const float* k, const float* v,
                                const float* dO, const float* m, const float* l,
                                const float* Dws, float* dk, float* dv, int BH, int T, int d,
                                float scale, const HeadView& xv, const HeadView& ov,
-                               const HeadView& gv, hipStream_t stream);
+                               const HeadView& gv, hipStream_t stream, float* ds = nullptr);
+// D = rowsum(dO o O) (views ov) into Dws, with the sums of launch_flash_bwd_dq_f32's D.
+void launch_bwd_d_rows_f32(const float* dO, const float* O, const HeadView& ov, float* Dws,
+                           int BH, int T, int d, hipStream_t stream);
+// dQ = scale * dS K on the fp32 MFMA (k rows: view kv; dq: view gv).
+void launch_flash_bwd_dq_ds_f32(const float* k, const HeadView& kv, const float* ds, float* dq,
+                                const HeadView& gv, int BH, int T, int d, float scale,
+                                hipStream_t stream);
 
 void launch_flash_fwd_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                            uint16_t* o, float* m_out, float* l_out, int BH, int T, int d,

@@ -285,8 +285,9 @@ int attn_packed_causal_backward_dkdv_f32(const float* qkv, const float* do_ptr,
  * Stage 1 above computes S and dP again for dQ, two thirds of its fp32 MFMA work; here the
  * dK/dV stage hands them over as dS.  ds_workspace: attn_f32_ds_workspace_bytes(B, H, T,
  * d_head) bytes (B*H heads of n x n fp32, n = T rounded up to 32), 16-byte aligned; its
- * contents need no initialisation.  D, dK and dV bitwise those of the two-stage order, dQ
- * within fp32 rounding of its. */
+ * contents need no initialisation.  That function returns 0 where the byte count exceeds
+ * SIZE_MAX, and the entry points reject such shapes with ATTN_ERROR_INVALID_DIM.  D, dK and
+ * dV bitwise those of the two-stage order, dQ within fp32 rounding of its. */
 size_t attn_f32_ds_workspace_bytes(int B, int H, int T, int d_head);
 int attn_packed_causal_backward_ds_f32(const float* qkv, const float* o, const float* do_ptr,
                                        const float* m_ptr, const float* l_ptr, float* dqkv,

@@ -215,6 +215,17 @@ def test_f32x3_validation(lib):
     # the fp32 MFMA backward in the dS-first order
     assert raw.attn_f32_ds_workspace_bytes(2, 3, 40, 64) == 6 * 64 * 64 * 4
     assert raw.attn_f32_ds_workspace_bytes(2, 3, 0, 64) == 0
+    # shapes the dimension checks accept but whose dS bytes pass SIZE_MAX: reported as 0
+    # and rejected before any launch (T = 2^26 - 1 at d = 32; 4 * 4095 * 2^52 > 2^64)
+    big_T = (1 << 26) - 1
+    assert raw.attn_f32_ds_workspace_bytes(1, 4095, big_T, 32) == 0
+    assert raw.attn_f32_ds_workspace_bytes(1, 1023, big_T, 32) == 1023 * 4 << 52
+    assert lib.call("attn_packed_causal_backward_ds_f32", FAKE, FAKE, FAKE, FAKE, FAKE, FAKE,
+                    FAKE, FAKE, 1, 4095, big_T, 32, f(0.125), None) == INVALID_DIM
+    assert lib.call("attn_fused_causal_backward_dkdv_ds_f32", FAKE, FAKE, FAKE, FAKE, FAKE,
+                    FAKE, FAKE, 1, 4095, big_T, 32, f(0.125), None) == INVALID_DIM
+    assert lib.call("attn_causal_backward_dq_ds_f32", FAKE, FAKE, FAKE, 1, 4095, big_T, 32,
+                    f(0.125), None) == INVALID_DIM
     for fam in ("packed", "fused"):
         one = lambda ds=FAKE, ws=FAKE, d=64: lib.call(
             f"attn_{fam}_causal_backward_ds_f32", FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, ws, ds, 1,

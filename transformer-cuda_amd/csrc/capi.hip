@@ -211,9 +211,13 @@ int packed_backward_dkdv(const E* qkv, const E* dO, const float* m, const float*
 // ---- fp32 MFMA backward in the dS-first order: D; dK/dV writing dS into a caller
 // workspace (B*H heads of n x n fp32, n = T rounded up to 32); dQ = scale * dS K.
 
+// Elements of the dS area, or 0 when its byte count does not fit in size_t (shapes the
+// dimension checks accept reach 4 * 2^12 * 2^52 bytes).
 size_t ds_f32_elems(int B, int H, int T) {
-    const size_t n = static_cast<size_t>(tcamd::ds_rows(T));
-    return static_cast<size_t>(B) * H * n * n;
+    const size_t n = static_cast<size_t>(tcamd::ds_rows(T));  // <= 2^26: n*n fits
+    const size_t bh = static_cast<size_t>(B) * H;
+    if (bh > (SIZE_MAX / sizeof(float)) / (n * n)) return 0;
+    return bh * n * n;
 }
 
 int packed_backward_prep_f32(const float* o, const float* dO, float* ws, int B, int H, int T,
@@ -234,6 +238,7 @@ int packed_backward_dkdv_ds_f32(const float* qkv, const float* dO, const float* 
     if (ds == nullptr) return ATTN_ERROR_NULL_POINTER;
     const int st = check_packed_bwd(qkv, dO, m, l, dqkv, ws, B, H, T, d, scale);
     if (st != ATTN_SUCCESS) return st;
+    if (ds_f32_elems(B, H, T) == 0) return ATTN_ERROR_INVALID_DIM;
     if (!aligned16(ds)) return ATTN_ERROR_MISALIGNED;
     const size_t C = static_cast<size_t>(H) * d;
     const tcamd::HeadView xv = tcamd::packed_qkv_view(H, T, d);
@@ -249,6 +254,7 @@ int backward_dq_ds_f32(const float* qkv, float* dqkv, const float* ds, int B, in
     if (qkv == nullptr || dqkv == nullptr || ds == nullptr) return ATTN_ERROR_NULL_POINTER;
     const int st = check_packed(B, H, T, d, scale);
     if (st != ATTN_SUCCESS) return st;
+    if (ds_f32_elems(B, H, T) == 0) return ATTN_ERROR_INVALID_DIM;
     if (!aligned16(qkv) || !aligned16(dqkv) || !aligned16(ds)) return ATTN_ERROR_MISALIGNED;
     const size_t C = static_cast<size_t>(H) * d;
     const tcamd::HeadView xv = tcamd::packed_qkv_view(H, T, d);
@@ -263,6 +269,7 @@ int packed_backward_ds_f32(const float* qkv, const float* o, const float* dO, co
     if (o == nullptr || ds == nullptr) return ATTN_ERROR_NULL_POINTER;
     int st = check_packed_bwd(qkv, dO, m, l, dqkv, ws, B, H, T, d, scale);
     if (st != ATTN_SUCCESS) return st;
+    if (ds_f32_elems(B, H, T) == 0) return ATTN_ERROR_INVALID_DIM;     // before any launch
     if (!aligned16(o) || !aligned16(ds)) return ATTN_ERROR_MISALIGNED;  // before any launch
     st = packed_backward_prep_f32(o, dO, ws, B, H, T, d, merged, stream);
     if (st != ATTN_SUCCESS) return st;

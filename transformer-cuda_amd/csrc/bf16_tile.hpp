@@ -430,15 +430,27 @@ __device__ __forceinline__ bf16x8 stat_chunk(float x, int half) {
     return __builtin_bit_cast(bf16x8, v);
 }
 
+// CUs per XCD of the MI355X (256 CUs in 8 XCDs).
+constexpr int kCusPerXcd = 32;
+
 // Workgroup id -> (head bh, block b) in rank order: b = nb-1-rank when `descending`, else
-// b = rank; when BH % 8 == 0, every block of a head on one XCD (workgroup i runs on XCD
-// i % 8), so a head's tiles stay in one L2.
-__device__ __forceinline__ void map_block(int id, int BH, int nb, bool descending, int& bh,
-                                          int& b) {
+// b = rank, so the heaviest causal blocks start first.  When BH % 8 == 0, every block of a
+// head is on one XCD (workgroup i runs on XCD i % 8), so a head's tiles stay in one L2.
+// `serpentine` (wave-uniform; for grids the device holds at once): the XCD's workgroups take
+// the heaviest-first order in rounds of one per CU with every other full round reversed, so
+// a CU, which then holds the j-th workgroups of consecutive rounds, pairs heavy blocks with
+// light ones (at config 2, three blocks per CU: causal work 12-14 units per CU instead of
+// 10-17).  Grids that do not fit at once keep the plain order: there the heaviest blocks
+// must start first.
+__device__ __forceinline__ void map_block(int id, int BH, int nb, bool descending,
+                                          bool serpentine, int& bh, int& b) {
     int rank;
     if ((BH & 7) == 0) {
         const int hpx = BH >> 3;
-        const int slot = id >> 3;
+        int slot = id >> 3;
+        const int round = slot / kCusPerXcd;
+        if (serpentine && (round & 1) && (round + 1) * kCusPerXcd <= hpx * nb)
+            slot = round * kCusPerXcd + (kCusPerXcd - 1 - slot % kCusPerXcd);
         bh = (id & 7) * hpx + slot % hpx;
         rank = slot / hpx;
     } else {

@@ -50,6 +50,7 @@
 #include "bf16_tile.hpp"
 #include "device_common.hpp"
 #include "launch.hpp"
+#include "sched.hpp"
 
 namespace tcamd {
 namespace {
@@ -295,6 +296,7 @@ struct DqArgs {
     HeadView qv, kv, ov, gv;
     size_t pstride;
     uint16_t* gp;  // dO planes out (NP = 3; laid out as k's), or null
+    int serp;      // map_block's serpentine order (set at launch)
 };
 
 // NSUB = 2: 256 queries per workgroup, wave w owns sub-blocks w (0) and 7-w (1).
@@ -314,7 +316,7 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_bwd_dq_bf16_kernel(DqArgs
     const int half = lane >> 5;
     const int T = a.T;
     int bh, blk;
-    map_block(blockIdx.x, a.BH, nblk, true, bh, blk);
+    map_block(blockIdx.x, a.BH, nblk, true, a.serp != 0, bh, blk);
     const int q0 = blk * kBlock;
     const int qj0 = q0 + kSub * wave;
     const int qj1 = NSUB == 2 ? q0 + kSub * (2 * kWaves - 1 - wave) : qj0;
@@ -573,7 +575,7 @@ __global__ __launch_bounds__(kWave* NW, NP == 1 ? 1 : 2) void flash_bwd_dkdv_bf1
     const int half = lane >> 5;
     const int T = a.T;
     int bh, blk;
-    map_block(blockIdx.x, a.BH, nblk, false, bh, blk);  // block 0 sees every query
+    map_block(blockIdx.x, a.BH, nblk, false, false, bh, blk);  // block 0 sees every query
     const int k0 = blk * kBlock;
     const int kw = k0 + kSub * wave;
     const int kj = kw + col;
@@ -897,7 +899,7 @@ __global__ __launch_bounds__(kWave * kWaves, D >= 128 ? 1 : 2) void flash_bwd_dk
     const int half = lane >> 5;
     const int T = a.T;
     int bh, blk;
-    map_block(blockIdx.x, a.BH, nblk, false, bh, blk);
+    map_block(blockIdx.x, a.BH, nblk, false, false, bh, blk);
     const int k0 = blk * kBlock;
     const int kw = k0 + kSub * wave;
     const int kj = kw + col;
@@ -1201,6 +1203,7 @@ struct DqDsArgs {
     HeadView kv, gv;
     size_t pstride;
     int ds_n;
+    int serp;  // map_block's serpentine order (set at launch)
 };
 
 // dQ^T += K^T dS^T over 32-key tiles: 128 queries per workgroup, one 32-query sub-block per
@@ -1233,7 +1236,7 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_bwd_dq_ds_kernel(DqDsArgs
     const int half = lane >> 5;
     const int T = a.T;
     int bh, blk;
-    map_block(blockIdx.x, a.BH, nblk, true, bh, blk);
+    map_block(blockIdx.x, a.BH, nblk, true, a.serp != 0, bh, blk);
     const int q0 = blk * QB;
     const int qj = q0 + kSub * wave;
     const uint16_t* kh = a.k + a.kv.off(bh);
@@ -1367,11 +1370,12 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_bwd_dq_ds_kernel(DqDsArgs
 }
 
 template <int D, int NSUB, int NP>
-void dq_launch(const DqArgs<NP>& a, hipStream_t stream) {
+void dq_launch(DqArgs<NP> a, hipStream_t stream) {
     constexpr int kBlock = kWaves * NSUB * kSub;
     const int nblk = (a.T + kBlock - 1) / kBlock;
-    hipLaunchKernelGGL((flash_bwd_dq_bf16_kernel<D, NSUB, NP>), dim3(a.BH * nblk),
-                       dim3(kWave * kWaves), 0, stream, a, nblk);
+    const auto kernel = flash_bwd_dq_bf16_kernel<D, NSUB, NP>;
+    a.serp = a.BH * nblk <= resident_capacity(kernel, kWave * kWaves, 0) ? 1 : 0;
+    hipLaunchKernelGGL(kernel, dim3(a.BH * nblk), dim3(kWave * kWaves), 0, stream, a, nblk);
 }
 
 template <int D, int NP>
@@ -1476,15 +1480,12 @@ void launch_bwd_prep_f32x3(const float* o, const float* dO, const HeadView& ov,
 void launch_flash_bwd_dq_ds_f32x3(const uint16_t* k, const HeadView& kv, size_t pstride,
                                   const float* ds, float* dq, const HeadView& gv, int BH, int T,
                                   int d, float scale, hipStream_t stream) {
-    const DqDsArgs a{k, ds, dq, BH, T, scale, kv, gv, pstride, ds_rows(T)};
+    DqDsArgs a{k, ds, dq, BH, T, scale, kv, gv, pstride, ds_rows(T), 0};
     constexpr int kBlock = kWaves * kSub;
     const int nblk = (T + kBlock - 1) / kBlock;
-    if (d == 32)
-        hipLaunchKernelGGL((flash_bwd_dq_ds_kernel<32>), dim3(BH * nblk), dim3(kWave * kWaves), 0,
-                           stream, a, nblk);
-    else
-        hipLaunchKernelGGL((flash_bwd_dq_ds_kernel<64>), dim3(BH * nblk), dim3(kWave * kWaves), 0,
-                           stream, a, nblk);
+    const auto kernel = d == 32 ? flash_bwd_dq_ds_kernel<32> : flash_bwd_dq_ds_kernel<64>;
+    a.serp = BH * nblk <= resident_capacity(kernel, kWave * kWaves, 0) ? 1 : 0;
+    hipLaunchKernelGGL(kernel, dim3(BH * nblk), dim3(kWave * kWaves), 0, stream, a, nblk);
 }
 
 }  // namespace tcamd

@@ -41,6 +41,7 @@
 #include "device_common.hpp"
 #include "bf16_tile.hpp"
 #include "launch.hpp"
+#include "sched.hpp"
 
 namespace tcamd {
 namespace {
@@ -62,13 +63,27 @@ constexpr float kRescaleLog2 = 8.0f;  // raise the running max only beyond p = 2
 template <int NP, int NSUB>
 constexpr bool kFold = NP == 1 && NSUB == 1;
 
+// Bytes of one K or V (plane) tile in LDS: the swizzled tile without the padding after its
+// last 8-row block, which separates that block from no other row of the tile (every read
+// stays inside one tile, and moving a whole tile keeps each read's banks distinct).  Three
+// planes at d = 64 then take 52.5 KB per workgroup instead of 54, and three workgroups fit
+// the 160 KB of LDS.
+template <int D, int NP>
+constexpr uint32_t kFwdTile = Swz<D, kKeyTile<NP>>::kBytes - Swz<D, kKeyTile<NP>>::kPad;
+
+// Workgroups per CU the compiler is asked to fit in registers: three for the three-plane
+// kernel at d = 64 with one sub-block per wave (168 VGPRs, no spills), which the LDS above
+// then also allows.
+template <int D, int NSUB, int NP>
+constexpr int kFwdMinBlocks = (D == 64 && NSUB == 1 && NP == 3) ? 3 : 1;
+
 // Double-buffered K and V tiles, NP planes each.  The row stores of Q's planes and of O go
 // through LDS stages inside an idle buffer (d >= 64; at d = 32 four stages do not fit).
 template <int D, int NP>
 struct FwdSmem {
-    uint16_t k[2][NP][Swz<D, kKeyTile<NP>>::kBytes / 2];
-    uint16_t v[2][NP][Swz<D, kKeyTile<NP>>::kBytes / 2];
-    static_assert(D < 64 || 2 * kStageBytes<D, NP> <= NP * Swz<D, kKeyTile<NP>>::kBytes,
+    uint16_t k[2][NP][kFwdTile<D, NP> / 2];
+    uint16_t v[2][NP][kFwdTile<D, NP> / 2];
+    static_assert(D < 64 || 2 * kStageBytes<D, NP> <= NP * kFwdTile<D, NP>,
                   "two wave stages per idle K (or V) buffer");
 };
 template <int D>
@@ -173,7 +188,7 @@ __device__ __forceinline__ void half_step(int kb, const uint32_t (&ka)[D / 16],
                                           const bf16x8 (&q1)[D / 16][NP], SubState<D>& st0,
                                           SubState<D>& st1, int qj0, int qj1, int col, int half,
                                           float c, const bf16x8& one) {
-    constexpr uint32_t kPlane = Swz<D, kKeyTile<NP>>::kBytes;
+    constexpr uint32_t kPlane = kFwdTile<D, NP>;
     f32x16 s0 = f32x16{}, s1 = f32x16{};
     if constexpr (FOLD) {  // -m_used into every score of the query
         s1 = mfma_32x32x16_bf16(one, st1.xs, s1);
@@ -214,22 +229,23 @@ using OutT = std::conditional_t<NP == 1, uint16_t, float>;
 // q is bf16 like k; NP = 3: Q comes from the fp32 tensor qf (view qv) and is split here,
 // and its planes are written to qp (laid out as k's) when qp is not null.
 template <int D, int NSUB, int NP>
-__global__ __launch_bounds__(kWave* kWaves) void flash_fwd_bf16_kernel(
+__global__ __launch_bounds__(kWave* kWaves, (kFwdMinBlocks<D, NSUB, NP>)) void flash_fwd_bf16_kernel(
     const uint16_t* __restrict__ q, const float* __restrict__ qf,
     const uint16_t* __restrict__ k, const uint16_t* __restrict__ v, OutT<NP>* __restrict__ o,
     float* __restrict__ m_out, float* __restrict__ l_out, int BH, int T, float scale, int nblk,
-    HeadView xv, HeadView qv, HeadView ov, size_t pstride, uint16_t* __restrict__ qp) {
+    HeadView xv, HeadView qv, HeadView ov, size_t pstride, uint16_t* __restrict__ qp,
+    int serp) {
     constexpr int KT = kKeyTile<NP>;
     constexpr int kHalves = KT / 32;  // 32-key half tiles per tile
     using S = Swz<D, KT>;
-    constexpr uint32_t kBuf = NP * S::kBytes;  // one K (or V) buffer: NP plane tiles
+    constexpr uint32_t kBuf = NP * kFwdTile<D, NP>;  // one K (or V) buffer: NP plane tiles
     __shared__ __attribute__((aligned(1024))) FwdSmem<D, NP> sm;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     const int lane = threadIdx.x & (kWave - 1);
     const int col = lane & 31;
     const int half = lane >> 5;
     int bh, blk;
-    map_block(blockIdx.x, BH, nblk, true, bh, blk);
+    map_block(blockIdx.x, BH, nblk, true, serp != 0, bh, blk);
     constexpr int kBlock = kWaves * NSUB * kSub;
     const int q0 = blk * kBlock;
     const int qj0 = q0 + kSub * wave;                                     // sub-block 0
@@ -273,10 +289,10 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_fwd_bf16_kernel(
         const uint32_t buf = static_cast<uint32_t>(kt & 1) * kBuf;
 #pragma unroll
         for (int i = 0; i < NP; ++i) {
-            dma_tile<D, kWaves, KT>(kh + i * pstride, kt * KT, T, k_lds + buf + i * S::kBytes,
-                                    wave, lane, xrs);
-            dma_tile<D, kWaves, KT>(vh + i * pstride, kt * KT, T, v_lds + buf + i * S::kBytes,
-                                    wave, lane, xrs);
+            dma_tile<D, kWaves, KT>(kh + i * pstride, kt * KT, T,
+                                    k_lds + buf + i * kFwdTile<D, NP>, wave, lane, xrs);
+            dma_tile<D, kWaves, KT>(vh + i * pstride, kt * KT, T,
+                                    v_lds + buf + i * kFwdTile<D, NP>, wave, lane, xrs);
         }
     };
     copy_tile(0);
@@ -385,9 +401,11 @@ template <int D, int NSUB, int NP>
 void fwd_launch(const FwdArgs<NP>& a, hipStream_t stream) {
     constexpr int kBlock = kWaves * NSUB * kSub;
     const int nblk = (a.T + kBlock - 1) / kBlock;
-    hipLaunchKernelGGL((flash_fwd_bf16_kernel<D, NSUB, NP>), dim3(a.BH * nblk),
-                       dim3(kWave * kWaves), 0, stream, a.q, a.qf, a.k, a.v, a.o, a.m_out,
-                       a.l_out, a.BH, a.T, a.scale, nblk, a.xv, a.qv, a.ov, a.pstride, a.qp);
+    const auto kernel = flash_fwd_bf16_kernel<D, NSUB, NP>;
+    const int serp = a.BH * nblk <= resident_capacity(kernel, kWave * kWaves, 0) ? 1 : 0;
+    hipLaunchKernelGGL(kernel, dim3(a.BH * nblk), dim3(kWave * kWaves), 0, stream, a.q, a.qf,
+                       a.k, a.v, a.o, a.m_out, a.l_out, a.BH, a.T, a.scale, nblk, a.xv, a.qv,
+                       a.ov, a.pstride, a.qp, serp);
 }
 
 template <int D, int NP>

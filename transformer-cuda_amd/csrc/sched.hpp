@@ -106,11 +106,10 @@ inline bool stream_is_capturing(hipStream_t stream) {
     return st != hipStreamCaptureStatusNone;
 }
 
-// Host side: persistent grid size: every resident workgroup slot of the device, a multiple
-// of kXcds, and no more workgroups than tasks (rounded up).  The resident capacity is cached
-// per (thread, kernel, device).
+// Host side: the workgroups of `kernel` (block threads, lds_bytes of dynamic LDS) that the
+// device holds at once, cached per (thread, kernel, device).
 template <typename Kernel>
-int persistent_grid(Kernel kernel, int block, size_t lds_bytes, long long n_tasks) {
+int resident_capacity(Kernel kernel, int block, size_t lds_bytes) {
     struct Entry {
         const void* fn;
         int dev;
@@ -136,7 +135,14 @@ int persistent_grid(Kernel kernel, int block, size_t lds_bytes, long long n_task
         cache[cache_next] = Entry{fn, dev, cap};
         cache_next = (cache_next + 1) % 16;
     }
-    long long g = cap;
+    return cap;
+}
+
+// Host side: persistent grid size: every resident workgroup slot of the device, a multiple
+// of kXcds, and no more workgroups than tasks (rounded up).
+template <typename Kernel>
+int persistent_grid(Kernel kernel, int block, size_t lds_bytes, long long n_tasks) {
+    long long g = resident_capacity(kernel, block, lds_bytes);
     const long long want = ((n_tasks + kXcds - 1) / kXcds) * kXcds;
     if (want < g) g = want;
     g = (g / kXcds) * kXcds;

@@ -1,7 +1,8 @@
 """Forward + backward captured into a HIP graph (torch.cuda.graph) and replayed: every replay
 equals the ordinary (eager) calls bitwise.  Covers the fp32 MFMA path, whose persistent
 kernels pull tasks from device-side counters in eager mode and switch to the static
-schedule under capture, the three-plane fp32 path and the bf16 path.  Replays run in
+schedule under capture (also in the dS-first order), the three-plane fp32 path and the bf16
+path.  Replays run in
 series with eager launches of the same kernel families between them (which take queue
 slots), and the outputs are cleared before every replay so each replay must write them."""
 import pytest
@@ -59,6 +60,43 @@ def test_graph_fp32_tiled(lib, d):
     with torch.cuda.graph(g):
         run(*outs)
     _replay_and_check(g, outs[:6], lambda: run(*scratch), want[:6])
+
+
+@pytest.mark.gpu
+def test_graph_fp32_packed_ds(lib):
+    """The fp32 MFMA backward in the dS-first order (its dK/dV stage is a persistent kernel:
+    queue in eager mode, static schedule under capture)."""
+    B, H, T, d = 2, 4, 517, 64
+    scale = default_scale(d)
+    q, k, v, do = _inputs(B, H, T, d, torch.float32, 14)
+    qkv = torch.stack([q, k, v], 0).permute(1, 3, 0, 2, 4).reshape(B, T, 3 * H * d).contiguous()
+    r = B * H * T
+    nds = lib.f32_ds_workspace_bytes(B, H, T, d) // 4
+
+    def run(o, m, l, dqkv, ws, ds):
+        lib.packed_causal_attention_forward(qkv, o, B, H, T, d, scale, m, l)
+        lib.packed_causal_attention_backward_ds(qkv, o, do, m, l, dqkv, ws, ds, B, H, T, d,
+                                                scale)
+
+    mk = lambda: (torch.empty_like(q), q.new_empty(r), q.new_empty(r), torch.empty_like(qkv),
+                  q.new_empty(r), q.new_empty(nds))
+    want = mk()
+    run(*want)
+    torch.cuda.synchronize()
+    scratch, outs = mk(), mk()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        run(*outs)
+    for rep in range(3):
+        for t in outs[:5]:
+            t.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for name, got, exp in zip(("o", "m", "l", "dqkv", "D"), outs[:5], want[:5]):
+            assert torch.equal(got, exp), f"replay {rep}: {name} differs from eager"
+        run(*scratch)
+        torch.cuda.synchronize()
 
 
 @pytest.mark.gpu

@@ -2,9 +2,9 @@
 equals the ordinary (eager) calls bitwise.  Covers the fp32 MFMA path, whose persistent
 kernels pull tasks from device-side counters in eager mode and switch to the static
 schedule under capture (also in the dS-first order), the three-plane fp32 path and the bf16
-path.  Replays run in
-series with eager launches of the same kernel families between them (which take queue
-slots), and the outputs are cleared before every replay so each replay must write them."""
+path.  Replays run in series with eager launches of the same kernel families between them
+(which take queue slots), and the outputs are cleared before every replay so each replay
+must write them."""
 import pytest
 import torch
 

@@ -36,13 +36,18 @@ convention: fwd 2*B*H*T^2*d, bwd 5*B*H*T^2*d), divided by the wall-clock time of
 timed steps.  Before the W warmup steps, untimed steps run for --ramp-s seconds (ramp_s in
 the line, default 0.5) so that the GPU's clocks have left their idle state: a few
 milliseconds of warmup alone leave the timed steps partly at ramp-up clocks (config 2:
-~10% below the steady rate).  The roofline object describes the dominant kernel (the longest average
-duration, measured with HIP events recorded on the launch stream around every kernel of
-every timed step) against its algorithmic FLOPs:
+~10% below the steady rate).  The roofline object describes the dominant kernel (the launch
+with the most algorithmic work, the dK/dV stage on every path; its average duration is
+measured with HIP events recorded on the launch stream around it in every timed step)
+against its algorithmic FLOPs:
     forward 2 units, backward dK/dV 4 units (S recompute, dP, dV, dK), backward dQ 1 unit
     (dQ; its S and dP recomputes, where it makes them, duplicate work already counted), unit =
     B*H*T^2*d.  bwd_prep_x3 is HBM-bound: it reads O and dO (fp32) and writes the three bf16
     planes of dO and D, 14*B*H*T*d + 4*B*H*T bytes.
+The other kernels' durations (the line's "kernels" table) come from a separate pass after the
+timed steps, with an event after every launch: each event record takes about 2.5 us of GPU
+time, so events around all five launches of the config-2 step would add about 16 us to a
+343 us step.
 For the x3 path the roofline is the bf16 MFMA's: achieved = 6 x the algorithmic FLOPs (six
 bf16 plane products per fp32 product) per second against the bf16 peak, with the fp32
 algorithmic rate (TFLOP/s, not a fraction of any peak) beside it.
@@ -282,9 +287,17 @@ class PathRunner:
         elem = 2 if self.dtype == "bf16" else 4
         return 6.0 * self.B * self.T * self.C * elem, "byte"
 
-    def timed(self, steps, warmup, ramp_s=0.0):
-        """Time `steps` steps after `ramp_s` seconds of untimed steps and `warmup` more;
-        per-kernel durations from events on the launch stream."""
+    def dominant(self):
+        """Name of the launch with the most algorithmic FLOPs (the dK/dV stage)."""
+        flop = [(self.kernel_work(n)[0], n) for n, _ in self.launches()
+                if self.kernel_work(n)[1] == "flop"]
+        return max(flop)[1]
+
+    def timed(self, steps, warmup, ramp_s=0.0, breakdown_steps=20):
+        """Time `steps` steps after `ramp_s` seconds of untimed steps and `warmup` more, with
+        events on the launch stream around the dominant launch of every step only; then the
+        other launches' durations from `breakdown_steps` more steps (not timed) with an event
+        after every launch."""
         torch = self.torch
         t_end = time.perf_counter() + ramp_s
         while time.perf_counter() < t_end:
@@ -296,21 +309,36 @@ class PathRunner:
         torch.cuda.synchronize()
         stream = torch.cuda.current_stream()
         launches = self.launches()
-        evs = [[torch.cuda.Event(enable_timing=True) for _ in range(len(launches) + 1)]
+        dom = self.dominant()
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
                for _ in range(steps)]
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         for i in range(steps):
-            evs[i][0].record(stream)
-            for j, (_, fn) in enumerate(launches):
-                fn()
-                evs[i][j + 1].record(stream)
+            for name, fn in launches:
+                if name == dom:
+                    evs[i][0].record(stream)
+                    fn()
+                    evs[i][1].record(stream)
+                else:
+                    fn()
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
+        dom_ms = sum(a.elapsed_time(b) for a, b in evs) / steps
+        n = max(1, breakdown_steps)
+        evb = [[torch.cuda.Event(enable_timing=True) for _ in range(len(launches) + 1)]
+               for _ in range(n)]
+        for i in range(n):
+            evb[i][0].record(stream)
+            for j, (_, fn) in enumerate(launches):
+                fn()
+                evb[i][j + 1].record(stream)
+        torch.cuda.synchronize()
         per_kernel = {}
         for j, (name, _) in enumerate(launches):
-            ms = [evs[i][j].elapsed_time(evs[i][j + 1]) for i in range(steps)]
+            ms = [evb[i][j].elapsed_time(evb[i][j + 1]) for i in range(n)]
             per_kernel[name] = sum(ms) / len(ms)
+        per_kernel[dom] = dom_ms  # the timed steps' own measurement
         return wall, per_kernel
 
     def outputs_finite(self):
@@ -355,7 +383,7 @@ def measured_traffic(config, dtype, kernel):
 
 
 def roofline_of(runner, per_kernel, config):
-    name = max(per_kernel, key=per_kernel.get)
+    name = runner.dominant()
     amount, kind = runner.kernel_work(name)
     sec = per_kernel[name] * 1e-3
     extra = {}

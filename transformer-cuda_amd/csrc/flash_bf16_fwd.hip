@@ -48,10 +48,12 @@ namespace {
 
 using namespace bf16t;
 
-// Keys per LDS tile: 64 for bf16; 32 for three planes, whose double-buffered K and V tiles
-// then take 55 KB at d = 64 (two workgroups per CU) instead of 110 KB.
-template <int NP>
-constexpr int kKeyTile = NP == 1 ? kRowTile : 32;
+// Keys per LDS tile: 64 for bf16 at d <= 64.  32 at d = 128, where double-buffered 64-key K
+// and V tiles (68 KB) leave room for two workgroups per CU and 32-key ones for three, which
+// the kernel's 168 VGPRs allow (config 4 forward 551 -> 499 us); 32 for three planes, whose
+// double-buffered tiles then take 52.5 KB at d = 64 (three workgroups per CU) instead of 105.
+template <int D, int NP>
+constexpr int kKeyTile = (NP == 1 && D < 128) ? kRowTile : 32;
 constexpr float kRescaleLog2 = 8.0f;  // raise the running max only beyond p = 2^8
 
 // Folded softmax (bf16 operands, one sub-block per wave): Q is held times c = scale*log2 e
@@ -69,7 +71,7 @@ constexpr bool kFold = NP == 1 && NSUB == 1;
 // planes at d = 64 then take 52.5 KB per workgroup instead of 54, and three workgroups fit
 // the 160 KB of LDS.
 template <int D, int NP>
-constexpr uint32_t kFwdTile = Swz<D, kKeyTile<NP>>::kBytes - Swz<D, kKeyTile<NP>>::kPad;
+constexpr uint32_t kFwdTile = Swz<D, kKeyTile<D, NP>>::kBytes - Swz<D, kKeyTile<D, NP>>::kPad;
 
 // Workgroups per CU the compiler is asked to fit in registers: three for the three-plane
 // kernel at d = 64 with one sub-block per wave (168 VGPRs, no spills), which the LDS above
@@ -83,11 +85,15 @@ template <int D, int NP>
 struct FwdSmem {
     uint16_t k[2][NP][kFwdTile<D, NP> / 2];
     uint16_t v[2][NP][kFwdTile<D, NP> / 2];
-    static_assert(D < 64 || 2 * kStageBytes<D, NP> <= NP * kFwdTile<D, NP>,
-                  "two wave stages per idle K (or V) buffer");
+    static_assert(D < 64 || 2 * kStageBytes<D, NP> <= 2 * NP * kFwdTile<D, NP>,
+                  "two wave stages per K (or V) array");
 };
 template <int D>
 constexpr bool kStaged = D >= 64;
+// The output's wave stages go into the buffer without the last tile when two fit there (no
+// barrier needed), else into the whole K and V arrays after one more barrier.
+template <int D, int NP>
+constexpr bool kStageIdle = 2 * kStageBytes<D, NP> <= NP * kFwdTile<D, NP>;
 
 // Maximum and sum of a lane's 16 scores as balanced trees (dependency depth 3 and 4 instead
 // of 8 and 16 for a running reduction).
@@ -235,7 +241,7 @@ __global__ __launch_bounds__(kWave* kWaves, (kFwdMinBlocks<D, NSUB, NP>)) void f
     float* __restrict__ m_out, float* __restrict__ l_out, int BH, int T, float scale, int nblk,
     HeadView xv, HeadView qv, HeadView ov, size_t pstride, uint16_t* __restrict__ qp,
     int serp) {
-    constexpr int KT = kKeyTile<NP>;
+    constexpr int KT = kKeyTile<D, NP>;
     constexpr int kHalves = KT / 32;  // 32-key half tiles per tile
     using S = Swz<D, KT>;
     constexpr uint32_t kBuf = NP * kFwdTile<D, NP>;  // one K (or V) buffer: NP plane tiles
@@ -347,9 +353,16 @@ __global__ __launch_bounds__(kWave* kWaves, (kFwdMinBlocks<D, NSUB, NP>)) void f
     for (; hh < hend; ++hh) tile_sync(hh);
 
     // After the last tile barrier no wave reads, and no copy writes, the buffer that does not
-    // hold the last tile.
-    const uint32_t ostage = wave_stage(lds_addr(sm.k[ntile & 1][0]), lds_addr(sm.v[ntile & 1][0]),
-                                       wave, kStageBytes<D, NP>);
+    // hold the last tile; after one more barrier, no wave reads either buffer.
+    uint32_t ostage;
+    if constexpr (kStageIdle<D, NP>) {
+        ostage = wave_stage(lds_addr(sm.k[ntile & 1][0]), lds_addr(sm.v[ntile & 1][0]), wave,
+                            kStageBytes<D, NP>);
+    } else {
+        __syncthreads();
+        ostage = wave_stage(lds_addr(sm.k[0][0]), lds_addr(sm.v[0][0]), wave,
+                            kStageBytes<D, NP>);
+    }
 #pragma unroll
     for (int j = 2 - NSUB; j < 2; ++j) {
         const SubState<D>& st = j == 0 ? st0 : st1;

@@ -7,9 +7,9 @@
 //
 // Layout of the work.  A workgroup of 4 waves (one per SIMD of a CU) owns 256 queries of one
 // (b, h) head, as 8 sub-blocks of 32; wave w computes sub-blocks w and 7-w, so the causal
-// work of the four waves is equal.  K and V stream through LDS in 64-key tiles, double
-// buffered and shared by the four waves; each K fragment read from LDS feeds the MFMAs of
-// both sub-blocks of a wave.  Workgroups are issued heaviest query block first, with every
+// work of the four waves is equal.  K and V stream through LDS in 64-key tiles (32 at
+// d = 128 and for three planes; kKeyTile), double buffered and shared by the four waves;
+// each K fragment read from LDS feeds the MFMAs of both sub-blocks of a wave.  Workgroups are issued heaviest query block first, with every
 // block of a head on one XCD when the number of heads is a multiple of 8.
 //
 // Per 32-key half tile and sub-block:

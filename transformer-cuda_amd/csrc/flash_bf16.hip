@@ -42,6 +42,11 @@
 // joins at the half tile that holds its first key (the only one it masks).  A wave handles
 // both half tiles of a 64-query tile per step, so the MFMAs of one overlap the softmax
 // arithmetic of the other.
+//
+// With NP = 3 the backward also runs in the dS-first order (its section below): D and the
+// planes of dO first (bwd_prep_f32x3_kernel), then stage 2 writing dS in fp32 as well, then
+// dQ = scale * dS K from the stored dS (flash_bwd_dq_ds_kernel), without stage 1's second
+// computation of S and dP.
 #include <math.h>
 
 #include <type_traits>

@@ -35,6 +35,11 @@
 // Summation.  The backward kernels accumulate each 32-row tile's contraction in a fresh
 // MFMA accumulator and add the tile totals into the running sum (two-level summation), so
 // the fp32 rounding error grows with the number of tiles, not with the sequence length.
+//
+// The backward also runs in the dS-first order: D alone (d_rows_f32_kernel, the dQ
+// kernel's sums), the dK/dV kernel writing dS as well (its DS form), then dQ = scale * dS K
+// from the stored dS (flash_bwd_dq_ds_f32_kernel), which leaves out the dQ kernel's second
+// computation of S and dP.
 #include <math.h>
 
 #include "device_common.hpp"

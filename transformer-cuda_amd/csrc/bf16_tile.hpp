@@ -461,19 +461,19 @@ __device__ __forceinline__ void map_block(int id, int BH, int nb, bool descendin
 }
 
 // map_block's plain order (rank order, one XCD per head when BH % 8 == 0) with the XCD's
-// heads taken G at a time: each group's blocks, heaviest first, before the next group's, so
-// that fewer heads' tiles compete for the XCD's L2.  G = 0, or heads per XCD not a multiple
-// of G: map_block's order.
-__device__ __forceinline__ void map_block_grouped(int id, int BH, int nb, int G, int& bh,
-                                                  int& b) {
+// heads taken G at a time: each group's blocks, heaviest first (the last block first when
+// descending), before the next group's, so that fewer heads' tiles compete for the XCD's L2.
+// G = 0, or heads per XCD not a multiple of G: map_block's order.
+__device__ __forceinline__ void map_block_grouped(int id, int BH, int nb, int G, bool descending,
+                                                  int& bh, int& b) {
     const int hpx = BH >> 3;
     if (G > 0 && (BH & 7) == 0 && hpx % G == 0) {
         const int slot = id >> 3;
         const int g = slot / (G * nb), r = slot % (G * nb);
         bh = (id & 7) * hpx + g * G + r % G;
-        b = r / G;
+        b = descending ? nb - 1 - r / G : r / G;
     } else {
-        map_block(id, BH, nb, false, false, bh, b);
+        map_block(id, BH, nb, descending, false, bh, b);
     }
 }
 

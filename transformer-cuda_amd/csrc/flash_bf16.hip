@@ -905,7 +905,7 @@ __global__ __launch_bounds__(kWave * kWaves, D >= 128 ? 1 : 2) void flash_bwd_dk
     const int half = lane >> 5;
     const int T = a.T;
     int bh, blk;
-    map_block_grouped(blockIdx.x, a.BH, nblk, a.group, bh, blk);
+    map_block_grouped(blockIdx.x, a.BH, nblk, a.group, false, bh, blk);
     const int k0 = blk * kBlock;
     const int kw = k0 + kSub * wave;
     const int kj = kw + col;
@@ -1393,18 +1393,6 @@ void dq_dispatch(const DqArgs<NP>& a, hipStream_t stream) {
         dq_launch<D, (D >= 128 ? 1 : 2), NP>(a, stream);
 }
 
-// Heads per group for the bf16 dK/dV kernel's block order: 8 when each XCD holds a multiple
-// of 8 heads and a group's blocks fill its XCD's resident slots at least twice, so that the
-// heaviest-first order within the group still balances the CUs; else 0 (no groups).  At
-// config 3 (32 heads per XCD, 16 key blocks each, 64 slots per XCD): dK/dV 284 -> 277 us and
-// the step -1.6%; with a group filling the slots only once (T = 1024) it was 1 us slower.
-inline int dkdv_head_group(int BH, int nblk, int resident) {
-    constexpr int G = 8;
-    const int hpx = BH / kXcds;
-    if (BH % kXcds != 0 || hpx % G != 0 || hpx == G) return 0;
-    return static_cast<long long>(G) * nblk >= 2LL * (resident / kXcds) ? G : 0;
-}
-
 template <int D, int NP>
 void dkdv_dispatch(DkdvArgs<NP> a, hipStream_t stream) {
     constexpr int NW = kWaves;
@@ -1412,7 +1400,8 @@ void dkdv_dispatch(DkdvArgs<NP> a, hipStream_t stream) {
     const int nblk = (a.T + kBlock - 1) / kBlock;
     if constexpr (NP == 1) {
         const auto kernel = flash_bwd_dkdv_bf16_pipe_kernel<D>;
-        a.group = dkdv_head_group(a.BH, nblk, resident_capacity(kernel, kWave * NW, 0));
+        // B16 H16 T2048 d64: G = 8, dK/dV 284 -> 277 us, its fetches beyond L2 2.7x -> 1.0x
+        a.group = head_group(a.BH, nblk, resident_capacity(kernel, kWave * NW, 0));
         hipLaunchKernelGGL(kernel, dim3(a.BH * nblk), dim3(kWave * NW), 0, stream, a, nblk);
     } else if (a.ds != nullptr) {
         hipLaunchKernelGGL((flash_bwd_dkdv_bf16_kernel<D, NW, NP, true>), dim3(a.BH * nblk),

@@ -233,7 +233,8 @@ using OutT = std::conditional_t<NP == 1, uint16_t, float>;
 // NSUB = 1: 128 queries per workgroup, wave w owns sub-block w (1) (small grids).
 // k, v: plane 0 of NP bf16 planes, pstride elements apart (xv addresses a plane).  NP = 1:
 // q is bf16 like k; NP = 3: Q comes from the fp32 tensor qf (view qv) and is split here,
-// and its planes are written to qp (laid out as k's) when qp is not null.
+// and its planes are written to qp (laid out as k's) when qp is not null.  serp picks the
+// block order: 1 map_block's serpentine, 0 its plain order, -G heads in groups of G.
 template <int D, int NSUB, int NP>
 __global__ __launch_bounds__(kWave* kWaves, (kFwdMinBlocks<D, NSUB, NP>)) void flash_fwd_bf16_kernel(
     const uint16_t* __restrict__ q, const float* __restrict__ qf,
@@ -251,7 +252,10 @@ __global__ __launch_bounds__(kWave* kWaves, (kFwdMinBlocks<D, NSUB, NP>)) void f
     const int col = lane & 31;
     const int half = lane >> 5;
     int bh, blk;
-    map_block(blockIdx.x, BH, nblk, true, serp != 0, bh, blk);
+    if (serp < 0)
+        map_block_grouped(blockIdx.x, BH, nblk, -serp, true, bh, blk);
+    else
+        map_block(blockIdx.x, BH, nblk, true, serp != 0, bh, blk);
     constexpr int kBlock = kWaves * NSUB * kSub;
     const int q0 = blk * kBlock;
     const int qj0 = q0 + kSub * wave;                                     // sub-block 0
@@ -415,7 +419,10 @@ void fwd_launch(const FwdArgs<NP>& a, hipStream_t stream) {
     constexpr int kBlock = kWaves * NSUB * kSub;
     const int nblk = (a.T + kBlock - 1) / kBlock;
     const auto kernel = flash_fwd_bf16_kernel<D, NSUB, NP>;
-    const int serp = a.BH * nblk <= resident_capacity(kernel, kWave * kWaves, 0) ? 1 : 0;
+    // grids the device holds at once: the serpentine order (1); larger ones: heads in groups
+    // (-G; B16 H16 T2048 d64: G = 16, forward 173 -> 167 us), or the plain order (0)
+    const int res = resident_capacity(kernel, kWave * kWaves, 0);
+    const int serp = a.BH * nblk <= res ? 1 : -head_group(a.BH, nblk, res);
     hipLaunchKernelGGL(kernel, dim3(a.BH * nblk), dim3(kWave * kWaves), 0, stream, a.q, a.qf,
                        a.k, a.v, a.o, a.m_out, a.l_out, a.BH, a.T, a.scale, nblk, a.xv, a.qv,
                        a.ov, a.pstride, a.qp, serp);

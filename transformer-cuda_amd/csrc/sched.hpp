@@ -149,4 +149,19 @@ int persistent_grid(Kernel kernel, int block, size_t lds_bytes, long long n_task
     return static_cast<int>(g < kXcds ? kXcds : g);
 }
 
+// Host side: heads per group for map_block_grouped, for a grid of BH heads times nblk blocks
+// that `resident` workgroups cover in more than one round: the smallest power of two G with
+// 8 <= G < the heads per XCD, dividing them, whose G*nblk blocks fill the XCD's resident
+// slots at least twice, so that the heaviest-first order inside a group still balances the
+// CUs; 0 (no groups) if there is none.  Measured on the bf16 kernels: groups filling the
+// slots only once, and groups of fewer than 8 heads, ran slower than no groups.
+inline int head_group(int BH, int nblk, int resident) {
+    if (BH % kXcds != 0) return 0;
+    const int hpx = BH / kXcds;
+    const long long slots = resident / kXcds;
+    for (int G = 8; G < hpx; G *= 2)
+        if (hpx % G == 0 && static_cast<long long>(G) * nblk >= 2 * slots) return G;
+    return 0;
+}
+
 }  // namespace tcamd

@@ -442,8 +442,8 @@ constexpr int kCusPerXcd = 32;
 // light ones (at config 2, three blocks per CU: causal work 12-14 units per CU instead of
 // 10-17).  Grids that do not fit at once keep the plain order: there the heaviest blocks
 // must start first.
-__device__ __forceinline__ void map_block(int id, int BH, int nb, bool descending,
-                                          bool serpentine, int& bh, int& b) {
+__host__ __device__ __forceinline__ void map_block(int id, int BH, int nb, bool descending,
+                                                   bool serpentine, int& bh, int& b) {
     int rank;
     if ((BH & 7) == 0) {
         const int hpx = BH >> 3;
@@ -464,8 +464,8 @@ __device__ __forceinline__ void map_block(int id, int BH, int nb, bool descendin
 // heads taken G at a time: each group's blocks, heaviest first (the last block first when
 // descending), before the next group's, so that fewer heads' tiles compete for the XCD's L2.
 // G = 0, or heads per XCD not a multiple of G: map_block's order.
-__device__ __forceinline__ void map_block_grouped(int id, int BH, int nb, int G, bool descending,
-                                                  int& bh, int& b) {
+__host__ __device__ __forceinline__ void map_block_grouped(int id, int BH, int nb, int G,
+                                                           bool descending, int& bh, int& b) {
     const int hpx = BH >> 3;
     if (G > 0 && (BH & 7) == 0 && hpx % G == 0) {
         const int slot = id >> 3;

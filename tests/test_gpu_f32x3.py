@@ -366,3 +366,41 @@ def test_tiled_launchers_equal_packed(lib, kv_ready):
            "dv": dv.cpu(), "D": D.cpu()}
     for n in got:
         assert torch.equal(got[n], want[n]), n
+
+
+def _bf16_rne_bits(x):
+    """Round-to-nearest-even bf16 bits of finite fp32 values (numpy, from the bit layout)."""
+    b = x.astype(np.float32).view(np.uint32).astype(np.uint64)
+    return ((b + 0x7FFF + ((b >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def _bits_to_f32(h):
+    return (h.astype(np.uint32) << 16).view(np.float32)
+
+
+def test_kv_planes_bitwise(lib):
+    """The forward's k and v planes in the workspace (tensors 1 and 2: three head-major bf16
+    planes each, N = B*H*T*d elements apart) against the split restated from its definition:
+    x0 = bf16(x), x1 = bf16(x - x0), x2 = bf16(x - x0 - x1), round to nearest even, compared
+    bit for bit.  Magnitudes span 1e-3..1e3 so that every plane is populated; odd T and
+    element counts cover both halves of the pairs the kernel converts together."""
+    B, H, T, d = 2, 3, 77, 64
+    g = torch.Generator(device="cpu").manual_seed(31)
+    mag = torch.pow(10.0, torch.rand((B, T, 3 * H * d), generator=g) * 6 - 3)
+    qkv = torch.randn((B, T, 3 * H * d), generator=g) * mag
+    ws = planes(lib, B, H, T, d)
+    o = torch.empty((B, H, T, d), device="cuda:0")
+    m = torch.empty((B, H, T), device="cuda:0")
+    l = torch.empty_like(m)
+    lib.packed_causal_attention_forward_f32x3(qkv.to("cuda:0"), o, B, H, T, d, 0.125, ws, m, l)
+    torch.cuda.synchronize()
+    N = B * H * T * d
+    got = ws.cpu().numpy()[: 4 * 3 * N * 2].view(np.uint16).reshape(4, 3, N)
+    _, k, v = heads(qkv, B, H, T, d)
+    for tensor, x in ((1, k), (2, v)):
+        r = x.numpy().reshape(-1).astype(np.float32)
+        for i in range(3):
+            want = _bf16_rne_bits(r)
+            mism = int(np.count_nonzero(got[tensor, i] != want))
+            assert mism == 0, f"tensor {tensor} plane {i}: {mism} of {N} differ"
+            r = (r - _bits_to_f32(want)).astype(np.float32)

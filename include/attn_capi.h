@@ -227,7 +227,12 @@ int attn_tiled_causal_backward_dkdv_f32(const float* q, const float* k, const fl
 /* ------------------------------------------------------------------------------------------
  * Tiled causal attention, bf16 fast path (no reference counterpart: the reference is
  * fp32-only).  bf16 Q/K/V/O/dO/dQ/dK/dV, fp32 statistics, fp32 accumulation on
- * v_mfma_f32_32x32x16_bf16.  Same stats contract and workspace size (B*H*T floats) as fp32.
+ * v_mfma_f32_32x32x16_bf16.  Same stats contract P_ij = exp(scale*q_i.k_j - m_i) / l_i and
+ * workspace size (B*H*T floats) as fp32, and the same log-sum-exp m + ln l, but m_out is the
+ * forward's reference value rather than the row maximum: the maximum over the row's first 32
+ * keys, raised to a later block's maximum only where the exponentials against it grow large
+ * (a row sum of 2^16 over a 32-key block at d_head 32 and 64, an exponent above 8 at 128),
+ * and l_out the sum against it.  The backward entry points take either form.
  * ------------------------------------------------------------------------------------------ */
 int attn_tiled_causal_forward_bf16(const attn_bf16* q, const attn_bf16* k, const attn_bf16* v,
                                    attn_bf16* out, int B, int H, int T, int d_head, float scale,
@@ -289,6 +294,12 @@ int attn_packed_causal_backward_dkdv_f32(const float* qkv, const float* do_ptr,
  * SIZE_MAX, and the entry points reject such shapes with ATTN_ERROR_INVALID_DIM.  D, dK and
  * dV bitwise those of the two-stage order, dQ within fp32 rounding of its. */
 size_t attn_f32_ds_workspace_bytes(int B, int H, int T, int d_head);
+/* 1 where a caller that chooses the order per shape should take the dS-first order: d_head
+ * 32, 64 or 128 and ds_workspace at most 16 GiB (the same limit as the three-plane path's);
+ * 0 elsewhere, where the two-stage entry points above need no T^2 workspace.  On the fp32
+ * MFMA the dS-first backward measured 0.78-0.88x the two-stage time at d_head 32, 64 and 128
+ * (T 1024 to 8192). */
+int attn_f32_backward_uses_ds(int B, int H, int T, int d_head);
 int attn_packed_causal_backward_ds_f32(const float* qkv, const float* o, const float* do_ptr,
                                        const float* m_ptr, const float* l_ptr, float* dqkv,
                                        float* d_workspace, float* ds_workspace, int B, int H,
@@ -397,6 +408,12 @@ int attn_fused_causal_backward_dkdv_bf16(const attn_bf16* qkv, const attn_bf16* 
  * src/kernels/attention.cu:518-1012).
  * ------------------------------------------------------------------------------------------ */
 size_t attn_f32x3_workspace_bytes(int B, int H, int T, int d_head);
+/* The two parts of that workspace on their own: the planes (4 x 3 x B*H*T*d_head bf16) and
+ * the dS area (0 where attn_f32x3_backward_uses_ds is 0).  attn_f32x3_workspace_bytes is
+ * their sum.  A caller that keeps the planes of several layers alive between their forward
+ * and backward (a training step) needs only one dS area: dS lives inside one backward call. */
+size_t attn_f32x3_planes_bytes(int B, int H, int T, int d_head);
+size_t attn_f32x3_ds_workspace_bytes(int B, int H, int T, int d_head);
 /* 1 when the one-call backwards take the dS-first order (three stages: prep, dkdv_ds, dq_ds;
  * d_head 64 and dS at most 16 GiB), 0 when they take the two-stage order (dq, then dkdv).
  * The dS-first order saves the dQ stage's recomputation of S and dP for 8 bytes of HBM
@@ -418,6 +435,21 @@ int attn_fused_causal_backward_f32x3(const float* qkv, const float* o, const flo
                                      float* d_workspace, int B, int H, int T, int d_head,
                                      float scale, void* planes, int kv_planes_ready,
                                      hipStream_t stream);
+/* The one-call backwards with dS in a separate buffer: `planes` of at least
+ * attn_f32x3_planes_bytes, ds_workspace of attn_f32x3_ds_workspace_bytes (16-byte aligned,
+ * no initialisation needed; NULL allowed where that size is 0, i.e. where the two-stage order
+ * is taken).  Otherwise as attn_packed_causal_backward_f32x3 / attn_fused_causal_backward_f32x3,
+ * with the same results bitwise. */
+int attn_packed_causal_backward_ds_f32x3(const float* qkv, const float* o, const float* do_ptr,
+                                         const float* m_ptr, const float* l_ptr, float* dqkv,
+                                         float* d_workspace, float* ds_workspace, int B, int H,
+                                         int T, int d_head, float scale, void* planes,
+                                         int kv_planes_ready, hipStream_t stream);
+int attn_fused_causal_backward_ds_f32x3(const float* qkv, const float* o, const float* do_ptr,
+                                        const float* m_ptr, const float* l_ptr, float* dqkv,
+                                        float* d_workspace, float* ds_workspace, int B, int H,
+                                        int T, int d_head, float scale, void* planes,
+                                        int kv_planes_ready, hipStream_t stream);
 /* The three stages of the dS-first order, in order: prep writes the planes of dO (and of q,
  * k, v unless kv_planes_ready) and D; dkdv_ds (one function for both layouts: it reads dO
  * only through its planes) writes dK and dV into dqkv and dS into `planes`; dq_ds writes dQ

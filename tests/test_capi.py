@@ -40,8 +40,11 @@ def test_every_declared_symbol_is_exported(lib):
 def test_binding_covers_header(lib):
     declared = set(declared_symbols()) - {"attn_status_string", "attn_version",
                                           "attn_f32x3_workspace_bytes",
+                                          "attn_f32x3_planes_bytes",
+                                          "attn_f32x3_ds_workspace_bytes",
                                           "attn_f32x3_backward_uses_ds",
-                                          "attn_f32_ds_workspace_bytes"}
+                                          "attn_f32_ds_workspace_bytes",
+                                          "attn_f32_backward_uses_ds"}
     assert declared == set(lib.SIGNATURES)
 
 
@@ -247,6 +250,41 @@ def test_f32x3_validation(lib):
                     f(0.125), None, None, MISALIGNED, None) == MISALIGN
     assert lib.call("attn_tiled_causal_backward_f32x3", *([FAKE] * 11), 1, 2, 8, 128,
                     f(0.125), FAKE, 1, None) == BAD_HEAD_DIM
+
+
+def test_f32x3_separate_ds_validation(lib):
+    """The workspace split into planes and dS, and the one-call backwards that take them
+    apart: sizes add up, dS is required exactly where the dS-first order runs."""
+    f = ctypes.c_float
+    raw = lib.raw()
+    for shape in ((2, 3, 40, 64), (2, 3, 40, 32), (1, 16, 16416, 64), (8, 12, 1024, 64)):
+        planes, ds = raw.attn_f32x3_planes_bytes(*shape), raw.attn_f32x3_ds_workspace_bytes(*shape)
+        assert planes == 4 * 3 * shape[0] * shape[1] * shape[2] * shape[3] * 2
+        assert planes + ds == raw.attn_f32x3_workspace_bytes(*shape)
+        assert (ds > 0) == lib.f32x3_backward_uses_ds(*shape)
+    assert raw.attn_f32x3_ds_workspace_bytes(2, 3, 40, 64) == 6 * 64 * 64 * 4
+    assert raw.attn_f32x3_planes_bytes(0, 3, 40, 64) == 0
+    for fam in ("packed", "fused"):
+        one = lambda ds=FAKE, planes=FAKE, d=64, T=8: lib.call(
+            f"attn_{fam}_causal_backward_ds_f32x3", FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, ds,
+            1, 2, T, d, f(0.125), planes, 1, None)
+        assert one(ds=None) == NULLPTR           # d = 64: the dS-first order needs dS
+        assert one(ds=MISALIGNED) == MISALIGN
+        assert one(planes=None) == NULLPTR
+        assert one(d=128) == BAD_HEAD_DIM
+        assert one(planes=MISALIGNED, ds=None, d=32) == MISALIGN  # two-stage: dS not needed
+
+
+def test_f32_backward_order_gate(lib):
+    """attn_f32_backward_uses_ds: the dS-first order of the fp32 MFMA backward where its dS
+    fits 16 GiB, at every supported head size; the two-stage order beyond."""
+    assert lib.f32_backward_uses_ds(8, 12, 1024, 64)
+    assert lib.f32_backward_uses_ds(8, 12, 1024, 32) and lib.f32_backward_uses_ds(2, 16, 2048, 128)
+    assert lib.f32_backward_uses_ds(1, 16, 16384, 64)        # 16 GiB exactly
+    assert not lib.f32_backward_uses_ds(1, 16, 16416, 64)
+    assert not lib.f32_backward_uses_ds(1, 4095, (1 << 26) - 1, 32)  # bytes past SIZE_MAX
+    assert not lib.f32_backward_uses_ds(8, 12, 1024, 48)
+    assert not lib.f32_backward_uses_ds(0, 12, 1024, 64)
 
 
 def test_python_launchers_reject_host_tensors(lib):

@@ -55,12 +55,19 @@ def test_shapes_vs_oracle(lib, T, d):
     got = gpu_fwd_bwd(lib, q, k, v, do, scale, dtype=torch.bfloat16)
     _check(got, want, tag=f"T={T} d={d}")
     # The forward holds Q times c = scale*log2 e rounded to bf16 (2^-9 relative per element),
-    # so a score scale*q.k moves by at most 2^-9 scale sum_e |q_e k_e|; m and the
-    # log-sum-exp m + ln l move by at most the largest such bound over the row's keys.
+    # so a score scale*q.k moves by at most 2^-9 scale sum_e |q_e k_e|, and the log-sum-exp
+    # m + ln l by at most the largest such bound over the row's keys.  m is the forward's
+    # reference value: the maximum over the row's first 32 keys (its scores moved the same
+    # way, and carried to 16 bits), at most the row maximum.
     aq, ak = np.abs(q.astype(np.float64)), np.abs(k.astype(np.float64))
     bound = 2.0 ** -9 * scale * aq @ np.swapaxes(ak, -1, -2)
-    bound = np.where(np.tril(np.ones((T, T), bool)), bound, 0.0).max(-1) + 1e-6
-    assert np.all(np.abs(got["m"] - want.m.numpy()) <= bound), "m"
+    causal = np.tril(np.ones((T, T), bool))
+    bound = np.where(causal, bound, 0.0).max(-1) + 1e-6
+    s = scale * q.astype(np.float64) @ np.swapaxes(k.astype(np.float64), -1, -2)
+    first32 = np.where(causal & (np.arange(T) < 32)[None, :], s, -np.inf).max(-1)
+    mag = np.abs(want.m.numpy()) * 2.0 ** -15
+    assert np.all(got["m"] >= first32 - bound - mag), "m: at least the maximum over keys 0..31"
+    assert np.all(got["m"] <= want.m.numpy() + bound + mag), "m: at most the row maximum"
     lse = got["m"] + np.log(got["l"])
     assert np.all(np.abs(lse - want.lse.numpy()) <= bound), "m + ln l"
 
@@ -114,3 +121,57 @@ def test_config3_full(lib):
 def test_config4_full(lib):
     """B2 H16 T8192 d128, Q and K scaled by 0.5 (peaky softmax)."""
     _full_config(lib, 2, 16, 8192, 128, 42, 0.5, oracle_heads=[(0, 0), (1, 15)])
+
+
+def _bf16(x):
+    return ref.bf16_round(np.asarray(x, np.float32))
+
+
+@pytest.mark.parametrize("d", [32, 64, 128])
+@pytest.mark.parametrize("jump", [2.5, 9.0])
+def test_reference_raise(lib, d, jump):
+    """Scores that rise far above the first 32 keys' maximum later in the row: the first 32
+    keys point away from q, every later key along it (scale*q.k = -jump^2, then +jump^2, in
+    natural units, plus noise).  jump 2.5: rows from 32 on see their second block of keys
+    ~18 (log2 units) above the first block's maximum, so the forward raises its reference
+    value from the LDS tile; jump 9: ~234 above it, where 2^(s - m) overflows to inf before
+    the raise.  O and the log-sum-exp are checked against a float64 restatement that rounds
+    c*q to bf16 as the kernel holds it (the difference left is the bf16 P of the PV
+    products); the backward's dK and dV against the fp32 oracle at the bf16 gate."""
+    B, H, T = 1, 2, 256
+    rng = np.random.default_rng(7 + d)
+    u = rng.standard_normal((B, H, 1, d)).astype(np.float32)
+    u /= np.linalg.norm(u, axis=-1, keepdims=True)
+    a = jump * np.sqrt(np.sqrt(d))  # scale*q.k = a^2 / sqrt(d) = jump^2 along u
+    noise = lambda n: 0.1 * rng.standard_normal((B, H, n, d)).astype(np.float32)
+    q = _bf16(a * u + noise(T))
+    k = np.concatenate([-a * u + noise(32), a * u + noise(T - 32)], axis=2)
+    k = _bf16(k)
+    v = _bf16(rng.standard_normal((B, H, T, d)))
+    do = _bf16(rng.standard_normal((B, H, T, d)))
+    scale = default_scale(d)
+    got = gpu_fwd_bwd(lib, q, k, v, do, scale, dtype=torch.bfloat16)
+    for n in ("o", "m", "l", "dq", "dk", "dv"):
+        assert np.isfinite(got[n]).all(), n
+    # forward against float64 with the kernel's bf16(c*q)
+    c = np.float32(scale * math.log2(math.e))
+    qc = _bf16(q * c).astype(np.float64) / np.float64(c)
+    s = scale * qc @ np.swapaxes(k.astype(np.float64), -1, -2)
+    s = np.where(np.tril(np.ones((T, T), bool)), s, -np.inf)
+    lse = np.log(np.exp(s - s.max(-1, keepdims=True)).sum(-1)) + s.max(-1)
+    o = np.exp(s - lse[..., None]) @ v.astype(np.float64)
+    e = rel_l2(got["o"], o)
+    rise = (s[..., 32:, :].max(-1) - s[..., 32:, :32].max(-1)).min() * math.log2(math.e)
+    print(f"d={d} jump={jump}: O rel-L2 {e:.2e}, rows 32+: row max - first-32 max >= "
+          f"{float(rise):.1f} (log2)")
+    assert e <= 1e-2
+    glse = got["m"] + np.log(got["l"])
+    assert np.abs(glse - lse).max() <= 1e-3 * np.abs(lse).max() + 1e-3
+    # The backward from these statistics: dK and dV (which take P from them directly)
+    # within the bf16 gate of the fp32 oracle.  dQ is printed only: with scores of +-jump^2
+    # its error is the backward's own bf16 rounding of c*K, 2^-9 of each score, multiplied by
+    # the large keys it sums (2.8e-2 at d = 32, jump 2.5), whatever statistics it is given.
+    want = ref.attention_fwd_bwd(q, k, v, do, scale, dtype=torch.float32)
+    print(f"raise d={d} jump={jump}: dQ rel-L2 {rel_l2(got['dq'], want.dq.numpy()):.2e}")
+    if jump <= 2.5:
+        _check(got, want, names=("dk", "dv"), tag=f"raise d={d}")

@@ -404,3 +404,45 @@ def test_kv_planes_bitwise(lib):
             mism = int(np.count_nonzero(got[tensor, i] != want))
             assert mism == 0, f"tensor {tensor} plane {i}: {mism} of {N} differ"
             r = (r - _bits_to_f32(want)).astype(np.float32)
+
+
+@pytest.mark.parametrize("merged", [False, True])
+@pytest.mark.parametrize("d", [64, 32])
+def test_separate_ds_equals_combined(lib, merged, d):
+    """attn_{packed,fused}_causal_backward_ds_f32x3: the planes in a buffer of their own size
+    and dS in another (NaN-filled, or absent where the shape takes the two-stage order) give
+    bitwise the one-call backward's D and dqkv with the combined workspace."""
+    B, H, T = 2, 3, 200
+    scale = default_scale(d)
+    g = torch.Generator(device="cpu").manual_seed(11 + d)
+    qkv = torch.randn((B, T, 3 * H * d), generator=g).to("cuda:0")
+    do = torch.randn((B, H, T, d), generator=g).to("cuda:0")
+    if merged:
+        do = do.permute(0, 2, 1, 3).reshape(B, T, H * d).contiguous()
+    fam = "fused" if merged else "packed"
+    o = torch.empty((B, T, H * d) if merged else (B, H, T, d), device="cuda:0")
+    m = torch.empty((B, H, T), device="cuda:0")
+    l = torch.empty_like(m)
+    outs = []
+    for split in (False, True):
+        if split:
+            ws = torch.full((lib.f32x3_planes_bytes(B, H, T, d),), 255, dtype=torch.uint8,
+                            device="cuda:0")
+            nds = lib.f32x3_ds_workspace_bytes(B, H, T, d)
+            assert (nds > 0) == (d == 64)
+            ds = torch.full((nds // 4,), float("nan"), device="cuda:0") if nds else None
+        else:
+            ws = planes(lib, B, H, T, d)
+        getattr(lib, f"{fam}_causal_attention_forward_f32x3")(qkv, o, B, H, T, d, scale, ws, m, l)
+        dqkv = torch.full_like(qkv, float("nan"))
+        D = torch.full_like(m, float("nan"))
+        if split:
+            getattr(lib, f"{fam}_causal_attention_backward_ds_f32x3")(
+                qkv, o, do, m, l, dqkv, D, ds, B, H, T, d, scale, ws, True)
+        else:
+            getattr(lib, f"{fam}_causal_attention_backward_f32x3")(
+                qkv, o, do, m, l, dqkv, D, B, H, T, d, scale, ws, True)
+        torch.cuda.synchronize()
+        outs.append((o.clone(), dqkv.clone(), D.clone()))
+    for name, a, b in zip(("o", "dqkv", "D"), *outs):
+        assert torch.equal(a, b), name

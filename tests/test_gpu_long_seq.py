@@ -2,10 +2,12 @@
 two-stage and dS-first backwards) and the three-plane path (dS-first at d = 64) against the
 fp64 restatement of the reference.  fp32 summation noise grows with T in any fp32
 implementation, so each result's max-abs distance to fp64 is bounded by torch fp32's own
-distance at the same shape, floored at the 1e-5 gate: within 2x for the fp32 MFMA path
-(measured 0.7-1.2x: its compensated tile sums), within 3x for the three-plane path
-(measured: O and dQ 0.5-2.5x; dK and dV 2.9-3.3x, 4.6e-6 to 6.3e-6, because they sum the
-whole query range in the MFMA accumulator; under the gate).  And bf16 at T = 16384."""
+distance at the same shape: within 2x for the fp32 MFMA path (measured 0.7-1.2x: its
+compensated tile sums) and within 3x for the three-plane path (measured: O 0.5-1.1x, dQ
+1.6-2.5x, dK and dV 0.7-1.1x: they sum the whole query range in the MFMA accumulator, the
+smaller terms of the last queries first), with no floor: a summation order that let the error
+grow with T (the ascending walk measured 2.9-3.3x for dK and dV) fails here.  And bf16 at
+T = 16384."""
 import numpy as np
 import pytest
 import torch
@@ -67,7 +69,7 @@ def test_long_sequences_against_fp64(lib, B, H, T):
             ours, theirs = max_abs(x.numpy(), w), max_abs(getattr(w32, n).numpy(), w)
             print(f"T={T} {path} {n}: |gpu-fp64| {ours:.2e}  |torch32-fp64| {theirs:.2e}")
             assert np.isfinite(x.numpy()).all(), f"{path} {n}"
-            assert ours <= max(1e-5, factor[path] * theirs), f"{path} {n}: {ours:.3e}"
+            assert ours <= factor[path] * theirs, f"{path} {n}: {ours:.3e}"
 
 
 def test_bf16_long_sequence_against_oracle(lib):

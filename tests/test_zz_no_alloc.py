@@ -2,13 +2,14 @@
 allocated) against attn_tiled_causal_backward_f32 (D in a caller workspace): bitwise equal
 dq, dk, dv, on two calls in a row, the second with a smaller problem, so that a stale D
 from the first call in the shared scratch would show."""
-import ctypes
-
 import pytest
 import torch
 
 from oracle import attention_ref as ref
 from gpu_util import default_scale, to_dev
+
+# Problems beyond the scratch are rejected before any launch; that validation is checked
+# on the CPU (tests/test_capi.py), where no kernel can run.
 
 
 def _case(lib, B, H, T, d, seed):
@@ -40,12 +41,3 @@ def test_noalloc_backward_two_calls_second_smaller(lib):
 def test_noalloc_backward_at_scratch_limit(lib):
     # B*H*T = 2^22 rows exactly: the largest problem the scratch holds
     _case(lib, 32, 1024, 128, 32, seed=8)
-
-
-@pytest.mark.gpu
-def test_noalloc_backward_rejects_beyond_limit(lib):
-    B, H, T, d = 1, 1025, 4096, 32
-    t = torch.empty(16, device="cuda:0")
-    status = lib.call("attn_tiled_causal_backward_f32_noalloc", *([t.data_ptr()] * 10), B, H, T,
-                      d, ctypes.c_float(0.125), None)
-    assert status == 7  # ATTN_ERROR_SCRATCH_LIMIT, nothing launched

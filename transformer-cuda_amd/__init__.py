@@ -105,6 +105,10 @@ SIGNATURES = {
         [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P, _I, _P],
     "attn_fused_causal_backward_f32x3":
         [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P, _I, _P],
+    "attn_packed_causal_backward_ds_f32x3":
+        [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P, _I, _P],
+    "attn_fused_causal_backward_ds_f32x3":
+        [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P, _I, _P],
     "attn_packed_causal_backward_ds_f32":
         [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P],
     "attn_fused_causal_backward_ds_f32":
@@ -146,6 +150,12 @@ _lib.attn_f32_ds_workspace_bytes.argtypes = [_I, _I, _I, _I]
 _lib.attn_f32_ds_workspace_bytes.restype = ctypes.c_size_t
 _lib.attn_f32x3_backward_uses_ds.argtypes = [_I, _I, _I, _I]
 _lib.attn_f32x3_backward_uses_ds.restype = ctypes.c_int
+_lib.attn_f32x3_planes_bytes.argtypes = [_I, _I, _I, _I]
+_lib.attn_f32x3_planes_bytes.restype = ctypes.c_size_t
+_lib.attn_f32x3_ds_workspace_bytes.argtypes = [_I, _I, _I, _I]
+_lib.attn_f32x3_ds_workspace_bytes.restype = ctypes.c_size_t
+_lib.attn_f32_backward_uses_ds.argtypes = [_I, _I, _I, _I]
+_lib.attn_f32_backward_uses_ds.restype = ctypes.c_int
 
 
 def raw():
@@ -524,11 +534,31 @@ def f32x3_backward_uses_ds(B, H, T, d_head):
     return bool(_lib.attn_f32x3_backward_uses_ds(B, H, T, d_head))
 
 
-def _planes_ptr(planes, B, H, T, d_head):
-    need = f32x3_workspace_bytes(B, H, T, d_head)
+def f32x3_planes_bytes(B, H, T, d_head):
+    """Bytes of the planes alone (without the dS area) of the *_f32x3 workspace."""
+    return int(_lib.attn_f32x3_planes_bytes(B, H, T, d_head))
+
+
+def f32x3_ds_workspace_bytes(B, H, T, d_head):
+    """Bytes of the dS area of the *_f32x3 backward (0 where it takes the two-stage order)."""
+    return int(_lib.attn_f32x3_ds_workspace_bytes(B, H, T, d_head))
+
+
+def f32_backward_uses_ds(B, H, T, d_head):
+    """Whether a per-shape caller should take the fp32 dS-first order (include/attn_capi.h)."""
+    return bool(_lib.attn_f32_backward_uses_ds(B, H, T, d_head))
+
+
+def _planes_ptr(planes, B, H, T, d_head, need=None):
+    need = f32x3_workspace_bytes(B, H, T, d_head) if need is None else need
     if planes is not None and planes.numel() * planes.element_size() < need:
         raise ValueError(f"planes: needs {need} bytes")
     return _ptr(planes, None, None, "planes")
+
+
+def _planes_only_ptr(planes, B, H, T, d_head):
+    """A workspace that entry points reading no dS take: the planes alone suffice."""
+    return _planes_ptr(planes, B, H, T, d_head, f32x3_planes_bytes(B, H, T, d_head))
 
 
 def _qkv_forward_f32x3(family, qkv, out, B, H, T, d_head, scale, planes, m_out, l_out,
@@ -538,7 +568,7 @@ def _qkv_forward_f32x3(family, qkv, out, B, H, T, d_head, scale, planes, m_out, 
     check(call(f"attn_{family}_causal_forward_f32x3", _ptr(qkv, f32, 3 * n, "qkv"),
                _ptr(out, f32, n, "out"), B, H, T, d_head, float(scale),
                _ptr(m_out, f32, r, "m_out"), _ptr(l_out, f32, r, "l_out"),
-               _planes_ptr(planes, B, H, T, d_head), _stream(stream)),
+               _planes_only_ptr(planes, B, H, T, d_head), _stream(stream)),
           f"{family}_causal_attention_forward_f32x3")
 
 
@@ -582,6 +612,40 @@ def fused_causal_attention_backward_f32x3(qkv, o, dO, m, l, dqkv, workspace, B, 
                         planes, kv_planes_ready, stream)
 
 
+def _backward_ds_f32x3(family, qkv, o, dO, m, l, dqkv, workspace, ds_workspace, B, H, T,
+                       d_head, scale, planes, kv_planes_ready, stream):
+    n, r = B * H * T * d_head, B * H * T
+    f32 = _dt(False)
+    need = f32x3_ds_workspace_bytes(B, H, T, d_head)
+    if need and (ds_workspace is None or ds_workspace.numel() * ds_workspace.element_size() < need):
+        raise ValueError(f"ds_workspace: needs {need} bytes")
+    check(call(f"attn_{family}_causal_backward_ds_f32x3", _ptr(qkv, f32, 3 * n, "qkv"),
+               _ptr(o, f32, n, "o"), _ptr(dO, f32, n, "dO"), _ptr(m, f32, r, "m"),
+               _ptr(l, f32, r, "l"), _ptr(dqkv, f32, 3 * n, "dqkv"),
+               _ptr(workspace, f32, r, "workspace"),
+               _ptr(ds_workspace, None, None, "ds_workspace"), B, H, T, d_head, float(scale),
+               _planes_only_ptr(planes, B, H, T, d_head),
+               1 if kv_planes_ready else 0, _stream(stream)),
+          f"{family}_causal_attention_backward_ds_f32x3")
+
+
+def packed_causal_attention_backward_ds_f32x3(qkv, o, dO, m, l, dqkv, workspace, ds_workspace,
+                                              B, H, T, d_head, scale, planes,
+                                              kv_planes_ready=False, stream=None):
+    """packed_causal_attention_backward_f32x3 with the planes (f32x3_planes_bytes) and dS
+    (f32x3_ds_workspace_bytes; None where that is 0) in separate buffers."""
+    _backward_ds_f32x3("packed", qkv, o, dO, m, l, dqkv, workspace, ds_workspace, B, H, T,
+                       d_head, scale, planes, kv_planes_ready, stream)
+
+
+def fused_causal_attention_backward_ds_f32x3(qkv, o, dO, m, l, dqkv, workspace, ds_workspace,
+                                             B, H, T, d_head, scale, planes,
+                                             kv_planes_ready=False, stream=None):
+    """fused_causal_attention_backward_f32x3 with the planes and dS in separate buffers."""
+    _backward_ds_f32x3("fused", qkv, o, dO, m, l, dqkv, workspace, ds_workspace, B, H, T,
+                       d_head, scale, planes, kv_planes_ready, stream)
+
+
 def _backward_prep_f32x3(family, qkv, o, dO, workspace, B, H, T, d_head, planes,
                          kv_planes_ready, stream):
     n, r = B * H * T * d_head, B * H * T
@@ -589,7 +653,7 @@ def _backward_prep_f32x3(family, qkv, o, dO, workspace, B, H, T, d_head, planes,
     check(call(f"attn_{family}_causal_backward_prep_f32x3", _ptr(qkv, f32, 3 * n, "qkv"),
                _ptr(o, f32, n, "o"), _ptr(dO, f32, n, "dO"),
                _ptr(workspace, f32, r, "workspace"), B, H, T, d_head,
-               _planes_ptr(planes, B, H, T, d_head), 1 if kv_planes_ready else 0,
+               _planes_only_ptr(planes, B, H, T, d_head), 1 if kv_planes_ready else 0,
                _stream(stream)), f"{family}_causal_attention_backward_prep_f32x3")
 
 
@@ -653,7 +717,7 @@ def causal_attention_backward_dkdv_f32x3(qkv, m, l, workspace, dqkv, B, H, T, d_
     check(call("attn_causal_backward_dkdv_f32x3", _ptr(qkv, f32, 3 * n, "qkv"),
                _ptr(m, f32, r, "m"), _ptr(l, f32, r, "l"), _ptr(workspace, f32, r, "workspace"),
                _ptr(dqkv, f32, 3 * n, "dqkv"), B, H, T, d_head, float(scale),
-               _planes_ptr(planes, B, H, T, d_head), _stream(stream)),
+               _planes_only_ptr(planes, B, H, T, d_head), _stream(stream)),
           "causal_attention_backward_dkdv_f32x3")
 
 
@@ -666,7 +730,7 @@ def tiled_causal_attention_forward_f32x3(q, k, v, out, B, H, T, d_head, scale, p
     check(call("attn_tiled_causal_forward_f32x3", _ptr(q, f32, n, "q"), _ptr(k, f32, n, "k"),
                _ptr(v, f32, n, "v"), _ptr(out, f32, n, "out"), B, H, T, d_head, float(scale),
                _ptr(m_out, f32, r, "m_out"), _ptr(l_out, f32, r, "l_out"),
-               _planes_ptr(planes, B, H, T, d_head), _stream(stream)),
+               _planes_only_ptr(planes, B, H, T, d_head), _stream(stream)),
           "tiled_causal_attention_forward_f32x3")
 
 

@@ -310,6 +310,11 @@ size_t ds_elems(int B, int H, int T) {
 float* ds_area(void* planes, size_t N) {
     return reinterpret_cast<float*>(plane_tensor(planes, N, kPlaneTensors));
 }
+// The dS area of a combined workspace (attn_f32x3_workspace_bytes): after the planes.
+float* combined_ds(void* planes, int B, int H, int T, int d) {
+    return planes == nullptr ? nullptr : ds_area(planes, plane_elems(B, H, T, d));
+}
+
 // The one-call backward's order.  dS-first (dK/dV writing dS, then dQ = dS K) saves the dQ
 // stage's S and dP products, 48 of its 74 MFMAs per tile at d = 64, for 8 bytes of HBM
 // traffic per stored element; measured faster at d = 64 (0.86-0.93x from T = 512 to 8192)
@@ -432,47 +437,51 @@ int packed_backward_prep_f32x3(const float* qkv, const float* o, const float* dO
     return launch_status();
 }
 
+// ds: the dS area (ds_elems fp32, 16-byte aligned): after the planes in a workspace of
+// attn_f32x3_workspace_bytes, or a separate buffer of attn_f32x3_ds_workspace_bytes.
 int packed_backward_dkdv_ds_f32x3(const float* qkv, const float* m, const float* l,
                                   const float* ws, float* dqkv, int B, int H, int T, int d,
-                                  float scale, void* planes, hipStream_t stream) {
+                                  float scale, void* planes, float* ds, hipStream_t stream) {
     if (qkv == nullptr || m == nullptr || l == nullptr || ws == nullptr || dqkv == nullptr ||
-        planes == nullptr)
+        planes == nullptr || ds == nullptr)
         return ATTN_ERROR_NULL_POINTER;
     int st = check_f32x3(B, H, T, d, scale);
     if (st != ATTN_SUCCESS) return st;
     st = check_uses_ds(B, H, T, d);
     if (st != ATTN_SUCCESS) return st;
-    if (!aligned16(qkv) || !aligned16(dqkv) || !aligned16(planes)) return ATTN_ERROR_MISALIGNED;
+    if (!aligned16(qkv) || !aligned16(dqkv) || !aligned16(planes) || !aligned16(ds))
+        return ATTN_ERROR_MISALIGNED;
     const size_t N = plane_elems(B, H, T, d), C = static_cast<size_t>(H) * d;
     const tcamd::HeadView xv = tcamd::packed_qkv_view(H, T, d);
     clear_error();
     tcamd::launch_flash_bwd_dkdv_f32x3(plane_tensor(planes, N, 0), plane_tensor(planes, N, 3),
                                        tcamd::head_major_view(H, T, d), N, qkv + C, qkv + 2 * C,
                                        xv, m, l, ws, dqkv + C, dqkv + 2 * C, xv, B * H, T, d,
-                                       scale, stream, ds_area(planes, N));
+                                       scale, stream, ds);
     return launch_status();
 }
 
 int packed_backward_dq_ds_f32x3(float* dqkv, int B, int H, int T, int d, float scale,
-                                const void* planes, hipStream_t stream) {
-    if (dqkv == nullptr || planes == nullptr) return ATTN_ERROR_NULL_POINTER;
+                                const void* planes, const float* ds, hipStream_t stream) {
+    if (dqkv == nullptr || planes == nullptr || ds == nullptr) return ATTN_ERROR_NULL_POINTER;
     int st = check_f32x3(B, H, T, d, scale);
     if (st != ATTN_SUCCESS) return st;
     st = check_uses_ds(B, H, T, d);
     if (st != ATTN_SUCCESS) return st;
-    if (!aligned16(dqkv) || !aligned16(planes)) return ATTN_ERROR_MISALIGNED;
+    if (!aligned16(dqkv) || !aligned16(planes) || !aligned16(ds)) return ATTN_ERROR_MISALIGNED;
     const size_t N = plane_elems(B, H, T, d);
     void* pl = const_cast<void*>(planes);
     clear_error();
     tcamd::launch_flash_bwd_dq_ds_f32x3(plane_tensor(pl, N, 1), tcamd::head_major_view(H, T, d),
-                                        N, ds_area(pl, N), dqkv, tcamd::packed_qkv_view(H, T, d),
-                                        B * H, T, d, scale, stream);
+                                        N, ds, dqkv, tcamd::packed_qkv_view(H, T, d), B * H, T,
+                                        d, scale, stream);
     return launch_status();
 }
 
+// ds: the dS area where uses_ds (ignored, and may be null, elsewhere).
 int packed_backward_f32x3(const float* qkv, const float* o, const float* dO, const float* m,
                           const float* l, float* dqkv, float* ws, int B, int H, int T, int d,
-                          float scale, void* planes, int kv_ready, bool merged,
+                          float scale, void* planes, float* ds, int kv_ready, bool merged,
                           hipStream_t stream) {
     if (o == nullptr || planes == nullptr) return ATTN_ERROR_NULL_POINTER;
     int st = check_packed_bwd(qkv, dO, m, l, dqkv, ws, B, H, T, d, scale);
@@ -484,11 +493,14 @@ int packed_backward_f32x3(const float* qkv, const float* o, const float* dO, con
         return packed_backward_dkdv_f32x3(qkv, m, l, ws, dqkv, B, H, T, d, scale, planes,
                                           stream);
     }
+    if (ds == nullptr) return ATTN_ERROR_NULL_POINTER;                  // before any launch
+    if (!aligned16(ds) || !aligned16(planes)) return ATTN_ERROR_MISALIGNED;  // before any launch
     st = packed_backward_prep_f32x3(qkv, o, dO, ws, B, H, T, d, planes, kv_ready, merged, stream);
     if (st != ATTN_SUCCESS) return st;
-    st = packed_backward_dkdv_ds_f32x3(qkv, m, l, ws, dqkv, B, H, T, d, scale, planes, stream);
+    st = packed_backward_dkdv_ds_f32x3(qkv, m, l, ws, dqkv, B, H, T, d, scale, planes, ds,
+                                       stream);
     if (st != ATTN_SUCCESS) return st;
-    return packed_backward_dq_ds_f32x3(dqkv, B, H, T, d, scale, planes, stream);
+    return packed_backward_dq_ds_f32x3(dqkv, B, H, T, d, scale, planes, ds, stream);
 }
 
 // ---- the same path from separate head-major q, k, v (the reference's tiled launchers) ----
@@ -1174,6 +1186,12 @@ size_t attn_f32_ds_workspace_bytes(int B, int H, int T, int d_head) {
     return ds_f32_elems(B, H, T) * sizeof(float);
 }
 
+int attn_f32_backward_uses_ds(int B, int H, int T, int d_head) {
+    if (d_head != 32 && d_head != 64 && d_head != 128) return 0;
+    const size_t bytes = attn_f32_ds_workspace_bytes(B, H, T, d_head);
+    return bytes != 0 && bytes <= kDsMaxBytes ? 1 : 0;
+}
+
 int attn_packed_causal_backward_ds_f32(const float* qkv, const float* o, const float* do_ptr,
                                        const float* m_ptr, const float* l_ptr, float* dqkv,
                                        float* d_workspace, float* ds_workspace, int B, int H,
@@ -1218,11 +1236,20 @@ int attn_causal_backward_dq_ds_f32(const float* qkv, float* dqkv, const float* d
     return backward_dq_ds_f32(qkv, dqkv, ds_workspace, B, H, T, d_head, scale, stream);
 }
 
-size_t attn_f32x3_workspace_bytes(int B, int H, int T, int d_head) {
+size_t attn_f32x3_planes_bytes(int B, int H, int T, int d_head) {
     if (B <= 0 || H <= 0 || T <= 0 || d_head <= 0) return 0;
     return static_cast<size_t>(kPlaneTensors) * kPlanes * plane_elems(B, H, T, d_head) *
-               sizeof(uint16_t) +
-           (uses_ds(B, H, T, d_head) ? ds_elems(B, H, T) * sizeof(float) : 0);
+           sizeof(uint16_t);
+}
+
+size_t attn_f32x3_ds_workspace_bytes(int B, int H, int T, int d_head) {
+    if (B <= 0 || H <= 0 || T <= 0 || d_head <= 0 || !uses_ds(B, H, T, d_head)) return 0;
+    return ds_elems(B, H, T) * sizeof(float);
+}
+
+size_t attn_f32x3_workspace_bytes(int B, int H, int T, int d_head) {
+    return attn_f32x3_planes_bytes(B, H, T, d_head) +
+           attn_f32x3_ds_workspace_bytes(B, H, T, d_head);
 }
 
 int attn_f32x3_backward_uses_ds(int B, int H, int T, int d_head) {
@@ -1250,7 +1277,8 @@ int attn_packed_causal_backward_f32x3(const float* qkv, const float* o, const fl
                                       float scale, void* planes, int kv_planes_ready,
                                       hipStream_t stream) {
     return packed_backward_f32x3(qkv, o, do_ptr, m_ptr, l_ptr, dqkv, d_workspace, B, H, T,
-                                 d_head, scale, planes, kv_planes_ready, false, stream);
+                                 d_head, scale, planes, combined_ds(planes, B, H, T, d_head),
+                                 kv_planes_ready, false, stream);
 }
 
 int attn_fused_causal_backward_f32x3(const float* qkv, const float* o, const float* do_ptr,
@@ -1259,7 +1287,28 @@ int attn_fused_causal_backward_f32x3(const float* qkv, const float* o, const flo
                                      float scale, void* planes, int kv_planes_ready,
                                      hipStream_t stream) {
     return packed_backward_f32x3(qkv, o, do_ptr, m_ptr, l_ptr, dqkv, d_workspace, B, H, T,
-                                 d_head, scale, planes, kv_planes_ready, true, stream);
+                                 d_head, scale, planes, combined_ds(planes, B, H, T, d_head),
+                                 kv_planes_ready, true, stream);
+}
+
+int attn_packed_causal_backward_ds_f32x3(const float* qkv, const float* o, const float* do_ptr,
+                                         const float* m_ptr, const float* l_ptr, float* dqkv,
+                                         float* d_workspace, float* ds_workspace, int B, int H,
+                                         int T, int d_head, float scale, void* planes,
+                                         int kv_planes_ready, hipStream_t stream) {
+    return packed_backward_f32x3(qkv, o, do_ptr, m_ptr, l_ptr, dqkv, d_workspace, B, H, T,
+                                 d_head, scale, planes, ds_workspace, kv_planes_ready, false,
+                                 stream);
+}
+
+int attn_fused_causal_backward_ds_f32x3(const float* qkv, const float* o, const float* do_ptr,
+                                        const float* m_ptr, const float* l_ptr, float* dqkv,
+                                        float* d_workspace, float* ds_workspace, int B, int H,
+                                        int T, int d_head, float scale, void* planes,
+                                        int kv_planes_ready, hipStream_t stream) {
+    return packed_backward_f32x3(qkv, o, do_ptr, m_ptr, l_ptr, dqkv, d_workspace, B, H, T,
+                                 d_head, scale, planes, ds_workspace, kv_planes_ready, true,
+                                 stream);
 }
 
 int attn_packed_causal_backward_prep_f32x3(const float* qkv, const float* o,
@@ -1283,12 +1332,15 @@ int attn_causal_backward_dkdv_ds_f32x3(const float* qkv, const float* m_ptr, con
                                        int T, int d_head, float scale, void* planes,
                                        hipStream_t stream) {
     return packed_backward_dkdv_ds_f32x3(qkv, m_ptr, l_ptr, d_workspace, dqkv, B, H, T, d_head,
-                                         scale, planes, stream);
+                                         scale, planes, combined_ds(planes, B, H, T, d_head),
+                                         stream);
 }
 
 int attn_causal_backward_dq_ds_f32x3(float* dqkv, int B, int H, int T, int d_head, float scale,
                                      const void* planes, hipStream_t stream) {
-    return packed_backward_dq_ds_f32x3(dqkv, B, H, T, d_head, scale, planes, stream);
+    return packed_backward_dq_ds_f32x3(
+        dqkv, B, H, T, d_head, scale, planes,
+        combined_ds(const_cast<void*>(planes), B, H, T, d_head), stream);
 }
 
 int attn_packed_causal_backward_dq_f32x3(const float* qkv, const float* o,

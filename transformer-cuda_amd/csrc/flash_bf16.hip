@@ -75,6 +75,14 @@ constexpr int kKeyTileDq = NP == 1 ? kRowTile : 32;
 template <int NP>
 constexpr int kQueryTile = NP == 1 ? kRowTile : 32;
 
+// The three-plane dK/dV stage walks its query tiles from the last to the first.  dK and dV
+// accumulate over every query in the MFMA accumulator (no register is left for compensated
+// tile sums), and for a key the terms P_ij dO_i and dS_ij q_i shrink with the query index
+// i (P_ij ~ 1/(i+1)): added small ones first, each is rounded against a smaller partial
+// sum.
+template <int NP>
+constexpr bool kDesc = NP == 3;
+
 // K and V tiles of stage 1 (as the forward's), NP planes each.  At d >= 64 the row stores of
 // dO's planes and of dQ go through LDS stages inside an idle buffer.
 template <int D, int NP>
@@ -595,6 +603,9 @@ __global__ __launch_bounds__(kWave* NW, NP == 1 ? 1 : 2) void flash_bwd_dkdv_bf1
 
     const int t0 = k0 / KT;
     const int ntile = (T + KT - 1) / KT;
+    // Three planes walk the query tiles downward (kDesc): the last tile first, the
+    // workgroup's first key's tile last.
+    const int tfirst = kDesc<NP> ? ntile - 1 : t0;
     const uint32_t q_lds = lds_addr(sm.q[0][0]);
     const uint32_t g_lds = lds_addr(sm.g[0][0]);
     const uint32_t qx_lds = lds_addr(sm.qx[0]);
@@ -610,7 +621,7 @@ __global__ __launch_bounds__(kWave* NW, NP == 1 ? 1 : 2) void flash_bwd_dkdv_bf1
                                 wave, lane, grs);
         }
     };
-    copy_tile(t0);
+    copy_tile(tfirst);
     // Wave 0 stages the statistics of a tile through VGPRs: lane i < KT holds query KT*t + i.
     float st_m = 0.0f, st_l = 1.0f, st_d = 0.0f;
     auto load_stats = [&](int t) {
@@ -626,7 +637,7 @@ __global__ __launch_bounds__(kWave* NW, NP == 1 ? 1 : 2) void flash_bwd_dkdv_bf1
         }
     };
     if (wave == 0 && lane < KT) {
-        load_stats(t0);
+        load_stats(tfirst);
         const u16x8 z = u16x8{};  // the constant zeros of the statistic chunks
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
@@ -652,7 +663,8 @@ __global__ __launch_bounds__(kWave* NW, NP == 1 ? 1 : 2) void flash_bwd_dkdv_bf1
     lane_offsets<D>(lane, roff, troff);
     const uint32_t soff = static_cast<uint32_t>(col * 16);  // statistic chunk of row col
 
-    // Tile kt: wait for its copies, publish its statistics, barrier, start the next copy.
+    // Tile kt: wait for its copies, publish its statistics, barrier, start the next copy
+    // (tile kt - 1 when descending).
     auto tile_sync = [&](int kt) {
         wait_vm<0>();  // this wave's copies (and statistics loads) of tile kt landed
         if (wave == 0 && lane < KT) {  // terms of -lse2 (-1e30 for padded queries: P = 0), -D
@@ -660,10 +672,11 @@ __global__ __launch_bounds__(kWave* NW, NP == 1 ? 1 : 2) void flash_bwd_dkdv_bf1
             *reinterpret_cast<u16x4*>(&sm.qx[kt & 1][lane * 8]) = stat_terms<NP>(nl);
             *reinterpret_cast<u16x4*>(&sm.gx[kt & 1][lane * 8]) = stat_terms<NP>(-st_d);
         }
-        __syncthreads();  // every wave's copies landed; tile kt-1 is no longer read
-        if (kt + 1 < ntile) {
-            if (wave == 0 && lane < KT) load_stats(kt + 1);
-            copy_tile(kt + 1);
+        __syncthreads();  // every wave's copies landed; the previous tile is no longer read
+        const int nt = kDesc<NP> ? kt - 1 : kt + 1;
+        if (kDesc<NP> ? nt >= t0 : nt < ntile) {
+            if (wave == 0 && lane < KT) load_stats(nt);
+            copy_tile(nt);
         }
     };
     // Operand addresses of half tile hh (queries 32*hh ..).
@@ -765,16 +778,31 @@ __global__ __launch_bounds__(kWave* NW, NP == 1 ? 1 : 2) void flash_bwd_dkdv_bf1
                                                           kj, half, dso);
         };
         const int tstart = kw < T ? kw / KT : ntile;
-        int kt = t0;
-        for (; kt < tstart; ++kt) tile_sync(kt);
-        if (kt < ntile) {
-            tile_sync(kt);
-            step(kt, std::true_type{});
-            ++kt;
-        }
-        for (; kt < ntile; ++kt) {
-            tile_sync(kt);
-            step(kt, std::false_type{});
+        if constexpr (kDesc<NP>) {
+            // Downward: the wave's unmasked tiles, its diagonal tile, then barriers only.
+            int kt = ntile - 1;
+            for (; kt > tstart; --kt) {
+                tile_sync(kt);
+                step(kt, std::false_type{});
+            }
+            if (kt == tstart && kt < ntile) {
+                tile_sync(kt);
+                step(kt, std::true_type{});
+                --kt;
+            }
+            for (; kt >= t0; --kt) tile_sync(kt);
+        } else {
+            int kt = t0;
+            for (; kt < tstart; ++kt) tile_sync(kt);
+            if (kt < ntile) {
+                tile_sync(kt);
+                step(kt, std::true_type{});
+                ++kt;
+            }
+            for (; kt < ntile; ++kt) {
+                tile_sync(kt);
+                step(kt, std::false_type{});
+            }
         }
     } else {
         // Half tiles before hstart (= kw/32, the one holding the wave's first key) hold only

@@ -37,6 +37,7 @@
 #include <math.h>
 
 #include <type_traits>
+#include <utility>
 
 #include "device_common.hpp"
 #include "bf16_tile.hpp"
@@ -112,13 +113,14 @@ __device__ __forceinline__ float sum_tree16(const f32x16& s) {
     return (t[0] + t[2]) + (t[1] + t[3]);
 }
 
-// Per-wave softmax state of one 32-query sub-block.  Folded: m_used and m_true are
-// in log2 units of c*q.k, and xs carries the terms of -m_used; otherwise in units of q.k.
+// Per-wave softmax state of one 32-query sub-block.  Folded: m_used is in log2 units of
+// c*q.k, xs carries the terms of -m_used, and m_true is not kept (the exported m is m_used);
+// otherwise in units of q.k.
 template <int D>
 struct SubState {
     f32x16 acc[D / 32];  // O^T accumulator
     float m_used;        // max the exponentials are taken against
-    float m_true;        // running max of the scores
+    float m_true;        // running max of the scores (unfolded)
     float l;             // running sum of the exponentials against m_used
     bf16x8 xs;           // folded: statistic chunk of -m_used
 };
@@ -137,7 +139,6 @@ __device__ __forceinline__ void softmax_step(f32x16& s, SubState<D>& st, bf16x8 
     mx = xhalf_max(mx);
     if constexpr (FOLD) {
         // s = c*q.k - m_used already
-        st.m_true = fmaxf(st.m_true, mx + st.m_used);
         const bool first = st.l == 0.0f;  // l >= 1 after the first tile
         if (__builtin_amdgcn_ballot_w64(first || mx > kRescaleLog2) != 0) {
             // the first tile sets the maximum, later ones only raise it; the new offset is
@@ -385,16 +386,282 @@ __global__ __launch_bounds__(kWave* kWaves, (kFwdMinBlocks<D, NSUB, NP>)) void f
             if constexpr (!kStaged<D>) store_row<D>(o + ooff, qi, half, st.acc, 1.0f / st.l, ors);
             if (half == 0) {
                 const size_t r = static_cast<size_t>(bh) * T + qi;
-                // m = scale * max_j q.k; l relative to that maximum
+                // folded (bf16): the reference value the exponentials were taken against and
+                // the sum against it; otherwise m = scale * max_j q.k, l relative to it
                 if constexpr (kFold<NP, NSUB>) {
-                    if (m_out != nullptr) m_out[r] = st.m_true * (1.0f / kLog2e);
-                    if (l_out != nullptr) l_out[r] = st.l * exp2_fast(st.m_used - st.m_true);
+                    if (m_out != nullptr) m_out[r] = st.m_used * (1.0f / kLog2e);
+                    if (l_out != nullptr) l_out[r] = st.l;
                 } else {
                     if (m_out != nullptr) m_out[r] = st.m_true * scale;
                     if (l_out != nullptr)
                         l_out[r] = st.l * exp2_fast((st.m_used - st.m_true) * c);
                 }
             }
+        }
+    }
+}
+
+
+template <int... Is, typename F>
+__device__ __forceinline__ void static_for_impl(std::integer_sequence<int, Is...>, F&& f) {
+    (f(std::integral_constant<int, Is>{}), ...);
+}
+// f(integral_constant<int, 0>) ... f(integral_constant<int, N-1>), in order.
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    static_for_impl(std::make_integer_sequence<int, N>{}, f);
+}
+
+// ---------------------------------------------------------------------------------------
+// The bf16 forward (NP = 1): one 32-query sub-block per wave, folded softmax, and a
+// reference maximum that is set once and raised only when a row's sums grow large.
+//
+// On a SIMD the VALU and MFMA work of these kernels mostly add up rather than overlap
+// (counters at config 3: the kernel above keeps the VALU issuing 74% of its cycles and the
+// MFMA busy 46%, ~90% of the cycles one or the other), so its time follows the VALU work per
+// MFMA.  Per 32-key half tile and wave it issues 9 MFMAs and about 80 VALU instructions, a
+// row maximum (a max tree, a cross-half swap and a wave vote) among them.  Here the
+// exponentials are taken against M, set to the row's maximum over the wave's first half tile
+// and carried by the fold's (hi, lo) terms; no maximum is formed after that.  Instead each
+// half tile's row sum of P = 2^(s - M), which l needs anyway, is compared with 2^16: only a
+// row whose scores rose more than ~11 (log2 units) above M (or an inf or NaN) makes the wave
+// recompute the half tile's scores from the same LDS tile, raise M to their maximum and scale
+// the accumulator and l down (raise_ref).  For unit-variance scores the maximum over 32 keys
+// is within ~3 of the maximum over thousands, so the wave never takes that path there; the
+// accumulated P stay below 2^11 per element as they stayed below 2^8 with the running
+// maximum.  (m, l) = (M, l) honour the statistics contract P_ij = exp(scale*q_i.k_j - m_i) /
+// l_i with the log-sum-exp m + ln l; m is a score of the row's first keys (or the maximum of
+// a later half tile that raised it), not necessarily the row maximum.  Every LDS address of
+// the unrolled loop is a lane offset plus a constant.  Per half tile at d = 64: 9 MFMAs and
+// 16 v_exp_f32, 8 conversions, the 17 steps of the row sum and a compare of VALU work.
+// ---------------------------------------------------------------------------------------
+
+constexpr float kRaiseSum = 65536.0f;  // a half tile's row sum that makes M rise
+
+template <int D>
+struct FoldState {
+    f32x16 acc[D / 32];  // O^T
+    float l;             // row sum of 2^(s - M)
+    float m_used;        // M, log2 units of c*q.k
+    bf16x8 xs;           // statistic chunk of -M (zero before the first half tile)
+};
+
+// The (hi, lo) terms of -m as the fold's statistic chunk; M := -(hi + lo), m to 16 bits.
+template <int D>
+__device__ __forceinline__ void set_ref(FoldState<D>& st, float m, int half) {
+    const u16x4 t = stat_terms<1>(-m);
+    st.m_used = -(bf16_bits_to_f32(t[0]) + bf16_bits_to_f32(t[1]));
+    u16x8 x = u16x8{};
+    if (half == 0) {
+        x[0] = t[0];
+        x[1] = t[1];
+    }
+    st.xs = __builtin_bit_cast(bf16x8, x);
+}
+
+// S^T - M of one half tile: the fold step, then K (cQ)^T over the head dimension.
+template <int D, bool FOLD, bool MASK>
+__device__ __forceinline__ f32x16 fold_scores(uint32_t kbase, const uint32_t (&koff)[D / 16],
+                                              const bf16x8 (&qr)[D / 16], const FoldState<D>& st,
+                                              int kb, int qj, int col, int half,
+                                              const bf16x8& one) {
+    f32x16 s = f32x16{};
+    if constexpr (FOLD) s = mfma_32x32x16_bf16(one, st.xs, s);
+#pragma unroll
+    for (int i = 0; i < D / 16; ++i) s = mfma_32x32x16_bf16(lds_b128(koff[i] + kbase), qr[i], s);
+    if constexpr (MASK) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+            if (kb + acc_row(r, half) > qj + col) s[r] = -INFINITY;
+    }
+    return s;
+}
+
+// One half tile: K rows at kbase + koff[st], V^T at vbase + voff[dt] (LDS byte addresses).
+// FIRST: the wave's first half tile, which sets M.  MASK: the half tile holds keys past some
+// of the sub-block's queries.
+template <int D, bool FIRST, bool MASK>
+__device__ __forceinline__ void fold_half(uint32_t kbase, uint32_t vbase,
+                                          const uint32_t (&koff)[D / 16],
+                                          const uint32_t (&voff)[D / 32],
+                                          const bf16x8 (&qr)[D / 16], FoldState<D>& st, int kb,
+                                          int qj, int col, int half, const bf16x8& one) {
+    f32x16 s = fold_scores<D, !FIRST, MASK>(kbase, koff, qr, st, kb, qj, col, half, one);
+    if constexpr (FIRST) {
+        set_ref(st, xhalf_max(max_tree16(s)), half);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[r] -= st.m_used;
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s[r] = exp2_fast(s[r]);
+    float ts = xhalf_sum(sum_tree16(s));
+    if constexpr (!FIRST) {
+        if (__builtin_expect(__builtin_amdgcn_ballot_w64(!(ts < kRaiseSum)) != 0, 0)) {
+            // Rare: a row's sum reached kRaiseSum (or is not finite).  The scores again from
+            // the same LDS tile, M raised to their maximum where that is larger, the
+            // accumulator and l scaled to the new M, and P against it.
+            s = fold_scores<D, true, MASK>(kbase, koff, qr, st, kb, qj, col, half, one);
+            const float mx = xhalf_max(max_tree16(s));  // relative to M
+            if (mx > 0.0f) {
+                const float m_old = st.m_used;
+                set_ref(st, m_old + mx, half);
+                const float shift = st.m_used - m_old;
+                const float alpha = exp2_fast(-shift);
+                st.l *= alpha;
+#pragma unroll
+                for (int dt = 0; dt < D / 32; ++dt) st.acc[dt] *= alpha;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) s[r] -= shift;
+            }
+#pragma unroll
+            for (int r = 0; r < 16; ++r) s[r] = exp2_fast(s[r]);
+            ts = xhalf_sum(sum_tree16(s));
+        }
+    }
+    st.l += ts;
+    bf16x8 pb[2];
+    pb[0] = pack_b(s, 0);
+    pb[1] = pack_b(s, 1);
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+            st.acc[dt] = mfma_32x32x16_bf16(
+                lds_tr(voff[dt] + vbase + u * Swz<D>::rows(16), Swz<D>::rows(8)), pb[u],
+                st.acc[dt]);
+    }
+}
+
+template <int D>
+__global__ __launch_bounds__(kWave* kWaves, D >= 128 ? 3 : 4) void flash_fwd_fold_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+    const uint16_t* __restrict__ v, uint16_t* __restrict__ o, float* __restrict__ m_out,
+    float* __restrict__ l_out, int BH, int T, float scale, int nblk, HeadView xv, HeadView ov,
+    int serp) {
+    constexpr int KT = kKeyTile<D, 1>;
+    constexpr int kHalves = KT / 32;
+    constexpr int kPer = 2 * kHalves;  // half tiles per round of the two buffers
+    using S = Swz<D, KT>;
+    constexpr uint32_t kTile = kFwdTile<D, 1>;
+    __shared__ __attribute__((aligned(1024))) FwdSmem<D, 1> sm;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & (kWave - 1);
+    const int col = lane & 31;
+    const int half = lane >> 5;
+    int bh, blk;
+    if (serp < 0)
+        map_block_grouped(blockIdx.x, BH, nblk, -serp, true, bh, blk);
+    else
+        map_block(blockIdx.x, BH, nblk, true, serp != 0, bh, blk);
+    constexpr int kBlock = kWaves * kSub;
+    const int q0 = blk * kBlock;
+    const int qj = q0 + kSub * wave;
+    const size_t xoff = xv.off(bh), ooff = ov.off(bh);
+    const int xrs = xv.row;
+    const uint16_t* kh = k + xoff;
+    const uint16_t* vh = v + xoff;
+    const float c = scale * kLog2e;
+
+    bf16x8 qr[D / 16];  // c*Q, rounded to bf16 again
+    load_rowop<D>(qr, q + xoff, qj + col, T, half, xrs);
+#pragma unroll
+    for (int st = 0; st < D / 16; ++st) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            qr[st][e] = static_cast<__bf16>(static_cast<float>(qr[st][e]) * c);
+    }
+
+    const int kend = min(T, q0 + kBlock);
+    const int ntile = (kend + KT - 1) / KT;
+    const uint32_t k_lds = lds_addr(sm.k[0][0]);
+    const uint32_t v_lds = lds_addr(sm.v[0][0]);
+    auto copy_tile = [&](int kt) {
+        const uint32_t buf = static_cast<uint32_t>(kt & 1) * kTile;
+        dma_tile<D, kWaves, KT>(kh, kt * KT, T, k_lds + buf, wave, lane, xrs);
+        dma_tile<D, kWaves, KT>(vh, kt * KT, T, v_lds + buf, wave, lane, xrs);
+    };
+    copy_tile(0);
+
+    uint32_t koff[D / 16], voff[D / 32];
+    lane_offsets<D>(lane, koff, voff);
+
+    FoldState<D> st;
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt) st.acc[dt] = f32x16{};
+    st.l = 0.0f;
+    st.m_used = 0.0f;
+    st.xs = bf16x8{};
+    const bf16x8 one = ones_chunk<1>(half);
+
+    const int nhalf_t = (T + 31) / 32;
+    const int hB = min(qj / 32 + 1, nhalf_t);  // half tiles of this wave; the last one masks
+    const int hend = kHalves * ntile;
+    // Tile barrier at the first half of a tile: this wave's copies of tile hh/kHalves landed,
+    // every wave's too, and the other buffer is no longer read: the next tile goes there.
+    auto sync_at = [&](int hh) {
+        if (hh % kHalves == 0) {
+            wait_vm<0>();
+            __syncthreads();
+            const int kt = hh / kHalves;
+            if (kt + 1 < ntile) copy_tile(kt + 1);
+        }
+    };
+    // Half tile hh with hh % kPer == P (compile time): every LDS address a constant offset.
+    auto step = [&](int hh, auto Pc) {
+        constexpr int P = decltype(Pc)::value;
+        constexpr uint32_t base = static_cast<uint32_t>(P / kHalves) * kTile +
+                                  static_cast<uint32_t>(P % kHalves) * S::rows(32);
+        if constexpr (P % kHalves == 0) {
+            wait_vm<0>();
+            __syncthreads();
+            const int kt = hh / kHalves;
+            if (kt + 1 < ntile) copy_tile(kt + 1);
+        }
+        fold_half<D, false, false>(k_lds + base, v_lds + base, koff, voff, qr, st, 32 * hh, qj,
+                                   col, half, one);
+    };
+    // Any half tile, its buffer and half at run time (the steps outside the unrolled loop).
+    auto step_any = [&](int hh, auto first, auto mask) {
+        sync_at(hh);
+        const uint32_t base = static_cast<uint32_t>((hh / kHalves) & 1) * kTile +
+                              static_cast<uint32_t>(hh % kHalves) * S::rows(32);
+        fold_half<D, decltype(first)::value, decltype(mask)::value>(
+            k_lds + base, v_lds + base, koff, voff, qr, st, 32 * hh, qj, col, half, one);
+    };
+    // hh = 0 sets M1 (masked when it is also the diagonal); then the unmasked half tiles,
+    // kPer at a time with constant addresses; then the diagonal one.
+    if (hB == 1) step_any(0, std::true_type{}, std::true_type{});
+    else step_any(0, std::true_type{}, std::false_type{});
+    int hh = 1;
+    const int hsteady = hB - 1;
+    for (; hh < hsteady && hh % kPer != 0; ++hh) step_any(hh, std::false_type{}, std::false_type{});
+    for (; hh + kPer <= hsteady; hh += kPer)
+        static_for<kPer>([&](auto Pc) { step(hh + decltype(Pc)::value, Pc); });
+    for (; hh < hsteady; ++hh) step_any(hh, std::false_type{}, std::false_type{});
+    if (hh < hB) {
+        step_any(hh, std::false_type{}, std::true_type{});
+        ++hh;
+    }
+    for (; hh < hend; ++hh) sync_at(hh);
+
+    uint32_t ostage;
+    if constexpr (kStageIdle<D, 1>) {
+        ostage = wave_stage(lds_addr(sm.k[ntile & 1][0]), lds_addr(sm.v[ntile & 1][0]), wave,
+                            kStageBytes<D, 1>);
+    } else {
+        __syncthreads();
+        ostage = wave_stage(lds_addr(sm.k[0][0]), lds_addr(sm.v[0][0]), wave,
+                            kStageBytes<D, 1>);
+    }
+    const int qi = qj + col;
+    if constexpr (kStaged<D>)
+        store_row_staged<D>(o + ooff, qj, T, lane, st.acc, 1.0f / st.l, ov.row, ostage);
+    if (qi < T) {
+        if constexpr (!kStaged<D>) store_row<D>(o + ooff, qi, half, st.acc, 1.0f / st.l, ov.row);
+        if (half == 0) {
+            const size_t r = static_cast<size_t>(bh) * T + qi;
+            if (m_out != nullptr) m_out[r] = st.m_used * (1.0f / kLog2e);
+            if (l_out != nullptr) l_out[r] = st.l;
         }
     }
 }
@@ -428,9 +695,22 @@ void fwd_launch(const FwdArgs<NP>& a, hipStream_t stream) {
                        a.ov, a.pstride, a.qp, serp);
 }
 
+template <int D>
+void fwd_fold_launch(const FwdArgs<1>& a, hipStream_t stream) {
+    constexpr int kBlock = kWaves * kSub;
+    const int nblk = (a.T + kBlock - 1) / kBlock;
+    const auto kernel = flash_fwd_fold_kernel<D>;
+    const int res = resident_capacity(kernel, kWave * kWaves, 0);
+    const int serp = a.BH * nblk <= res ? 1 : -head_group(a.BH, nblk, res);
+    hipLaunchKernelGGL(kernel, dim3(a.BH * nblk), dim3(kWave * kWaves), 0, stream, a.q, a.k,
+                       a.v, a.o, a.m_out, a.l_out, a.BH, a.T, a.scale, nblk, a.xv, a.ov, serp);
+}
+
 template <int D, int NP>
 void fwd_dispatch(const FwdArgs<NP>& a, hipStream_t stream) {
-    if constexpr (NP == 1 || D >= 128) {
+    if constexpr (NP == 1 && D <= 64) {
+        fwd_fold_launch<D>(a, stream);
+    } else if constexpr (NP == 1 || D >= 128) {
         // bf16 operands: one sub-block per wave at every size.  Its folded softmax (one
         // v_exp_f32 and no fma per score, 110 VGPRs: four waves per SIMD) outruns two
         // sub-blocks' balanced causal work (168 VGPRs, three waves): config 3 -4%,

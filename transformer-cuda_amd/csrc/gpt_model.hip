@@ -7,9 +7,9 @@
 // (gpt_config.attention_mode): the fused path of this build (attention from the packed QKV
 // projection output straight into the merged-heads layout, three launches per layer and
 // direction) on the fp32 MFMA or, fused_x3, on the bf16 MFMA with fp32 operands as three
-// bf16 planes (a plane workspace per layer, kept from the forward to the backward), the
-// reference's tiled launcher sequence (split-transpose, tiled attention, head merge), or the
-// reference's default materialised sequence (T x T scores).
+// bf16 planes (a plane workspace per layer, kept from the forward to the backward, and one
+// dS area for all layers), the reference's tiled launcher sequence (split-transpose, tiled
+// attention, head merge), or the reference's default materialised sequence (T x T scores).
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <rocblas/rocblas.h>
@@ -90,7 +90,8 @@ struct gpt_model {
     // backward scratch shared by the layers
     float *d_x = nullptr, *d_ln = nullptr, *d_qkv = nullptr, *d_merged = nullptr,
           *d_ffn_a = nullptr, *d_ffn_b = nullptr, *ws = nullptr, *colsum = nullptr, *splitk = nullptr,
-          *attn_ds = nullptr,  // fused fp32 attention: the backward's dS, shared by the layers
+          *attn_ds = nullptr,  // fused modes: the backward's dS, shared by the layers (null
+                               // where the shape takes the two-stage backward)
           *norm = nullptr, *proj = nullptr;
     float *dq = nullptr, *dk = nullptr, *dv = nullptr, *d_attn_out = nullptr;  // split modes
     float *scores = nullptr, *dprobs = nullptr, *dscores = nullptr;          // materialised
@@ -256,15 +257,20 @@ int attention_backward(gpt_model* m, LayerActs& a, hipStream_t s) {
     const float scale = 1.0f / sqrtf(static_cast<float>(d));
     attn_mark(m, s);
     switch (c.attention_mode) {
-        case GPT_ATTN_FUSED:  // dS-first: dK/dV write dS, dQ is computed from it
-            TRY(attn_fused_causal_backward_ds_f32(a.qkv, a.merged, m->d_merged, a.attn_m,
-                                                  a.attn_l, m->d_qkv, m->ws, m->attn_ds, B, H, T,
-                                                  d, scale, s));
+        case GPT_ATTN_FUSED:
+            if (m->attn_ds != nullptr)  // dS-first: dK/dV write dS, dQ is computed from it
+                TRY(attn_fused_causal_backward_ds_f32(a.qkv, a.merged, m->d_merged, a.attn_m,
+                                                      a.attn_l, m->d_qkv, m->ws, m->attn_ds, B, H,
+                                                      T, d, scale, s));
+            else  // dS above its size limit: the two-stage order, no T^2 workspace
+                TRY(attn_fused_causal_backward_f32(a.qkv, a.merged, m->d_merged, a.attn_m,
+                                                   a.attn_l, m->d_qkv, m->ws, B, H, T, d, scale,
+                                                   s));
             break;
         case GPT_ATTN_FUSED_X3:  // the layer's qkv and planes are the forward's
-            TRY(attn_fused_causal_backward_f32x3(a.qkv, a.merged, m->d_merged, a.attn_m,
-                                                 a.attn_l, m->d_qkv, m->ws, B, H, T, d, scale,
-                                                 a.planes, 1, s));
+            TRY(attn_fused_causal_backward_ds_f32x3(a.qkv, a.merged, m->d_merged, a.attn_m,
+                                                    a.attn_l, m->d_qkv, m->ws, m->attn_ds, B, H, T,
+                                                    d, scale, a.planes, 1, s));
             break;
         case GPT_ATTN_TILED_SPLIT:
             TRY(attn_head_merge_transpose_backward_f32(m->d_merged, m->d_attn_out, B, H, T, d,
@@ -338,11 +344,10 @@ int create(const gpt_config& c, gpt_model* m) {
         TRY(alloc(m, &a.ffn1, BT * F));
         TRY(alloc(m, &a.gelu, BT * F));
         TRY(alloc(m, &a.out, BT * C));
-        if (c.attention_mode == GPT_ATTN_FUSED_X3) {
-            const size_t bytes = attn_f32x3_workspace_bytes(static_cast<int>(B),
-                                                            static_cast<int>(H),
-                                                            static_cast<int>(T),
-                                                            static_cast<int>(C / H));
+        if (c.attention_mode == GPT_ATTN_FUSED_X3) {  // the planes only: dS is shared below
+            const size_t bytes = attn_f32x3_planes_bytes(static_cast<int>(B), static_cast<int>(H),
+                                                         static_cast<int>(T),
+                                                         static_cast<int>(C / H));
             TRY(alloc(m, &a.planes, static_cast<long long>((bytes + 3) / 4)));
         }
         if (c.attention_mode == GPT_ATTN_TILED_SPLIT ||
@@ -369,11 +374,18 @@ int create(const gpt_config& c, gpt_model* m) {
     TRY(alloc(m, &m->d_ffn_b, BT * F));
     TRY(alloc(m, &m->proj, BT * C));
     TRY(alloc(m, &m->ws, B * H * T));
-    if (c.attention_mode == GPT_ATTN_FUSED) {
-        const size_t bytes = attn_f32_ds_workspace_bytes(static_cast<int>(B), static_cast<int>(H),
-                                                         static_cast<int>(T),
-                                                         static_cast<int>(C / H));
-        TRY(alloc(m, &m->attn_ds, static_cast<long long>((bytes + 3) / 4)));
+    {
+        // One dS area for all layers (dS lives within one layer's backward call), where the
+        // shape takes the dS-first order: the fp32 MFMA backward up to its 16 GiB limit, the
+        // three-plane backward where attn_f32x3_ds_workspace_bytes is not 0.
+        const int iB = static_cast<int>(B), iH = static_cast<int>(H), iT = static_cast<int>(T),
+                  id = static_cast<int>(C / H);
+        size_t bytes = 0;
+        if (c.attention_mode == GPT_ATTN_FUSED && attn_f32_backward_uses_ds(iB, iH, iT, id))
+            bytes = attn_f32_ds_workspace_bytes(iB, iH, iT, id);
+        if (c.attention_mode == GPT_ATTN_FUSED_X3)
+            bytes = attn_f32x3_ds_workspace_bytes(iB, iH, iT, id);
+        if (bytes > 0) TRY(alloc(m, &m->attn_ds, static_cast<long long>((bytes + 3) / 4)));
     }
     long long sk = head_splitk(c) ? static_cast<long long>(kHeadSplitK) * BT * C : 0;
     if (weight_splitk(c)) sk = std::max(sk, weight_splitk_floats(c));

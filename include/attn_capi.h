@@ -143,6 +143,31 @@ int attn_gemm_create(attn_gemm_handle* handle);
 int attn_gemm_destroy(attn_gemm_handle handle);
 /* Device ordinal the handle is bound to, or -1 for a NULL handle. */
 int attn_gemm_device(attn_gemm_handle handle);
+/* No counterpart in the reference: attn_matmul_batched_strided_f32 (alpha 1, beta 0) for
+ * operands with the structure of causal attention, which lets it skip work the causal mask
+ * makes unused.  The materialised attention entry points below run their six products
+ * through it.  `causal`:
+ *   ATTN_GEMM_FULL       the full product (as attn_matmul_batched_strided_f32);
+ *   ATTN_GEMM_LOWER_OUT  M == N; only C[i][j] with j <= i is needed (scores for a causal
+ *                        softmax): 128 x 128 blocks of C wholly above the diagonal are not
+ *                        written;
+ *   ATTN_GEMM_LOWER_A    M == K; op(A)[i][k] == 0 for k > i (causal probabilities): those
+ *                        terms are not computed;
+ *   ATTN_GEMM_UPPER_A    M == K; op(A)[i][k] == 0 for k < i (their transpose): likewise.
+ * The results equal the full product's for finite inputs (the skipped terms are exact
+ * zeros; the skipped outputs are not written).  Other validation as the full product's;
+ * ATTN_ERROR_INVALID_VALUE for an unknown `causal`, ATTN_ERROR_INVALID_DIM for M, N, K that
+ * do not fit it. */
+typedef enum attn_gemm_causal {
+    ATTN_GEMM_FULL = 0,
+    ATTN_GEMM_LOWER_OUT = 1,
+    ATTN_GEMM_LOWER_A = 2,
+    ATTN_GEMM_UPPER_A = 3
+} attn_gemm_causal;
+int attn_matmul_batched_strided_causal_f32(const float* A, const float* B, float* C, int M,
+                                           int N, int K, long long strideA, long long strideB,
+                                           long long strideC, int batch_count, int transA,
+                                           int transB, int causal, hipStream_t stream);
 /* Replaces matmul_batched_strided with its handle argument, include/kernels/matmul.cuh:44-58:
  * attn_matmul_batched_strided_f32 run through `handle` (ATTN_ERROR_NULL_POINTER if NULL). */
 int attn_matmul_batched_strided_f32_h(attn_gemm_handle handle, const float* A, const float* B,
@@ -152,14 +177,21 @@ int attn_matmul_batched_strided_f32_h(attn_gemm_handle handle, const float* A, c
                                       hipStream_t stream);
 
 /* The reference's materialised forward (src/model.cu:313-332), scores and probs (B*H*T, T):
- *   scores = Q K^T  ->  probs = causal_softmax_forward(scores, scale)  ->  out = probs V. */
+ *   scores = Q K^T  ->  probs = causal_softmax_forward(scores, scale)  ->  out = probs V.
+ * The contractions skip what the causal mask makes unused: scores is written where j <= i
+ * (and in the rest of each 128 x 128 block that crosses the diagonal; blocks wholly above it
+ * are left as they were, and the softmax never reads them), and out = probs V runs over
+ * the nonzero part of probs only.  probs is written in full (zeros above the diagonal), and
+ * out equals the full product's for finite inputs. */
 int attn_materialized_causal_forward_f32(const float* q, const float* k, const float* v,
                                          float* scores, float* probs, float* out, int B, int H,
                                          int T, int d_head, float scale, hipStream_t stream);
 
 /* The reference's materialised backward (src/model.cu:617-650): dprobs = dO V^T,
  * dv = probs^T dO, dscores = causal_softmax_backward(dprobs, probs, scale), dq = dscores K,
- * dk = dscores^T Q.  dprobs and dscores are (B*H*T, T) scratch; dq, dk, dv are overwritten. */
+ * dk = dscores^T Q.  dprobs and dscores are (B*H*T, T) scratch; dq, dk, dv are overwritten.
+ * As in the forward, dprobs is written only in the 128 x 128 blocks at or below the
+ * diagonal, and the four products with probs or dscores run over their nonzero parts. */
 int attn_materialized_causal_backward_f32(const float* q, const float* k, const float* v,
                                           const float* probs, const float* dout, float* dprobs,
                                           float* dscores, float* dq, float* dk, float* dv,

@@ -252,6 +252,20 @@ def test_f32x3_validation(lib):
                     f(0.125), FAKE, 1, None) == BAD_HEAD_DIM
 
 
+def test_causal_gemm_validation(lib):
+    """attn_matmul_batched_strided_causal_f32 rejects, before any launch, an unknown causal
+    structure and shapes that do not fit the one given."""
+    g = lambda causal=1, M=64, N=64, K=64, A=FAKE: lib.call(
+        "attn_matmul_batched_strided_causal_f32", A, FAKE, FAKE, M, N, K, M * K, K * N, M * N,
+        2, 0, 0, causal, None)
+    assert g(causal=4) == BAD_VALUE and g(causal=-1) == BAD_VALUE
+    assert g(causal=lib.GEMM_LOWER_OUT, N=32) == INVALID_DIM      # needs M == N
+    assert g(causal=lib.GEMM_LOWER_A, K=32) == INVALID_DIM        # needs M == K
+    assert g(causal=lib.GEMM_UPPER_A, K=32) == INVALID_DIM
+    assert g(A=None) == NULLPTR
+    assert g(M=0, N=0) == INVALID_DIM
+
+
 def test_f32x3_separate_ds_validation(lib):
     """The workspace split into planes and dS, and the one-call backwards that take them
     apart: sizes add up, dS is required exactly where the dS-first order runs."""

@@ -145,3 +145,61 @@ def test_materialized_config2_vs_oracle_and_tiled(lib):
         for name in ("o", "dq", "dk", "dv"):
             err = max_abs(sl(got[name]), getattr(want, name).numpy())
             assert err <= 1e-5, f"{name} head ({b},{h}): max-abs {err:.3e}"
+
+
+@pytest.mark.parametrize("T,d", [(1024, 64), (300, 32), (129, 128)])
+def test_causal_gemm_equals_full_product(lib, T, d):
+    """attn_matmul_batched_strided_causal_f32 on causally structured operands: the outputs it
+    writes equal the full product's bitwise (the terms it skips are exact zeros, the outputs
+    it skips lie in 128 x 128 blocks above the diagonal, which stay as they were)."""
+    BH = 3
+    g = torch.Generator(device="cpu").manual_seed(T + d)
+    x = torch.randn((BH, T, d), generator=g).to("cuda:0")
+    y = torch.randn((BH, T, d), generator=g).to("cuda:0")
+    lower = torch.tril(torch.randn((BH, T, T), generator=g)).to("cuda:0").contiguous()
+    sh, ss = T * d, T * T
+    cases = [  # (A, B, M, N, K, sA, sB, transA, transB, causal)
+        (x, y, T, T, d, sh, sh, False, True, lib.GEMM_LOWER_OUT),   # Q K^T
+        (lower, y, T, d, T, ss, sh, False, False, lib.GEMM_LOWER_A),  # P V, dS K
+        (lower, y, T, d, T, ss, sh, True, False, lib.GEMM_UPPER_A),   # P^T dO, dS^T Q
+    ]
+    for A, Bm, M, N, K, sA, sB, ta, tb, causal in cases:
+        full = torch.full((BH, M, N), float("nan"), device="cuda:0")
+        part = torch.full((BH, M, N), float("nan"), device="cuda:0")
+        lib.matmul_batched_strided(A, Bm, full, M, N, K, sA, sB, M * N, BH, ta, tb)
+        lib.matmul_batched_strided_causal(A, Bm, part, M, N, K, sA, sB, M * N, BH, ta, tb,
+                                          causal)
+        torch.cuda.synchronize()
+        if causal == lib.GEMM_LOWER_OUT:
+            i = torch.arange(M, device="cuda:0")
+            blk = (i[None, :] // 128) > (i[:, None] // 128)  # blocks wholly above the diagonal
+            assert torch.isnan(part[:, blk]).all(), "skipped blocks must stay unwritten"
+            assert torch.equal(part[:, ~blk], full[:, ~blk]), f"causal {causal}"
+        else:
+            assert torch.equal(part, full), f"causal {causal}"
+
+
+def test_materialized_equals_its_launch_sequence(lib):
+    """The materialised entry points equal, bitwise, their launch sequence run through the
+    public pieces (the causal GEMM and the softmax kernels), which is what bench.py times
+    launch by launch."""
+    B, H, T, d = 2, 3, 256, 64
+    q, k, v, do = (to_dev(x) for x in ref.seeded_inputs(B, H, T, d, seed=3))
+    scale = default_scale(d)
+    got = materialized(lib, *(x.cpu().numpy() for x in (q, k, v, do)), B, H, T, d, scale)
+    BH, sh, ss = B * H, T * d, T * T
+    sq = lambda: torch.full((BH * T, T), float("nan"), device="cuda:0")
+    scores, probs, dprobs, dscores = sq(), sq(), sq(), sq()
+    out, dq, dk, dv = (torch.empty_like(q) for _ in range(4))
+    gm = lib.matmul_batched_strided_causal
+    gm(q, k, scores, T, T, d, sh, sh, ss, BH, False, True, lib.GEMM_LOWER_OUT)
+    lib.causal_softmax_forward(scores, probs, B, H, T, scale)
+    gm(probs, v, out, T, d, T, ss, sh, sh, BH, False, False, lib.GEMM_LOWER_A)
+    gm(do, v, dprobs, T, T, d, sh, sh, ss, BH, False, True, lib.GEMM_LOWER_OUT)
+    gm(probs, do, dv, T, d, T, ss, sh, sh, BH, True, False, lib.GEMM_UPPER_A)
+    lib.causal_softmax_backward(dprobs, probs, dscores, B, H, T, scale)
+    gm(dscores, k, dq, T, d, T, ss, sh, sh, BH, False, False, lib.GEMM_LOWER_A)
+    gm(dscores, q, dk, T, d, T, ss, sh, sh, BH, True, False, lib.GEMM_UPPER_A)
+    torch.cuda.synchronize()
+    for name, t in (("o", out), ("dq", dq), ("dk", dk), ("dv", dv)):
+        assert np.array_equal(got[name], t.cpu().numpy()), name

@@ -24,6 +24,15 @@ if not os.path.exists(LIB_PATH):
     raise ImportError(
         f"{LIB_PATH} is not built; run __graft_entry__.build() (make -C transformer-cuda_amd)")
 
+# One HIP runtime per process.  torch bundles its own libamdhip64 (the same soname as the
+# system one this library links against): loaded after this library, it would come in as a
+# second runtime, whose device memory and streams this library's runtime does not see (its
+# launches then fail with hipErrorNoDevice).  torch first makes this library bind to torch's.
+try:
+    import torch  # noqa: F401
+except ImportError:  # no torch: the system runtime (C callers, the host-only tests)
+    pass
+
 _lib = ctypes.CDLL(LIB_PATH)
 
 STATUS = {
@@ -61,6 +70,8 @@ SIGNATURES = {
     "attn_gemm_device": [_P],
     "attn_matmul_batched_strided_f32_h":
         [_P, _P, _P, _P, _I, _I, _I, _L, _L, _L, _I, _I, _I, _F, _F, _P],
+    "attn_matmul_batched_strided_causal_f32":
+        [_P, _P, _P, _I, _I, _I, _L, _L, _L, _I, _I, _I, _I, _P],
     "attn_materialized_causal_forward_f32": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P],
     "attn_packed_causal_forward_f32": [_P, _P, _I, _I, _I, _I, _F, _P, _P, _P],
     "attn_packed_causal_backward_f32": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P],
@@ -302,6 +313,22 @@ def matmul_batched_strided(A, B, C, M, N, K, strideA, strideB, strideC, batch_co
                _ptr(C, f32, last * strideC + M * N, "C"), M, N, K, strideA, strideB, strideC,
                batch_count, int(bool(transA)), int(bool(transB)), float(alpha), float(beta),
                _stream(stream)), "matmul_batched_strided")
+
+
+GEMM_FULL, GEMM_LOWER_OUT, GEMM_LOWER_A, GEMM_UPPER_A = range(4)  # attn_gemm_causal
+
+
+def matmul_batched_strided_causal(A, B, C, M, N, K, strideA, strideB, strideC, batch_count,
+                                  transA, transB, causal, stream=None):
+    """matmul_batched_strided (alpha 1, beta 0) skipping what a causal structure makes unused
+    (attn_matmul_batched_strided_causal_f32: GEMM_LOWER_OUT, GEMM_LOWER_A, GEMM_UPPER_A)."""
+    f32 = _dt(False)
+    last = batch_count - 1
+    check(call("attn_matmul_batched_strided_causal_f32",
+               _ptr(A, f32, last * strideA + M * K, "A"), _ptr(B, f32, last * strideB + K * N, "B"),
+               _ptr(C, f32, last * strideC + M * N, "C"), M, N, K, strideA, strideB, strideC,
+               batch_count, int(bool(transA)), int(bool(transB)), int(causal), _stream(stream)),
+          "matmul_batched_strided_causal")
 
 
 def materialized_causal_attention_forward(q, k, v, scores, probs, out, B, H, T, d_head, scale,

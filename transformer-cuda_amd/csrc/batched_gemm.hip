@@ -142,11 +142,13 @@ __device__ __forceinline__ int op_off(int r, int kp) {
 }
 
 // WM waves along M, 4 / WM along N; each wave computes I x J MFMA blocks of 32 x 32.
+// tri (GemmTri): the causal structure the caller guarantees (k chunks of 16 and tiles of
+// 128 rows align with it, so a tile's k range is cut at chunk boundaries).
 template <bool TA, bool TB, int WM, int I, int J>
 __global__ __launch_bounds__(kThreads) void bgemm_f32_tiled_kernel(
     const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M,
     int N, int K, long long sA, long long sB, long long sC, float alpha, float beta,
-    int tiles_m, int tiles_n) {
+    int tiles_m, int tiles_n, int tri) {
     constexpr int WN = 4 / WM;
     constexpr int BM = 32 * I * WM, BN = 32 * J * WN;
     constexpr int kA4 = BM * kTK / 4 / kThreads;  // float4 of A per thread per chunk
@@ -157,8 +159,11 @@ __global__ __launch_bounds__(kThreads) void bgemm_f32_tiled_kernel(
     const long long id = blockIdx.x;
     const long long batch = id / tiles;
     const int t = static_cast<int>(id - batch * tiles);
-    const int m0 = (t / tiles_n) * BM;
+    // lower-triangular A: the last row blocks carry the longest k ranges, so they go first
+    const int mt = tri == kGemmLowerA ? tiles_m - 1 - t / tiles_n : t / tiles_n;
+    const int m0 = mt * BM;
     const int n0 = (t % tiles_n) * BN;
+    if (tri == kGemmLowerOut && n0 > m0 + BM - 1) return;  // the whole tile is above the diagonal
     const float* Ab = A + batch * sA;
     const float* Bb = B + batch * sB;
     float* Cb = C + batch * sC;
@@ -229,13 +234,18 @@ __global__ __launch_bounds__(kThreads) void bgemm_f32_tiled_kernel(
     for (int i = 0; i < I; ++i)
 #pragma unroll
         for (int j = 0; j < J; ++j) acc[i][j] = f32x16{};
-    const int nk = (K + kTK - 1) / kTK;
+    // k chunks kc0 .. nk-1: where op(A) is triangular, the chunks of its nonzero part only
+    int kc0 = 0, nk = (K + kTK - 1) / kTK;
+    if (tri == kGemmLowerA) nk = min(nk, (m0 + BM + kTK - 1) / kTK);
+    if (tri == kGemmUpperA) kc0 = min(nk, m0 / kTK);
     const int kh = lane >> 5;
     const int rl = lane & 31;
-    load(0);
-    store(0);
+    if (kc0 < nk) {
+        load(kc0 * kTK);
+        store(kc0 & 1);
+    }
     __syncthreads();
-    for (int kc = 0; kc < nk; ++kc) {
+    for (int kc = kc0; kc < nk; ++kc) {
         const int buf = kc & 1;
         if (kc + 1 < nk) load((kc + 1) * kTK);
         float a[I][8], b[J][8];
@@ -289,18 +299,20 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 
 template <bool TA, bool TB>
 void launch_tiled(const float* A, const float* B, float* C, int M, int N, int K, long long sA,
                   long long sB, long long sC, int batch, float alpha, float beta,
-                  hipStream_t stream) {
+                  hipStream_t stream, GemmTri tri) {
     const dim3 b(kThreads);
     if (N <= 64) {  // 128 x 64: each wave 32 x 64
         const int tm = (M + 127) / 128, tn = (N + 63) / 64;
         hipLaunchKernelGGL((bgemm_f32_tiled_kernel<TA, TB, 4, 1, 2>),
                            dim3(static_cast<unsigned>(static_cast<long long>(tm) * tn * batch)), b,
-                           0, stream, A, B, C, M, N, K, sA, sB, sC, alpha, beta, tm, tn);
+                           0, stream, A, B, C, M, N, K, sA, sB, sC, alpha, beta, tm, tn,
+                           static_cast<int>(tri));
     } else {  // 128 x 128: each wave 64 x 64
         const int tm = (M + 127) / 128, tn = (N + 127) / 128;
         hipLaunchKernelGGL((bgemm_f32_tiled_kernel<TA, TB, 2, 2, 2>),
                            dim3(static_cast<unsigned>(static_cast<long long>(tm) * tn * batch)), b,
-                           0, stream, A, B, C, M, N, K, sA, sB, sC, alpha, beta, tm, tn);
+                           0, stream, A, B, C, M, N, K, sA, sB, sC, alpha, beta, tm, tn,
+                           static_cast<int>(tri));
     }
 }
 
@@ -308,7 +320,8 @@ void launch_tiled(const float* A, const float* B, float* C, int M, int N, int K,
 
 void launch_batched_gemm_f32(const float* A, const float* B, float* C, int M, int N, int K,
                              long long sA, long long sB, long long sC, int batch, bool transA,
-                             bool transB, float alpha, float beta, hipStream_t stream) {
+                             bool transB, float alpha, float beta, hipStream_t stream,
+                             GemmTri tri) {
     // 16-byte loads need the contiguous dimension of each operand (K or M for A, N or K for
     // B) a multiple of 4 and 16-byte aligned bases and batch strides
     const bool vec = ((transA ? M : K) % 4 == 0) && ((transB ? K : N) % 4 == 0) &&
@@ -316,18 +329,23 @@ void launch_batched_gemm_f32(const float* A, const float* B, float* C, int M, in
     if (vec) {
         if (transA) {
             if (transB)
-                launch_tiled<true, true>(A, B, C, M, N, K, sA, sB, sC, batch, alpha, beta, stream);
+                launch_tiled<true, true>(A, B, C, M, N, K, sA, sB, sC, batch, alpha, beta, stream,
+                                         tri);
             else
-                launch_tiled<true, false>(A, B, C, M, N, K, sA, sB, sC, batch, alpha, beta, stream);
+                launch_tiled<true, false>(A, B, C, M, N, K, sA, sB, sC, batch, alpha, beta, stream,
+                                          tri);
         } else {
             if (transB)
-                launch_tiled<false, true>(A, B, C, M, N, K, sA, sB, sC, batch, alpha, beta, stream);
+                launch_tiled<false, true>(A, B, C, M, N, K, sA, sB, sC, batch, alpha, beta, stream,
+                                          tri);
             else
                 launch_tiled<false, false>(A, B, C, M, N, K, sA, sB, sC, batch, alpha, beta,
-                                           stream);
+                                           stream, tri);
         }
         return;
     }
+    // the scalar kernel computes every product in full (tri only skips exact zeros or
+    // unread outputs, so the full product is always a valid result)
     const int tiles_m = (M + kBM - 1) / kBM;
     const int tiles_n = (N + kBN - 1) / kBN;
     const long long grid = static_cast<long long>(tiles_m) * tiles_n * batch;

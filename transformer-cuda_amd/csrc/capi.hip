@@ -754,6 +754,27 @@ int attn_matmul_batched_strided_f32(const float* A, const float* B, float* C, in
     return launch_status();
 }
 
+int attn_matmul_batched_strided_causal_f32(const float* A, const float* B, float* C, int M,
+                                           int N, int K, long long strideA, long long strideB,
+                                           long long strideC, int batch_count, int transA,
+                                           int transB, int causal, hipStream_t stream) {
+    if (A == nullptr || B == nullptr || C == nullptr) return ATTN_ERROR_NULL_POINTER;
+    if (causal < ATTN_GEMM_FULL || causal > ATTN_GEMM_UPPER_A) return ATTN_ERROR_INVALID_VALUE;
+    if (causal == ATTN_GEMM_LOWER_OUT && M != N) return ATTN_ERROR_INVALID_DIM;
+    if ((causal == ATTN_GEMM_LOWER_A || causal == ATTN_GEMM_UPPER_A) && M != K)
+        return ATTN_ERROR_INVALID_DIM;
+    if (M <= 0 || N <= 0 || K <= 0) return ATTN_ERROR_INVALID_DIM;
+    if (batch_count <= 0 || strideA < 0 || strideB < 0 || strideC < 0)
+        return ATTN_ERROR_INVALID_VALUE;
+    const int64_t tiles = ((static_cast<int64_t>(M) + 63) / 64) * ((static_cast<int64_t>(N) + 63) / 64);
+    if (tiles * batch_count > kInt32Max) return ATTN_ERROR_INVALID_DIM;
+    clear_error();
+    tcamd::launch_batched_gemm_f32(A, B, C, M, N, K, strideA, strideB, strideC, batch_count,
+                                   transA != 0, transB != 0, 1.0f, 0.0f, stream,
+                                   static_cast<tcamd::GemmTri>(causal));
+    return launch_status();
+}
+
 struct attn_gemm_context {
     int device;
 };
@@ -804,14 +825,15 @@ int attn_materialized_causal_forward_f32(const float* q, const float* k, const f
     const int BH = B * H;
     const long long sh = static_cast<long long>(T) * d_head, ss = static_cast<long long>(T) * T;
     clear_error();
-    // src/model.cu:314-320: scores = Q K^T (alpha 1; the scale is applied in the softmax)
+    // src/model.cu:314-320: scores = Q K^T (alpha 1; the scale is applied in the softmax).
+    // The causal softmax reads only j <= i: tiles wholly above the diagonal are not computed.
     tcamd::launch_batched_gemm_f32(q, k, scores, T, T, d_head, sh, sh, ss, BH, false, true,
-                                   1.0f, 0.0f, stream);
+                                   1.0f, 0.0f, stream, tcamd::kGemmLowerOut);
     tcamd::launch_causal_softmax_fwd_f32(scores, probs, static_cast<int64_t>(BH) * T, T, scale,
                                          stream);
-    // src/model.cu:326-332: out = probs V
+    // src/model.cu:326-332: out = probs V (probs is zero above the diagonal)
     tcamd::launch_batched_gemm_f32(probs, v, out, T, d_head, T, ss, sh, sh, BH, false, false,
-                                   1.0f, 0.0f, stream);
+                                   1.0f, 0.0f, stream, tcamd::kGemmLowerA);
     return launch_status();
 }
 
@@ -829,20 +851,20 @@ int attn_materialized_causal_backward_f32(const float* q, const float* k, const 
     const int BH = B * H;
     const long long sh = static_cast<long long>(T) * d_head, ss = static_cast<long long>(T) * T;
     clear_error();
-    // src/model.cu:618-623: dprobs = dO V^T
+    // src/model.cu:618-623: dprobs = dO V^T (the softmax backward reads only j <= i)
     tcamd::launch_batched_gemm_f32(dout, v, dprobs, T, T, d_head, sh, sh, ss, BH, false, true,
-                                   1.0f, 0.0f, stream);
-    // :626-631: dv = probs^T dO
+                                   1.0f, 0.0f, stream, tcamd::kGemmLowerOut);
+    // :626-631: dv = probs^T dO (probs^T is zero below the diagonal)
     tcamd::launch_batched_gemm_f32(probs, dout, dv, T, d_head, T, ss, sh, sh, BH, true, false,
-                                   1.0f, 0.0f, stream);
-    // :634: dscores = softmax backward (scale inside)
+                                   1.0f, 0.0f, stream, tcamd::kGemmUpperA);
+    // :634: dscores = softmax backward (scale inside; zero above the diagonal)
     tcamd::launch_causal_softmax_bwd_f32(dprobs, probs, dscores, static_cast<int64_t>(BH) * T,
                                          T, scale, stream);
     // :637-642: dq = dscores K;  :644-649: dk = dscores^T Q
     tcamd::launch_batched_gemm_f32(dscores, k, dq, T, d_head, T, ss, sh, sh, BH, false, false,
-                                   1.0f, 0.0f, stream);
+                                   1.0f, 0.0f, stream, tcamd::kGemmLowerA);
     tcamd::launch_batched_gemm_f32(dscores, q, dk, T, d_head, T, ss, sh, sh, BH, true, false,
-                                   1.0f, 0.0f, stream);
+                                   1.0f, 0.0f, stream, tcamd::kGemmUpperA);
     return launch_status();
 }
 

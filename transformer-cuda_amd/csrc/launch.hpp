@@ -31,10 +31,24 @@ void launch_causal_softmax_fwd_f32(const float* scores, float* probs, int64_t ro
 void launch_causal_softmax_bwd_f32(const float* dprobs, const float* probs, float* dscores,
                                    int64_t rows, int T, float scale, hipStream_t stream);
 
+// Causal structure a batched GEMM may exploit (the materialised attention's contractions;
+// the public matmul_batched_strided always computes the full product):
+//   kGemmFull     the full product;
+//   kGemmLowerOut C is needed only at col <= row (S = QK^T, dP = dO V^T, read only by the
+//                 causal softmax): output tiles wholly above the diagonal are not written;
+//   kGemmLowerA   op(A)[m][k] = 0 for k > m (A = P or dS, whose upper triangle the softmax
+//                 writes as zeros): the k loop of a tile stops after its last row;
+//   kGemmUpperA   op(A)[m][k] = 0 for k < m (op(A) = P^T or dS^T): the k loop of a tile
+//                 starts at its first row.
+// Skipped terms are exact zeros, so for finite inputs the results equal the full product's.
+// (The same values as attn_gemm_causal of the C ABI.)
+enum GemmTri { kGemmFull = 0, kGemmLowerOut = 1, kGemmLowerA = 2, kGemmUpperA = 3 };
+
 // Row-major strided-batched C = alpha*op(A)*op(B) + beta*C, C (M x N) with ldc = N.
 void launch_batched_gemm_f32(const float* A, const float* B, float* C, int M, int N, int K,
                              long long sA, long long sB, long long sC, int batch, bool transA,
-                             bool transB, float alpha, float beta, hipStream_t stream);
+                             bool transB, float alpha, float beta, hipStream_t stream,
+                             GemmTri tri = kGemmFull);
 
 void launch_dot_do_o_f32(const float* dO, const float* O, float* D, int64_t rows, int d,
                          hipStream_t stream);

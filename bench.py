@@ -152,6 +152,9 @@ def parse_args():
                          "mode (0 skips it)")
     ap.add_argument("--gpt-modes", default="fused_x3,fused,tiled_split,materialized",
                     help="attention modes of the training-step measurement (comma separated)")
+    ap.add_argument("--materialized-only", action="store_true",
+                    help="instead of the bench: only the materialised mode's timed launches "
+                         "(config 2, fp32; the secondary line's measurement), one JSON line")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="instead of the bench: run 10 plain device copies of MIB MiB (the "
                          "known-size kernel that scales rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -696,6 +699,9 @@ def main():
     if args.copy_calibration:
         return copy_calibration(args.copy_calibration)
     lib = load_lib()
+    if args.materialized_only:
+        print(json.dumps(materialized(lib, args.steps, args.seed)), flush=True)
+        return 0
     B, H, T, d, cdt, qk = CONFIGS[args.config]
     dtype = args.dtype or cdt
     path = args.path or ("x3" if dtype == "f32" and d <= 64 else "packed")

@@ -540,6 +540,11 @@ def secondary(lib, cfg, dtype, steps, seed, path="packed", ramp_s=0.0, cpu_s=0.0
     return out
 
 
+# The materialised entry points run the softmax with zero_block 128: the products read a
+# probability row only up to the end of its 128-column diagonal block.
+MAT_ZERO_BLOCK = 128
+
+
 def materialized(lib, steps, seed):
     """The reference's materialised mode (src/model.cu:313-332 forward, 617-650 backward) at
     config 2 fp32, launch by launch as attn_materialized_causal_{forward,backward}_f32 run it:
@@ -549,7 +554,8 @@ def materialized(lib, steps, seed):
     with the longest average, a GEMM, against the fp32 MFMA peak with its algorithmic work
     (one unit B*H*T^2*d: the causal half of the full product); the softmax kernels' rates
     are HBM rates of the bytes they must move (forward: the causal half of S read, P written
-    in full; backward: the causal halves of dP and P read, dS written in full)."""
+    where the products read it, up to the end of each row's 128-column diagonal block;
+    backward: the causal halves of dP and P read, dS written likewise)."""
     import torch
     B, H, T, d, _, _ = CONFIGS["c2"]
     g = torch.Generator(device="cpu").manual_seed(seed)
@@ -564,12 +570,13 @@ def materialized(lib, steps, seed):
         lambda: L.matmul_batched_strided_causal(A, Bm, C, M, N, K, sA, sB, sC, BH, ta, tb, tri))
     launches = [
         ("gemm_qk", gemm(q, k, scores, T, T, d, sh, sh, ss, False, True, L.GEMM_LOWER_OUT)),
-        ("softmax_fwd", lambda: L.causal_softmax_forward(scores, probs, B, H, T, scale)),
+        ("softmax_fwd", lambda: L.causal_softmax_forward(scores, probs, B, H, T, scale,
+                                                         zero_block=MAT_ZERO_BLOCK)),
         ("gemm_pv", gemm(probs, v, out, T, d, T, ss, sh, sh, False, False, L.GEMM_LOWER_A)),
         ("gemm_dp", gemm(do, v, dprobs, T, T, d, sh, sh, ss, False, True, L.GEMM_LOWER_OUT)),
         ("gemm_dv", gemm(probs, do, dv, T, d, T, ss, sh, sh, True, False, L.GEMM_UPPER_A)),
         ("softmax_bwd", lambda: L.causal_softmax_backward(dprobs, probs, dscores, B, H, T,
-                                                          scale)),
+                                                          scale, zero_block=MAT_ZERO_BLOCK)),
         ("gemm_dq", gemm(dscores, k, dq, T, d, T, ss, sh, sh, False, False, L.GEMM_LOWER_A)),
         ("gemm_dk", gemm(dscores, q, dk, T, d, T, ss, sh, sh, True, False, L.GEMM_UPPER_A)),
     ]
@@ -597,8 +604,9 @@ def materialized(lib, steps, seed):
     torch.cuda.synchronize()
     unit = float(B * H * T * T * d)
     half = B * H * T * (T + 1) / 2.0 * 4  # bytes of the causal half of one T x T matrix set
-    full = B * H * T * T * 4.0
-    alg = {"softmax_fwd": (half + full, "byte"), "softmax_bwd": (2 * half + full, "byte")}
+    zb = MAT_ZERO_BLOCK  # bytes written: row i up to min(T, (i // zb + 1) * zb)
+    blk = B * H * 4.0 * sum(min(T, (i // zb + 1) * zb) for i in range(T))
+    alg = {"softmax_fwd": (half + blk, "byte"), "softmax_bwd": (2 * half + blk, "byte")}
     kernels = {}
     for j, (name, _) in enumerate(launches):
         t = sum(ev[i][j].elapsed_time(ev[i][j + 1]) for i in range(steps)) / steps

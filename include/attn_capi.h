@@ -114,6 +114,18 @@ int attn_causal_softmax_forward_f32(const float* scores, float* probs, int B, in
 /* Replaces causal_softmax_backward, include/kernels/attention.cuh:80-89. */
 int attn_causal_softmax_backward_f32(const float* dprobs, const float* probs, float* dscores,
                                      int B, int H, int T, float scale, hipStream_t stream);
+/* No counterpart in the reference: the two softmax passes above with the zeros above the
+ * diagonal written only up to the end of the zero_block-column block that holds the diagonal,
+ * min(T, (i / zero_block + 1) * zero_block); the rest of each row is left as it was.  The
+ * materialised attention entry points below run them with zero_block = 128, where their
+ * products stop reading.  zero_block = 0 writes the whole suffix (as the functions above);
+ * ATTN_ERROR_INVALID_VALUE unless zero_block is 0 or a positive multiple of 4. */
+int attn_causal_softmax_forward_blocked_f32(const float* scores, float* probs, int B, int H,
+                                            int T, float scale, int zero_block,
+                                            hipStream_t stream);
+int attn_causal_softmax_backward_blocked_f32(const float* dprobs, const float* probs,
+                                             float* dscores, int B, int H, int T, float scale,
+                                             int zero_block, hipStream_t stream);
 
 /* ------------------------------------------------------------------------------------------
  * Materialised path: strided-batched fp32 GEMM (v_mfma_f32_32x32x2_f32) and the reference's
@@ -181,8 +193,10 @@ int attn_matmul_batched_strided_f32_h(attn_gemm_handle handle, const float* A, c
  * The contractions skip what the causal mask makes unused: scores is written where j <= i
  * (and in the rest of each 128 x 128 block that crosses the diagonal; blocks wholly above it
  * are left as they were, and the softmax never reads them), and out = probs V runs over
- * the nonzero part of probs only.  probs is written in full (zeros above the diagonal), and
- * out equals the full product's for finite inputs. */
+ * the nonzero part of probs only.  probs is written where j <= i and, as zeros, in the rest
+ * of each 128 x 128 block that crosses the diagonal (the softmax with zero_block = 128); the
+ * blocks wholly above the diagonal are left as they were, and nothing reads them.  out equals
+ * the full product's for finite inputs. */
 int attn_materialized_causal_forward_f32(const float* q, const float* k, const float* v,
                                          float* scores, float* probs, float* out, int B, int H,
                                          int T, int d_head, float scale, hipStream_t stream);
@@ -190,8 +204,9 @@ int attn_materialized_causal_forward_f32(const float* q, const float* k, const f
 /* The reference's materialised backward (src/model.cu:617-650): dprobs = dO V^T,
  * dv = probs^T dO, dscores = causal_softmax_backward(dprobs, probs, scale), dq = dscores K,
  * dk = dscores^T Q.  dprobs and dscores are (B*H*T, T) scratch; dq, dk, dv are overwritten.
- * As in the forward, dprobs is written only in the 128 x 128 blocks at or below the
- * diagonal, and the four products with probs or dscores run over their nonzero parts. */
+ * As in the forward, dprobs and dscores are written only in the 128 x 128 blocks at or
+ * below the diagonal (dscores with zeros above the diagonal inside them), and the four
+ * products with probs or dscores run over their nonzero parts. */
 int attn_materialized_causal_backward_f32(const float* q, const float* k, const float* v,
                                           const float* probs, const float* dout, float* dprobs,
                                           float* dscores, float* dq, float* dk, float* dv,

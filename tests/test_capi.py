@@ -98,6 +98,13 @@ def test_split_and_softmax_validation(lib):
                     None) == NULLPTR
     assert lib.call("attn_causal_softmax_backward_f32", FAKE, FAKE, FAKE, 1, 1, 4,
                     f(float("nan")), None) == BAD_VALUE
+    for zb in (-1, 6):
+        assert lib.call("attn_causal_softmax_forward_blocked_f32", FAKE, FAKE, 1, 1, 4, f(1.0),
+                        zb, None) == BAD_VALUE
+    assert lib.call("attn_causal_softmax_backward_blocked_f32", FAKE, None, FAKE, 1, 1, 4,
+                    f(1.0), 128, None) == NULLPTR
+    assert lib.call("attn_causal_softmax_backward_blocked_f32", FAKE, FAKE, FAKE, 1, 0, 4,
+                    f(1.0), 128, None) == INVALID_DIM
     assert lib.call("attn_head_merge_transpose_forward_f32", FAKE, FAKE, 0, 1, 4, 8,
                     None) == INVALID_DIM
 

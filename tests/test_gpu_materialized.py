@@ -64,13 +64,15 @@ def test_gemm_vs_fp64(lib, M, N, K, ta, tb):
 
 
 @pytest.mark.parametrize("M,N,K", [(4, 4, 4), (100, 68, 132), (260, 64, 1024), (132, 200, 36),
-                                   (512, 516, 64), (36, 8, 20)])
+                                   (512, 516, 64), (36, 8, 20), (100, 200, 48), (36, 8, 16),
+                                   (300, 60, 160)])
 @pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
 @pytest.mark.parametrize("pad", [0, 4])
 def test_gemm_vectorized_vs_fp64(lib, M, N, K, ta, tb, pad):
     """Operands whose contiguous dimension is a multiple of 4 elements, with 16-byte aligned
-    batch strides, take the 16-byte-load kernel (128 x 128 tiles, or 128 x 64 for N <= 64):
-    ragged against both tile shapes, every transpose combination, packed and padded batches."""
+    batch strides, take the 16-byte-load kernels (128 x 128 tiles, or 128 x 64 for N <= 64),
+    the copy-pipelined one where K is a multiple of 16: ragged against both tile shapes, every
+    transpose combination, packed and padded batches."""
     rng = np.random.default_rng(M * 7919 + N * 31 + K + 2 * ta + tb + pad)
     batch = 3
     sA, sB, sC = M * K + pad, K * N + pad, M * N + pad
@@ -124,7 +126,12 @@ def test_materialized_vs_oracle(lib, B, H, T, d):
     for name in ("o", "dq", "dk", "dv"):
         err = max_abs(got[name], getattr(want, name).numpy())
         assert err <= 1e-5, f"{name}: max-abs {err:.3e}"
-    assert np.all(got["probs"][..., np.triu(np.ones((T, T), bool), 1)] == 0)
+    # probs: zeros above the diagonal up to the end of its 128-column block, untouched after
+    i = np.arange(T)
+    inside = i[None, :] < np.minimum((i[:, None] // 128 + 1) * 128, T)
+    upper = np.triu(np.ones((T, T), bool), 1)
+    assert np.all(got["probs"][..., upper & inside] == 0)
+    assert np.isnan(got["probs"][..., ~inside]).all()
 
 
 def test_materialized_config2_vs_oracle_and_tiled(lib):
@@ -181,8 +188,8 @@ def test_causal_gemm_equals_full_product(lib, T, d):
 
 def test_materialized_equals_its_launch_sequence(lib):
     """The materialised entry points equal, bitwise, their launch sequence run through the
-    public pieces (the causal GEMM and the softmax kernels), which is what bench.py times
-    launch by launch."""
+    public pieces (the causal GEMM and the softmax kernels with zero_block 128), which is what
+    bench.py times launch by launch."""
     B, H, T, d = 2, 3, 256, 64
     q, k, v, do = (to_dev(x) for x in ref.seeded_inputs(B, H, T, d, seed=3))
     scale = default_scale(d)
@@ -193,11 +200,11 @@ def test_materialized_equals_its_launch_sequence(lib):
     out, dq, dk, dv = (torch.empty_like(q) for _ in range(4))
     gm = lib.matmul_batched_strided_causal
     gm(q, k, scores, T, T, d, sh, sh, ss, BH, False, True, lib.GEMM_LOWER_OUT)
-    lib.causal_softmax_forward(scores, probs, B, H, T, scale)
+    lib.causal_softmax_forward(scores, probs, B, H, T, scale, zero_block=128)
     gm(probs, v, out, T, d, T, ss, sh, sh, BH, False, False, lib.GEMM_LOWER_A)
     gm(do, v, dprobs, T, T, d, sh, sh, ss, BH, False, True, lib.GEMM_LOWER_OUT)
     gm(probs, do, dv, T, d, T, ss, sh, sh, BH, True, False, lib.GEMM_UPPER_A)
-    lib.causal_softmax_backward(dprobs, probs, dscores, B, H, T, scale)
+    lib.causal_softmax_backward(dprobs, probs, dscores, B, H, T, scale, zero_block=128)
     gm(dscores, k, dq, T, d, T, ss, sh, sh, BH, False, False, lib.GEMM_LOWER_A)
     gm(dscores, q, dk, T, d, T, ss, sh, sh, BH, True, False, lib.GEMM_UPPER_A)
     torch.cuda.synchronize()

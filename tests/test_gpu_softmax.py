@@ -62,3 +62,28 @@ def test_odd_T_scalar_path_and_offset_pointer(lib):
     torch.cuda.synchronize()
     np.testing.assert_allclose(out[1:].cpu().numpy(), co.causal_softmax_fwd(s, B, H, T, 1.0),
                                atol=2e-7)
+
+
+@pytest.mark.parametrize("T,zb", [(300, 128), (1024, 128), (2052, 128), (13, 4), (64, 8)])
+def test_blocked_zeros(lib, T, zb):
+    """zero_block: the written part of every row equals the full-suffix pass bitwise, the
+    zeros stop at the end of the zero_block-column block holding the diagonal, and the rest of
+    the row keeps what was there (register and streaming paths, vector and scalar rows)."""
+    B, H = 1, 2
+    rng = np.random.default_rng(T + zb)
+    sg = to_dev((rng.standard_normal((B, H, T, T)) * 3).astype(np.float32))
+    dpg = to_dev(rng.standard_normal((B, H, T, T)).astype(np.float32))
+    scale = 0.37
+    p_full, ds_full = torch.empty_like(sg), torch.empty_like(sg)
+    lib.causal_softmax_forward(sg, p_full, B, H, T, scale)
+    lib.causal_softmax_backward(dpg, p_full, ds_full, B, H, T, scale)
+    p_blk = torch.full_like(sg, float("nan"))
+    ds_blk = torch.full_like(sg, float("nan"))
+    lib.causal_softmax_forward(sg, p_blk, B, H, T, scale, zero_block=zb)
+    lib.causal_softmax_backward(dpg, p_full, ds_blk, B, H, T, scale, zero_block=zb)
+    torch.cuda.synchronize()
+    i = torch.arange(T, device="cuda:0")
+    written = i[None, :] < torch.clamp((i[:, None] // zb + 1) * zb, max=T)
+    for full, blk in ((p_full, p_blk), (ds_full, ds_blk)):
+        assert torch.equal(blk[..., written], full[..., written])
+        assert torch.isnan(blk[..., ~written]).all()

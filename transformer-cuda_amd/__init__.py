@@ -63,6 +63,8 @@ SIGNATURES = {
     "attn_head_merge_transpose_backward_f32": [_P, _P, _I, _I, _I, _I, _P],
     "attn_causal_softmax_forward_f32": [_P, _P, _I, _I, _I, _F, _P],
     "attn_causal_softmax_backward_f32": [_P, _P, _P, _I, _I, _I, _F, _P],
+    "attn_causal_softmax_forward_blocked_f32": [_P, _P, _I, _I, _I, _F, _I, _P],
+    "attn_causal_softmax_backward_blocked_f32": [_P, _P, _P, _I, _I, _I, _F, _I, _P],
     "attn_matmul_batched_strided_f32":
         [_P, _P, _P, _I, _I, _I, _L, _L, _L, _I, _I, _I, _F, _F, _P],
     "attn_gemm_create": [_P],
@@ -283,22 +285,35 @@ def head_merge_transpose_backward(dout, din, B, H, T, d_head, stream=None):
           "head_merge_transpose_backward")
 
 
-def causal_softmax_forward(scores, probs, B, H, T, scale, stream=None):
-    """Reference: include/kernels/attention.cuh:21-31."""
+def causal_softmax_forward(scores, probs, B, H, T, scale, stream=None, zero_block=None):
+    """Reference: include/kernels/attention.cuh:21-31.  zero_block (no counterpart in the
+    reference): write the zeros above the diagonal only up to the end of the zero_block-column
+    block that holds it (attn_causal_softmax_forward_blocked_f32)."""
     n = B * H * T * T
     f32 = _dt(False)
-    check(call("attn_causal_softmax_forward_f32", _ptr(scores, f32, n, "scores"),
-               _ptr(probs, f32, n, "probs"), B, H, T, float(scale), _stream(stream)),
-          "causal_softmax_forward")
+    args = (_ptr(scores, f32, n, "scores"), _ptr(probs, f32, n, "probs"), B, H, T, float(scale))
+    if zero_block is None:
+        check(call("attn_causal_softmax_forward_f32", *args, _stream(stream)),
+              "causal_softmax_forward")
+    else:
+        check(call("attn_causal_softmax_forward_blocked_f32", *args, int(zero_block),
+                   _stream(stream)), "causal_softmax_forward_blocked")
 
 
-def causal_softmax_backward(dprobs, probs, dscores, B, H, T, scale, stream=None):
-    """Reference: include/kernels/attention.cuh:80-89."""
+def causal_softmax_backward(dprobs, probs, dscores, B, H, T, scale, stream=None,
+                            zero_block=None):
+    """Reference: include/kernels/attention.cuh:80-89.  zero_block as in
+    causal_softmax_forward (attn_causal_softmax_backward_blocked_f32)."""
     n = B * H * T * T
     f32 = _dt(False)
-    check(call("attn_causal_softmax_backward_f32", _ptr(dprobs, f32, n, "dprobs"),
-               _ptr(probs, f32, n, "probs"), _ptr(dscores, f32, n, "dscores"), B, H, T,
-               float(scale), _stream(stream)), "causal_softmax_backward")
+    args = (_ptr(dprobs, f32, n, "dprobs"), _ptr(probs, f32, n, "probs"),
+            _ptr(dscores, f32, n, "dscores"), B, H, T, float(scale))
+    if zero_block is None:
+        check(call("attn_causal_softmax_backward_f32", *args, _stream(stream)),
+              "causal_softmax_backward")
+    else:
+        check(call("attn_causal_softmax_backward_blocked_f32", *args, int(zero_block),
+                   _stream(stream)), "causal_softmax_backward_blocked")
 
 
 def matmul_batched_strided(A, B, C, M, N, K, strideA, strideB, strideC, batch_count, transA,

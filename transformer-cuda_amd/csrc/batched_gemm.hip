@@ -20,13 +20,20 @@
 // materialised attention with d_head % 4 == 0 and T % 4 == 0), a second kernel runs: each
 // wave computes 64 x 64 of C as 2 x 2 MFMA blocks (every LDS operand read feeds two MFMAs)
 // in a 128 x 128 workgroup tile, or 32 x 64 in a 128 x 64 tile for N <= 64, and global loads
-// move 16 bytes per lane.
+// move 16 bytes per lane.  Where K is also a multiple of 16 (every materialised attention
+// call with d_head % 16 == 0 and T % 16 == 0), the copy-pipelined kernel below replaces it:
+// operand tiles go HBM -> LDS directly with up to three k chunks in flight, workgroups are
+// laid out so that each XCD works through a contiguous range of tiles, and the causal forms
+// enumerate only the tiles the mask leaves (square output) or pair long and short row tiles
+// (triangular A, 64 x 64 tiles).
 #include <stdint.h>
 
 #include <type_traits>
 
 #include "device_common.hpp"
 #include "launch.hpp"
+#include "lds_dma.hpp"
+#include "sched.hpp"
 
 namespace tcamd {
 namespace {
@@ -39,7 +46,7 @@ template <bool TA, bool TB>
 __global__ __launch_bounds__(kThreads) void bgemm_f32_kernel(
     const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M,
     int N, int K, long long sA, long long sB, long long sC, float alpha, float beta,
-    int tiles_m, int tiles_n) {
+    int tiles_m, int tiles_n, int tri) {
     __shared__ float As[2][kBK][kBM + kPad];
     __shared__ float Bs[2][kBK][kBN + kPad];
     const long long tiles = static_cast<long long>(tiles_m) * tiles_n;
@@ -95,14 +102,19 @@ __global__ __launch_bounds__(kThreads) void bgemm_f32_kernel(
     };
 
     f32x16 acc = f32x16{};
-    const int nk = (K + kBK - 1) / kBK;
-    load(0);
-    store(0);
+    // k chunks kc0 .. nk-1: where op(A) is triangular, the chunks of its nonzero part only
+    int kc0 = 0, nk = (K + kBK - 1) / kBK;
+    if (tri == kGemmLowerA) nk = min(nk, (m0 + kBM + kBK - 1) / kBK);
+    if (tri == kGemmUpperA) kc0 = min(nk, m0 / kBK);
+    if (kc0 < nk) {
+        load(kc0 * kBK);
+        store(kc0 & 1);
+    }
     __syncthreads();
     const int ar = 32 * wm + (lane & 31);
     const int bc = 32 * wn + (lane & 31);
     const int kh = lane >> 5;
-    for (int kc = 0; kc < nk; ++kc) {
+    for (int kc = kc0; kc < nk; ++kc) {
         const int buf = kc & 1;
         if (kc + 1 < nk) load((kc + 1) * kBK);
 #pragma unroll
@@ -294,13 +306,225 @@ __global__ __launch_bounds__(kThreads) void bgemm_f32_tiled_kernel(
     }
 }
 
+// ---------------------------------------------------------------------------------------
+// Copy-pipelined kernel (K % 16 == 0, 16-byte loads).  The operand tiles of a k chunk go
+// HBM -> LDS with global_load_lds_dwordx4, S chunks in flight, so the HBM latency of a chunk
+// is covered by the MFMA work of the S - 1 chunks before it instead of one.  A copy writes
+// 1 KB of LDS contiguously (lane i: bytes 16i ..), so the layout is chosen by which global
+// 16 bytes each lane fetches:
+//   * k-contiguous operand (row form): row r of the tile holds its 16 k as four 16-byte
+//     chunks, chunk c at slot c ^ ((r / 4) % 4); lane (r, kh) reads chunks 2kh, 2kh + 1
+//     (k = 8kh .. 8kh + 7) with two 16-byte reads, 16 rows of a read on distinct banks;
+//   * row-contiguous operand (k form): k-row k of the tile holds R floats, 16-byte chunk c
+//     at slot c ^ (8 * ((k / 8) % 2)); lane (r, kh) reads k = 8kh + s at step s, 4 bytes,
+//     the two lane halves on the two halves of the banks.
+// MFMA step s contracts k = s (lanes 0-31) and k = 8 + s (lanes 32-63) of the chunk.
+// Rows past M (or N) are fetched from the last valid row (or 4-column group): they only feed
+// outputs that are not stored.
+// ---------------------------------------------------------------------------------------
+template <bool KC, int R>
+__device__ __forceinline__ void dma_operand(const float* base, int ld, int r0, int rlim, int k0,
+                                            uint32_t lds, int wave, int lane) {
+    constexpr int kInst = R * kTK * 4 / 1024;
+    static_assert(kInst % (kThreads / kWave) == 0, "copies split evenly over the waves");
+#pragma unroll
+    for (int i = wave; i < kInst; i += kThreads / kWave) {
+        const int p = i * kWave + lane;  // 16-byte slot of the tile
+        uint32_t voff;
+        if constexpr (KC) {
+            const int r = p >> 2;
+            const int c = (p & 3) ^ ((r >> 2) & 3);
+            const int rr = min(r0 + r, rlim - 1);
+            voff = static_cast<uint32_t>((static_cast<long long>(rr) * ld + k0 + 4 * c) * 4);
+        } else {
+            constexpr int kCpr = R / 4;  // chunks per k-row
+            const int k = p / kCpr;
+            const int c = (p % kCpr) ^ (((k >> 3) & 1) << 3);
+            const int rr = min(r0 + 4 * c, rlim - 4);
+            voff = static_cast<uint32_t>((static_cast<long long>(k0 + k) * ld + rr) * 4);
+        }
+        dma_dwordx4(base, lds + static_cast<uint32_t>(i) * 1024u, voff);
+    }
+}
+
+// Lane (rl, kh)'s eight k of 32-row block `blk` of an operand tile at LDS float address t:
+// x[s] = element (32 blk + rl, 8kh + s).
+template <bool KC, int R>
+__device__ __forceinline__ void read_operand(const float* t, int blk, int rl, int kh,
+                                             float (&x)[8]) {
+    const int r = 32 * blk + rl;
+    if constexpr (KC) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int c = 2 * kh + h;
+            const f32x4 v = *reinterpret_cast<const f32x4*>(t + r * kTK + ((c ^ ((r >> 2) & 3)) << 2));
+#pragma unroll
+            for (int e = 0; e < 4; ++e) x[4 * h + e] = v[e];
+        }
+    } else {
+        const int rs = r ^ (kh << 5);  // chunk slot swizzle 8 * kh, in floats
+#pragma unroll
+        for (int s = 0; s < 8; ++s) x[s] = t[(8 * kh + s) * R + rs];
+    }
+}
+
+// Jobs: a batch's jobs are its (row tile, column tile) pairs, row-major, except that
+//   * TRI (ATTN lower-triangular output, square tiles): only the tiles at or below the
+//     diagonal, (0,0), (1,0), (1,1), (2,0), ...;
+//   * PAIR (for a triangular A): job (p, nt) computes row tiles tiles_m - 1 - p and p one
+//     after the other (p < tiles_m / 2, and the middle row tile of an odd count alone), so
+//     that every job covers the same number of k chunks.
+// The dispatcher deals workgroups to the 8 XCDs round-robin; workgroup w runs job
+// (w % 8) * per + w / 8 (per = the grid / 8), so each XCD works through one contiguous
+// eighth of the jobs and its L2 serves the operand tiles those jobs share.
+template <bool TA, bool TB, int WM, int I, int J, int S, bool PAIR, bool TRI>
+__global__ __launch_bounds__(kThreads) void bgemm_f32_dma_kernel(
+    const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M,
+    int N, int K, long long sA, long long sB, long long sC, float alpha, float beta,
+    int tiles_m, int tiles_n, int tri, long long jobs) {
+    constexpr int WN = 4 / WM;
+    constexpr int BM = 32 * I * WM, BN = 32 * J * WN;
+    constexpr int kA = BM * kTK, kB = BN * kTK;  // floats of each operand per stage
+    constexpr bool KA = !TA, KB = TB;            // k-contiguous in memory
+    __shared__ __attribute__((aligned(1024))) float lds[S][kA + kB];
+    const long long per = gridDim.x / kXcds;
+    const long long job = (blockIdx.x % kXcds) * per + blockIdx.x / kXcds;
+    if (job >= jobs) return;
+    const int rows = PAIR ? (tiles_m + 1) / 2 : tiles_m;
+    const long long tiles = TRI ? static_cast<long long>(tiles_m) * (tiles_m + 1) / 2
+                                : static_cast<long long>(rows) * tiles_n;
+    const long long batch = job / tiles;
+    const int t = static_cast<int>(job - batch * tiles);
+    int p, nt;
+    if constexpr (TRI) {  // t = p (p + 1) / 2 + nt, nt <= p
+        p = static_cast<int>((sqrtf(8.0f * t + 1.0f) - 1.0f) * 0.5f);
+        while (p * (p + 1) / 2 > t) --p;
+        while ((p + 1) * (p + 2) / 2 <= t) ++p;
+        nt = t - p * (p + 1) / 2;
+    } else {
+        p = t / tiles_n;
+        nt = t % tiles_n;
+    }
+    const int n0 = nt * BN;
+    const float* Ab = A + batch * sA;
+    const float* Bb = B + batch * sB;
+    float* Cb = C + batch * sC;
+    const int lda = TA ? M : K;
+    const int ldb = TB ? K : N;
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
+    const int wm = wave % WM, wn = wave / WM;
+    const int kh = lane >> 5, rl = lane & 31;
+    const uint32_t lds0 = lds_addr(&lds[0][0]);
+    constexpr uint32_t kStageBytes = (kA + kB) * 4;
+    // copy instructions per wave per chunk
+    constexpr int kPerWave = (kA + kB) * 4 / 1024 / (kThreads / kWave);
+
+    const int nparts = PAIR && 2 * p + 1 != tiles_m ? 2 : 1;
+    for (int part = 0; part < nparts; ++part) {
+        const int mt = PAIR ? (part == 0 ? tiles_m - 1 - p : p) : p;
+        const int m0 = mt * BM;
+        if (tri == kGemmLowerOut && n0 > m0 + BM - 1) continue;  // wholly above the diagonal
+        int kc0 = 0, nk = K / kTK;
+        if (tri == kGemmLowerA) nk = min(nk, (m0 + BM + kTK - 1) / kTK);
+        if (tri == kGemmUpperA) kc0 = min(nk, m0 / kTK);
+        auto issue = [&](int kc) {
+            const uint32_t st = lds0 + static_cast<uint32_t>((kc - kc0) % S) * kStageBytes;
+            dma_operand<KA, BM>(Ab, lda, m0, M, kc * kTK, st, wave, lane);
+            dma_operand<KB, BN>(Bb, ldb, n0, N, kc * kTK, st + kA * 4, wave, lane);
+        };
+
+        f32x16 acc[I][J];
+#pragma unroll
+        for (int i = 0; i < I; ++i)
+#pragma unroll
+            for (int j = 0; j < J; ++j) acc[i][j] = f32x16{};
+        if (part > 0) __syncthreads();  // the previous part's last chunk is no longer read
+#pragma unroll
+        for (int s = 0; s < S - 1; ++s)
+            if (kc0 + s < nk) issue(kc0 + s);
+        for (int kc = kc0; kc < nk; ++kc) {
+            // chunks issued after kc: kc + 1 .. min(nk - 1, kc + S - 2); the first wait of a
+            // part also covers the previous part's stores, so it waits for everything
+            if (kc == kc0) wait_vm<0>();
+            else wait_vm_at_most(min(nk - 1 - kc, S - 2) * kPerWave);
+            __syncthreads();  // chunk kc landed for every wave; chunk kc - 1 is no longer read
+            if (kc + S - 1 < nk) issue(kc + S - 1);
+            const float* st = &lds[(kc - kc0) % S][0];
+            float a[I][8], b[J][8];
+#pragma unroll
+            for (int i = 0; i < I; ++i) read_operand<KA, BM>(st, I * wm + i, rl, kh, a[i]);
+#pragma unroll
+            for (int j = 0; j < J; ++j) read_operand<KB, BN>(st + kA, J * wn + j, rl, kh, b[j]);
+#pragma unroll
+            for (int s = 0; s < 8; ++s)
+#pragma unroll
+                for (int i = 0; i < I; ++i)
+#pragma unroll
+                    for (int j = 0; j < J; ++j)
+                        acc[i][j] = mfma_32x32x2_f32(a[i][s], b[j][s], acc[i][j]);
+        }
+
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            const int col = n0 + 32 * (J * wn + j) + rl;
+            if (col >= N) continue;
+#pragma unroll
+            for (int i = 0; i < I; ++i) {
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    const int row = m0 + 32 * (I * wm + i) + acc_row(v, kh);
+                    if (row < M) {
+                        float* q = Cb + static_cast<long long>(row) * N + col;
+                        *q = beta == 0.0f ? alpha * acc[i][j][v]
+                                          : fmaf(alpha, acc[i][j][v], beta * *q);
+                    }
+                }
+            }
+        }
+    }
+}
+
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+template <bool TA, bool TB, int WM, int I, int J, int S, bool PAIR, bool TRI = false>
+void launch_dma(const float* A, const float* B, float* C, int M, int N, int K, long long sA,
+                long long sB, long long sC, int batch, float alpha, float beta,
+                hipStream_t stream, GemmTri tri) {
+    constexpr int BM = 32 * I * WM, BN = 32 * J * (4 / WM);
+    const int tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN;
+    const long long tiles = TRI ? static_cast<long long>(tm) * (tm + 1) / 2
+                                : static_cast<long long>(PAIR ? (tm + 1) / 2 : tm) * tn;
+    const long long jobs = tiles * batch;
+    const long long per = (jobs + kXcds - 1) / kXcds;
+    hipLaunchKernelGGL((bgemm_f32_dma_kernel<TA, TB, WM, I, J, S, PAIR, TRI>),
+                       dim3(static_cast<unsigned>(per * kXcds)), dim3(kThreads), 0, stream, A, B,
+                       C, M, N, K, sA, sB, sC, alpha, beta, tm, tn, static_cast<int>(tri), jobs);
+}
 
 template <bool TA, bool TB>
 void launch_tiled(const float* A, const float* B, float* C, int M, int N, int K, long long sA,
                   long long sB, long long sC, int batch, float alpha, float beta,
                   hipStream_t stream, GemmTri tri) {
     const dim3 b(kThreads);
+    // the copy-pipelined kernel addresses each batch's operands with 32-bit byte offsets
+    const long long lim = 0xffffffffLL;
+    if (K % kTK == 0 && 4LL * M * K <= lim && 4LL * K * N <= lim) {
+        if (N > 64 && tri == kGemmLowerOut)  // 128 x 128 tiles at or below the diagonal
+            launch_dma<TA, TB, 2, 2, 2, 3, false, true>(A, B, C, M, N, K, sA, sB, sC, batch,
+                                                        alpha, beta, stream, tri);
+        else if (N > 64)  // 128 x 128: each wave 64 x 64
+            launch_dma<TA, TB, 2, 2, 2, 3, false>(A, B, C, M, N, K, sA, sB, sC, batch, alpha,
+                                                  beta, stream, tri);
+        else if (tri == kGemmLowerA || tri == kGemmUpperA)  // 64 x 64 row tiles in pairs
+            launch_dma<TA, TB, 2, 1, 1, 4, true>(A, B, C, M, N, K, sA, sB, sC, batch, alpha,
+                                                 beta, stream, tri);
+        else  // 128 x 64: each wave 32 x 64
+            launch_dma<TA, TB, 4, 1, 2, 3, false>(A, B, C, M, N, K, sA, sB, sC, batch, alpha,
+                                                  beta, stream, tri);
+        return;
+    }
     if (N <= 64) {  // 128 x 64: each wave 32 x 64
         const int tm = (M + 127) / 128, tn = (N + 63) / 64;
         hipLaunchKernelGGL((bgemm_f32_tiled_kernel<TA, TB, 4, 1, 2>),
@@ -344,26 +568,28 @@ void launch_batched_gemm_f32(const float* A, const float* B, float* C, int M, in
         }
         return;
     }
-    // the scalar kernel computes every product in full (tri only skips exact zeros or
-    // unread outputs, so the full product is always a valid result)
+    // the scalar kernel skips the zero part of a triangular A as the others do (so no kernel
+    // reads a lower-triangular A past the end of the 128-column block holding the diagonal)
+    // and writes every output
     const int tiles_m = (M + kBM - 1) / kBM;
     const int tiles_n = (N + kBN - 1) / kBN;
     const long long grid = static_cast<long long>(tiles_m) * tiles_n * batch;
     const dim3 g(static_cast<unsigned>(grid)), b(kThreads);
+    const int tr = static_cast<int>(tri);
     if (transA) {
         if (transB)
             hipLaunchKernelGGL((bgemm_f32_kernel<true, true>), g, b, 0, stream, A, B, C, M, N,
-                               K, sA, sB, sC, alpha, beta, tiles_m, tiles_n);
+                               K, sA, sB, sC, alpha, beta, tiles_m, tiles_n, tr);
         else
             hipLaunchKernelGGL((bgemm_f32_kernel<true, false>), g, b, 0, stream, A, B, C, M, N,
-                               K, sA, sB, sC, alpha, beta, tiles_m, tiles_n);
+                               K, sA, sB, sC, alpha, beta, tiles_m, tiles_n, tr);
     } else {
         if (transB)
             hipLaunchKernelGGL((bgemm_f32_kernel<false, true>), g, b, 0, stream, A, B, C, M, N,
-                               K, sA, sB, sC, alpha, beta, tiles_m, tiles_n);
+                               K, sA, sB, sC, alpha, beta, tiles_m, tiles_n, tr);
         else
             hipLaunchKernelGGL((bgemm_f32_kernel<false, false>), g, b, 0, stream, A, B, C, M,
-                               N, K, sA, sB, sC, alpha, beta, tiles_m, tiles_n);
+                               N, K, sA, sB, sC, alpha, beta, tiles_m, tiles_n, tr);
     }
 }
 

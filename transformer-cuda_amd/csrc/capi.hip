@@ -710,29 +710,62 @@ int attn_head_merge_transpose_backward_f32(const float* dout, float* din, int B,
 
 // ---- materialised softmax ---------------------------------------------------------------
 
-int attn_causal_softmax_forward_f32(const float* scores, float* probs, int B, int H, int T,
-                                    float scale, hipStream_t stream) {
+namespace {
+
+int softmax_fwd(const float* scores, float* probs, int B, int H, int T, float scale,
+                int zero_block, hipStream_t stream) {
     if (scores == nullptr || probs == nullptr) return ATTN_ERROR_NULL_POINTER;
     if (B <= 0 || H <= 0 || T <= 0) return ATTN_ERROR_INVALID_DIM;
-    if (!isfinite(scale)) return ATTN_ERROR_INVALID_VALUE;
+    if (!isfinite(scale) || zero_block < 0 || zero_block % 4 != 0)
+        return ATTN_ERROR_INVALID_VALUE;
     const int64_t rows = static_cast<int64_t>(B) * H * T;
     if ((rows + 3) / 4 > kInt32Max) return ATTN_ERROR_INVALID_DIM;
     clear_error();
-    tcamd::launch_causal_softmax_fwd_f32(scores, probs, rows, T, scale, stream);
+    tcamd::launch_causal_softmax_fwd_f32(scores, probs, rows, T, scale, stream, zero_block);
     return launch_status();
+}
+
+int softmax_bwd(const float* dprobs, const float* probs, float* dscores, int B, int H, int T,
+                float scale, int zero_block, hipStream_t stream) {
+    if (dprobs == nullptr || probs == nullptr || dscores == nullptr)
+        return ATTN_ERROR_NULL_POINTER;
+    if (B <= 0 || H <= 0 || T <= 0) return ATTN_ERROR_INVALID_DIM;
+    if (!isfinite(scale) || zero_block < 0 || zero_block % 4 != 0)
+        return ATTN_ERROR_INVALID_VALUE;
+    const int64_t rows = static_cast<int64_t>(B) * H * T;
+    if ((rows + 3) / 4 > kInt32Max) return ATTN_ERROR_INVALID_DIM;
+    clear_error();
+    tcamd::launch_causal_softmax_bwd_f32(dprobs, probs, dscores, rows, T, scale, stream,
+                                         zero_block);
+    return launch_status();
+}
+
+// The materialised attention's products read a probability (or dscores) row only up to the
+// end of the 128-column block that holds its diagonal, so the softmax zeroes no further.
+constexpr int kMatZeroBlock = 128;
+
+}  // namespace
+
+int attn_causal_softmax_forward_f32(const float* scores, float* probs, int B, int H, int T,
+                                    float scale, hipStream_t stream) {
+    return softmax_fwd(scores, probs, B, H, T, scale, 0, stream);
 }
 
 int attn_causal_softmax_backward_f32(const float* dprobs, const float* probs, float* dscores,
                                      int B, int H, int T, float scale, hipStream_t stream) {
-    if (dprobs == nullptr || probs == nullptr || dscores == nullptr)
-        return ATTN_ERROR_NULL_POINTER;
-    if (B <= 0 || H <= 0 || T <= 0) return ATTN_ERROR_INVALID_DIM;
-    if (!isfinite(scale)) return ATTN_ERROR_INVALID_VALUE;
-    const int64_t rows = static_cast<int64_t>(B) * H * T;
-    if ((rows + 3) / 4 > kInt32Max) return ATTN_ERROR_INVALID_DIM;
-    clear_error();
-    tcamd::launch_causal_softmax_bwd_f32(dprobs, probs, dscores, rows, T, scale, stream);
-    return launch_status();
+    return softmax_bwd(dprobs, probs, dscores, B, H, T, scale, 0, stream);
+}
+
+int attn_causal_softmax_forward_blocked_f32(const float* scores, float* probs, int B, int H,
+                                            int T, float scale, int zero_block,
+                                            hipStream_t stream) {
+    return softmax_fwd(scores, probs, B, H, T, scale, zero_block, stream);
+}
+
+int attn_causal_softmax_backward_blocked_f32(const float* dprobs, const float* probs,
+                                             float* dscores, int B, int H, int T, float scale,
+                                             int zero_block, hipStream_t stream) {
+    return softmax_bwd(dprobs, probs, dscores, B, H, T, scale, zero_block, stream);
 }
 
 // ---- materialised path ------------------------------------------------------------------
@@ -830,8 +863,9 @@ int attn_materialized_causal_forward_f32(const float* q, const float* k, const f
     tcamd::launch_batched_gemm_f32(q, k, scores, T, T, d_head, sh, sh, ss, BH, false, true,
                                    1.0f, 0.0f, stream, tcamd::kGemmLowerOut);
     tcamd::launch_causal_softmax_fwd_f32(scores, probs, static_cast<int64_t>(BH) * T, T, scale,
-                                         stream);
-    // src/model.cu:326-332: out = probs V (probs is zero above the diagonal)
+                                         stream, kMatZeroBlock);
+    // src/model.cu:326-332: out = probs V (probs is zero above the diagonal, up to where the
+    // product reads it)
     tcamd::launch_batched_gemm_f32(probs, v, out, T, d_head, T, ss, sh, sh, BH, false, false,
                                    1.0f, 0.0f, stream, tcamd::kGemmLowerA);
     return launch_status();
@@ -857,9 +891,10 @@ int attn_materialized_causal_backward_f32(const float* q, const float* k, const 
     // :626-631: dv = probs^T dO (probs^T is zero below the diagonal)
     tcamd::launch_batched_gemm_f32(probs, dout, dv, T, d_head, T, ss, sh, sh, BH, true, false,
                                    1.0f, 0.0f, stream, tcamd::kGemmUpperA);
-    // :634: dscores = softmax backward (scale inside; zero above the diagonal)
+    // :634: dscores = softmax backward (scale inside; zero above the diagonal, up to where
+    // the two products read it)
     tcamd::launch_causal_softmax_bwd_f32(dprobs, probs, dscores, static_cast<int64_t>(BH) * T,
-                                         T, scale, stream);
+                                         T, scale, stream, kMatZeroBlock);
     // :637-642: dq = dscores K;  :644-649: dk = dscores^T Q
     tcamd::launch_batched_gemm_f32(dscores, k, dq, T, d_head, T, ss, sh, sh, BH, false, false,
                                    1.0f, 0.0f, stream, tcamd::kGemmLowerA);

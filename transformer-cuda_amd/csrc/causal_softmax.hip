@@ -8,6 +8,9 @@
 //
 // One wavefront per row.  Only the causal prefix j <= i is read; the masked suffix is
 // written as zeros without reading it, which halves the read traffic of a full-row pass.
+// With zero_block = Z > 0 the zeros stop at the end of the Z-column block that holds the
+// diagonal, (i / Z + 1) * Z: the materialised attention's products read a probability row
+// only up to there, so the rest of the suffix is neither read nor written.
 // Rows up to kCacheCols columns stay in registers (one read per element); longer rows
 // take a streaming two-pass path (online max/sum, then normalise).
 #include <float.h>
@@ -51,7 +54,8 @@ struct Vec<1> {
     __device__ static void set(T& x, int, float v) { x = v; }
 };
 
-// Zero columns [from, T) of a row; `from` need not be VEC-aligned.
+// Zero columns [from, T) of a row; `from` need not be VEC-aligned.  Columns past the last
+// multiple of VEC below T are written one by one, so T need not be VEC-aligned.
 template <int VEC>
 __device__ __forceinline__ void zero_suffix(float* row, int from, int T, int lane) {
     using V = Vec<VEC>;
@@ -76,7 +80,7 @@ __device__ __forceinline__ void zero_suffix(float* row, int from, int T, int lan
 template <int VEC>
 __global__ __launch_bounds__(kWave* kWavesPerBlock) void causal_softmax_fwd_kernel(
     const float* __restrict__ scores, float* __restrict__ probs, int64_t rows, int T,
-    float scale) {
+    float scale, int zero_block) {
     using V = Vec<VEC>;
     const int lane = threadIdx.x & (kWave - 1);
     const int64_t r = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + (threadIdx.x >> 6);
@@ -86,6 +90,7 @@ __global__ __launch_bounds__(kWave* kWavesPerBlock) void causal_softmax_fwd_kern
     float* p_row = probs + r * T;
     const int n = i + 1;  // valid columns
     const int nchunks = (n + VEC - 1) / VEC;
+    const int zend = zero_block > 0 ? min(T, (i / zero_block + 1) * zero_block) : T;
 
     if (nchunks <= kChunks * kWave) {
         typename V::T x[kChunks];
@@ -133,7 +138,7 @@ __global__ __launch_bounds__(kWave* kWavesPerBlock) void causal_softmax_fwd_kern
             }
         }
         // Columns of the last valid chunk beyond n were written as exp(-inf) * inv = 0.
-        zero_suffix<VEC>(p_row, nchunks * VEC, T, lane);
+        zero_suffix<VEC>(p_row, nchunks * VEC, zend, lane);
         return;
     }
 
@@ -171,13 +176,13 @@ __global__ __launch_bounds__(kWave* kWavesPerBlock) void causal_softmax_fwd_kern
             for (int e = 0; e < VEC && c * VEC + e < T; ++e) p_row[c * VEC + e] = V::get(x, e);
         }
     }
-    zero_suffix<VEC>(p_row, nchunks * VEC, T, lane);
+    zero_suffix<VEC>(p_row, nchunks * VEC, zend, lane);
 }
 
 template <int VEC>
 __global__ __launch_bounds__(kWave* kWavesPerBlock) void causal_softmax_bwd_kernel(
     const float* __restrict__ dprobs, const float* __restrict__ probs,
-    float* __restrict__ dscores, int64_t rows, int T, float scale) {
+    float* __restrict__ dscores, int64_t rows, int T, float scale, int zero_block) {
     using V = Vec<VEC>;
     const int lane = threadIdx.x & (kWave - 1);
     const int64_t r = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + (threadIdx.x >> 6);
@@ -188,6 +193,7 @@ __global__ __launch_bounds__(kWave* kWavesPerBlock) void causal_softmax_bwd_kern
     float* ds_row = dscores + r * T;
     const int n = i + 1;
     const int nchunks = (n + VEC - 1) / VEC;
+    const int zend = zero_block > 0 ? min(T, (i / zero_block + 1) * zero_block) : T;
 
     if (nchunks <= kChunks * kWave) {
         typename V::T pv[kChunks], dpv[kChunks];
@@ -225,7 +231,7 @@ __global__ __launch_bounds__(kWave* kWavesPerBlock) void causal_softmax_bwd_kern
                 }
             }
         }
-        zero_suffix<VEC>(ds_row, nchunks * VEC, T, lane);
+        zero_suffix<VEC>(ds_row, nchunks * VEC, zend, lane);
         return;
     }
 
@@ -255,7 +261,7 @@ __global__ __launch_bounds__(kWave* kWavesPerBlock) void causal_softmax_bwd_kern
             for (int e = 0; e < VEC && c * VEC + e < T; ++e) ds_row[c * VEC + e] = V::get(o, e);
         }
     }
-    zero_suffix<VEC>(ds_row, nchunks * VEC, T, lane);
+    zero_suffix<VEC>(ds_row, nchunks * VEC, zend, lane);
 }
 
 bool vec4_ok(const void* a, const void* b, const void* c, int T) {
@@ -267,28 +273,29 @@ bool vec4_ok(const void* a, const void* b, const void* c, int T) {
 }  // namespace
 
 void launch_causal_softmax_fwd_f32(const float* scores, float* probs, int64_t rows, int T,
-                                   float scale, hipStream_t stream) {
+                                   float scale, hipStream_t stream, int zero_block) {
     const dim3 grid(static_cast<unsigned>((rows + kWavesPerBlock - 1) / kWavesPerBlock));
     const dim3 block(kWave * kWavesPerBlock);
     if (vec4_ok(scores, probs, probs, T)) {
         hipLaunchKernelGGL(causal_softmax_fwd_kernel<4>, grid, block, 0, stream, scores, probs,
-                           rows, T, scale);
+                           rows, T, scale, zero_block);
     } else {
         hipLaunchKernelGGL(causal_softmax_fwd_kernel<1>, grid, block, 0, stream, scores, probs,
-                           rows, T, scale);
+                           rows, T, scale, zero_block);
     }
 }
 
 void launch_causal_softmax_bwd_f32(const float* dprobs, const float* probs, float* dscores,
-                                   int64_t rows, int T, float scale, hipStream_t stream) {
+                                   int64_t rows, int T, float scale, hipStream_t stream,
+                                   int zero_block) {
     const dim3 grid(static_cast<unsigned>((rows + kWavesPerBlock - 1) / kWavesPerBlock));
     const dim3 block(kWave * kWavesPerBlock);
     if (vec4_ok(dprobs, probs, dscores, T)) {
         hipLaunchKernelGGL(causal_softmax_bwd_kernel<4>, grid, block, 0, stream, dprobs, probs,
-                           dscores, rows, T, scale);
+                           dscores, rows, T, scale, zero_block);
     } else {
         hipLaunchKernelGGL(causal_softmax_bwd_kernel<1>, grid, block, 0, stream, dprobs, probs,
-                           dscores, rows, T, scale);
+                           dscores, rows, T, scale, zero_block);
     }
 }
 

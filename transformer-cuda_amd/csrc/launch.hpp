@@ -26,10 +26,13 @@ void launch_stripe_transpose(const void* src, ElemType src_t, void* dst, ElemTyp
                              const HeadPtrs& heads, bool to_heads, int B, int T, int S, int H,
                              int d, hipStream_t stream);
 
+// zero_block = 0: the masked suffix of every row is written as zeros (the reference's
+// semantics); Z > 0: only up to the end of the Z-column block that holds the diagonal.
 void launch_causal_softmax_fwd_f32(const float* scores, float* probs, int64_t rows, int T,
-                                   float scale, hipStream_t stream);
+                                   float scale, hipStream_t stream, int zero_block = 0);
 void launch_causal_softmax_bwd_f32(const float* dprobs, const float* probs, float* dscores,
-                                   int64_t rows, int T, float scale, hipStream_t stream);
+                                   int64_t rows, int T, float scale, hipStream_t stream,
+                                   int zero_block = 0);
 
 // Causal structure a batched GEMM may exploit (the materialised attention's contractions;
 // the public matmul_batched_strided always computes the full product):

@@ -354,6 +354,33 @@ inline void fused_causal_attention_backward_f32x3(const float* qkv, const float*
                         "fused_causal_attention_backward_f32x3");
 }
 
+// The same backwards with dS in its own buffer: `planes` of attn_f32x3_planes_bytes (kept
+// per layer from the forward), `ds_workspace` of attn_f32x3_ds_workspace_bytes (one buffer
+// may serve every layer: dS lives inside one call).  Results bitwise those above.
+inline void packed_causal_attention_backward_ds_f32x3(
+    const float* qkv, const float* o, const float* do_ptr, const float* m_ptr,
+    const float* l_ptr, float* dqkv, float* d_workspace, float* ds_workspace, int B, int H,
+    int T, int d_head, float scale, void* planes, bool kv_planes_ready = true,
+    hipStream_t stream = nullptr) {
+    tcamd::check_status(
+        attn_packed_causal_backward_ds_f32x3(qkv, o, do_ptr, m_ptr, l_ptr, dqkv, d_workspace,
+                                             ds_workspace, B, H, T, d_head, scale, planes,
+                                             kv_planes_ready ? 1 : 0, stream),
+        "packed_causal_attention_backward_ds_f32x3");
+}
+
+inline void fused_causal_attention_backward_ds_f32x3(
+    const float* qkv, const float* o, const float* do_ptr, const float* m_ptr,
+    const float* l_ptr, float* dqkv, float* d_workspace, float* ds_workspace, int B, int H,
+    int T, int d_head, float scale, void* planes, bool kv_planes_ready = true,
+    hipStream_t stream = nullptr) {
+    tcamd::check_status(
+        attn_fused_causal_backward_ds_f32x3(qkv, o, do_ptr, m_ptr, l_ptr, dqkv, d_workspace,
+                                            ds_workspace, B, H, T, d_head, scale, planes,
+                                            kv_planes_ready ? 1 : 0, stream),
+        "fused_causal_attention_backward_ds_f32x3");
+}
+
 // The reference's tiled launchers (separate head-major tensors) for fp32 on the bf16 matrix
 // cores; `planes` as above.
 inline void tiled_causal_attention_forward_f32x3(const float* q, const float* k, const float* v,

@@ -20,7 +20,10 @@
 // (sched.hpp), which balances the very unequal causal blocks across CUs and keeps a head's
 // K/V in one XCD's L2.  A workgroup is four wavefronts, one per SIMD; the four split the
 // task's tiles into contiguous ranges, each with private LDS tiles, and merge their partial
-// results through LDS at the end of the task (the only workgroup barriers).
+// results through LDS at the end of the task (the only workgroup barriers).  The forward also
+// has a form on shared tiles (flash_fwd_f32_shared_kernel: 128 queries per workgroup, K/V
+// tiles double-buffered and shared by the four waves, XCD-aware static block order), which
+// runs where it measures faster (fwd_on_shared_tiles).
 //
 // Staging.  The 32-row tiles streamed over the sequence (K/V, or Q/dO) are copied from HBM
 // straight into LDS with global_load_lds_dwordx4 (16 bytes per lane, 1 KB of the tile per
@@ -42,6 +45,7 @@
 // computation of S and dP.
 #include <math.h>
 
+#include "bf16_tile.hpp"
 #include "device_common.hpp"
 #include "launch.hpp"
 #include "lds_dma.hpp"
@@ -470,6 +474,144 @@ TCAMD_F32_KERNEL(kFwdWaves) void flash_fwd_f32_kernel(
         }
         __syncthreads();
         task = __builtin_amdgcn_readfirstlane(s_next);  // the same in every lane
+    }
+}
+
+// --------------------------------------------------------------------------------------
+// Forward on shared tiles.  A workgroup owns 128 queries of one (b, h), wave w the 32 at
+// q0 + 32w; the 32-key K and V tiles are double-buffered in LDS and shared by the four
+// waves, which copy each tile together (copy instructions w, w + 4, ... of it) one tile
+// ahead, with one barrier per tile.  Wave w runs key tiles 0 .. its diagonal tile and then
+// only joins the barriers; it owns its queries' (O, m, l), so nothing is merged.  Per tile
+// and wave: S^T = K Q^T (D/2 MFMAs), the online softmax of mma_rows' accumulator, and
+// O^T += V^T P^T (D/2 MFMAs), as in the per-wave kernel above.
+// --------------------------------------------------------------------------------------
+template <int D>
+struct FwdSharedLds {
+    static constexpr int KS = FwdLds<D>::KS;
+    static constexpr int VS = FwdLds<D>::VS;
+    float k[2][kTile * KS];
+    float v[2][kTile * VS];
+};
+constexpr int kFwdSharedWaves = 4;
+
+// Copy instructions i = wave, wave + 4, ... of one tile's plan (TileShape), this lane's
+// source offsets precomputed.
+template <int D, int STRIDE>
+struct SharedTileCopy : TileShape<D, STRIDE> {
+    using S = TileShape<D, STRIDE>;
+    static constexpr int kPer = (S::kInst + kFwdSharedWaves - 1) / kFwdSharedWaves;
+    uint32_t voff[kPer];
+    __device__ void init(int wave, int lane, int rs) {
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+            int r, b;
+            S::row_byte(min(wave + kFwdSharedWaves * j, S::kInst - 1), lane, r, b);
+            voff[j] = static_cast<uint32_t>(r * rs * 4 + b);
+        }
+    }
+    __device__ void copy(const float* __restrict__ head, int row0, int T, uint32_t lds, int wave,
+                         int lane, int rs) const {
+        const float* base = head + static_cast<size_t>(row0) * rs;
+        const bool whole = row0 + kTile <= T;
+        const uint32_t last = S::last(row0, T, rs);
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+            const int i = wave + kFwdSharedWaves * j;
+            if (i < S::kInst && S::active(i, lane))
+                dma_dwordx4(base, lds + static_cast<uint32_t>(1024 * i),
+                            whole ? voff[j] : min(voff[j], last));
+        }
+    }
+};
+
+template <int D>
+__global__ __launch_bounds__(kWave* kFwdSharedWaves) void flash_fwd_f32_shared_kernel(
+    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
+    float* __restrict__ o, float* __restrict__ m_out, float* __restrict__ l_out, int BH, int T,
+    float scale, int nblk, HeadView xv, HeadView ov, int serp) {
+    using L_t = FwdSharedLds<D>;
+    constexpr int KS = L_t::KS, VS = L_t::VS;
+    __shared__ __attribute__((aligned(1024))) L_t L;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+    const int lane = threadIdx.x & (kWave - 1);
+    const int col = lane & 31;
+    const int half = lane >> 5;
+    int bh, blk;
+    if (serp < 0)
+        bf16t::map_block_grouped(blockIdx.x, BH, nblk, -serp, true, bh, blk);
+    else
+        bf16t::map_block(blockIdx.x, BH, nblk, true, serp != 0, bh, blk);
+    const int q0 = blk * kTile * kFwdSharedWaves;
+    const int qj = q0 + kTile * wave;
+    const int qi = qj + col;
+    const size_t xoff = wave_uniform(xv.off(bh)), ooff = wave_uniform(ov.off(bh));
+    const float* kh = k + xoff;
+    const float* vh = v + xoff;
+    const float c = scale * kLog2e;
+
+    SharedTileCopy<D, KS> kc;
+    SharedTileCopy<D, VS> vc;
+    kc.init(wave, lane, xv.row);
+    vc.init(wave, lane, xv.row);
+    const int ntile = (min(T, q0 + kTile * kFwdSharedWaves) + kTile - 1) / kTile;
+    const uint32_t k_lds = lds_addr(&L.k[0][0]), v_lds = lds_addr(&L.v[0][0]);
+    constexpr uint32_t kKBuf = kTile * KS * 4, kVBuf = kTile * VS * 4;
+    auto copy_tile = [&](int t) {
+        const uint32_t b = static_cast<uint32_t>(t & 1);
+        kc.copy(kh, t * kTile, T, k_lds + b * kKBuf, wave, lane, xv.row);
+        vc.copy(vh, t * kTile, T, v_lds + b * kVBuf, wave, lane, xv.row);
+    };
+    copy_tile(0);
+
+    float qreg[D / 2];
+    load_row_half<D>(qreg, q + xoff, qi, T, half, xv.row);
+    f32x16 acc[D / 32];
+    zero(acc);
+    float m_raw = -INFINITY;  // running max of the raw scores q.k (scale > 0)
+    float l_i = 0.0f;
+    // this wave's last key tile (its diagonal one); none if its queries start at or past T
+    const int tlast = qj < T ? qj / kTile : -1;
+    for (int t = 0; t < ntile; ++t) {
+        wait_vm<0>();     // this wave's copies of tile t landed ...
+        __syncthreads();  // ... and every wave's; tile t-1 is no longer read by anyone
+        if (t + 1 < ntile) copy_tile(t + 1);
+        if (t > tlast) continue;
+        const float* Ks = &L.k[t & 1][0];
+        const float* Vs = &L.v[t & 1][0];
+        f32x16 s = mma_rows<D>(Ks + col * KS + half * (D / 2), qreg, f32x16{});
+        if (t == tlast) {  // diagonal tile
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                if (t * kTile + acc_row(r, half) > qi) s[r] = -INFINITY;
+        }
+        float mx = s[0];
+#pragma unroll
+        for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[r]);
+        mx = xhalf_max(mx);
+        const float m_new = fmaxf(m_raw, mx);
+        const float alpha = exp2_fast((m_raw - m_new) * c);  // 0 on the first tile
+        const float mc = m_new * c;
+        float rs = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            s[r] = exp2_fast(fmaf(s[r], c, -mc));
+            rs += s[r];
+        }
+        rs = xhalf_sum(rs);
+        l_i = l_i * alpha + rs;
+        m_raw = m_new;
+#pragma unroll
+        for (int dt = 0; dt < D / 32; ++dt) acc[dt] *= alpha;
+        mma_cols<D, VS>(Vs, col, half, s, acc);
+    }
+    if (qi < T) {
+        store_acc_row<D>(o + ooff, qi, half, acc, 1.0f / l_i, ov.row);
+        if (half == 0) {
+            // max_j scale*s_j = scale * max_j s_j exactly (rounding is monotone)
+            if (m_out != nullptr) m_out[static_cast<size_t>(bh) * T + qi] = m_raw * scale;
+            if (l_out != nullptr) l_out[static_cast<size_t>(bh) * T + qi] = l_i;
+        }
     }
 }
 
@@ -1028,10 +1170,29 @@ QueueSlot* launch_slot(Family f, std::atomic<unsigned>& ticket, hipStream_t stre
     return base + next_queue_slot(ticket);
 }
 
+// The forward on shared tiles (flash_fwd_f32_shared_kernel) where it is the faster one, else
+// the persistent per-wave kernel.  Measured forward (one process, us, per-wave -> shared):
+// d = 64: B16 H12 T512 92 -> 79, B8 H12 T1024 142 -> 134, B8 H16 T2048 623 -> 562,
+// B4 H12 T2048 237 -> 239, B2 H12 T4096 439 -> 464, B1 H12 T8192 886 -> 1086 (its static
+// block order balances long causal ranges worse than the persistent queue); d = 128:
+// B8 H12 T1024 314 -> 249, B2 H16 T2048 355 -> 299, B1 H16 T8192 2443 -> 2349; d = 32:
+// B8 H12 T1024 72 -> 74.
+bool fwd_on_shared_tiles(int D, int T) { return D == 128 || (D == 64 && T <= 2048); }
+
 template <int D>
 void fwd_dispatch(const float* q, const float* k, const float* v, float* o, float* m_out,
                   float* l_out, int BH, int T, float scale, const HeadView& xv,
                   const HeadView& ov, hipStream_t stream) {
+    if (fwd_on_shared_tiles(D, T)) {
+        constexpr int kBlock = kTile * kFwdSharedWaves;
+        const int nblk = (T + kBlock - 1) / kBlock;
+        const auto kernel = flash_fwd_f32_shared_kernel<D>;
+        const int res = resident_capacity(kernel, kWave * kFwdSharedWaves, 0);
+        const int serp = BH * nblk <= res ? 1 : -head_group(BH, nblk, res);
+        hipLaunchKernelGGL(kernel, dim3(BH * nblk), dim3(kWave * kFwdSharedWaves), 0, stream, q,
+                           k, v, o, m_out, l_out, BH, T, scale, nblk, xv, ov, serp);
+        return;
+    }
     const int nqb = (T + kTile - 1) / kTile;
     bool ok = true;
     QueueSlot* slot = launch_slot(Family::Fwd, g_fwd_ticket, stream, ok);

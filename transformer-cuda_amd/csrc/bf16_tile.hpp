@@ -30,13 +30,21 @@ __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_ex
 
 // A 64-row x D bf16 tile in LDS.  Rows are grouped in blocks of 8; row r, 16-byte chunk c
 // is at byte (r/8)*B + (r%8)*2D + 16*(c ^ swz(r)), where B = 8 rows + kPad bytes.
-//   * swz(r) = 2*(r%4) + (r/4)%2 (d >= 64) gives the 8 rows of a block 8 distinct chunk
-//     slots, and the 4 rows x 2 chunks that a 16-lane group of a transposing read touches
-//     (rows inside one block) 8 distinct slots.
+//   * d = 64 (a row is half a 256-byte bank line): swz(r) = 2*(r%4) + (r/4)%2 gives the 8
+//     rows of a block 8 distinct chunk slots, and the 4 rows x 2 chunks that a 16-lane group
+//     of a transposing read touches (rows inside one block) 8 distinct slots; consecutive
+//     rows sit on alternate halves of the bank line.
+//   * d = 128 (a row is a whole bank line, so every row of a block starts on bank 0): with
+//     i = r%8 = (i2 i1 i0), swz = 8*i1 + 4*i0 + 2*i2 + i1, i.e. 0 4 9 13 2 6 11 15.  Its low
+//     three bits differ over the 8 rows of a block (row reads, below), and its high two
+//     bits over rows 0-3 and over rows 4-7, so the 4 rows x 4 chunks of the 32 lanes of a
+//     transposing read (chunks 4m .. 4m+3, swizzled to 4-chunk groups m ^ (swz/4)) cover 16
+//     distinct slots, all 64 banks (2*(r%4) + (r/4)%2 put rows r and r^1 on the same four
+//     slots there: two-way conflicts).
 //   * The LDS serves 16 lanes of a 16-byte read per cycle (64 banks x 4 bytes), so a row
 //     read (lane i: row i, same chunk) covers 16 rows, i.e. two blocks; kPad = 128 bytes
-//     after each block (d >= 64) moves the second block's rows to the other half of the
-//     256-byte bank line, where they meet no slot of the first block.
+//     after each block (d >= 64) moves the second block's rows by half a bank line, where
+//     they meet no slot of the first block.
 // Both the swizzle and the padding repeat every 8 rows, so a row offset that is a multiple
 // of 8 is a constant byte offset (rows()).
 template <int D, int ROWS = kRowTile>
@@ -56,7 +64,12 @@ struct Swz {
         return static_cast<uint32_t>((i * 1024 / kBlockData) * kBlockBytes + (i * 1024) % kBlockData);
     }
     __device__ static int swz(int r) {
-        return kCpr >= 8 ? 2 * (r & 3) + ((r >> 2) & 1) : (r & (kCpr - 1));
+        if constexpr (kCpr >= 16) {
+            const int i0 = r & 1, i1 = (r >> 1) & 1, i2 = (r >> 2) & 1;
+            return 8 * i1 + 4 * i0 + 2 * i2 + i1;
+        } else {
+            return kCpr >= 8 ? 2 * (r & 3) + ((r >> 2) & 1) : (r & (kCpr - 1));
+        }
     }
     __device__ static uint32_t off(int r, int c) {
         return static_cast<uint32_t>((r >> 3) * kBlockBytes + (r & 7) * kRowBytes +

@@ -961,6 +961,133 @@ TCAMD_F32_KERNEL(kDkdvWaves) void flash_bwd_dkdv_f32_kernel(
 }
 
 // --------------------------------------------------------------------------------------
+// dK/dV on shared tiles.  A workgroup owns 128 keys of one (b, h), wave w the 32 at
+// k0 + 32w; the 32-query Q and dO tiles are double-buffered in LDS and shared by the four
+// waves, which copy each tile together one tile ahead, with one barrier per tile.  Wave w
+// starts at its diagonal tile (t0 + w) and runs to the last; the per-tile products are those
+// of dkdv_chunk (each in a fresh accumulator, added into the running sums), the statistics
+// of a tile staged in LDS by wave 0.  No merge: each wave owns its keys' dK and dV.
+// --------------------------------------------------------------------------------------
+template <int D>
+struct DkdvSharedLds {
+    static constexpr int QS = DkdvLds<D>::QS;
+    float q[2][kTile * QS];
+    float g[2][kTile * QS];
+    float st[2][2][kTile];  // [buffer][lse2, D][query of the tile]
+};
+
+template <int D, bool DS>
+__global__ __launch_bounds__(kWave* kFwdSharedWaves) void flash_bwd_dkdv_f32_shared_kernel(
+    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
+    const float* __restrict__ dO, const float* __restrict__ m, const float* __restrict__ l,
+    const float* __restrict__ Dws, float* __restrict__ dk, float* __restrict__ dv, int BH,
+    int T, float scale, int nblk, HeadView xv, HeadView ov, HeadView gv,
+    float* __restrict__ ds, int ds_n, int serp) {
+    using L_t = DkdvSharedLds<D>;
+    constexpr int QS = L_t::QS;
+    __shared__ __attribute__((aligned(1024))) L_t L;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+    const int lane = threadIdx.x & (kWave - 1);
+    const int col = lane & 31;
+    const int half = lane >> 5;
+    int bh, blk;
+    bf16t::map_block(blockIdx.x, BH, nblk, false, serp != 0, bh, blk);  // block 0: every query
+    const int k0 = blk * kTile * kFwdSharedWaves;
+    const int kw = k0 + kTile * wave;
+    const int kj = kw + col;
+    const size_t xoff = wave_uniform(xv.off(bh)), ooff = wave_uniform(ov.off(bh)),
+                 goff = wave_uniform(gv.off(bh));
+    const size_t stat_off = static_cast<size_t>(bh) * T;
+    const float* qh = q + xoff;
+    const float* gh = dO + ooff;
+    const float c = scale * kLog2e;
+
+    SharedTileCopy<D, QS> qc, gc;
+    qc.init(wave, lane, xv.row);
+    gc.init(wave, lane, ov.row);
+    const int t0 = k0 / kTile;
+    const int ntile = (T + kTile - 1) / kTile;
+    const uint32_t q_lds = lds_addr(&L.q[0][0]), g_lds = lds_addr(&L.g[0][0]);
+    constexpr uint32_t kBuf = kTile * QS * 4;
+    auto copy_tile = [&](int t) {
+        const uint32_t b = static_cast<uint32_t>(t & 1) * kBuf;
+        qc.copy(qh, t * kTile, T, q_lds + b, wave, lane, xv.row);
+        gc.copy(gh, t * kTile, T, g_lds + b, wave, lane, ov.row);
+    };
+    // Lane (col, half) of wave 0: statistic `half` of query row0 + col: 0: lse2 = m*log2 e +
+    // log2 l, so that P = 2^(s*c - lse2); 1: D.  Padded query rows: lse2 = +inf (P = 0), D = 0.
+    auto load_stat = [&](int row0) -> float {
+        const int r = row0 + col;
+        if (r >= T) return half == 0 ? INFINITY : 0.0f;
+        if (half == 0)
+            return fmaf(m[stat_off + r], kLog2e, __builtin_amdgcn_logf(l[stat_off + r]));
+        return Dws[stat_off + r];
+    };
+    if (wave == 0) L.st[t0 & 1][half][col] = load_stat(t0 * kTile);
+    copy_tile(t0);
+
+    float kreg[D / 2], vreg[D / 2];
+    load_row_half<D>(kreg, k + xoff, kj, T, half, xv.row);
+    load_row_half<D>(vreg, v + xoff, kj, T, half, xv.row);
+    f32x16 dk_acc[D / 32], dv_acc[D / 32];
+    zero(dk_acc);
+    zero(dv_acc);
+    float* ds_head = nullptr;
+    if constexpr (DS) ds_head = ds + static_cast<size_t>(bh) * ds_n * ds_n;
+    // this wave's first query tile (its diagonal one); none if its keys start at or past T
+    const int tw = kw < T ? kw / kTile : ntile;
+    for (int t = t0; t < ntile; ++t) {
+        const bool more = t + 1 < ntile;
+        wait_vm<0>();     // this wave's copies (and statistics) of tile t landed ...
+        __syncthreads();  // ... and every wave's; tile t-1 is no longer read by anyone
+        float st_n = 0.0f;
+        if (more) {
+            if (wave == 0) st_n = load_stat((t + 1) * kTile);
+            copy_tile(t + 1);
+        }
+        if (t >= tw) {
+            const float* Qs = &L.q[t & 1][0];
+            const float* Gs = &L.g[t & 1][0];
+            const float* St0 = &L.st[t & 1][0][0];
+            const float* St1 = &L.st[t & 1][1][0];
+            f32x16 s = mma_rows<D>(Qs + col * QS + half * (D / 2), kreg, f32x16{});
+            f32x16 dp = mma_rows<D>(Gs + col * QS + half * (D / 2), vreg, f32x16{});
+            f32x16 dsv;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int qr = acc_row(r, half);
+                float p = exp2_fast(fmaf(s[r], c, -St0[qr]));
+                if (t == tw && qr < col) p = 0.0f;  // diagonal tile: query < key
+                s[r] = p;
+                dsv[r] = p * (dp[r] - St1[qr]);
+            }
+            if constexpr (DS) {
+                // dS of the tile, query-major: row t*32 + acc_row(r, half), column kj; a 32-lane
+                // store covers one query's 32 keys (128 bytes).  Keys past T get zeros.
+                float* row = ds_head + static_cast<size_t>(t * kTile) * ds_n;
+                const uint32_t loff = static_cast<uint32_t>(4 * half * ds_n + kj);
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    row[static_cast<size_t>(8 * (r / 4) + r % 4) * ds_n + loff] =
+                        kj < T ? dsv[r] : 0.0f;
+            }
+            f32x16 part[D / 32];
+            zero(part);
+            mma_cols<D, QS>(Gs, col, half, s, part);
+            add_into(dv_acc, part);
+            zero(part);
+            mma_cols<D, QS>(Qs, col, half, dsv, part);
+            add_into(dk_acc, part);
+        }
+        if (more && wave == 0) L.st[(t + 1) & 1][half][col] = st_n;
+    }
+    if (kj < T) {
+        store_acc_row<D>(dk + goff, kj, half, dk_acc, scale, gv.row);
+        store_acc_row<D>(dv + goff, kj, half, dv_acc, 1.0f, gv.row);
+    }
+}
+
+// --------------------------------------------------------------------------------------
 // The dS-first backward order: D first (the dQ kernel's sums, alone), then dK/dV writing dS
 // (DS = true above), then dQ = scale * dS K from the stored dS, whose products (one of the
 // dQ kernel's three) are then all that dQ costs.
@@ -1178,6 +1305,7 @@ QueueSlot* launch_slot(Family f, std::atomic<unsigned>& ticket, hipStream_t stre
 // B8 H12 T1024 314 -> 249, B2 H16 T2048 355 -> 299, B1 H16 T8192 2443 -> 2349; d = 32:
 // B8 H12 T1024 72 -> 74.
 bool fwd_on_shared_tiles(int D, int T) { return D == 128 || (D == 64 && T <= 2048); }
+constexpr bool kDkdvShared = true;
 
 template <int D>
 void fwd_dispatch(const float* q, const float* k, const float* v, float* o, float* m_out,
@@ -1224,6 +1352,16 @@ void dkdv_launch(const float* q, const float* k, const float* v, const float* dO
                  const float* m, const float* l, const float* Dws, float* dk, float* dv, int BH,
                  int T, float scale, const HeadView& xv, const HeadView& ov, const HeadView& gv,
                  float* ds, hipStream_t stream) {
+    if (kDkdvShared && fwd_on_shared_tiles(D, T)) {
+        constexpr int kBlock = kTile * kFwdSharedWaves;
+        const int nblk = (T + kBlock - 1) / kBlock;
+        const auto kernel = flash_bwd_dkdv_f32_shared_kernel<D, DS>;
+        const int serp = BH * nblk <= resident_capacity(kernel, kWave * kFwdSharedWaves, 0);
+        hipLaunchKernelGGL(kernel, dim3(BH * nblk), dim3(kWave * kFwdSharedWaves), 0, stream, q,
+                           k, v, dO, m, l, Dws, dk, dv, BH, T, scale, nblk, xv, ov, gv, ds,
+                           ds_rows(T), serp);
+        return;
+    }
     const int nkb = (T + kTile - 1) / kTile;
     bool ok = true;
     QueueSlot* slot = launch_slot(Family::Dkdv, g_dkdv_ticket, stream, ok);

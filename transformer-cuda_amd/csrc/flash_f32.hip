@@ -23,7 +23,9 @@
 // results through LDS at the end of the task (the only workgroup barriers).  The forward also
 // has a form on shared tiles (flash_fwd_f32_shared_kernel: 128 queries per workgroup, K/V
 // tiles double-buffered and shared by the four waves, XCD-aware static block order), which
-// runs where it measures faster (fwd_on_shared_tiles).
+// runs where it measures faster (fwd_on_shared_tiles); so do the two backward stages
+// (flash_bwd_dq_f32_shared_kernel, flash_bwd_dkdv_f32_shared_kernel: 128 queries or keys
+// per workgroup, the streamed tiles shared the same way).
 //
 // Staging.  The 32-row tiles streamed over the sequence (K/V, or Q/dO) are copied from HBM
 // straight into LDS with global_load_lds_dwordx4 (16 bytes per lane, 1 KB of the tile per
@@ -784,6 +786,112 @@ TCAMD_F32_KERNEL(kDqWaves) void flash_bwd_dq_f32_kernel(
 }
 
 // --------------------------------------------------------------------------------------
+// Backward stage 1 on shared tiles.  A workgroup owns 128 queries of one (b, h), wave w the
+// 32 at q0 + 32w; the 32-key K and V tiles are double-buffered in LDS and shared by the four
+// waves, which copy each tile together one tile ahead, with one barrier per tile.  Wave w
+// runs key tiles 0 .. its diagonal tile with Q, dO in VGPRs; the per-tile products are those
+// of dq_chunk (each in a fresh accumulator, added into the running sum).  No merge: each wave
+// owns its queries' dQ and D.
+// --------------------------------------------------------------------------------------
+template <int D>
+struct DqSharedLds {
+    static constexpr int KS = DqLds<D>::KS;
+    float k[2][kTile * KS];
+    float v[2][kTile * KS];
+};
+
+template <int D>
+__global__ __launch_bounds__(kWave* kFwdSharedWaves) void flash_bwd_dq_f32_shared_kernel(
+    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
+    const float* __restrict__ o, const float* __restrict__ dO, const float* __restrict__ m,
+    const float* __restrict__ l, float* __restrict__ dq, float* __restrict__ Dws, int BH,
+    int T, float scale, int nblk, HeadView xv, HeadView ov, HeadView gv, int serp) {
+    using L_t = DqSharedLds<D>;
+    constexpr int KS = L_t::KS;
+    static_assert(DqLds<D>::KS == DqLds<D>::VS, "K and V tiles share one copy plan");
+    __shared__ __attribute__((aligned(1024))) L_t L;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+    const int lane = threadIdx.x & (kWave - 1);
+    const int col = lane & 31;
+    const int half = lane >> 5;
+    int bh, blk;
+    if (serp < 0)
+        bf16t::map_block_grouped(blockIdx.x, BH, nblk, -serp, true, bh, blk);
+    else
+        bf16t::map_block(blockIdx.x, BH, nblk, true, serp != 0, bh, blk);
+    const int q0 = blk * kTile * kFwdSharedWaves;
+    const int qj = q0 + kTile * wave;
+    const int qi = qj + col;
+    const bool row_ok = qi < T;
+    const size_t xoff = wave_uniform(xv.off(bh)), ooff = wave_uniform(ov.off(bh)),
+                 goff = wave_uniform(gv.off(bh));
+    const size_t stat_off = static_cast<size_t>(bh) * T;
+    const float* kh = k + xoff;
+    const float* vh = v + xoff;
+    const float c = scale * kLog2e;
+
+    SharedTileCopy<D, KS> kc;
+    kc.init(wave, lane, xv.row);
+    const int ntile = (min(T, q0 + kTile * kFwdSharedWaves) + kTile - 1) / kTile;
+    const uint32_t k_lds = lds_addr(&L.k[0][0]), v_lds = lds_addr(&L.v[0][0]);
+    constexpr uint32_t kBuf = kTile * KS * 4;
+    auto copy_tile = [&](int t) {
+        const uint32_t b = static_cast<uint32_t>(t & 1) * kBuf;
+        kc.copy(kh, t * kTile, T, k_lds + b, wave, lane, xv.row);
+        kc.copy(vh, t * kTile, T, v_lds + b, wave, lane, xv.row);
+    };
+    copy_tile(0);
+
+    float qreg[D / 2];
+    float doreg[D / 2];
+    load_row_half<D>(qreg, q + xoff, qi, T, half, xv.row);
+    load_row_half<D>(doreg, dO + ooff, qi, T, half, ov.row);
+    // D_i from this lane's half row of O, completed across the halves (the same fma chains
+    // as the per-wave kernel's, so the same bits).
+    float Dval;
+    {
+        float orow[D / 2];
+        load_row_half<D>(orow, o + ooff, qi, T, half, ov.row);
+        float pd = 0.0f;
+#pragma unroll
+        for (int j = 0; j < D / 2; ++j) pd = fmaf(doreg[j], orow[j], pd);
+        Dval = xhalf_sum(pd);
+    }
+    // P_ij = 2^(s*c - lse2), lse2 = m*log2 e + log2 l; +inf on padded rows
+    const float lse2 =
+        row_ok ? fmaf(m[stat_off + qi], kLog2e, __builtin_amdgcn_logf(l[stat_off + qi]))
+               : INFINITY;
+    f32x16 acc[D / 32];
+    zero(acc);
+    // this wave's last key tile (its diagonal one); none if its queries start at or past T
+    const int tlast = qj < T ? qj / kTile : -1;
+    for (int t = 0; t < ntile; ++t) {
+        wait_vm<0>();     // this wave's copies of tile t landed ...
+        __syncthreads();  // ... and every wave's; tile t-1 is no longer read by anyone
+        if (t + 1 < ntile) copy_tile(t + 1);
+        if (t > tlast) continue;
+        const float* Ks = &L.k[t & 1][0];
+        const float* Vs = &L.v[t & 1][0];
+        f32x16 dp = mma_rows<D>(Vs + col * KS + half * (D / 2), doreg, f32x16{});
+        f32x16 s = mma_rows<D>(Ks + col * KS + half * (D / 2), qreg, f32x16{});
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            float p = exp2_fast(fmaf(s[r], c, -lse2));
+            if (t == tlast && t * kTile + acc_row(r, half) > qi) p = 0.0f;
+            s[r] = p * (dp[r] - Dval);  // dS^T (without the scale)
+        }
+        f32x16 part[D / 32];
+        zero(part);
+        mma_cols<D, KS>(Ks, col, half, s, part);
+        add_into(acc, part);
+    }
+    if (row_ok) {
+        store_acc_row<D>(dq + goff, qi, half, acc, scale, gv.row);
+        if (half == 0) Dws[stat_off + qi] = Dval;
+    }
+}
+
+// --------------------------------------------------------------------------------------
 // Backward stage 2 (key-parallel):
 //     dV_j = sum_i P_ij dO_i,   dK_j = scale * sum_i P_ij (dP_ij - D_i) q_i.
 // Task = key block kb (query tiles kb .. nb-1); wave w runs query tiles kb + [n*w/4,
@@ -1306,6 +1414,10 @@ QueueSlot* launch_slot(Family f, std::atomic<unsigned>& ticket, hipStream_t stre
 // B8 H12 T1024 72 -> 74.
 bool fwd_on_shared_tiles(int D, int T) { return D == 128 || (D == 64 && T <= 2048); }
 constexpr bool kDkdvShared = true;
+// The dQ stage on shared tiles under the same rule; measured dQ (us, per-wave -> shared):
+// d = 64: B8 H12 T1024 197 -> 196, B16 H12 T512 123 -> 117, B4 H12 T2048 355 -> 345,
+// B8 H16 T2048 861 -> 876; d = 128: B2 H16 T2048 484 -> 454, B8 H12 T1024 390 -> 386.
+constexpr bool kDqShared = true;
 
 template <int D>
 void fwd_dispatch(const float* q, const float* k, const float* v, float* o, float* m_out,
@@ -1336,6 +1448,16 @@ void dq_dispatch(const float* q, const float* k, const float* v, const float* o,
                  const float* dO, const float* m, const float* l, float* dq, float* Dws, int BH,
                  int T, float scale, const HeadView& xv, const HeadView& ov, const HeadView& gv,
                  hipStream_t stream) {
+    if (kDqShared && fwd_on_shared_tiles(D, T)) {
+        constexpr int kBlock = kTile * kFwdSharedWaves;
+        const int nblk = (T + kBlock - 1) / kBlock;
+        const auto kernel = flash_bwd_dq_f32_shared_kernel<D>;
+        const int res = resident_capacity(kernel, kWave * kFwdSharedWaves, 0);
+        const int serp = BH * nblk <= res ? 1 : -head_group(BH, nblk, res);
+        hipLaunchKernelGGL(kernel, dim3(BH * nblk), dim3(kWave * kFwdSharedWaves), 0, stream, q,
+                           k, v, o, dO, m, l, dq, Dws, BH, T, scale, nblk, xv, ov, gv, serp);
+        return;
+    }
     const int nqb = (T + kTile - 1) / kTile;
     bool ok = true;
     QueueSlot* slot = launch_slot(Family::Dq, g_dq_ticket, stream, ok);

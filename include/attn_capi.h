@@ -336,10 +336,11 @@ int attn_packed_causal_backward_dkdv_f32(const float* qkv, const float* do_ptr,
  * v blocks of dqkv and dS into ds_workspace; dq_ds writes the q block of dqkv as scale * dS K.
  * Stage 1 above computes S and dP again for dQ, two thirds of its fp32 MFMA work; here the
  * dK/dV stage hands them over as dS.  ds_workspace: attn_f32_ds_workspace_bytes(B, H, T,
- * d_head) bytes (B*H heads of n x n fp32, n = T rounded up to 32), 16-byte aligned; its
- * contents need no initialisation.  That function returns 0 where the byte count exceeds
- * SIZE_MAX, and the entry points reject such shapes with ATTN_ERROR_INVALID_DIM.  D, dK and
- * dV bitwise those of the two-stage order, dQ within fp32 rounding of its. */
+ * d_head) bytes (B*H heads of n x n fp32, n = T rounded up to 32, held as 32 x 32 tiles in
+ * a layout private to the two stages), 16-byte aligned; its contents need no initialisation.
+ * That function returns 0 where the byte count exceeds SIZE_MAX, and the entry points reject
+ * such shapes with ATTN_ERROR_INVALID_DIM.  D, dK and dV bitwise those of the two-stage
+ * order, dQ within fp32 rounding of its. */
 size_t attn_f32_ds_workspace_bytes(int B, int H, int T, int d_head);
 /* 1 where a caller that chooses the order per shape should take the dS-first order: d_head
  * 32, 64 or 128 and ds_workspace at most 16 GiB (the same limit as the three-plane path's);
@@ -447,7 +448,8 @@ int attn_fused_causal_backward_dkdv_bf16(const attn_bf16* qkv, const attn_bf16* 
  * `planes` is caller-owned device memory of attn_f32x3_workspace_bytes(B, H, T, d_head)
  * bytes (16-byte aligned): the planes of q, k, v and dO (4 x 3 x B*H*T*d_head bf16), then,
  * where attn_f32x3_backward_uses_ds(B, H, T, d_head) is 1, dS: B*H x n x n fp32 with n = T
- * rounded up to 32 (the one-call backward's dK/dV stage writes it for its dQ stage).  The forward writes the planes of q, k and v; a backward with
+ * rounded up to 32, in 32 x 32 tiles (the one-call backward's dK/dV stage writes it for its
+ * dQ stage).  The forward writes the planes of q, k and v; a backward with
  * kv_planes_ready = 1 reuses them (the caller guarantees that qkv and the workspace are
  * unchanged since that forward), with 0 it splits q, k and v again.  The backward's
  * d_workspace is the B*H*T floats of D, as in the other backward entry points.

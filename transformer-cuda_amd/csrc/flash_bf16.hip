@@ -464,10 +464,10 @@ __device__ __forceinline__ void dkdv_scores(const HalfAddr<D>& a, const bf16x8 (
     }
 }
 
-// Where a wave's dS values of a 32-query step go: row qb of its head's dS (wave-uniform),
-// rows ld elements apart; the lane's element of accumulator row r is at
-// row + (8*(r/4) + r%4)*ld + lane_off (lane_off = 4*half*ld + key).  zero: the lane's key
-// lies past T (written as zeros).
+// Where a wave's dS values of a 32-query step go: the step's dS tile (wave-uniform; rows
+// ld = 32 elements apart); the lane's element of accumulator row r is at
+// row + (8*(r/4) + r%4)*ld + lane_off (lane_off = 4*half*ld + the key's column in the tile).
+// zero: the lane's key lies past T (written as zeros).
 struct DsOut {
     float* row = nullptr;
     int ld = 0;
@@ -529,11 +529,14 @@ __device__ __forceinline__ void dkdv_update(const HalfAddr<D>& a, f32x16& s, con
         }
 #pragma unroll
         for (int r = 0; r < 16; ++r) s[r] *= dp[r];
-        if constexpr (DS) {  // a 32-lane store covers one query's 32 keys (128 bytes)
+        // a 32-lane store covers one query's 32 keys (128 bytes); nontemporal, so that dS
+        // (read once, by the next kernel) does not push the Q/dO plane tiles out of L2 (config
+        // 2 step 346.7 -> 343.1 us; the fp32 kernel's plain stores measured faster there)
+        if constexpr (DS) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 float* row = dso.row + static_cast<size_t>(8 * (r / 4) + r % 4) * dso.ld;
-                row[dso.lane_off] = dso.zero ? 0.0f : s[r];
+                __builtin_nontemporal_store(dso.zero ? 0.0f : s[r], row + dso.lane_off);
             }
         }
 #pragma unroll
@@ -566,9 +569,8 @@ struct DkdvArgs {
     HeadView qv, gtv, kv, gv;
     size_t pstride;
     // NP = 3, optional: dS out (fp32), for a dQ stage that reads it instead of recomputing S
-    // and dP.  Head bh: ds_n x ds_n (T rounded up to 32) from ds + bh*ds_n*ds_n, rows =
-    // queries, columns = keys; written where query >= the first key of the key's 32-key
-    // block, keys >= T as zeros.
+    // and dP: the 32 x 32 tiles of ds_tile (ds_n = T rounded up to 32) at or below the
+    // diagonal, keys >= T as zeros.
     float* ds = nullptr;
     int ds_n = 0;
     int group = 0;  // heads per group of map_block_grouped (NP = 1; set at launch), 0: none
@@ -769,9 +771,10 @@ __global__ __launch_bounds__(kWave* NW, NP == 1 ? 1 : 2) void flash_bwd_dkdv_bf1
             dkdv_scores<D, NP>(h, kr, vr, one, s1, dp1);
             DsOut dso;
             if constexpr (DS) {
-                dso.row = a.ds + (static_cast<size_t>(bh) * a.ds_n + KT * kt) * a.ds_n;
-                dso.ld = a.ds_n;
-                dso.lane_off = static_cast<uint32_t>(4 * half * a.ds_n + kj);
+                static_assert(!DS || KT == 32, "dS tiles are 32 queries deep");
+                dso.row = a.ds + ds_tile(bh, a.ds_n, kt, kw / 32);
+                dso.ld = 32;
+                dso.lane_off = static_cast<uint32_t>(4 * half * 32 + col);
                 dso.zero = kj >= T;
             }
             dkdv_update<D, decltype(mask)::value, NP, DS>(h, s1, dp1, dk_acc, dv_acc, KT * kt,
@@ -1294,21 +1297,21 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_bwd_dq_ds_kernel(DqDsArgs
     // key tiles 0 .. qj/32 (the last one the diagonal); none when the wave's queries start past
     // T.  Rows qj + col < ds_n when qj < T.
     const int nmine = qj < T ? min(qj / KT + 1, ntile) : 0;
-    const float* sbase = a.ds + (static_cast<size_t>(bh) * a.ds_n + min(qj, a.ds_n - 32)) * a.ds_n;
+    const float* sbase = a.ds + ds_tile(bh, a.ds_n, min(qj, a.ds_n - 32) / 32, 0);
     // A slot holds the tile's 32 query rows of 32 keys (128 bytes); 16-byte chunk c of row r
     // at r*128 + 16*(c ^ ((r/2) % 8)).  Copy j: lane i fills slot bytes 1024j + 16i, row
-    // 8j + i/8, so 8 lanes read one whole row.
+    // 8j + i/8, so 8 lanes read one whole row and a copy one contiguous 1 KB of the tile.
     uint32_t soff[kLoads];
 #pragma unroll
     for (int j = 0; j < kLoads; ++j) {
         const int r = 8 * j + lane / 8;
         const int c = (lane % 8) ^ ((r >> 1) & 7);
-        soff[j] = static_cast<uint32_t>((r * a.ds_n + 4 * c) * 4);
+        soff[j] = static_cast<uint32_t>((r * 32 + 4 * c) * 4);
     }
     const uint32_t s_lds = lds_addr(sms[wave][0]);
     constexpr uint32_t kSlot = kLoads * 1024;
     auto copy_ds = [&](int kt) {
-        const float* b = sbase + KT * kt;
+        const float* b = sbase + static_cast<size_t>(kt) * 1024;  // tile (qj/32, kt)
 #pragma unroll
         for (int j = 0; j < kLoads; ++j)
             dma_dwordx4(b, s_lds + static_cast<uint32_t>(kt & 1) * kSlot + 1024 * j, soff[j]);

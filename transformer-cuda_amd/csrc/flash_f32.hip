@@ -967,15 +967,14 @@ __device__ __forceinline__ void dkdv_chunk(const float* __restrict__ qh,
             ds[r] = p * (dp[r] - St[1][qr]);
         }
         if constexpr (DS) {
-            // dS of the tile, query-major: row t*32 + acc_row(r, half), column kj; a 32-lane
+            // dS tile (t, kb) of the head (ds_tile): row acc_row(r, half), column col; a 32-lane
             // store covers one query's 32 keys (128 bytes).  Keys past T get zeros.
             const int kj = kb * kTile + col;
-            float* row = ds_head + static_cast<size_t>(t * kTile) * ds_n;
-            const uint32_t loff = static_cast<uint32_t>(4 * half * ds_n + kj);
+            float* tile = ds_head + ds_tile(0, ds_n, t, kb);
+            const uint32_t loff = static_cast<uint32_t>(4 * half * kTile + col);
 #pragma unroll
             for (int r = 0; r < 16; ++r)
-                row[static_cast<size_t>(8 * (r / 4) + r % 4) * ds_n + loff] =
-                    kj < T ? ds[r] : 0.0f;
+                tile[(8 * (r / 4) + r % 4) * kTile + loff] = kj < T ? ds[r] : 0.0f;
         }
         f32x16 part[D / 32];
         zero(part);
@@ -993,8 +992,8 @@ __device__ __forceinline__ void dkdv_chunk(const float* __restrict__ qh,
     }
 }
 
-// DS: dS written out as well (ds: B*H heads of ds_n x ds_n fp32, rows = queries), for the
-// dQ-from-dS kernel below.
+// DS: dS written out as well (the tiles of ds_tile at or below the diagonal, ds_n = T
+// rounded up to 32), for the dQ-from-dS kernel below.
 template <int D, bool DS>
 TCAMD_F32_KERNEL(kDkdvWaves) void flash_bwd_dkdv_f32_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
@@ -1170,14 +1169,13 @@ __global__ __launch_bounds__(kWave* kFwdSharedWaves) void flash_bwd_dkdv_f32_sha
                 dsv[r] = p * (dp[r] - St1[qr]);
             }
             if constexpr (DS) {
-                // dS of the tile, query-major: row t*32 + acc_row(r, half), column kj; a 32-lane
-                // store covers one query's 32 keys (128 bytes).  Keys past T get zeros.
-                float* row = ds_head + static_cast<size_t>(t * kTile) * ds_n;
-                const uint32_t loff = static_cast<uint32_t>(4 * half * ds_n + kj);
+                // dS tile (t, kw/32) of the head (ds_tile): row acc_row(r, half), column col; a
+                // 32-lane store covers one query's 32 keys (128 bytes).  Keys past T get zeros.
+                float* tile = ds_head + ds_tile(0, ds_n, t, kw / kTile);
+                const uint32_t loff = static_cast<uint32_t>(4 * half * kTile + col);
 #pragma unroll
                 for (int r = 0; r < 16; ++r)
-                    row[static_cast<size_t>(8 * (r / 4) + r % 4) * ds_n + loff] =
-                        kj < T ? dsv[r] : 0.0f;
+                    tile[(8 * (r / 4) + r % 4) * kTile + loff] = kj < T ? dsv[r] : 0.0f;
             }
             f32x16 part[D / 32];
             zero(part);
@@ -1300,19 +1298,20 @@ __global__ __launch_bounds__(kWave * 4) void flash_bwd_dq_ds_f32_kernel(
     // key tiles 0 .. qj/32 (the last one the diagonal); none when the wave's queries start past
     // T.  Rows qj + col < ds_n when qj < T.
     const int nmine = qj < T ? min(qj / kTile + 1, ntile) : 0;
-    const float* sbase = ds + (static_cast<size_t>(bh) * ds_n + min(qj, ds_n - kTile)) * ds_n;
+    const float* sbase = ds + ds_tile(bh, ds_n, min(qj, ds_n - kTile) / kTile, 0);
     // A slot holds the tile's 32 query rows of 32 keys; 16-byte chunk c of row r at
-    // r*128 + 16*(c ^ ((r/2) % 8)).  Copy j: lane i fills slot bytes 1024j + 16i, row 8j + i/8.
+    // r*128 + 16*(c ^ ((r/2) % 8)).  Copy j: lane i fills slot bytes 1024j + 16i, row 8j + i/8
+    // (one contiguous 1 KB of the tile).
     uint32_t soff[kLoads];
 #pragma unroll
     for (int j = 0; j < kLoads; ++j) {
         const int r = 8 * j + lane / 8;
         const int c = (lane % 8) ^ ((r >> 1) & 7);
-        soff[j] = static_cast<uint32_t>((r * ds_n + 4 * c) * 4);
+        soff[j] = static_cast<uint32_t>((r * kTile + 4 * c) * 4);
     }
     const uint32_t s_lds = lds_addr(sms[wave][0]);
     auto copy_ds = [&](int kt) {
-        const float* b = sbase + kTile * kt;
+        const float* b = sbase + static_cast<size_t>(kt) * 1024;  // tile (qj/32, kt)
 #pragma unroll
         for (int j = 0; j < kLoads; ++j)
             dma_dwordx4(b, s_lds + static_cast<uint32_t>(kt & 1) * kSlot + 1024 * j, soff[j]);

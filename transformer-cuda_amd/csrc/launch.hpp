@@ -122,9 +122,8 @@ void launch_flash_bwd_dq_f32x3(const float* q, const HeadView& qv, const uint16_
                                float* Dws, int BH, int T, int d, float scale,
                                hipStream_t stream);
 // Stage 2 (dK, dV): q and dO plane tensors (view tv), k and v fp32 rows (view kv); dk, dv
-// fp32 (view gv).  Unless ds is null, dS is written out as well (fp32), for
-// launch_flash_bwd_dq_ds_f32x3: head bh at ds + bh*n*n, n = ds_rows(T), rows = queries,
-// columns = keys (keys >= T: zeros), below the diagonal in 32 x 32 blocks.
+// fp32 (view gv).  Unless ds is null, dS is written out as well (fp32, the tiles of ds_tile
+// at or below the diagonal; keys >= T: zeros), for launch_flash_bwd_dq_ds_f32x3.
 void launch_flash_bwd_dkdv_f32x3(const uint16_t* q, const uint16_t* dO, const HeadView& tv,
                                  size_t pstride, const float* k, const float* v,
                                  const HeadView& kv, const float* m, const float* l,
@@ -133,6 +132,13 @@ void launch_flash_bwd_dkdv_f32x3(const uint16_t* q, const uint16_t* dO, const He
                                  float* ds = nullptr);
 // The side of a head's square dS: T rounded up to 32.
 constexpr int ds_rows(int T) { return (T + 31) / 32 * 32; }
+// The dS area of the dS-first backwards: B*H heads of n x n fp32 (n = ds_rows(T)), each as
+// (n/32) x (n/32) tiles of 32 queries x 32 keys; tile (qt, kt) of head bh is 4 KB contiguous
+// from element ds_tile(bh, n, qt, kt), rows (queries) of 128 bytes.  The dK/dV stage writes
+// the tiles with kt <= qt and the dQ stage reads them, each tile as one contiguous block.
+constexpr size_t ds_tile(int bh, int n, int qt, int kt) {
+    return ((static_cast<size_t>(bh) * (n / 32) + qt) * (n / 32) + kt) * 1024;
+}
 // Before stage 2 when stage 1 comes after it: D = rowsum(dO o O) into Dws (the same
 // operations as stage 1's) and the planes of dO (laid out as k's, view kv).
 void launch_bwd_prep_f32x3(const float* o, const float* dO, const HeadView& ov,

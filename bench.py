@@ -300,11 +300,13 @@ class PathRunner:
                 if self.kernel_work(n)[1] == "flop"]
         return max(flop)[1]
 
-    def timed(self, steps, warmup, ramp_s=0.0, breakdown_steps=20):
+    def timed(self, steps, warmup, ramp_s=0.0, breakdown_steps=20, event_every=None):
         """Time `steps` steps after `ramp_s` seconds of untimed steps and `warmup` more, with
-        events on the launch stream around the dominant launch of every step only; then the
-        other launches' durations from `breakdown_steps` more steps (not timed) with an event
-        after every launch."""
+        events on the launch stream around the dominant launch of every `event_every`-th
+        timed step only (default steps // 20: about 20 sampled steps spread over the run, every
+        step below 40; an event record costs GPU time between launches); then the other
+        launches' durations from `breakdown_steps` more steps (not timed) with an event after
+        every launch."""
         torch = self.torch
         t_end = time.perf_counter() + ramp_s
         while time.perf_counter() < t_end:
@@ -317,21 +319,24 @@ class PathRunner:
         stream = torch.cuda.current_stream()
         launches = self.launches()
         dom = self.dominant()
-        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-               for _ in range(steps)]
+        every = event_every if event_every else max(1, steps // 20)
+        sampled = range(0, steps, every)
+        evs = {i: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+               for i in sampled}
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         for i in range(steps):
+            ev = evs.get(i)
             for name, fn in launches:
-                if name == dom:
-                    evs[i][0].record(stream)
+                if ev is not None and name == dom:
+                    ev[0].record(stream)
                     fn()
-                    evs[i][1].record(stream)
+                    ev[1].record(stream)
                 else:
                     fn()
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
-        dom_ms = sum(a.elapsed_time(b) for a, b in evs) / steps
+        dom_ms = sum(a.elapsed_time(b) for a, b in evs.values()) / len(evs)
         n = max(1, breakdown_steps)
         evb = [[torch.cuda.Event(enable_timing=True) for _ in range(len(launches) + 1)]
                for _ in range(n)]

@@ -78,6 +78,24 @@ def test_shapes_vs_oracle(lib, T, d):
     np.testing.assert_allclose(got["l"], want.l.numpy(), rtol=1e-5)
 
 
+@pytest.mark.parametrize("d,T", [(64, 2048), (64, 2080), (128, 2080)])
+def test_shared_tile_boundary_vs_oracle(lib, d, T):
+    """Either side of the sequence length where the fp32 kernels change form (d = 64: the
+    forward, dQ and dK/dV on tiles shared by a 128-row workgroup up to T = 2048, the
+    persistent per-wave kernels beyond; d = 128: shared at every T)."""
+    B, H = 1, 2
+    q, k, v, do = ref.seeded_inputs(B, H, T, d, seed=T + d)
+    scale = default_scale(d)
+    want = ref.attention_fwd_bwd(q, k, v, do, scale, dtype=torch.float32)
+    got = gpu_fwd_bwd(lib, q, k, v, do, scale)
+    for n in ("o", "dq", "dk", "dv"):
+        e = max_abs(got[n], getattr(want, n).numpy())
+        print(f"T={T} d={d} {n}: max-abs {e:.2e}")
+        assert e <= TOL, n
+    assert max_abs(got["m"], want.m.numpy()) <= TOL
+    np.testing.assert_allclose(got["l"], want.l.numpy(), rtol=1e-5)
+
+
 def test_reference_kat_exact(lib):
     """tests/test_kernels.cu:210-284 with the exact answer (O=1, dQ=dK=0, dV closed form)."""
     T, d = 8, 32

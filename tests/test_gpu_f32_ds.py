@@ -51,8 +51,10 @@ def both_orders(lib, qkv, do, B, H, T, d, scale, merged):
     return o, two, D2, one, D1
 
 
+# (1, 2, 2048, 64) and (1, 2, 2080, 64): either side of the length where the d = 64 kernels
+# change from the shared-tile to the per-wave form
 SHAPES = [(1, 1, 1, 64), (2, 3, 17, 32), (1, 2, 100, 64), (2, 2, 257, 128), (2, 4, 640, 64),
-          (1, 1, 1000, 32), (2, 3, 300, 128)]
+          (1, 1, 1000, 32), (2, 3, 300, 128), (1, 2, 2048, 64), (1, 2, 2080, 64)]
 
 
 @pytest.mark.parametrize("B,H,T,d", SHAPES)

@@ -47,6 +47,8 @@
 // computation of S and dP.
 #include <math.h>
 
+#include <type_traits>
+
 #include "bf16_tile.hpp"
 #include "device_common.hpp"
 #include "launch.hpp"
@@ -1322,17 +1324,30 @@ __global__ __launch_bounds__(kWave * 4) void flash_bwd_dq_ds_f32_kernel(
     if (1 < nmine) copy_ds(1);
     f32x16 acc[D / 32];
     zero(acc);
-    for (int kt = 0; kt < ntile; ++kt) {
+    // Every wave issues kMaxCopy copies per K tile when the tile's copy instructions divide
+    // evenly among the waves.  STEADY: kt + 2 < nmine (the wave has two more tiles of its own,
+    // and nmine <= ntile), so the copies in flight, and the waits, are constants; the steps
+    // before the last two of the wave's own run in a loop of their own, without the general
+    // case's branches.
+    constexpr bool kEven = Sh::kInst % kWv == 0;
+    auto step = [&](int kt, auto steady_c) {
+        constexpr bool steady = decltype(steady_c)::value && kEven;
         // this wave's copies of K tile kt landed: outstanding may be only its dS of tile kt
         // and tile kt+1's copies ...
-        wait_vm_at_most((kt < nmine ? kLoads : 0) + (kt + 1 < ntile ? ncopy : 0) +
-                        (kt + 1 < nmine ? kLoads : 0));
+        if constexpr (steady)
+            wait_vm<2 * kLoads + kMaxCopy>();
+        else
+            wait_vm_at_most((kt < nmine ? kLoads : 0) + (kt + 1 < ntile ? ncopy : 0) +
+                            (kt + 1 < nmine ? kLoads : 0));
         __syncthreads();  // ... and every wave's; tile kt-1's buffer is no longer read
-        if (kt + 2 < ntile) copy_tile(kt + 2, lds_addr(smk[(kt + 2) % NB]));
-        if (kt >= nmine) continue;
+        if (steady || kt + 2 < ntile) copy_tile(kt + 2, lds_addr(smk[(kt + 2) % NB]));
+        if (!steady && kt >= nmine) return;
         // dS of tile kt landed: outstanding may be only tile kt+1's and K tile kt+2's copies
-        wait_vm_at_most((kt + 1 < ntile ? ncopy : 0) + (kt + 1 < nmine ? kLoads : 0) +
-                        (kt + 2 < ntile ? ncopy : 0));
+        if constexpr (steady)
+            wait_vm<kLoads + 2 * kMaxCopy>();
+        else
+            wait_vm_at_most((kt + 1 < ntile ? ncopy : 0) + (kt + 1 < nmine ? kLoads : 0) +
+                            (kt + 2 < ntile ? ncopy : 0));
         // B operand in accumulator layout: element r = key acc_row(r, half) = 8(r/4) +
         // 4 half + r%4 of this lane's query: run j = r/4, chunk 2j + half of the row
         f32x16 sb;
@@ -1344,7 +1359,7 @@ __global__ __launch_bounds__(kWave * 4) void flash_bwd_dq_ds_f32_kernel(
 #pragma unroll
             for (int e = 0; e < 4; ++e) sb[4 * j + e] = x[e];
         }
-        if (kt + 2 < nmine) {
+        if (steady || kt + 2 < nmine) {
             wait_lds();  // the slot's reads are done before the copy into it starts
             copy_ds(kt + 2);
         }
@@ -1352,7 +1367,10 @@ __global__ __launch_bounds__(kWave * 4) void flash_bwd_dq_ds_f32_kernel(
         zero(part);
         mma_cols<D, KS>(smk[kt % NB], col, half, sb, part);
         add_into(acc, part);
-    }
+    };
+    int kt = 0;
+    for (; kt + 2 < nmine; ++kt) step(kt, std::true_type{});
+    for (; kt < ntile; ++kt) step(kt, std::false_type{});
     const int qi = qj + col;
     if (qi < T) store_acc_row<D>(dq + gv.off(bh), qi, half, acc, scale, gv.row);
 }

@@ -150,12 +150,23 @@ __device__ __forceinline__ void load_operand(bf16x8 (&dst)[D / 16][NP],
 // Stage 1: D and dQ.
 // ---------------------------------------------------------------------------------------
 
+// How -lse2 and -D enter S^T and dP^T.  A lane holds one query, so its statistic is the same
+// in all 16 rows of its accumulator: with INIT each product's accumulator starts from the
+// statistic itself (a 16-register copy per lane, kept for the whole task: 32 VGPRs per
+// sub-block, no MFMA; the statistic exact in fp32); without it, from one more contraction
+// step, the A operand `one` times a statistic chunk ((hi, lo) bf16 terms; 8 VGPRs per
+// sub-block, two more MFMAs per half tile).  INIT where the registers allow it: one
+// sub-block per wave.
+template <int NSUB>
+constexpr bool kDqStatInit = NSUB == 1;
+
 // One 32-query sub-block of a wave.
 template <int D, int NP>
 struct DqSub {
     bf16x8 q[D / 16][NP];  // c * Q row of query col (B operand over d)
     bf16x8 g[D / 16][NP];  // dO row
     bf16x8 xs, xd;         // statistic chunks: -lse2 (-1e30 for padded queries: P = 0), -D
+    f32x16 ls, ld;         // INIT: -lse2 and -D in every row
     f32x16 acc[D / 32];    // dQ^T
 };
 
@@ -190,7 +201,7 @@ __device__ __forceinline__ float chunk_dot_tree(const float* __restrict__ gp,
 // pre-multiplied by c = scale*log2 e (NP = 1: rounded to bf16, one extra rounding of ~2^-9
 // relative per element; NP = 3: in fp32, then split), so that the scores come out in the
 // log2 domain.  D = rowsum(dO o O) in fp32 from the stored O and dO.
-template <int D, int NP>
+template <int D, int NP, bool INIT>
 __device__ __forceinline__ void dq_init(DqSub<D, NP>& sb, const InT<NP>* __restrict__ qh,
                                         const InT<NP>* __restrict__ oh,
                                         const InT<NP>* __restrict__ gh,
@@ -220,8 +231,16 @@ __device__ __forceinline__ void dq_init(DqSub<D, NP>& sb, const InT<NP>* __restr
         if (half == 0) Dws[stat_off + qi] = dlt;
         nl = -(m[stat_off + qi] * kLog2e + log2f(l[stat_off + qi]));
     }
-    sb.xs = stat_chunk<NP>(nl, half);
-    sb.xd = stat_chunk<NP>(-dlt, half);
+    if constexpr (INIT) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            sb.ls[r] = nl;
+            sb.ld[r] = -dlt;
+        }
+    } else {
+        sb.xs = stat_chunk<NP>(nl, half);
+        sb.xd = stat_chunk<NP>(-dlt, half);
+    }
 #pragma unroll
     for (int dt = 0; dt < D / 32; ++dt) sb.acc[dt] = f32x16{};
 }
@@ -248,8 +267,8 @@ __device__ __forceinline__ void dq_ds(f32x16& s, const f32x16& dp, bf16x8 (&db)[
 // One 32-key half tile for sub-block 1, and sub-block 0 too when BOTH.  ka/va: this lane's
 // row-read addresses in plane 0 of the K / V tile; kta: transposing-read addresses in plane
 // 0 of the K tile; plane i lies i tile sizes further.  -lse2 and -D enter S^T and dP^T as
-// one more contraction step: the A operand `one` times the sub-block's statistic chunks.
-template <int D, bool BOTH, int NP>
+// the products' initial accumulators (INIT) or as one more contraction step (kDqStatInit).
+template <int D, bool BOTH, int NP, bool INIT>
 __device__ __forceinline__ void dq_half(int kb, const uint32_t (&ka)[D / 16],
                                         const uint32_t (&va)[D / 16],
                                         const uint32_t (&kta)[D / 32], const bf16x8& one,
@@ -257,8 +276,13 @@ __device__ __forceinline__ void dq_half(int kb, const uint32_t (&ka)[D / 16],
                                         int col, int half) {
     constexpr uint32_t kPlane = Swz<D, kKeyTileDq<NP>>::kBytes;
     f32x16 s0, s1, p0, p1;
-    s1 = mfma_32x32x16_bf16(one, sb1.xs, f32x16{});
-    if constexpr (BOTH) s0 = mfma_32x32x16_bf16(one, sb0.xs, f32x16{});
+    if constexpr (INIT) {
+        s1 = sb1.ls;
+        if constexpr (BOTH) s0 = sb0.ls;
+    } else {
+        s1 = mfma_32x32x16_bf16(one, sb1.xs, f32x16{});
+        if constexpr (BOTH) s0 = mfma_32x32x16_bf16(one, sb0.xs, f32x16{});
+    }
 #pragma unroll
     for (int st = 0; st < D / 16; ++st) {
         bf16x8 a[NP];
@@ -267,8 +291,13 @@ __device__ __forceinline__ void dq_half(int kb, const uint32_t (&ka)[D / 16],
         s1 = mma_planes<NP>(a, sb1.q[st], s1);
         if constexpr (BOTH) s0 = mma_planes<NP>(a, sb0.q[st], s0);
     }
-    p1 = mfma_32x32x16_bf16(one, sb1.xd, f32x16{});
-    if constexpr (BOTH) p0 = mfma_32x32x16_bf16(one, sb0.xd, f32x16{});
+    if constexpr (INIT) {
+        p1 = sb1.ld;
+        if constexpr (BOTH) p0 = sb0.ld;
+    } else {
+        p1 = mfma_32x32x16_bf16(one, sb1.xd, f32x16{});
+        if constexpr (BOTH) p0 = mfma_32x32x16_bf16(one, sb0.xd, f32x16{});
+    }
 #pragma unroll
     for (int st = 0; st < D / 16; ++st) {
         bf16x8 a[NP];
@@ -358,12 +387,13 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_bwd_dq_bf16_kernel(DqArgs
     };
     copy_tile(0);
 
+    constexpr bool kInit = kDqStatInit<NSUB>;
     DqSub<D, NP> sb0, sb1;
-    dq_init<D, NP>(sb1, a.q + qoff, a.o + ooff, a.dO + ooff, a.m, a.l, a.Dws, a.qv.row,
-                   a.ov.row, stat_off, qj1 + col, T, half, c);
+    dq_init<D, NP, kInit>(sb1, a.q + qoff, a.o + ooff, a.dO + ooff, a.m, a.l, a.Dws, a.qv.row,
+                          a.ov.row, stat_off, qj1 + col, T, half, c);
     if constexpr (NSUB == 2)
-        dq_init<D, NP>(sb0, a.q + qoff, a.o + ooff, a.dO + ooff, a.m, a.l, a.Dws, a.qv.row,
-                       a.ov.row, stat_off, qj0 + col, T, half, c);
+        dq_init<D, NP, kInit>(sb0, a.q + qoff, a.o + ooff, a.dO + ooff, a.m, a.l, a.Dws,
+                              a.qv.row, a.ov.row, stat_off, qj0 + col, T, half, c);
     if constexpr (NP > 1) {
         if (a.gp != nullptr) {
             store_planes<D, NP>(a.gp + koff, a.pstride, sb1.g, qj1 + col, T, half);
@@ -401,11 +431,11 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_bwd_dq_bf16_kernel(DqArgs
     int hh = 0;
     for (; hh < hA; ++hh) {
         tile_sync(hh);
-        dq_half<D, true, NP>(32 * hh, ka, va, kta, one, sb0, sb1, qj0, qj1, col, half);
+        dq_half<D, true, NP, kInit>(32 * hh, ka, va, kta, one, sb0, sb1, qj0, qj1, col, half);
     }
     for (; hh < hB; ++hh) {
         tile_sync(hh);
-        dq_half<D, false, NP>(32 * hh, ka, va, kta, one, sb0, sb1, qj0, qj1, col, half);
+        dq_half<D, false, NP, kInit>(32 * hh, ka, va, kta, one, sb0, sb1, qj0, qj1, col, half);
     }
     for (; hh < hend; ++hh) tile_sync(hh);
 

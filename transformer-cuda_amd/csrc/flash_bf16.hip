@@ -18,16 +18,18 @@
 // the score product, whose rows are the contracted positions.  With NP = 3 the tiles come
 // from plane tensors in HBM and the register operands are split from the fp32 rows.
 //
-// Stage 1, per 32-key half tile and 32-query sub-block (d = 64, NP = 1: 14 MFMAs):
-//   S'^T = K (cQ)^T - lse2   A = K rows, B = c*Q (VGPRs), plus one contraction step
-//   dP'^T = V dO^T - D       A = V rows, B = dO (VGPRs), plus one contraction step
+// Stage 1, per 32-key half tile and 32-query sub-block (d = 64, NP = 1: 12 MFMAs):
+//   S'^T = K (cQ)^T - lse2   A = K rows, B = c*Q (VGPRs), accumulator from -lse2
+//   dP'^T = V dO^T - D       A = V rows, B = dO (VGPRs), accumulator from -D
 //   dS^T = 2^S'^T o dP'^T    lane l holds query l%32
 //   dQ^T += K^T dS^T         A = K^T (transposing reads of the K tile), B = dS^T
-// The per-query -lse2 and -D enter the products as one more 16-wide contraction step: the
-// A operand (1, 1, 0, ...) times a statistic chunk (hi, lo, 0, ...) (NP = 3: three ones and
-// three terms).  A workgroup owns 256 queries (d <= 64; wave w: sub-blocks w and 7-w, as the
-// forward) or 128 (one sub-block per wave: d = 128, small grids).  NP = 3 streams 32-key
-// tiles, so that the double-buffered K and V planes leave room for two workgroups per CU.
+// Lane l's -lse2 and -D are the same in all 16 rows of its accumulators: with one sub-block
+// per wave (bf16, d = 128, small grids; 128 queries per workgroup) the products start from
+// them (kDqStatInit); with two (three planes at d <= 64 on large grids: 256 queries, wave w
+// sub-blocks w and 7-w, as the forward) they enter as one more 16-wide contraction step,
+// the A operand (1, 1, 0, ...) times a statistic chunk (hi, lo, 0, ...) (NP = 3: three ones
+// and three terms).  NP = 3 streams 32-key tiles, so that the double-buffered K and V planes
+// leave room for two workgroups per CU.
 //
 // Stage 2, per 32-query half tile and a wave's 32 keys (d = 64, NP = 1: 18 MFMAs):
 //   S  = Q K^T        A = Q rows,  B = K (VGPRs)
@@ -1447,11 +1449,16 @@ void dq_launch(DqArgs<NP> a, hipStream_t stream) {
 
 template <int D, int NP>
 void dq_dispatch(const DqArgs<NP>& a, hipStream_t stream) {
-    // d = 128 holds one sub-block per wave (registers)
-    if (D >= 128 || use_single_subblock(a.BH, a.T))
+    // One sub-block per wave, whose statistics enter S^T and dP^T as initial accumulators
+    // (kDqStatInit), for bf16 (B16 H16 T2048 d64 dQ 230.3 -> 217.9 us, B8 H16 T2048 122.9 ->
+    // 112.8, against two sub-blocks with the fold step) and at d = 128 (registers); three
+    // planes keep two sub-blocks on grids that fill the chip.
+    if constexpr (NP == 1 || D >= 128)
+        dq_launch<D, 1, NP>(a, stream);
+    else if (use_single_subblock(a.BH, a.T))
         dq_launch<D, 1, NP>(a, stream);
     else
-        dq_launch<D, (D >= 128 ? 1 : 2), NP>(a, stream);
+        dq_launch<D, 2, NP>(a, stream);
 }
 
 template <int D, int NP>

@@ -422,7 +422,8 @@ __device__ __forceinline__ void static_for(F&& f) {
 // MFMA.  Per 32-key half tile and wave it issues 9 MFMAs and about 80 VALU instructions, a
 // row maximum (a max tree, a cross-half swap and a wave vote) among them.  Here the
 // exponentials are taken against M, set to the row's maximum over the wave's first half tile
-// and carried by the fold's (hi, lo) terms; no maximum is formed after that.  Instead each
+// and carried into the scores as their accumulators' initial value (kFwdStatInit); no
+// maximum is formed after that.  Instead each
 // half tile's row sum of P = 2^(s - M), which l needs anyway, is compared with 2^16: only a
 // row whose scores rose more than ~11 (log2 units) above M (or an inf or NaN) makes the wave
 // recompute the half tile's scores from the same LDS tile, raise M to their maximum and scale
@@ -432,11 +433,18 @@ __device__ __forceinline__ void static_for(F&& f) {
 // maximum.  (m, l) = (M, l) honour the statistics contract P_ij = exp(scale*q_i.k_j - m_i) /
 // l_i with the log-sum-exp m + ln l; m is a score of the row's first keys (or the maximum of
 // a later half tile that raised it), not necessarily the row maximum.  Every LDS address of
-// the unrolled loop is a lane offset plus a constant.  Per half tile at d = 64: 9 MFMAs and
+// the unrolled loop is a lane offset plus a constant.  Per half tile at d = 64: 8 MFMAs (9
+// with -M as a contraction step: config 3 forward 157.6 -> 151.6 us without it) and
 // 16 v_exp_f32, 8 conversions, the 17 steps of the row sum and a compare of VALU work.
 // ---------------------------------------------------------------------------------------
 
 constexpr float kRaiseSum = 65536.0f;  // a half tile's row sum that makes M rise
+
+// How -M enters S^T.  A lane holds one query, so M is the same in all 16 rows of its
+// accumulator: with kFwdStatInit the product starts from -M (a 16-register copy per lane,
+// exact in fp32), otherwise from one more contraction step, the A operand `one` times the
+// (hi, lo) bf16 terms of -M (M rounded to 16 bits so that the two terms hold it exactly).
+constexpr bool kFwdStatInit = true;
 
 template <int D>
 struct FoldState {
@@ -444,29 +452,37 @@ struct FoldState {
     float l;             // row sum of 2^(s - M)
     float m_used;        // M, log2 units of c*q.k
     bf16x8 xs;           // statistic chunk of -M (zero before the first half tile)
+    f32x16 ms;           // kFwdStatInit: -M in every row
 };
 
-// The (hi, lo) terms of -m as the fold's statistic chunk; M := -(hi + lo), m to 16 bits.
+// M := m (the fold: m to 16 bits, and its (hi, lo) terms as the statistic chunk).
 template <int D>
 __device__ __forceinline__ void set_ref(FoldState<D>& st, float m, int half) {
-    const u16x4 t = stat_terms<1>(-m);
-    st.m_used = -(bf16_bits_to_f32(t[0]) + bf16_bits_to_f32(t[1]));
-    u16x8 x = u16x8{};
-    if (half == 0) {
-        x[0] = t[0];
-        x[1] = t[1];
+    if constexpr (kFwdStatInit) {
+        st.m_used = m;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) st.ms[r] = -m;
+    } else {
+        const u16x4 t = stat_terms<1>(-m);
+        st.m_used = -(bf16_bits_to_f32(t[0]) + bf16_bits_to_f32(t[1]));
+        u16x8 x = u16x8{};
+        if (half == 0) {
+            x[0] = t[0];
+            x[1] = t[1];
+        }
+        st.xs = __builtin_bit_cast(bf16x8, x);
     }
-    st.xs = __builtin_bit_cast(bf16x8, x);
 }
 
-// S^T - M of one half tile: the fold step, then K (cQ)^T over the head dimension.
+// S^T - M of one half tile: -M (FOLD), then K (cQ)^T over the head dimension.
 template <int D, bool FOLD, bool MASK>
 __device__ __forceinline__ f32x16 fold_scores(uint32_t kbase, const uint32_t (&koff)[D / 16],
                                               const bf16x8 (&qr)[D / 16], const FoldState<D>& st,
                                               int kb, int qj, int col, int half,
                                               const bf16x8& one) {
     f32x16 s = f32x16{};
-    if constexpr (FOLD) s = mfma_32x32x16_bf16(one, st.xs, s);
+    if constexpr (FOLD && kFwdStatInit) s = st.ms;
+    if constexpr (FOLD && !kFwdStatInit) s = mfma_32x32x16_bf16(one, st.xs, s);
 #pragma unroll
     for (int i = 0; i < D / 16; ++i) s = mfma_32x32x16_bf16(lds_b128(koff[i] + kbase), qr[i], s);
     if constexpr (MASK) {

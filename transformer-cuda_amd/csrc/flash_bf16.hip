@@ -933,6 +933,12 @@ struct DkdvProgram {
     static constexpr int local(int i) {
         return i < 2 * kScores ? i % kScores : (i - 2 * kScores) % kUpd;
     }
+    // A half's score ops alternate between its two products, S' (even local index) and dP'
+    // (odd), so that consecutive MFMAs are independent (a lone dependent chain issues at
+    // about 3/4 of the MFMA rate with one wave per SIMD); step 0 of each is the statistic
+    // fold, steps 1..NS its head-dimension chunks.
+    static constexpr bool score_dp(int j) { return j % 2 == 1; }
+    static constexpr int score_step(int j) { return j / 2; }
     // Softmax task t (0..15) of a half runs at slot `slot(t, n)` of the n ops it overlaps:
     // tasks 0..7 take 2^S, mask and pack P for elements 2t, 2t+1; tasks 8..15 form and pack
     // dS for elements 2(t-8), 2(t-8)+1.
@@ -1050,10 +1056,14 @@ __global__ __launch_bounds__(kWave * kWaves, D >= 128 ? 1 : 2) void flash_bwd_dk
         constexpr uint32_t hb = static_cast<uint32_t>(BUF) * kBuf + static_cast<uint32_t>(h) * S::rows(32);
         constexpr uint32_t xb = static_cast<uint32_t>(BUF * KT + h * 32) * 16u;
         if constexpr (Prog::is_score(i)) {
-            if constexpr (j == 0) return lds_b128(soff + (qx_lds + xb));
-            else if constexpr (j <= NS) return lds_b128(roff[j - 1] + (q_lds + hb));
-            else if constexpr (j == NS + 1) return lds_b128(soff + (gx_lds + xb));
-            else return lds_b128(roff[j - NS - 2] + (g_lds + hb));
+            constexpr int st = Prog::score_step(j);
+            if constexpr (!Prog::score_dp(j)) {
+                if constexpr (st == 0) return lds_b128(soff + (qx_lds + xb));
+                else return lds_b128(roff[st - 1] + (q_lds + hb));
+            } else {
+                if constexpr (st == 0) return lds_b128(soff + (gx_lds + xb));
+                else return lds_b128(roff[st - 1] + (g_lds + hb));
+            }
         } else {
             constexpr int p = j / 2, dt = p / 2, u = p % 2;
             constexpr uint32_t off = hb + static_cast<uint32_t>(u) * Swz<D>::rows(16);
@@ -1066,10 +1076,14 @@ __global__ __launch_bounds__(kWave * kWaves, D >= 128 ? 1 : 2) void flash_bwd_dk
         constexpr int i = decltype(I)::value;
         constexpr int h = Prog::half(i), j = Prog::local(i);
         if constexpr (Prog::is_score(i)) {
-            if constexpr (j == 0) r.s[h] = mfma_32x32x16_bf16(x, one, f32x16{});
-            else if constexpr (j <= NS) r.s[h] = mfma_32x32x16_bf16(x, kr[j - 1][0], r.s[h]);
-            else if constexpr (j == NS + 1) r.dp[h] = mfma_32x32x16_bf16(x, one, f32x16{});
-            else r.dp[h] = mfma_32x32x16_bf16(x, vr[j - NS - 2][0], r.dp[h]);
+            constexpr int st = Prog::score_step(j);
+            if constexpr (!Prog::score_dp(j)) {
+                if constexpr (st == 0) r.s[h] = mfma_32x32x16_bf16(x, one, f32x16{});
+                else r.s[h] = mfma_32x32x16_bf16(x, kr[st - 1][0], r.s[h]);
+            } else {
+                if constexpr (st == 0) r.dp[h] = mfma_32x32x16_bf16(x, one, f32x16{});
+                else r.dp[h] = mfma_32x32x16_bf16(x, vr[st - 1][0], r.dp[h]);
+            }
         } else {
             constexpr int p = j / 2, dt = p / 2, u = p % 2;
             if constexpr (j % 2 == 0) dv_acc[dt] = mfma_32x32x16_bf16(x, r.p[h][u], dv_acc[dt]);

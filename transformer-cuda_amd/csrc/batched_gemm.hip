@@ -192,9 +192,9 @@ __global__ __launch_bounds__(kThreads) void bgemm_f32_tiled_kernel(
     // elements of the contiguous dimension.
     f32x4 ra[kA4], rb[kB4];
     auto load_op = [&](auto kcont, const float* src, int ld, int r0, int rlim, int k0, auto& reg,
-                       auto nfrag, auto rows) {
+                       auto nfrag) {
         constexpr bool KC = decltype(kcont)::value;
-        constexpr int NF = decltype(nfrag)::value, R = decltype(rows)::value;
+        constexpr int NF = decltype(nfrag)::value;
 #pragma unroll
         for (int i = 0; i < NF; ++i) {
             const int f = tid + kThreads * i;
@@ -208,9 +208,9 @@ __global__ __launch_bounds__(kThreads) void bgemm_f32_tiled_kernel(
                         : f32x4{};
         }
     };
-    auto store_op = [&](auto kcont, float* dst, const auto& reg, auto nfrag, auto rows) {
+    auto store_op = [&](auto kcont, float* dst, const auto& reg, auto nfrag) {
         constexpr bool KC = decltype(kcont)::value;
-        constexpr int NF = decltype(nfrag)::value, R = decltype(rows)::value;
+        constexpr int NF = decltype(nfrag)::value;
 #pragma unroll
         for (int i = 0; i < NF; ++i) {
             const int f = tid + kThreads * i;
@@ -230,15 +230,13 @@ __global__ __launch_bounds__(kThreads) void bgemm_f32_tiled_kernel(
     using KB = std::integral_constant<bool, TB>;   // B (K x N): rows over k when transposed
     using NA = std::integral_constant<int, kA4>;
     using NB = std::integral_constant<int, kB4>;
-    using RA = std::integral_constant<int, BM>;
-    using RB = std::integral_constant<int, BN>;
     auto load = [&](int k0) {
-        load_op(KA{}, Ab, lda, m0, M, k0, ra, NA{}, RA{});
-        load_op(KB{}, Bb, ldb, n0, N, k0, rb, NB{}, RB{});
+        load_op(KA{}, Ab, lda, m0, M, k0, ra, NA{});
+        load_op(KB{}, Bb, ldb, n0, N, k0, rb, NB{});
     };
     auto store = [&](int buf) {
-        store_op(KA{}, As[buf], ra, NA{}, RA{});
-        store_op(KB{}, Bs[buf], rb, NB{}, RB{});
+        store_op(KA{}, As[buf], ra, NA{});
+        store_op(KB{}, Bs[buf], rb, NB{});
     };
 
     f32x16 acc[I][J];

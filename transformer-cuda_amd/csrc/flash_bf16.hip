@@ -966,7 +966,6 @@ __global__ __launch_bounds__(kWave * kWaves, D >= 128 ? 1 : 2) void flash_bwd_dk
     using S = Swz<D, KT>;
     constexpr uint32_t kBuf = S::kBytes;  // one Q (or dO) buffer
     constexpr int kBlock = kWaves * kSub;
-    constexpr int NS = Prog::NS;
     __shared__ __attribute__((aligned(1024))) QgSmem<D, 1> sm;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & (kWave - 1);

@@ -23,13 +23,10 @@
 //   dP'^T = V dO^T - D       A = V rows, B = dO (VGPRs), accumulator from -D
 //   dS^T = 2^S'^T o dP'^T    lane l holds query l%32
 //   dQ^T += K^T dS^T         A = K^T (transposing reads of the K tile), B = dS^T
-// Lane l's -lse2 and -D are the same in all 16 rows of its accumulators: with one sub-block
-// per wave (bf16, d = 128, small grids; 128 queries per workgroup) the products start from
-// them (kDqStatInit); with two (three planes at d <= 64 on large grids: 256 queries, wave w
-// sub-blocks w and 7-w, as the forward) they enter as one more 16-wide contraction step,
-// the A operand (1, 1, 0, ...) times a statistic chunk (hi, lo, 0, ...) (NP = 3: three ones
-// and three terms).  NP = 3 streams 32-key tiles, so that the double-buffered K and V planes
-// leave room for two workgroups per CU.
+// Lane l's -lse2 and -D are the same in all 16 rows of its accumulators, so the products
+// start from them (no statistic contraction step).  A workgroup owns 128 queries, one
+// 32-query sub-block per wave.  NP = 3 streams 32-key tiles, so that the double-buffered K
+// and V planes leave room for two workgroups per CU.
 //
 // Stage 2, per 32-query half tile and a wave's 32 keys (d = 64, NP = 1: 18 MFMAs):
 //   S  = Q K^T        A = Q rows,  B = K (VGPRs)
@@ -152,23 +149,15 @@ __device__ __forceinline__ void load_operand(bf16x8 (&dst)[D / 16][NP],
 // Stage 1: D and dQ.
 // ---------------------------------------------------------------------------------------
 
-// How -lse2 and -D enter S^T and dP^T.  A lane holds one query, so its statistic is the same
-// in all 16 rows of its accumulator: with INIT each product's accumulator starts from the
-// statistic itself (a 16-register copy per lane, kept for the whole task: 32 VGPRs per
-// sub-block, no MFMA; the statistic exact in fp32); without it, from one more contraction
-// step, the A operand `one` times a statistic chunk ((hi, lo) bf16 terms; 8 VGPRs per
-// sub-block, two more MFMAs per half tile).  INIT where the registers allow it: one
-// sub-block per wave.
-template <int NSUB>
-constexpr bool kDqStatInit = NSUB == 1;
-
-// One 32-query sub-block of a wave.
+// The 32-query sub-block of a wave.  A lane holds one query, so its statistics are the same
+// in all 16 rows of its accumulators: S^T and dP^T start from them (a 16-register copy of
+// each per lane, kept for the whole task, exact in fp32), where one more contraction step
+// (the A operand ones times a statistic chunk) would cost two MFMAs per half tile.
 template <int D, int NP>
 struct DqSub {
     bf16x8 q[D / 16][NP];  // c * Q row of query col (B operand over d)
     bf16x8 g[D / 16][NP];  // dO row
-    bf16x8 xs, xd;         // statistic chunks: -lse2 (-1e30 for padded queries: P = 0), -D
-    f32x16 ls, ld;         // INIT: -lse2 and -D in every row
+    f32x16 ls, ld;         // -lse2 (-1e30 for padded queries: P = 0) and -D in every row
     f32x16 acc[D / 32];    // dQ^T
 };
 
@@ -203,7 +192,7 @@ __device__ __forceinline__ float chunk_dot_tree(const float* __restrict__ gp,
 // pre-multiplied by c = scale*log2 e (NP = 1: rounded to bf16, one extra rounding of ~2^-9
 // relative per element; NP = 3: in fp32, then split), so that the scores come out in the
 // log2 domain.  D = rowsum(dO o O) in fp32 from the stored O and dO.
-template <int D, int NP, bool INIT>
+template <int D, int NP>
 __device__ __forceinline__ void dq_init(DqSub<D, NP>& sb, const InT<NP>* __restrict__ qh,
                                         const InT<NP>* __restrict__ oh,
                                         const InT<NP>* __restrict__ gh,
@@ -233,15 +222,10 @@ __device__ __forceinline__ void dq_init(DqSub<D, NP>& sb, const InT<NP>* __restr
         if (half == 0) Dws[stat_off + qi] = dlt;
         nl = -(m[stat_off + qi] * kLog2e + log2f(l[stat_off + qi]));
     }
-    if constexpr (INIT) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            sb.ls[r] = nl;
-            sb.ld[r] = -dlt;
-        }
-    } else {
-        sb.xs = stat_chunk<NP>(nl, half);
-        sb.xd = stat_chunk<NP>(-dlt, half);
+    for (int r = 0; r < 16; ++r) {
+        sb.ls[r] = nl;
+        sb.ld[r] = -dlt;
     }
 #pragma unroll
     for (int dt = 0; dt < D / 32; ++dt) sb.acc[dt] = f32x16{};
@@ -266,51 +250,33 @@ __device__ __forceinline__ void dq_ds(f32x16& s, const f32x16& dp, bf16x8 (&db)[
     pack_planes<NP>(s, 1, db[1]);
 }
 
-// One 32-key half tile for sub-block 1, and sub-block 0 too when BOTH.  ka/va: this lane's
-// row-read addresses in plane 0 of the K / V tile; kta: transposing-read addresses in plane
-// 0 of the K tile; plane i lies i tile sizes further.  -lse2 and -D enter S^T and dP^T as
-// the products' initial accumulators (INIT) or as one more contraction step (kDqStatInit).
-template <int D, bool BOTH, int NP, bool INIT>
+// One 32-key half tile of the wave's sub-block.  ka/va: this lane's row-read addresses in
+// plane 0 of the K / V tile; kta: transposing-read addresses in plane 0 of the K tile; plane
+// i lies i tile sizes further.  S^T and dP^T start from -lse2 and -D.
+template <int D, int NP>
 __device__ __forceinline__ void dq_half(int kb, const uint32_t (&ka)[D / 16],
                                         const uint32_t (&va)[D / 16],
-                                        const uint32_t (&kta)[D / 32], const bf16x8& one,
-                                        DqSub<D, NP>& sb0, DqSub<D, NP>& sb1, int qj0, int qj1,
+                                        const uint32_t (&kta)[D / 32], DqSub<D, NP>& sb, int qj,
                                         int col, int half) {
     constexpr uint32_t kPlane = Swz<D, kKeyTileDq<NP>>::kBytes;
-    f32x16 s0, s1, p0, p1;
-    if constexpr (INIT) {
-        s1 = sb1.ls;
-        if constexpr (BOTH) s0 = sb0.ls;
-    } else {
-        s1 = mfma_32x32x16_bf16(one, sb1.xs, f32x16{});
-        if constexpr (BOTH) s0 = mfma_32x32x16_bf16(one, sb0.xs, f32x16{});
-    }
+    f32x16 s = sb.ls;
 #pragma unroll
     for (int st = 0; st < D / 16; ++st) {
         bf16x8 a[NP];
 #pragma unroll
         for (int i = 0; i < NP; ++i) a[i] = lds_b128(ka[st] + i * kPlane);
-        s1 = mma_planes<NP>(a, sb1.q[st], s1);
-        if constexpr (BOTH) s0 = mma_planes<NP>(a, sb0.q[st], s0);
+        s = mma_planes<NP>(a, sb.q[st], s);
     }
-    if constexpr (INIT) {
-        p1 = sb1.ld;
-        if constexpr (BOTH) p0 = sb0.ld;
-    } else {
-        p1 = mfma_32x32x16_bf16(one, sb1.xd, f32x16{});
-        if constexpr (BOTH) p0 = mfma_32x32x16_bf16(one, sb0.xd, f32x16{});
-    }
+    f32x16 p = sb.ld;
 #pragma unroll
     for (int st = 0; st < D / 16; ++st) {
         bf16x8 a[NP];
 #pragma unroll
         for (int i = 0; i < NP; ++i) a[i] = lds_b128(va[st] + i * kPlane);
-        p1 = mma_planes<NP>(a, sb1.g[st], p1);
-        if constexpr (BOTH) p0 = mma_planes<NP>(a, sb0.g[st], p0);
+        p = mma_planes<NP>(a, sb.g[st], p);
     }
-    bf16x8 d0[2][NP], d1[2][NP];
-    dq_ds<NP>(s1, p1, d1, kb, qj1, col, half);
-    if constexpr (BOTH) dq_ds<NP>(s0, p0, d0, kb, qj0, col, half);
+    bf16x8 d[2][NP];
+    dq_ds<NP>(s, p, d, kb, qj, col, half);
 #pragma unroll
     for (int dt = 0; dt < D / 32; ++dt) {
 #pragma unroll
@@ -319,8 +285,7 @@ __device__ __forceinline__ void dq_half(int kb, const uint32_t (&ka)[D / 16],
 #pragma unroll
             for (int i = 0; i < NP; ++i)
                 a[i] = lds_tr(kta[dt] + i * kPlane + u * Swz<D>::rows(16), Swz<D>::rows(8));
-            sb1.acc[dt] = mma_planes<NP>(a, d1[u], sb1.acc[dt]);
-            if constexpr (BOTH) sb0.acc[dt] = mma_planes<NP>(a, d0[u], sb0.acc[dt]);
+            sb.acc[dt] = mma_planes<NP>(a, d[u], sb.acc[dt]);
         }
     }
 }
@@ -343,16 +308,15 @@ struct DqArgs {
     int serp;      // map_block's serpentine order (set at launch)
 };
 
-// NSUB = 2: 256 queries per workgroup, wave w owns sub-blocks w (0) and 7-w (1).
-// NSUB = 1: 128 queries per workgroup, wave w owns sub-block w (1).
-template <int D, int NSUB, int NP>
+// 128 queries per workgroup, wave w owns the 32-query sub-block w.
+template <int D, int NP>
 __global__ __launch_bounds__(kWave* kWaves) void flash_bwd_dq_bf16_kernel(DqArgs<NP> a,
                                                                          int nblk) {
     constexpr int KT = kKeyTileDq<NP>;
     constexpr int kHalves = KT / 32;
     using S = Swz<D, KT>;
     constexpr uint32_t kBuf = NP * S::kBytes;  // one K (or V) buffer: NP plane tiles
-    constexpr int kBlock = kWaves * NSUB * kSub;
+    constexpr int kBlock = kWaves * kSub;
     __shared__ __attribute__((aligned(1024))) KvSmem<D, NP> sm;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     const int lane = threadIdx.x & (kWave - 1);
@@ -362,8 +326,7 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_bwd_dq_bf16_kernel(DqArgs
     int bh, blk;
     map_block(blockIdx.x, a.BH, nblk, true, a.serp != 0, bh, blk);
     const int q0 = blk * kBlock;
-    const int qj0 = q0 + kSub * wave;
-    const int qj1 = NSUB == 2 ? q0 + kSub * (2 * kWaves - 1 - wave) : qj0;
+    const int qj = q0 + kSub * wave;
     const size_t qoff = a.qv.off(bh), koff = a.kv.off(bh), ooff = a.ov.off(bh),
                  goff = a.gv.off(bh);
     const int krs = a.kv.row;
@@ -389,28 +352,18 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_bwd_dq_bf16_kernel(DqArgs
     };
     copy_tile(0);
 
-    constexpr bool kInit = kDqStatInit<NSUB>;
-    DqSub<D, NP> sb0, sb1;
-    dq_init<D, NP, kInit>(sb1, a.q + qoff, a.o + ooff, a.dO + ooff, a.m, a.l, a.Dws, a.qv.row,
-                          a.ov.row, stat_off, qj1 + col, T, half, c);
-    if constexpr (NSUB == 2)
-        dq_init<D, NP, kInit>(sb0, a.q + qoff, a.o + ooff, a.dO + ooff, a.m, a.l, a.Dws,
-                              a.qv.row, a.ov.row, stat_off, qj0 + col, T, half, c);
+    DqSub<D, NP> sb;
+    dq_init<D, NP>(sb, a.q + qoff, a.o + ooff, a.dO + ooff, a.m, a.l, a.Dws, a.qv.row,
+                   a.ov.row, stat_off, qj + col, T, half, c);
     if constexpr (NP > 1) {
-        if (a.gp != nullptr) {
-            store_planes<D, NP>(a.gp + koff, a.pstride, sb1.g, qj1 + col, T, half);
-            if constexpr (NSUB == 2)
-                store_planes<D, NP>(a.gp + koff, a.pstride, sb0.g, qj0 + col, T, half);
-        }
+        if (a.gp != nullptr) store_planes<D, NP>(a.gp + koff, a.pstride, sb.g, qj + col, T, half);
     }
-    const bf16x8 one = ones_chunk<NP>(half);
 
     uint32_t roff[D / 16], troff[D / 32];
     lane_offsets<D>(lane, roff, troff);
 
     const int nhalf_t = (T + 31) / 32;
-    const int hA = NSUB == 2 ? min(qj0 / 32 + 1, nhalf_t) : 0;
-    const int hB = min(qj1 / 32 + 1, nhalf_t);
+    const int hB = min(qj / 32 + 1, nhalf_t);  // half tiles of this wave; the last one masks
     const int hend = kHalves * ntile;
     uint32_t ka[D / 16], va[D / 16], kta[D / 32];
     auto tile_sync = [&](int hh) {
@@ -431,13 +384,9 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_bwd_dq_bf16_kernel(DqArgs
         for (int dt = 0; dt < D / 32; ++dt) kta[dt] = k_lds + base + troff[dt];
     };
     int hh = 0;
-    for (; hh < hA; ++hh) {
-        tile_sync(hh);
-        dq_half<D, true, NP, kInit>(32 * hh, ka, va, kta, one, sb0, sb1, qj0, qj1, col, half);
-    }
     for (; hh < hB; ++hh) {
         tile_sync(hh);
-        dq_half<D, false, NP, kInit>(32 * hh, ka, va, kta, one, sb0, sb1, qj0, qj1, col, half);
+        dq_half<D, NP>(32 * hh, ka, va, kta, sb, qj, col, half);
     }
     for (; hh < hend; ++hh) tile_sync(hh);
 
@@ -445,14 +394,9 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_bwd_dq_bf16_kernel(DqArgs
         // after the last tile barrier the buffer without the last tile is idle
         const uint32_t stage = wave_stage(lds_addr(sm.k[ntile & 1][0]),
                                           lds_addr(sm.v[ntile & 1][0]), wave, kStageBytes<D, NP>);
-        store_row_staged<D>(a.dq + goff, qj1, T, lane, sb1.acc, a.scale, a.gv.row, stage);
-        if constexpr (NSUB == 2)
-            store_row_staged<D>(a.dq + goff, qj0, T, lane, sb0.acc, a.scale, a.gv.row, stage);
+        store_row_staged<D>(a.dq + goff, qj, T, lane, sb.acc, a.scale, a.gv.row, stage);
     } else {
-        if (qj1 + col < T) store_row<D>(a.dq + goff, qj1 + col, half, sb1.acc, a.scale, a.gv.row);
-        if constexpr (NSUB == 2)
-            if (qj0 + col < T)
-                store_row<D>(a.dq + goff, qj0 + col, half, sb0.acc, a.scale, a.gv.row);
+        if (qj + col < T) store_row<D>(a.dq + goff, qj + col, half, sb.acc, a.scale, a.gv.row);
     }
 }
 
@@ -1451,27 +1395,16 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_bwd_dq_ds_kernel(DqDsArgs
     }
 }
 
-template <int D, int NSUB, int NP>
-void dq_launch(DqArgs<NP> a, hipStream_t stream) {
-    constexpr int kBlock = kWaves * NSUB * kSub;
-    const int nblk = (a.T + kBlock - 1) / kBlock;
-    const auto kernel = flash_bwd_dq_bf16_kernel<D, NSUB, NP>;
+// One 32-query sub-block per wave at every shape: with the statistics as initial
+// accumulators it measured faster than two sub-blocks per wave with the fold step (bf16
+// B16 H16 T2048 d64 dQ 230.3 -> 217.9 us, B8 H16 T2048 122.9 -> 112.8; three planes at d = 32
+// within 1%, bitwise the same).
+template <int D, int NP>
+void dq_dispatch(DqArgs<NP> a, hipStream_t stream) {
+    const int nblk = (a.T + kWaves * kSub - 1) / (kWaves * kSub);
+    const auto kernel = flash_bwd_dq_bf16_kernel<D, NP>;
     a.serp = a.BH * nblk <= resident_capacity(kernel, kWave * kWaves, 0) ? 1 : 0;
     hipLaunchKernelGGL(kernel, dim3(a.BH * nblk), dim3(kWave * kWaves), 0, stream, a, nblk);
-}
-
-template <int D, int NP>
-void dq_dispatch(const DqArgs<NP>& a, hipStream_t stream) {
-    // One sub-block per wave, whose statistics enter S^T and dP^T as initial accumulators
-    // (kDqStatInit), for bf16 (B16 H16 T2048 d64 dQ 230.3 -> 217.9 us, B8 H16 T2048 122.9 ->
-    // 112.8, against two sub-blocks with the fold step) and at d = 128 (registers); three
-    // planes keep two sub-blocks on grids that fill the chip.
-    if constexpr (NP == 1 || D >= 128)
-        dq_launch<D, 1, NP>(a, stream);
-    else if (use_single_subblock(a.BH, a.T))
-        dq_launch<D, 1, NP>(a, stream);
-    else
-        dq_launch<D, 2, NP>(a, stream);
 }
 
 template <int D, int NP>

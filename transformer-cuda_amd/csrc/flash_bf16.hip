@@ -233,13 +233,14 @@ __device__ __forceinline__ void dq_init(DqSub<D, NP>& sb, const InT<NP>* __restr
 
 // s = S'^T = K (cQ)^T - lse2, dp = dP'^T = V dO^T - D of keys kb.. (rows) x queries qj + col
 // (columns) -> dS^T = 2^s o dp as the two B operands (NP planes each) of dQ^T += K^T dS^T.
-// Keys past the query get P = 0.
-template <int NP>
+// MASK: the half tile crosses the diagonal of the sub-block (keys past the query get P = 0);
+// a compile-time flag, so that the other half tiles carry no compare and select per score.
+template <int NP, bool MASK>
 __device__ __forceinline__ void dq_ds(f32x16& s, const f32x16& dp, bf16x8 (&db)[2][NP], int kb,
                                       int qj, int col, int half) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) s[r] = exp2_fast(s[r]);
-    if (kb + 31 > qj) {  // the half tile crosses the diagonal of this sub-block
+    if constexpr (MASK) {
 #pragma unroll
         for (int r = 0; r < 16; ++r)
             if (kb + acc_row(r, half) > qj + col) s[r] = 0.0f;
@@ -250,10 +251,10 @@ __device__ __forceinline__ void dq_ds(f32x16& s, const f32x16& dp, bf16x8 (&db)[
     pack_planes<NP>(s, 1, db[1]);
 }
 
-// One 32-key half tile of the wave's sub-block.  ka/va: this lane's row-read addresses in
-// plane 0 of the K / V tile; kta: transposing-read addresses in plane 0 of the K tile; plane
-// i lies i tile sizes further.  S^T and dP^T start from -lse2 and -D.
-template <int D, int NP>
+// One 32-key half tile of the wave's sub-block (MASK: its diagonal one).  ka/va: this lane's
+// row-read addresses in plane 0 of the K / V tile; kta: transposing-read addresses in plane
+// 0 of the K tile; plane i lies i tile sizes further.  S^T and dP^T start from -lse2 and -D.
+template <int D, int NP, bool MASK>
 __device__ __forceinline__ void dq_half(int kb, const uint32_t (&ka)[D / 16],
                                         const uint32_t (&va)[D / 16],
                                         const uint32_t (&kta)[D / 32], DqSub<D, NP>& sb, int qj,
@@ -276,7 +277,7 @@ __device__ __forceinline__ void dq_half(int kb, const uint32_t (&ka)[D / 16],
         p = mma_planes<NP>(a, sb.g[st], p);
     }
     bf16x8 d[2][NP];
-    dq_ds<NP>(s, p, d, kb, qj, col, half);
+    dq_ds<NP, MASK>(s, p, d, kb, qj, col, half);
 #pragma unroll
     for (int dt = 0; dt < D / 32; ++dt) {
 #pragma unroll
@@ -383,10 +384,16 @@ __global__ __launch_bounds__(kWave* kWaves) void flash_bwd_dq_bf16_kernel(DqArgs
 #pragma unroll
         for (int dt = 0; dt < D / 32; ++dt) kta[dt] = k_lds + base + troff[dt];
     };
+    // the wave's half tiles 0 .. hB-2 unmasked, then its diagonal one (hB = 0: none)
     int hh = 0;
-    for (; hh < hB; ++hh) {
+    for (; hh + 1 < hB; ++hh) {
         tile_sync(hh);
-        dq_half<D, NP>(32 * hh, ka, va, kta, sb, qj, col, half);
+        dq_half<D, NP, false>(32 * hh, ka, va, kta, sb, qj, col, half);
+    }
+    if (hh < hB) {
+        tile_sync(hh);
+        dq_half<D, NP, true>(32 * hh, ka, va, kta, sb, qj, col, half);
+        ++hh;
     }
     for (; hh < hend; ++hh) tile_sync(hh);
 

@@ -46,7 +46,7 @@ def _check(got, want, names=("o", "dq", "dk", "dv"), tol=TOL, tag=""):
 
 
 @pytest.mark.parametrize("d", [32, 64, 128])
-@pytest.mark.parametrize("T", [1, 17, 64, 100, 257])
+@pytest.mark.parametrize("T", [1, 17, 33, 64, 100, 160, 257])
 def test_shapes_vs_oracle(lib, T, d):
     B, H = 2, 2
     q, k, v, do = _rounded(B, H, T, d, seed=T + d)
@@ -70,6 +70,20 @@ def test_shapes_vs_oracle(lib, T, d):
     assert np.all(got["m"] <= want.m.numpy() + bound + mag), "m: at most the row maximum"
     lse = got["m"] + np.log(got["l"])
     assert np.all(np.abs(lse - want.lse.numpy()) <= bound), "m + ln l"
+
+
+@pytest.mark.parametrize("B,H,T,d", [(2, 4, 300, 64), (1, 8, 160, 128), (2, 8, 383, 32),
+                                     (1, 16, 640, 64), (4, 64, 200, 64)])
+def test_xcd_block_order_ragged_vs_oracle(lib, B, H, T, d):
+    """B*H a multiple of 8: every kernel maps workgroups to heads XCD by XCD (serpentine
+    rounds where the grid fits on the device at once, rank order where it does not; the
+    head groups start at config 3's size, test_config3_full), at lengths that leave the last
+    block of each head partly past T."""
+    q, k, v, do = _rounded(B, H, T, d, seed=B * H + T + d)
+    scale = default_scale(d)
+    want = ref.attention_fwd_bwd(q, k, v, do, scale, dtype=torch.float32)
+    got = gpu_fwd_bwd(lib, q, k, v, do, scale, dtype=torch.bfloat16)
+    _check(got, want, tag=f"B={B} H={H} T={T} d={d}")
 
 
 def test_reference_kat(lib):

@@ -78,6 +78,22 @@ def test_shapes_vs_oracle(lib, T, d):
     np.testing.assert_allclose(got["l"], want.l.numpy(), rtol=1e-5)
 
 
+@pytest.mark.parametrize("B,H,T,d", [(2, 4, 300, 64), (1, 8, 160, 128), (2, 8, 383, 32),
+                                     (4, 64, 200, 64)])
+def test_xcd_block_order_ragged_vs_oracle(lib, B, H, T, d):
+    """B*H a multiple of 8, where the shared-tile kernels map workgroups to heads XCD by XCD
+    and the persistent ones fill per-XCD task queues, at lengths that leave the last block
+    of each head partly past T."""
+    q, k, v, do = ref.seeded_inputs(B, H, T, d, seed=B * H + T + d)
+    scale = default_scale(d)
+    want = ref.attention_fwd_bwd(q, k, v, do, scale, dtype=torch.float32)
+    got = gpu_fwd_bwd(lib, q, k, v, do, scale)
+    for n in ("o", "dq", "dk", "dv"):
+        assert max_abs(got[n], getattr(want, n).numpy()) <= TOL, n
+    assert max_abs(got["m"], want.m.numpy()) <= TOL
+    np.testing.assert_allclose(got["l"], want.l.numpy(), rtol=1e-5)
+
+
 @pytest.mark.parametrize("d,T", [(64, 2048), (64, 2080), (128, 2080)])
 def test_shared_tile_boundary_vs_oracle(lib, d, T):
     """Either side of the sequence length where the fp32 kernels change form (d = 64: the

@@ -51,7 +51,7 @@ def mfma_forward(lib, qkv, B, H, T, d, scale):
 
 
 SHAPES = [(1, 1, 1, 64), (2, 3, 17, 32), (1, 2, 100, 64), (2, 2, 257, 32), (2, 4, 640, 64),
-          (1, 2, 1000, 64)]
+          (1, 2, 1000, 64), (2, 8, 383, 32), (1, 8, 300, 64)]
 
 
 @pytest.mark.parametrize("B,H,T,d", SHAPES)
@@ -158,7 +158,7 @@ def x3_fwd_bwd(lib, qkv, do, B, H, T, d, scale, merged=False, kv_ready=True):
 
 
 BWD_SHAPES = [(1, 1, 1, 64), (2, 3, 17, 32), (1, 2, 100, 64), (2, 2, 257, 32),
-              (2, 4, 640, 64), (1, 1, 1000, 64)]
+              (2, 4, 640, 64), (1, 1, 1000, 64), (2, 8, 383, 32), (1, 8, 300, 64)]
 
 
 @pytest.mark.parametrize("B,H,T,d", BWD_SHAPES)

@@ -124,13 +124,19 @@ int resident_capacity(Kernel kernel, int block, size_t lds_bytes) {
     for (const Entry& e : cache)
         if (e.fn == fn && e.dev == dev) cap = e.cap;
     if (cap == 0) {
+        // a failed query falls back to a safe guess and clears its error, which the launch
+        // check after this call would otherwise report as the launch's
         int per_cu = 0, cus = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, block, lds_bytes) !=
-            hipSuccess)
+            hipSuccess) {
+            (void)hipGetLastError();
             per_cu = 1;
+        }
         if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
-            hipSuccess)
+            hipSuccess) {
+            (void)hipGetLastError();
             cus = 256;
+        }
         cap = (per_cu < 1 ? 1 : per_cu) * cus;
         cache[cache_next] = Entry{fn, dev, cap};
         cache_next = (cache_next + 1) % 16;
